@@ -1,0 +1,78 @@
+"""Builds libglacier_paged.so (gfx950 kernels + host runtime + C ABI) in-tree.
+
+    python glacier.serve_amd/build.py
+
+Every call recompiles.  hipcc cross-compiles for gfx950 without a GPU.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libglacier_paged.so"
+
+SOURCES = [
+    CSRC / "gsp_decode.hip",
+    CSRC / "gsp_pool_ops.hip",
+    CSRC / "gsp_runtime.cpp",
+    CSRC / "gsp_host_meta.cpp",
+    CSRC / "gsp_status.cpp",
+]
+
+ARCH = "gfx950"
+
+# Packed FP32 (v_pk_*_f32) is switched off for all device code.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def hipcc() -> str:
+    cand = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(cand).exists():
+        raise RuntimeError("hipcc not found: the HIP toolchain is required to build libglacier_paged.so")
+    return cand
+
+
+def build(verbose: bool = False) -> Path:
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [
+        hipcc(),
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-Wall",
+        "-Wno-unused-result",
+        "-fvisibility=hidden",
+        "-fvisibility-inlines-hidden",
+        f"-I{ROOT / 'include'}",
+        *DEVICE_FLAGS,
+        "-x",
+        "hip",
+        *[str(s) for s in SOURCES],
+        "-o",
+        str(tmp),
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, cwd=str(ROOT), capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
+    if verbose and res.stderr.strip():
+        # hipcc's host pass warns about the device-only target feature; keep the rest visible.
+        lines = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln]
+        if lines:
+            print("\n".join(lines))
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,251 @@
+// Host-side block metadata: the free-stack / refcount half of PagedBlockPool
+// (PagedBlockPool.cs:112-121,178-299,332-353) and BlockTable
+// (BlockTable.cs:13-117).  Pages themselves live in a device pool; an attached
+// pool receives the copy-on-write page copies.
+#include <algorithm>
+#include <atomic>
+#include <memory>
+#include <mutex>
+#include <vector>
+
+#include "../../include/glacier_paged.h"
+#include "gsp_status.h"
+
+struct gsp_block_allocator {
+    int32_t total = 0;
+    int32_t block_size = 0;
+    std::mutex stack_mu;
+    std::vector<int32_t> free_stack;  // back() is the top of the LIFO stack
+    std::unique_ptr<std::atomic<int32_t>[]> allocated;
+    std::unique_ptr<std::atomic<int32_t>[]> refs;
+    gsp_ctx* ctx = nullptr;
+    gsp_pool* pool = nullptr;
+
+    bool try_allocate(int32_t* id) {
+        int32_t b;
+        {
+            std::lock_guard<std::mutex> lk(stack_mu);
+            if (free_stack.empty()) {
+                *id = -1;
+                return false;
+            }
+            b = free_stack.back();
+            free_stack.pop_back();
+        }
+        allocated[b].store(1);
+        refs[b].store(1);
+        *id = b;
+        return true;
+    }
+
+    int32_t release(int32_t id) {
+        if (id < 0 || id >= total) return 0;
+        const int32_t remaining = refs[id].fetch_sub(1) - 1;
+        if (remaining < 0) {
+            refs[id].store(0);
+            return 0;
+        }
+        if (remaining == 0) {
+            int32_t expected = 1;
+            if (allocated[id].compare_exchange_strong(expected, 0)) {
+                std::lock_guard<std::mutex> lk(stack_mu);
+                free_stack.push_back(id);
+            }
+        }
+        return remaining;
+    }
+};
+
+struct gsp_block_table {
+    gsp_block_allocator* alloc = nullptr;
+    std::vector<int32_t> ids;
+    int32_t token_count = 0;
+};
+
+extern "C" {
+
+int gsp_block_allocator_create(int32_t total_blocks, int32_t block_size, gsp_block_allocator** out) {
+    gsp::clear_error();
+    if (!out) return gsp::fail(GSP_E_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (total_blocks < 1) return gsp::fail(GSP_E_INVALID_ARG, "totalBlocks must be >= 1 (got %d)", total_blocks);
+    if (block_size < 1) return gsp::fail(GSP_E_INVALID_ARG, "blockSize must be >= 1 (got %d)", block_size);
+    gsp_block_allocator* a = new gsp_block_allocator();
+    a->total = total_blocks;
+    a->block_size = block_size;
+    a->allocated.reset(new std::atomic<int32_t>[total_blocks]);
+    a->refs.reset(new std::atomic<int32_t>[total_blocks]);
+    a->free_stack.reserve(total_blocks);
+    // Pushing total-1 .. 0 leaves 0 on top: the first pop returns block 0.
+    for (int32_t i = total_blocks - 1; i >= 0; --i) {
+        a->allocated[i].store(0);
+        a->refs[i].store(0);
+        a->free_stack.push_back(i);
+    }
+    *out = a;
+    return GSP_OK;
+}
+
+void gsp_block_allocator_destroy(gsp_block_allocator* a) { delete a; }
+
+int gsp_block_allocator_attach_pool(gsp_block_allocator* a, gsp_ctx* ctx, gsp_pool* pool) {
+    gsp::clear_error();
+    if (!a) return gsp::fail(GSP_E_INVALID_ARG, "allocator is NULL");
+    if ((ctx == nullptr) != (pool == nullptr)) return gsp::fail(GSP_E_INVALID_ARG, "ctx and pool must both be set or both NULL");
+    if (pool) {
+        size_t kb = 0;
+        if (gsp_pool_arenas(pool, nullptr, nullptr, &kb, nullptr) != GSP_OK) return GSP_E_INVALID_ARG;
+    }
+    a->ctx = ctx;
+    a->pool = pool;
+    return GSP_OK;
+}
+
+int gsp_block_allocator_try_allocate(gsp_block_allocator* a, int32_t* block_id) {
+    gsp::clear_error();
+    if (!a || !block_id) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument"), 0;
+    return a->try_allocate(block_id) ? 1 : 0;
+}
+
+int gsp_block_allocator_retain(gsp_block_allocator* a, int32_t block_id) {
+    gsp::clear_error();
+    if (!a) return gsp::fail(GSP_E_INVALID_ARG, "allocator is NULL"), -1;
+    if (block_id < 0 || block_id >= a->total) {
+        gsp::fail(GSP_E_INVALID_ARG, "physicalBlockId %d out of range [0, %d)", block_id, a->total);
+        return -1;
+    }
+    return a->refs[block_id].fetch_add(1) + 1;
+}
+
+int gsp_block_allocator_release(gsp_block_allocator* a, int32_t block_id) {
+    gsp::clear_error();
+    if (!a) return 0;
+    return a->release(block_id);
+}
+
+int gsp_block_allocator_ref_count(const gsp_block_allocator* a, int32_t block_id) {
+    if (!a || block_id < 0 || block_id >= a->total) return 0;
+    return a->refs[block_id].load();
+}
+
+int gsp_block_allocator_free_count(const gsp_block_allocator* a) {
+    if (!a) return 0;
+    std::lock_guard<std::mutex> lk(const_cast<gsp_block_allocator*>(a)->stack_mu);
+    return (int)a->free_stack.size();
+}
+
+int gsp_block_allocator_total(const gsp_block_allocator* a) { return a ? a->total : 0; }
+
+int gsp_block_table_create(gsp_block_allocator* a, gsp_block_table** out) {
+    gsp::clear_error();
+    if (!a || !out) return gsp::fail(GSP_E_INVALID_ARG, "pool/out is NULL");
+    gsp_block_table* t = new gsp_block_table();
+    t->alloc = a;
+    t->ids.reserve(16);
+    *out = t;
+    return GSP_OK;
+}
+
+void gsp_block_table_destroy(gsp_block_table* t) { delete t; }
+
+int gsp_block_table_attach_prefix(gsp_block_table* t, const int32_t* ids, int32_t n, int32_t token_count) {
+    gsp::clear_error();
+    if (!t) return gsp::fail(GSP_E_INVALID_ARG, "table is NULL");
+    if (token_count < 0) return gsp::fail(GSP_E_INVALID_ARG, "tokenCount must be >= 0 (got %d)", token_count);
+    if (n < 0 || (n > 0 && !ids)) return gsp::fail(GSP_E_INVALID_ARG, "prefix span is invalid");
+    t->ids.insert(t->ids.end(), ids, ids + n);
+    t->token_count = token_count;
+    return GSP_OK;
+}
+
+int gsp_block_table_append_token(gsp_block_table* t, int32_t* block_id, int32_t* offset) {
+    gsp::clear_error();
+    if (!t || !block_id || !offset) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument"), 0;
+    gsp_block_allocator* a = t->alloc;
+    const int32_t bs = a->block_size;
+    if (t->token_count % bs == 0) {
+        int32_t nb;
+        if (!a->try_allocate(&nb)) {
+            *block_id = -1;
+            *offset = -1;
+            return 0;
+        }
+        t->ids.push_back(nb);
+    } else {
+        const int32_t last = t->ids.back();
+        if (gsp_block_allocator_ref_count(a, last) > 1) {
+            // Copy-on-write fork of a shared partial page (BlockTable.cs:60-73).
+            const int32_t in_block = t->token_count % bs;
+            int32_t forked;
+            if (!a->try_allocate(&forked)) {
+                *block_id = -1;
+                *offset = -1;
+                return 0;
+            }
+            if (a->pool) {
+                int rc = gsp_pool_copy_block(a->ctx, a->pool, last, forked, in_block);
+                if (rc) {
+                    a->release(forked);
+                    *block_id = -1;
+                    *offset = -1;
+                    return 0;
+                }
+            }
+            a->release(last);
+            t->ids.back() = forked;
+        }
+    }
+    *block_id = t->ids.back();
+    *offset = t->token_count % bs;
+    t->token_count++;
+    return 1;
+}
+
+int gsp_block_table_append_tokens(gsp_block_table* t, int32_t n) {
+    gsp::clear_error();
+    if (!t) return gsp::fail(GSP_E_INVALID_ARG, "table is NULL"), 0;
+    int32_t b, o, done = 0;
+    while (done < n && gsp_block_table_append_token(t, &b, &o)) ++done;
+    return done;
+}
+
+int gsp_block_table_token_location(const gsp_block_table* t, int32_t token, int32_t* block_id, int32_t* offset) {
+    gsp::clear_error();
+    if (!t || !block_id || !offset) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument");
+    const int32_t bs = t->alloc->block_size;
+    const int32_t idx = token < 0 ? -1 : token / bs;
+    if (idx < 0 || idx >= (int32_t)t->ids.size())
+        return gsp::fail(GSP_E_INVALID_ARG, "token %d has no block (table holds %zu)", token, t->ids.size());
+    *block_id = t->ids[idx];
+    *offset = token % bs;
+    return GSP_OK;
+}
+
+int gsp_block_table_block_id(const gsp_block_table* t, int32_t index) {
+    gsp::clear_error();
+    if (!t || index < 0 || index >= (int32_t)t->ids.size()) {
+        gsp::fail(GSP_E_INVALID_ARG, "block index %d out of range", index);
+        return -1;
+    }
+    return t->ids[index];
+}
+
+int gsp_block_table_token_count(const gsp_block_table* t) { return t ? t->token_count : 0; }
+
+int gsp_block_table_block_count(const gsp_block_table* t) { return t ? (int)t->ids.size() : 0; }
+
+int gsp_block_table_ids(const gsp_block_table* t, int32_t* out, int32_t cap) {
+    if (!t) return 0;
+    const int32_t n = (int32_t)t->ids.size();
+    if (out && cap > 0) std::copy(t->ids.begin(), t->ids.begin() + std::min(n, cap), out);
+    return n;
+}
+
+void gsp_block_table_release_all(gsp_block_table* t) {
+    if (!t) return;
+    for (int32_t id : t->ids) t->alloc->release(id);
+    t->ids.clear();
+    t->token_count = 0;
+}
+
+}  // extern "C"

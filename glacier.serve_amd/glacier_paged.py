@@ -1,0 +1,547 @@
+"""Python binding of libglacier_paged.so (ctypes over the C ABI in
+include/glacier_paged.h).
+
+Names follow the reference's C# API so that callers read like the reference:
+``BlockAllocator`` / ``BlockTable`` mirror the block-id half of
+``PagedBlockPool`` and ``BlockTable`` (PagedBlockPool.cs:178-299,
+BlockTable.cs:13-117); ``Context.compute_attention`` mirrors
+``PagedAttentionKernel.ComputeAttention`` (PagedAttentionKernel.cs:17-32);
+``Context.pack_step`` + ``Context.attention_step`` are the batched step the
+engine tick issues (ContinuousBatchEngine.cs:426-468).  Status codes become
+exceptions the way the reference throws: ``InvalidArgument`` is a
+``ValueError`` (ArgumentOutOfRangeException), ``OutOfMemory`` is pool/HBM
+exhaustion, ``Unsupported`` is a shape the GPU path rejects.
+
+Device pointers (q, out, k, v) are plain integers, e.g. ``tensor.data_ptr()``.
+There is no CPU fallback: if the library is missing this module raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+try:  # torch, when present, must own the process's HIP runtime: it ships its
+    # own libamdhip64 under another file name, and loading ours first would put
+    # two HIP runtimes into one process.
+    import torch  # noqa: F401
+except Exception:  # pragma: no cover - torch is optional for host-only use
+    torch = None
+
+LIB_PATH = Path(__file__).resolve().with_name("libglacier_paged.so")
+
+GSP_OK = 0
+GSP_E_INVALID_ARG = 1
+GSP_E_OOM = 2
+GSP_E_UNSUPPORTED = 3
+GSP_E_HIP = 4
+GSP_E_STATE = 5
+
+KV_F32 = 0
+KV_F16 = 1
+BLOCK_SIZE = 16
+
+
+class GspError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+class InvalidArgument(GspError, ValueError):
+    pass
+
+
+class OutOfMemory(GspError, MemoryError):
+    pass
+
+
+class Unsupported(GspError):
+    pass
+
+
+class HipError(GspError):
+    pass
+
+
+class StateError(GspError):
+    pass
+
+
+_EXC = {
+    GSP_E_INVALID_ARG: InvalidArgument,
+    GSP_E_OOM: OutOfMemory,
+    GSP_E_UNSUPPORTED: Unsupported,
+    GSP_E_HIP: HipError,
+    GSP_E_STATE: StateError,
+}
+
+i32 = ctypes.c_int32
+i32p = ctypes.POINTER(ctypes.c_int32)
+vp = ctypes.c_void_p
+fp = ctypes.POINTER(ctypes.c_float)
+
+
+class PoolDesc(ctypes.Structure):
+    _fields_ = [
+        ("total_blocks", i32),
+        ("layers", i32),
+        ("heads_kv", i32),
+        ("head_dim", i32),
+        ("v_head_dim", i32),
+        ("block_size", i32),
+        ("kv_dtype", i32),
+    ]
+
+
+class StepDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_rows", i32),
+        ("max_seq_len", i32),
+        ("positions", i32p),
+        ("q_lens", i32p),
+        ("token_counts", i32p),
+        ("bt_offsets", i32p),
+        ("bt_ids", i32p),
+    ]
+
+
+class StepInfo(ctypes.Structure):
+    _fields_ = [
+        ("num_rows", i32),
+        ("total_q", i32),
+        ("packed_pages", i32),
+        ("decode_units", i32),
+        ("prefill_tiles", i32),
+        ("pages_per_split", i32),
+        ("kv_tokens", ctypes.c_int64),
+        ("staging_bytes", ctypes.c_int64),
+    ]
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 256),
+        ("arch", ctypes.c_char * 64),
+        ("compute_units", i32),
+        ("wavefront_size", i32),
+        ("clock_khz", i32),
+        ("memory_clock_khz", i32),
+        ("memory_bus_width_bits", i32),
+        ("total_global_mem", ctypes.c_int64),
+        ("lds_per_block", ctypes.c_int64),
+    ]
+
+
+# name -> (restype, argtypes); every symbol declared in include/glacier_paged.h.
+_SIGNATURES = {
+    "gsp_last_error": (ctypes.c_char_p, []),
+    "gsp_abi_version": (ctypes.c_int, []),
+    "gsp_device_info_get": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(DeviceInfo)]),
+    "gsp_init": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(vp)]),
+    "gsp_shutdown": (None, [vp]),
+    "gsp_set_stream": (ctypes.c_int, [vp, vp]),
+    "gsp_get_stream": (vp, [vp]),
+    "gsp_sync": (ctypes.c_int, [vp]),
+    "gsp_pool_create": (ctypes.c_int, [vp, ctypes.POINTER(PoolDesc), ctypes.POINTER(vp)]),
+    "gsp_pool_wrap": (ctypes.c_int, [vp, ctypes.POINTER(PoolDesc), vp, vp, ctypes.POINTER(vp)]),
+    "gsp_pool_destroy": (None, [vp]),
+    "gsp_pool_arenas": (
+        ctypes.c_int,
+        [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
+    ),
+    "gsp_pool_write_tokens": (ctypes.c_int, [vp, vp, i32, i32, i32p, i32p, vp, vp]),
+    "gsp_pool_copy_block": (ctypes.c_int, [vp, vp, i32, i32, i32]),
+    "gsp_pool_upload": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
+    "gsp_pool_download": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
+    "gsp_step_pack": (ctypes.c_int, [vp, ctypes.POINTER(StepDesc)]),
+    "gsp_step_get_info": (ctypes.c_int, [vp, ctypes.POINTER(StepInfo)]),
+    "gsp_step_download": (ctypes.c_int, [vp, i32p, i32p, i32p]),
+    "gsp_set_split_pages": (ctypes.c_int, [vp, i32]),
+    "gsp_attention_step": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, ctypes.c_float, fp]),
+    "gsp_compute_attention": (
+        ctypes.c_int,
+        [vp, vp, i32, i32, i32, vp, vp, i32p, i32, i32, i32, i32, i32, i32, ctypes.c_float, fp, i32, fp],
+    ),
+    "gsp_block_allocator_create": (ctypes.c_int, [i32, i32, ctypes.POINTER(vp)]),
+    "gsp_block_allocator_destroy": (None, [vp]),
+    "gsp_block_allocator_attach_pool": (ctypes.c_int, [vp, vp, vp]),
+    "gsp_block_allocator_try_allocate": (ctypes.c_int, [vp, i32p]),
+    "gsp_block_allocator_retain": (ctypes.c_int, [vp, i32]),
+    "gsp_block_allocator_release": (ctypes.c_int, [vp, i32]),
+    "gsp_block_allocator_ref_count": (ctypes.c_int, [vp, i32]),
+    "gsp_block_allocator_free_count": (ctypes.c_int, [vp]),
+    "gsp_block_allocator_total": (ctypes.c_int, [vp]),
+    "gsp_block_table_create": (ctypes.c_int, [vp, ctypes.POINTER(vp)]),
+    "gsp_block_table_destroy": (None, [vp]),
+    "gsp_block_table_attach_prefix": (ctypes.c_int, [vp, i32p, i32, i32]),
+    "gsp_block_table_append_token": (ctypes.c_int, [vp, i32p, i32p]),
+    "gsp_block_table_append_tokens": (ctypes.c_int, [vp, i32]),
+    "gsp_block_table_token_location": (ctypes.c_int, [vp, i32, i32p, i32p]),
+    "gsp_block_table_block_id": (ctypes.c_int, [vp, i32]),
+    "gsp_block_table_token_count": (ctypes.c_int, [vp]),
+    "gsp_block_table_block_count": (ctypes.c_int, [vp]),
+    "gsp_block_table_ids": (ctypes.c_int, [vp, i32p, i32]),
+    "gsp_block_table_release_all": (None, [vp]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads libglacier_paged.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python glacier.serve_amd/build.py` "
+            "(there is no CPU fallback for the paged-attention step)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != GSP_OK:
+        msg = load().gsp_last_error().decode(errors="replace")
+        raise _EXC.get(rc, GspError)(rc, msg)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(i32p)
+
+
+def device_info(device: int = 0) -> DeviceInfo:
+    info = DeviceInfo()
+    _check(load().gsp_device_info_get(device, ctypes.byref(info)))
+    return info
+
+
+class Context:
+    """One device context (GpuContext + the runner's device state)."""
+
+    def __init__(self, device: int = 0):
+        lib = load()
+        h = vp()
+        _check(lib.gsp_init(device, ctypes.byref(h)))
+        self._h = h
+        self._lib = lib
+        self._keep = []
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.gsp_shutdown(self._h)
+            self._h = vp()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def set_stream(self, hip_stream: Optional[int]) -> None:
+        _check(self._lib.gsp_set_stream(self._h, vp(hip_stream or 0)))
+
+    def sync(self) -> None:
+        _check(self._lib.gsp_sync(self._h))
+
+    def set_split_pages(self, pages: int) -> None:
+        _check(self._lib.gsp_set_split_pages(self._h, int(pages)))
+
+    # ---- step packing -------------------------------------------------
+    def pack_step(
+        self,
+        positions: Sequence[int],
+        token_counts: Sequence[int],
+        bt_offsets: Sequence[int],
+        bt_ids: Sequence[int],
+        max_seq_len: int,
+        q_lens: Optional[Sequence[int]] = None,
+    ) -> StepInfo:
+        pos = _i32(positions)
+        tc = _i32(token_counts)
+        off = _i32(bt_offsets)
+        ids = _i32(bt_ids) if len(bt_ids) else np.zeros(1, np.int32)
+        ql = _i32(q_lens) if q_lens is not None else None
+        d = StepDesc()
+        d.num_rows = len(pos)
+        d.max_seq_len = int(max_seq_len)
+        d.positions = _ptr(pos)
+        d.q_lens = _ptr(ql) if ql is not None else ctypes.cast(None, i32p)
+        d.token_counts = _ptr(tc)
+        d.bt_offsets = _ptr(off)
+        d.bt_ids = _ptr(ids)
+        _check(self._lib.gsp_step_pack(self._h, ctypes.byref(d)))
+        return self.step_info()
+
+    def step_info(self) -> StepInfo:
+        info = StepInfo()
+        _check(self._lib.gsp_step_get_info(self._h, ctypes.byref(info)))
+        return info
+
+    def download_step(self):
+        info = self.step_info()
+        rows = np.zeros(info.num_rows + 1, np.int32)
+        ids = np.zeros(max(1, info.packed_pages), np.int32)
+        ctxl = np.zeros(max(1, info.total_q), np.int32)
+        _check(self._lib.gsp_step_download(self._h, _ptr(rows), _ptr(ids), _ptr(ctxl)))
+        return rows, ids[: info.packed_pages], ctxl[: info.total_q]
+
+    # ---- attention ------------------------------------------------------
+    def attention_step(
+        self, pool: "Pool", layer: int, n_heads: int, q_ptr: int, out_ptr: int, attn_scale: float, sink_logit=None
+    ) -> None:
+        sink = None
+        if sink_logit is not None:
+            sink = ctypes.pointer(ctypes.c_float(sink_logit))
+        _check(
+            self._lib.gsp_attention_step(
+                self._h, pool.handle, int(layer), int(n_heads), vp(q_ptr), vp(out_ptr), float(attn_scale), sink
+            )
+        )
+
+    def compute_attention(
+        self,
+        stage_layer: int,
+        model_layer: int,
+        pos: int,
+        q_ptr: int,
+        out_ptr: int,
+        block_table: "BlockTable | Sequence[int]",
+        pool: "Pool",
+        n_heads: int,
+        n_heads_kv: int,
+        head_dim: int,
+        v_head_dim: int,
+        attn_scale: float,
+        max_seq_len: int,
+        token_count: Optional[int] = None,
+        sink_logit=None,
+    ) -> None:
+        """PagedAttentionKernel.ComputeAttention (PagedAttentionKernel.cs:17-32) on the GPU."""
+        if isinstance(block_table, BlockTable):
+            ids = block_table.as_span()
+            tc = block_table.token_count
+        else:
+            ids = _i32(block_table)
+            tc = int(token_count)
+        n = len(ids)
+        arr = ids if n else np.zeros(1, np.int32)
+        sink = ctypes.pointer(ctypes.c_float(sink_logit)) if sink_logit is not None else None
+        _check(
+            self._lib.gsp_compute_attention(
+                self._h, pool.handle, int(stage_layer), int(model_layer), int(pos), vp(q_ptr), vp(out_ptr),
+                _ptr(arr), n, int(tc), int(n_heads), int(n_heads_kv), int(head_dim), int(v_head_dim),
+                float(attn_scale), None, int(max_seq_len), sink,
+            )
+        )
+
+
+class Pool:
+    """Device K/V arenas in the reference PagedBlockPool layout."""
+
+    def __init__(self, ctx: Context, handle: vp, desc: PoolDesc):
+        self._ctx = ctx
+        self._h = handle
+        self.desc = desc
+
+    @classmethod
+    def create(cls, ctx: Context, total_blocks: int, layers: int, heads_kv: int, head_dim: int,
+               kv_dtype: int = KV_F32, v_head_dim: int = -1, block_size: int = BLOCK_SIZE) -> "Pool":
+        d = PoolDesc(total_blocks, layers, heads_kv, head_dim, v_head_dim, block_size, kv_dtype)
+        h = vp()
+        _check(load().gsp_pool_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)))
+        d2 = PoolDesc.from_buffer_copy(d)
+        if d2.v_head_dim <= 0:
+            d2.v_head_dim = d2.head_dim
+        return cls(ctx, h, d2)
+
+    @classmethod
+    def wrap(cls, ctx: Context, k_ptr: int, v_ptr: int, total_blocks: int, layers: int, heads_kv: int,
+             head_dim: int, kv_dtype: int = KV_F32, v_head_dim: int = -1, block_size: int = BLOCK_SIZE) -> "Pool":
+        d = PoolDesc(total_blocks, layers, heads_kv, head_dim, v_head_dim, block_size, kv_dtype)
+        h = vp()
+        _check(load().gsp_pool_wrap(ctx.handle, ctypes.byref(d), vp(k_ptr), vp(v_ptr), ctypes.byref(h)))
+        d2 = PoolDesc.from_buffer_copy(d)
+        if d2.v_head_dim <= 0:
+            d2.v_head_dim = d2.head_dim
+        return cls(ctx, h, d2)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def destroy(self) -> None:
+        if self._h:
+            load().gsp_pool_destroy(self._h)
+            self._h = vp()
+
+    def arenas(self):
+        k, v = vp(), vp()
+        kb, vb = ctypes.c_size_t(), ctypes.c_size_t()
+        _check(load().gsp_pool_arenas(self._h, ctypes.byref(k), ctypes.byref(v), ctypes.byref(kb), ctypes.byref(vb)))
+        return k.value, v.value, kb.value, vb.value
+
+    def upload(self, which: int, data: np.ndarray, offset_bytes: int = 0) -> None:
+        data = np.ascontiguousarray(data)
+        _check(load().gsp_pool_upload(self._ctx.handle, self._h, which, offset_bytes, data.ctypes.data, data.nbytes))
+
+    def download(self, which: int, nbytes: int, offset_bytes: int = 0) -> np.ndarray:
+        buf = np.empty(nbytes, np.uint8)
+        _check(load().gsp_pool_download(self._ctx.handle, self._h, which, offset_bytes, buf.ctypes.data, nbytes))
+        return buf
+
+    def write_tokens(self, layer: int, block_ids, slots, k_ptr: int, v_ptr: int) -> None:
+        """PagedBlockPool.Store (PagedBlockPool.cs:151-161) for a batch of tokens."""
+        b = _i32(block_ids)
+        s = _i32(slots)
+        if len(b) != len(s):
+            raise ValueError("block_ids and slots differ in length")
+        _check(load().gsp_pool_write_tokens(self._ctx.handle, self._h, int(layer), len(b), _ptr(b), _ptr(s),
+                                            vp(k_ptr), vp(v_ptr)))
+
+    def copy_block_data(self, src: int, dst: int, valid_tokens: int) -> None:
+        """PagedBlockPool.CopyBlockData (PagedBlockPool.cs:304-327) on the device."""
+        _check(load().gsp_pool_copy_block(self._ctx.handle, self._h, int(src), int(dst), int(valid_tokens)))
+
+
+class BlockAllocator:
+    """Block-id half of PagedBlockPool: LIFO free stack with refcounts."""
+
+    def __init__(self, total_blocks: int, block_size: int = BLOCK_SIZE):
+        h = vp()
+        _check(load().gsp_block_allocator_create(int(total_blocks), int(block_size), ctypes.byref(h)))
+        self._h = h
+        self.block_size = block_size
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        if self._h:
+            load().gsp_block_allocator_destroy(self._h)
+            self._h = vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def attach_pool(self, ctx: Optional[Context], pool: Optional[Pool]) -> None:
+        _check(load().gsp_block_allocator_attach_pool(self._h, ctx.handle if ctx else None,
+                                                      pool.handle if pool else None))
+
+    def try_allocate_block(self):
+        bid = i32()
+        ok = load().gsp_block_allocator_try_allocate(self._h, ctypes.byref(bid))
+        return bool(ok), bid.value
+
+    def retain_block(self, block_id: int) -> int:
+        r = load().gsp_block_allocator_retain(self._h, int(block_id))
+        if r < 0:
+            _check(GSP_E_INVALID_ARG)
+        return r
+
+    def release_block(self, block_id: int) -> int:
+        return load().gsp_block_allocator_release(self._h, int(block_id))
+
+    free_block = release_block
+
+    def free_blocks(self, ids) -> None:
+        for b in ids:
+            self.release_block(int(b))
+
+    def get_ref_count(self, block_id: int) -> int:
+        return load().gsp_block_allocator_ref_count(self._h, int(block_id))
+
+    @property
+    def total_blocks(self) -> int:
+        return load().gsp_block_allocator_total(self._h)
+
+    @property
+    def free_blocks_count(self) -> int:
+        return load().gsp_block_allocator_free_count(self._h)
+
+    @property
+    def allocated_blocks_count(self) -> int:
+        return self.total_blocks - self.free_blocks_count
+
+
+class BlockTable:
+    """Per-sequence logical -> physical page table (BlockTable.cs:13-117)."""
+
+    def __init__(self, allocator: BlockAllocator):
+        h = vp()
+        _check(load().gsp_block_table_create(allocator.handle, ctypes.byref(h)))
+        self._h = h
+        self._alloc = allocator  # keeps the allocator alive
+
+    def close(self) -> None:
+        if self._h:
+            load().gsp_block_table_destroy(self._h)
+            self._h = vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def attach_prefix_blocks(self, ids, token_count: int) -> None:
+        a = _i32(ids)
+        _check(load().gsp_block_table_attach_prefix(self._h, _ptr(a) if len(a) else None, len(a), int(token_count)))
+
+    def append_token(self):
+        b, o = i32(), i32()
+        ok = load().gsp_block_table_append_token(self._h, ctypes.byref(b), ctypes.byref(o))
+        return bool(ok), b.value, o.value
+
+    def append_tokens(self, n: int) -> int:
+        """AppendToken n times; returns how many succeeded."""
+        return load().gsp_block_table_append_tokens(self._h, int(n))
+
+    def get_token_location(self, token: int):
+        b, o = i32(), i32()
+        _check(load().gsp_block_table_token_location(self._h, int(token), ctypes.byref(b), ctypes.byref(o)))
+        return b.value, o.value
+
+    def get_block_id(self, index: int) -> int:
+        r = load().gsp_block_table_block_id(self._h, int(index))
+        if r < 0:
+            _check(GSP_E_INVALID_ARG)
+        return r
+
+    @property
+    def token_count(self) -> int:
+        return load().gsp_block_table_token_count(self._h)
+
+    @property
+    def block_count(self) -> int:
+        return load().gsp_block_table_block_count(self._h)
+
+    def as_span(self) -> np.ndarray:
+        n = self.block_count
+        out = np.zeros(max(1, n), np.int32)
+        load().gsp_block_table_ids(self._h, _ptr(out), n)
+        return out[:n]
+
+    def release_all(self) -> None:
+        load().gsp_block_table_release_all(self._h)

@@ -1,0 +1,304 @@
+/*
+ * glacier_paged.h — C ABI of the MI355X (gfx950) ragged continuous-batch
+ * paged-attention step.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, never
+ * throws, and reports failure through a status code plus a thread-local
+ * message (gsp_last_error).  Status codes map onto the reference's failure
+ * behaviour:
+ *   GSP_E_INVALID_ARG  <-> ArgumentOutOfRangeException / ArgumentNullException
+ *                          (PagedAttentionKernel.cs:34-39, PagedBlockPool.cs:63-67,
+ *                           PagedTransformerRunner.cs:533-540)
+ *   GSP_E_OOM          <-> TryAllocateBlock == false / TryCreate == false
+ *                          (PagedBlockPool.cs:178-189, CudaPagedTransformerRunner.cs:126-132)
+ *   GSP_E_UNSUPPORTED  <-> IsModelSupportedOnGpu == false
+ *                          (CudaPagedTransformerRunner.cs:381-460)
+ *   GSP_E_HIP          <-> driver failure (CuDriver.Check)
+ *
+ * Threading: one gsp_ctx is driven by one thread at a time, as the reference
+ * engine drives its runner from a single loop thread
+ * (ContinuousBatchEngine.cs:333).  Distinct contexts are independent.  All
+ * device work of a context is enqueued on one HIP stream; calls return after
+ * enqueueing and gsp_sync() gives the reference's synchronous semantics.
+ *
+ * Ownership: the caller owns every host pointer for the duration of a call
+ * only (the library copies what it keeps into its own pinned staging); the
+ * library owns every allocation behind an opaque handle.  q/out/k/v device
+ * pointers passed to compute calls are caller-owned device memory.
+ */
+#ifndef GLACIER_PAGED_H
+#define GLACIER_PAGED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+#define GSP_ABI_VERSION 1
+#define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
+
+typedef enum gsp_status {
+    GSP_OK = 0,
+    GSP_E_INVALID_ARG = 1,
+    GSP_E_OOM = 2,
+    GSP_E_UNSUPPORTED = 3,
+    GSP_E_HIP = 4,
+    GSP_E_STATE = 5 /* call order violated, e.g. attention before a step was packed */
+} gsp_status;
+
+typedef enum gsp_kv_dtype {
+    GSP_KV_F32 = 0, /* host pool precision (PagedBlockPool.cs:36-37) */
+    GSP_KV_F16 = 1  /* device pool precision of the reference GPU runner
+                       (CudaPagedTransformerRunner.cs:118-119, KvCachePrecision.Fp16) */
+} gsp_kv_dtype;
+
+typedef struct gsp_ctx gsp_ctx;
+typedef struct gsp_pool gsp_pool;
+typedef struct gsp_block_allocator gsp_block_allocator;
+typedef struct gsp_block_table gsp_block_table;
+
+/* ------------------------------------------------------------------------ */
+/* Diagnostics                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* Message describing the last failing call on this thread ("" if none). */
+const char* gsp_last_error(void);
+
+int gsp_abi_version(void);
+
+typedef struct gsp_device_info {
+    char name[256];
+    char arch[64];          /* e.g. "gfx950" */
+    int32_t compute_units;
+    int32_t wavefront_size;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_width_bits;
+    int64_t total_global_mem;
+    int64_t lds_per_block;
+} gsp_device_info;
+
+/* Properties of HIP device `device`. */
+int gsp_device_info_get(int device, gsp_device_info* out);
+
+/* ------------------------------------------------------------------------ */
+/* Context: GpuContext + TryCreate / Dispose                                 */
+/* (CudaPagedTransformerRunner.cs:78-190, 490-523)                           */
+/* ------------------------------------------------------------------------ */
+
+/* Creates a context on HIP device `device` with its own stream.  Fails with
+ * GSP_E_UNSUPPORTED when no gfx950 device is present (the caller then keeps
+ * its CPU runner, as ContinuousBatchEngine.cs:139-168 does). */
+int gsp_init(int device, gsp_ctx** out);
+void gsp_shutdown(gsp_ctx* ctx);
+
+/* Replaces the context's stream with a caller-owned hipStream_t (NULL restores
+ * the context's own stream).  The caller keeps the stream alive. */
+int gsp_set_stream(gsp_ctx* ctx, void* hip_stream);
+void* gsp_get_stream(gsp_ctx* ctx);
+
+/* Blocks until all work enqueued on the context's stream has finished. */
+int gsp_sync(gsp_ctx* ctx);
+
+/* ------------------------------------------------------------------------ */
+/* Device KV pool: the device half of PagedBlockPool                         */
+/* Layout (PagedBlockPool.cs:77-83,128-131,140-143), element offsets:        */
+/*   K[block][layer][head_kv][slot < block_size][head_dim]                   */
+/*   V[block][layer][head_kv][slot < block_size][v_head_dim]                 */
+/* ------------------------------------------------------------------------ */
+
+typedef struct gsp_pool_desc {
+    int32_t total_blocks;
+    int32_t layers;
+    int32_t heads_kv;
+    int32_t head_dim;
+    int32_t v_head_dim;  /* <= 0 means head_dim (PagedBlockPool.cs:73) */
+    int32_t block_size;  /* must be 16 */
+    int32_t kv_dtype;    /* gsp_kv_dtype */
+} gsp_pool_desc;
+
+/* Allocates zero-initialised K and V arenas in HBM
+ * (CudaPagedTransformerRunner.cs:141-148).  GSP_E_OOM if they do not fit. */
+int gsp_pool_create(gsp_ctx* ctx, const gsp_pool_desc* desc, gsp_pool** out);
+
+/* Wraps caller-owned device arenas already laid out as above (the reference
+ * hands raw dKPool/dVPool pointers to its kernels,
+ * CudaPagedTransformerRunner.cs:352-360).  The library never frees them. */
+int gsp_pool_wrap(gsp_ctx* ctx, const gsp_pool_desc* desc, void* k_dev, void* v_dev,
+                  gsp_pool** out);
+void gsp_pool_destroy(gsp_pool* pool);
+
+/* Device addresses and byte sizes of the two arenas. */
+int gsp_pool_arenas(const gsp_pool* pool, void** k_dev, void** v_dev, size_t* k_bytes,
+                    size_t* v_bytes);
+
+/* PagedBlockPool.Store (PagedBlockPool.cs:151-161), batched: token i of `n`
+ * goes to slot slots[i] of block block_ids[i] in `layer`.  k_dev is
+ * [n][heads_kv][head_dim] fp32, v_dev is [n][heads_kv][v_head_dim] fp32 (device
+ * pointers); F16 pools round to nearest even on the device.  block_ids and
+ * slots are host arrays. */
+int gsp_pool_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n,
+                          const int32_t* block_ids, const int32_t* slots, const float* k_dev,
+                          const float* v_dev);
+
+/* PagedBlockPool.CopyBlockData (PagedBlockPool.cs:304-327): copies the first
+ * min(valid_tokens, block_size) slots of every layer and KV head of block
+ * `src` to block `dst`, on the device.  valid_tokens <= 0 is a no-op. */
+int gsp_pool_copy_block(gsp_ctx* ctx, gsp_pool* pool, int32_t src, int32_t dst,
+                        int32_t valid_tokens);
+
+/* Test/fixture support: synchronous byte copies between host memory and an
+ * arena (which: 0 = K, 1 = V). */
+int gsp_pool_upload(gsp_ctx* ctx, gsp_pool* pool, int32_t which, size_t offset_bytes,
+                    const void* host, size_t bytes);
+int gsp_pool_download(gsp_ctx* ctx, gsp_pool* pool, int32_t which, size_t offset_bytes,
+                      void* host, size_t bytes);
+
+/* ------------------------------------------------------------------------ */
+/* Step packing: replaces the per-sequence UploadBlockTable copies           */
+/* (CudaPagedTransformerRunner.cs:330-379) with one packed upload per step.  */
+/* ------------------------------------------------------------------------ */
+
+typedef struct gsp_step_desc {
+    int32_t num_rows;            /* B: sequences in this engine step */
+    int32_t max_seq_len;         /* maxSeqLen of the runner */
+    const int32_t* positions;    /* [B] position of the row's first query token */
+    const int32_t* q_lens;       /* [B] query tokens per row (NULL: all 1 = decode rows) */
+    const int32_t* token_counts; /* [B] BlockTable.TokenCount after slot allocation */
+    const int32_t* bt_offsets;   /* [B+1] CSR offsets into bt_ids */
+    const int32_t* bt_ids;       /* concatenated BlockTable.AsSpan() of each row */
+} gsp_step_desc;
+
+/* Validates and packs one engine step and uploads it with a single
+ * host-to-device copy on the context's stream.  Query token i of row b sits at
+ * pos = positions[b] + i and attends to
+ *     total = min(token_counts[b], pos + 1)           (PagedAttentionKernel.cs:41)
+ * tokens (causal for q_lens[b] > 1, PagedTransformerRunner.cs:454-474); a row
+ * whose every query token has total == 0 is skipped and its out rows are left
+ * untouched (PagedAttentionKernel.cs:42).  Only the first ceil(total/16) table
+ * entries of a row are packed.  Errors (GSP_E_INVALID_ARG):
+ *   max_seq_len <= 0; pos < 0 or pos + q_len - 1 >= max_seq_len
+ *   (PagedAttentionKernel.cs:34-37); token_counts[b] > max_seq_len (:38-39);
+ *   a row's table shorter than ceil(total/16); a block id outside the pool
+ *   (checked by gsp_attention_step against the pool). */
+int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc);
+
+/* Sizes of the packed step (for tests and the bench). */
+typedef struct gsp_step_info {
+    int32_t num_rows;
+    int32_t total_q;         /* query tokens in the step = sum of q_lens */
+    int32_t packed_pages;    /* bt entries actually packed */
+    int32_t decode_units;    /* work units of the split-KV decode kernel */
+    int32_t prefill_tiles;   /* work tiles of the MFMA prefill kernel */
+    int32_t pages_per_split; /* split size chosen for this step */
+    int64_t kv_tokens;       /* sum over rows of the longest total (KV tokens read once) */
+    int64_t staging_bytes;   /* bytes of the single host-to-device upload */
+} gsp_step_info;
+
+int gsp_step_get_info(const gsp_ctx* ctx, gsp_step_info* out);
+
+/* Downloads the packed CSR table as it lives in device memory:
+ * row_offsets[num_rows+1] and ids[packed_pages], plus ctx_lens[total_q] (the
+ * `total` of each query token).  Any output may be NULL.  Synchronous. */
+int gsp_step_download(gsp_ctx* ctx, int32_t* row_offsets, int32_t* ids, int32_t* ctx_lens);
+
+/* Pages per split-KV unit: 0 (default) lets the library choose from the step's
+ * size and the device's CU count; > 0 forces that many pages (for tests). */
+int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages);
+
+/* ------------------------------------------------------------------------ */
+/* Attention                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* PagedAttentionKernel.ComputeAttention (PagedAttentionKernel.cs:17-372)
+ * over every query token of the packed step at once.
+ *   q_dev   [total_q][n_heads][head_dim]  fp32, device
+ *   out_dev [total_q][n_heads][v_head_dim] fp32, device
+ * Query head h reads KV head h / (n_heads / heads_kv) (:44,50).  Scores are
+ * dot(q, k) * attn_scale (:64-65), softmax over the row's `total` tokens (:70),
+ * out = sum p_t v_t (:73-370).  sink_logit must be NULL: attention sinks are
+ * unsupported on the GPU path, as in CudaPagedTransformerRunner.cs:431.
+ * Supported: head_dim == v_head_dim in {64, 128}; n_heads % heads_kv == 0 and
+ * n_heads / heads_kv <= 8; block_size 16. */
+int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t n_heads,
+                       const float* q_dev, float* out_dev, float attn_scale,
+                       const float* sink_logit);
+
+/* Single-sequence drop-in for ComputeAttention with the reference's argument
+ * list (PagedAttentionKernel.cs:17-32): the BlockTable is passed as its id span
+ * plus TokenCount; head geometry must match the pool.  head_scores is not
+ * needed (online softmax) and is ignored.  Packs a one-row step and runs
+ * it; returns after enqueueing. */
+int gsp_compute_attention(gsp_ctx* ctx, const gsp_pool* pool, int32_t stage_layer,
+                          int32_t model_layer, int32_t pos, const float* q_dev, float* out_dev,
+                          const int32_t* block_ids, int32_t n_block_ids, int32_t token_count,
+                          int32_t n_heads, int32_t n_heads_kv, int32_t head_dim,
+                          int32_t v_head_dim, float attn_scale, float* head_scores,
+                          int32_t max_seq_len, const float* sink_logit);
+
+/* ------------------------------------------------------------------------ */
+/* Host metadata: the block-id half of PagedBlockPool and BlockTable         */
+/* (PagedBlockPool.cs:112-121,178-299; BlockTable.cs:13-117).  Host-only,    */
+/* no device work except the optional COW page copy.                         */
+/* ------------------------------------------------------------------------ */
+
+/* LIFO free stack seeded so the first allocation returns block 0
+ * (PagedBlockPool.cs:116-120).  total_blocks < 1 or block_size < 1 ->
+ * GSP_E_INVALID_ARG (:63-67). */
+int gsp_block_allocator_create(int32_t total_blocks, int32_t block_size,
+                               gsp_block_allocator** out);
+void gsp_block_allocator_destroy(gsp_block_allocator* a);
+
+/* Attaches a device pool so that copy-on-write forks copy page contents on the
+ * device (PagedBlockPool.TryForkBlock, :332-342).  NULL detaches; without a
+ * pool a fork only allocates, as the reference's metadata-only pool does. */
+int gsp_block_allocator_attach_pool(gsp_block_allocator* a, gsp_ctx* ctx, gsp_pool* pool);
+
+/* TryAllocateBlock (:178-189): 1 and *block_id on success, 0 and -1 if empty. */
+int gsp_block_allocator_try_allocate(gsp_block_allocator* a, int32_t* block_id);
+/* RetainBlock (:240-245): new refcount, or -1 with GSP_E_INVALID_ARG set. */
+int gsp_block_allocator_retain(gsp_block_allocator* a, int32_t block_id);
+/* ReleaseBlock (:251-279): remaining refcount; idempotent double free. */
+int gsp_block_allocator_release(gsp_block_allocator* a, int32_t block_id);
+int gsp_block_allocator_ref_count(const gsp_block_allocator* a, int32_t block_id);
+int gsp_block_allocator_free_count(const gsp_block_allocator* a);
+int gsp_block_allocator_total(const gsp_block_allocator* a);
+
+int gsp_block_table_create(gsp_block_allocator* a, gsp_block_table** out);
+void gsp_block_table_destroy(gsp_block_table* t);
+/* AttachPrefixBlocks (BlockTable.cs:31-39). */
+int gsp_block_table_attach_prefix(gsp_block_table* t, const int32_t* ids, int32_t n,
+                                  int32_t token_count);
+/* AppendToken (BlockTable.cs:46-80): 1 on success, 0 on pool exhaustion with
+ * the table unchanged and *block_id = *offset = -1. */
+int gsp_block_table_append_token(gsp_block_table* t, int32_t* block_id, int32_t* offset);
+/* AppendToken n times, as a prefill chunk reserves its slots
+ * (PagedTransformerRunner.cs:383-401); stops at the first failure.  Returns
+ * the number of tokens appended. */
+int gsp_block_table_append_tokens(gsp_block_table* t, int32_t n);
+/* GetTokenLocation (BlockTable.cs:86-91). */
+int gsp_block_table_token_location(const gsp_block_table* t, int32_t token, int32_t* block_id,
+                                   int32_t* offset);
+int gsp_block_table_block_id(const gsp_block_table* t, int32_t index);
+int gsp_block_table_token_count(const gsp_block_table* t);
+int gsp_block_table_block_count(const gsp_block_table* t);
+/* AsSpan (BlockTable.cs:103): copies up to cap ids; returns the block count. */
+int gsp_block_table_ids(const gsp_block_table* t, int32_t* out, int32_t cap);
+/* ReleaseAll (BlockTable.cs:108-116). */
+void gsp_block_table_release_all(gsp_block_table* t);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GLACIER_PAGED_H */

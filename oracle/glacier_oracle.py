@@ -1,0 +1,280 @@
+"""ctypes wrapper of liboracle.so — TEST INFRASTRUCTURE ONLY.
+
+The oracle is the CPU restatement of the reference's paged-attention path
+(PagedAttentionKernel.cs:17-372, PagedBlockPool.cs, BlockTable.cs).  Only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as
+the checker or the timed CPU baseline; the product never does.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+ORC_OK, ORC_E_RANGE, ORC_E_UNSUPPORTED = 0, 1, 2
+ISA_AUTO, ISA_SCALAR, ISA_AVX2, ISA_AVX512 = -1, 0, 1, 2
+
+i32 = ctypes.c_int32
+i32p = ctypes.POINTER(i32)
+f32p = ctypes.POINTER(ctypes.c_float)
+f64p = ctypes.POINTER(ctypes.c_double)
+vp = ctypes.c_void_p
+
+
+class OrcPool(ctypes.Structure):
+    _fields_ = [
+        ("k", f32p),
+        ("v", f32p),
+        ("total_blocks", i32),
+        ("layers", i32),
+        ("heads_kv", i32),
+        ("head_dim", i32),
+        ("v_head_dim", i32),
+        ("block_size", i32),
+    ]
+
+
+class OrcTable(ctypes.Structure):
+    _fields_ = [("ids", i32p), ("n_ids", i32), ("token_count", i32)]
+
+
+class ArgumentOutOfRange(ValueError):
+    """Where the reference throws ArgumentOutOfRangeException."""
+
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-B", "-C", str(HERE)], check=True, capture_output=True, text=True)
+    return LIB_PATH
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        build()
+    lib = ctypes.CDLL(str(LIB_PATH))
+    sig = {
+        "orc_host_isa": (ctypes.c_int, []),
+        "orc_compute_attention": (
+            ctypes.c_int,
+            [ctypes.POINTER(OrcPool), ctypes.POINTER(OrcTable), i32, i32, i32, f32p, f32p, i32, i32, i32, i32,
+             ctypes.c_float, f32p, i32, f32p, i32, i32],
+        ),
+        "orc_attention_step": (
+            ctypes.c_int,
+            [ctypes.POINTER(OrcPool), i32, i32, i32p, i32p, i32p, i32p, i32p, f32p, f32p, i32, ctypes.c_float, i32,
+             i32, i32],
+        ),
+        "orc_attention_fp64": (
+            ctypes.c_int,
+            [ctypes.POINTER(OrcPool), ctypes.POINTER(OrcTable), i32, i32, f32p, f64p, i32, ctypes.c_double, i32],
+        ),
+        "orc_alloc_create": (vp, [i32, i32]),
+        "orc_alloc_destroy": (None, [vp]),
+        "orc_alloc_try_allocate": (ctypes.c_int, [vp, i32p]),
+        "orc_alloc_retain": (ctypes.c_int, [vp, i32]),
+        "orc_alloc_release": (ctypes.c_int, [vp, i32]),
+        "orc_alloc_ref_count": (ctypes.c_int, [vp, i32]),
+        "orc_alloc_free_count": (ctypes.c_int, [vp]),
+        "orc_btab_create": (vp, [vp]),
+        "orc_btab_destroy": (None, [vp]),
+        "orc_btab_attach_prefix": (None, [vp, i32p, i32, i32]),
+        "orc_btab_append_token": (ctypes.c_int, [vp, i32p, i32p]),
+        "orc_btab_append_tokens": (ctypes.c_int, [vp, i32]),
+        "orc_btab_token_count": (ctypes.c_int, [vp]),
+        "orc_btab_ids": (ctypes.c_int, [vp, i32p, i32]),
+        "orc_btab_release_all": (None, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def host_isa() -> int:
+    return load().orc_host_isa()
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+class HostPool:
+    """fp32 K/V arenas in the reference layout [block][layer][hkv][slot][dim]."""
+
+    def __init__(self, k: np.ndarray, v: np.ndarray, block_size: int = 16):
+        assert k.ndim == 5 and v.ndim == 5, "arenas are [blocks, layers, heads_kv, block_size, dim]"
+        self.k = _f32(k)
+        self.v = _f32(v)
+        tb, layers, hkv, bs, d = self.k.shape
+        assert bs == block_size and self.v.shape[:4] == self.k.shape[:4]
+        self.struct = OrcPool(
+            self.k.ctypes.data_as(f32p), self.v.ctypes.data_as(f32p), tb, layers, hkv, d, self.v.shape[4], bs
+        )
+
+    @property
+    def heads_kv(self):
+        return self.struct.heads_kv
+
+    @property
+    def head_dim(self):
+        return self.struct.head_dim
+
+    @property
+    def v_head_dim(self):
+        return self.struct.v_head_dim
+
+
+def compute_attention(pool: HostPool, ids, token_count: int, layer: int, pos: int, q: np.ndarray, n_heads: int,
+                      attn_scale: float, max_seq_len: int, out: Optional[np.ndarray] = None, n_threads: int = 1,
+                      isa: int = ISA_AUTO, n_heads_kv: Optional[int] = None, head_dim: Optional[int] = None,
+                      v_head_dim: Optional[int] = None, sink_logit: Optional[float] = None) -> np.ndarray:
+    """ComputeAttention for one query token; `out` is left untouched when total == 0."""
+    q = _f32(q).reshape(-1)
+    if out is None:
+        out = np.zeros(n_heads * pool.v_head_dim, np.float32)
+    arr = _i32(ids)
+    n = len(arr)
+    if n == 0:
+        arr = np.zeros(1, np.int32)
+    tab = OrcTable(arr.ctypes.data_as(i32p), n, int(token_count))
+    sink = ctypes.pointer(ctypes.c_float(sink_logit)) if sink_logit is not None else None
+    rc = load().orc_compute_attention(
+        ctypes.byref(pool.struct), ctypes.byref(tab), layer, layer, pos, q.ctypes.data_as(f32p),
+        out.ctypes.data_as(f32p), n_heads, n_heads_kv if n_heads_kv is not None else pool.heads_kv,
+        head_dim if head_dim is not None else pool.head_dim, v_head_dim if v_head_dim is not None else pool.v_head_dim,
+        attn_scale, None, max_seq_len, sink, n_threads, isa)
+    if rc == ORC_E_RANGE:
+        raise ArgumentOutOfRange("ComputeAttention argument out of range")
+    if rc == ORC_E_UNSUPPORTED:
+        raise NotImplementedError("attention sinks are not restated")
+    return out
+
+
+def attention_step(pool: HostPool, layer: int, positions, token_counts, bt_offsets, bt_ids, q: np.ndarray,
+                   n_heads: int, attn_scale: float, max_seq_len: int, q_lens=None, out: Optional[np.ndarray] = None,
+                   n_threads: int = 1, isa: int = ISA_AUTO) -> np.ndarray:
+    pos = _i32(positions)
+    tc = _i32(token_counts)
+    off = _i32(bt_offsets)
+    ids = _i32(bt_ids) if len(bt_ids) else np.zeros(1, np.int32)
+    ql = _i32(q_lens) if q_lens is not None else None
+    total_q = int(ql.sum()) if ql is not None else len(pos)
+    q = _f32(q)
+    if out is None:
+        out = np.zeros((total_q, n_heads, pool.v_head_dim), np.float32)
+    rc = load().orc_attention_step(
+        ctypes.byref(pool.struct), layer, len(pos), pos.ctypes.data_as(i32p),
+        ql.ctypes.data_as(i32p) if ql is not None else None, tc.ctypes.data_as(i32p), off.ctypes.data_as(i32p),
+        ids.ctypes.data_as(i32p), q.ctypes.data_as(f32p), out.ctypes.data_as(f32p), n_heads, attn_scale,
+        max_seq_len, n_threads, isa)
+    if rc == ORC_E_RANGE:
+        raise ArgumentOutOfRange("attention step argument out of range")
+    if rc != ORC_OK:
+        raise RuntimeError(f"oracle status {rc}")
+    return out
+
+
+def attention_fp64(pool: HostPool, ids, token_count: int, layer: int, pos: int, q: np.ndarray, n_heads: int,
+                   attn_scale: float, max_seq_len: int) -> np.ndarray:
+    q = _f32(q).reshape(-1)
+    out = np.zeros(n_heads * pool.v_head_dim, np.float64)
+    arr = _i32(ids)
+    n = len(arr)
+    if n == 0:
+        arr = np.zeros(1, np.int32)
+    tab = OrcTable(arr.ctypes.data_as(i32p), n, int(token_count))
+    rc = load().orc_attention_fp64(ctypes.byref(pool.struct), ctypes.byref(tab), layer, pos, q.ctypes.data_as(f32p),
+                                   out.ctypes.data_as(f64p), n_heads, attn_scale, max_seq_len)
+    if rc != ORC_OK:
+        raise ArgumentOutOfRange("fp64 attention argument out of range")
+    return out
+
+
+class Alloc:
+    """Free stack + refcounts restated from PagedBlockPool.cs:112-121,178-299."""
+
+    def __init__(self, total_blocks: int, block_size: int = 16):
+        self._h = load().orc_alloc_create(total_blocks, block_size)
+        if not self._h:
+            raise ArgumentOutOfRange("totalBlocks and blockSize must be >= 1")
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            load().orc_alloc_destroy(self._h)
+            self._h = None
+
+    def try_allocate_block(self):
+        b = i32()
+        ok = load().orc_alloc_try_allocate(self._h, ctypes.byref(b))
+        return bool(ok), b.value
+
+    def retain_block(self, bid: int) -> int:
+        r = load().orc_alloc_retain(self._h, bid)
+        if r < 0:
+            raise ArgumentOutOfRange("physicalBlockId")
+        return r
+
+    def release_block(self, bid: int) -> int:
+        return load().orc_alloc_release(self._h, bid)
+
+    def get_ref_count(self, bid: int) -> int:
+        return load().orc_alloc_ref_count(self._h, bid)
+
+    @property
+    def free_blocks_count(self) -> int:
+        return load().orc_alloc_free_count(self._h)
+
+
+class BTab:
+    """BlockTable restated from BlockTable.cs:13-117 (metadata only)."""
+
+    def __init__(self, alloc: Alloc):
+        self._alloc = alloc
+        self._h = load().orc_btab_create(alloc._h)
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            load().orc_btab_destroy(self._h)
+            self._h = None
+
+    def attach_prefix_blocks(self, ids, token_count: int) -> None:
+        a = _i32(ids) if len(ids) else np.zeros(1, np.int32)
+        load().orc_btab_attach_prefix(self._h, a.ctypes.data_as(i32p), len(ids), token_count)
+
+    def append_token(self):
+        b, o = i32(), i32()
+        ok = load().orc_btab_append_token(self._h, ctypes.byref(b), ctypes.byref(o))
+        return bool(ok), b.value, o.value
+
+    def append_tokens(self, n: int) -> int:
+        return load().orc_btab_append_tokens(self._h, n)
+
+    @property
+    def token_count(self) -> int:
+        return load().orc_btab_token_count(self._h)
+
+    def as_span(self) -> np.ndarray:
+        n = load().orc_btab_ids(self._h, None, 0)
+        out = np.zeros(max(1, n), np.int32)
+        load().orc_btab_ids(self._h, out.ctypes.data_as(i32p), n)
+        return out[:n]
+
+    def release_all(self) -> None:
+        load().orc_btab_release_all(self._h)
