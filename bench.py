@@ -88,8 +88,12 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
 
     step = getattr(workloads, name)()
     q, k, v = workloads.device_values(torch, step)
+    torch.cuda.synchronize()
     ctx = gsp.Context(0)
-    stream = torch.cuda.current_stream()
+    # A dedicated torch stream: the library launches on it and the events below
+    # are recorded on it (torch's default stream is the null handle).
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     ctx.set_stream(stream.cuda_stream)
     pool = gsp.Pool.wrap(ctx, k.data_ptr(), v.data_ptr(), step.total_blocks, 1, step.n_kv, step.head_dim,
                          gsp.KV_F16 if step.kv_dtype == "f16" else gsp.KV_F32)

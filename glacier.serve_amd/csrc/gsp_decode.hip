@@ -22,9 +22,8 @@
 // rows with lane shuffles.  Each wave walks every kDecodeWaves-th page of the
 // unit; the four waves of a workgroup merge through LDS.  A query token whose
 // pages were cut into several units (split-KV, FlashDecoding style) writes
-// (max, sum, unnormalised out) partials; the last unit to finish, found with a
-// device-scope counter, merges them with the log-sum-exp rescale and resets
-// the counter, so one launch serves both passes.
+// (max, sum, unnormalised out) partials that the merge kernel combines with
+// the log-sum-exp rescale.
 #include "gsp_internal.h"
 
 namespace gsp {
@@ -74,7 +73,6 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
     __shared__ float sh_o[kDecodeWaves][G][D];
     __shared__ float sh_m[kDecodeWaves][G];
     __shared__ float sh_l[kDecodeWaves][G];
-    __shared__ int sh_last;
 
     const DecodeUnit u = a.units[blockIdx.x];
     const int kvh = blockIdx.y;
@@ -234,37 +232,6 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
             }
         }
     }
-    if (single) return;
-
-    // Publish the partial, then let the last unit of this (query, KV head) merge.
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const int prev = atomicAdd(&a.counters[(int64_t)u.qi * a.n_kv + kvh], 1);
-        sh_last = (prev == u.nsplit - 1);
-    }
-    __syncthreads();
-    if (!sh_last) return;
-    __threadfence();
-
-    for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
-        const int g = idx / D;
-        const int e = idx - g * D;
-        const int h = h0 + g;
-        float M = -INFINITY;
-        for (int sp = 0; sp < u.nsplit; ++sp)
-            M = fmaxf(M, a.part_ml[(((int64_t)u.slot + sp) * a.n_heads + h) * 2]);
-        float L = 0.f;
-        float O = 0.f;
-        for (int sp = 0; sp < u.nsplit; ++sp) {
-            const int64_t sidx = ((int64_t)u.slot + sp) * a.n_heads + h;
-            const float f = fast_exp2(a.part_ml[sidx * 2] - M);
-            L = fmaf(a.part_ml[sidx * 2 + 1], f, L);
-            O = fmaf(a.part_o[sidx * D + e], f, O);
-        }
-        a.out[((int64_t)u.qi * a.n_heads + h) * D + e] = O / L;
-    }
-    if (tid == 0) atomicExch(&a.counters[(int64_t)u.qi * a.n_kv + kvh], 0);
 }
 
 template <int D, typename KT, int G>

@@ -1,0 +1,307 @@
+// Matrix-core (MFMA) decode kernel of the paged-attention step, gfx950.
+//
+// Same contract as the DPP decode kernel (PagedAttentionKernel.cs:17-372 over
+// every query token of a packed step), but the GQA group turns each 16-token
+// page into two small dense contractions that run on the matrix cores:
+//
+//   S^T[token][head] = K_page[16 x d] . (Q_group * scale * log2 e)^T   (v_mfma_f32_16x16x4f32, M = tokens, N = heads)
+//   O[head][e]      += P[16 heads x 16 tokens] . V_page[16 x d]          (v_mfma_f32_16x16x4f32, M = heads, K = tokens)
+//
+// Heads of the group beyond G are zero padding (G <= 16).  MFMA operand
+// layouts (lane l, n = l % 16, g = l / 16):
+//   QK step kk = 4j + i uses d = 16j + 4g + i:  A = K[token n][d],  B = Q[head n][d]
+//   result: lane holds S[head n][token 4g + r], r = 0..3
+//   PV step kk uses token 4g + kk:  A = P[head n][token 4g + kk] (the lane's own r = kk),
+//   B = V[token 4g + kk][e], e = 64c + 4n + i for output block 4c + i
+//   result: lane holds O[head 4g + r][e].
+// So each lane reads 16-byte pieces of K rows and V rows straight into MFMA
+// operands; the softmax needs one max-reduction across the four lane groups
+// per page and four exp2 per lane.  Page loads are raw buffer loads whose
+// descriptor covers only the page's valid tokens: slots past the context read
+// as zero in hardware (no fetch, no NaN from stale slots reaches P.V).  Each
+// wave streams every kDecodeWaves-th page of its unit with the next page's
+// loads in flight while the current one is computed; the four waves merge
+// through LDS.  Split units write (max, sum, unnormalised out) partials that
+// merge_partials_kernel combines in a second launch.
+#include "gsp_internal.h"
+
+namespace gsp {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef int i4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const void* base, int bytes) {
+    // Raw buffer (stride 0) of `bytes` bytes; offsets at or past the end read 0.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// 4 consecutive elements of a K/V row at element offset `off`, as fp32.
+template <typename KT>
+__device__ __forceinline__ f4 load4(__amdgpu_buffer_rsrc_t r, int off);
+
+template <>
+__device__ __forceinline__ f4 load4<float>(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4, 0, 0));
+}
+
+template <>
+__device__ __forceinline__ f4 load4<_Float16>(__amdgpu_buffer_rsrc_t r, int off) {
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    const u2 raw = __builtin_amdgcn_raw_buffer_load_b64(r, off * 2, 0, 0);
+    const h4 h = __builtin_bit_cast(h4, raw);
+    return f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
+template <int D>
+struct PageRegs {
+    f4 k[D / 16];          // K[token n][16j + 4g .. +3]
+    f4 v[4][D / 64];       // V[token 4g + kk][64c + 4n .. +3]
+};
+
+template <int D, typename KT>
+__device__ __forceinline__ void load_page(PageRegs<D>& pr, const KT* kpage, const KT* vpage, int ntok, int n,
+                                          int g) {
+    const int bytes = ntok * D * (int)sizeof(KT);
+    const __amdgpu_buffer_rsrc_t rk = page_rsrc(kpage, bytes);
+    const __amdgpu_buffer_rsrc_t rv = page_rsrc(vpage, bytes);
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) pr.k[j] = load4<KT>(rk, n * D + 16 * j + 4 * g);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int c = 0; c < D / 64; ++c) pr.v[kk][c] = load4<KT>(rv, (4 * g + kk) * D + 64 * c + 4 * n);
+}
+
+template <int D>
+struct WaveState {
+    f4 o[D / 16];  // O[head 4g + r][64c + 4n + i] for block b = 4c + i
+    float m;       // running max (log2 units) of head n
+    float l;       // partial sum of head n over this lane's tokens
+};
+
+template <int D>
+__device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D>& pr, const f4 (&q)[D / 16],
+                                             int ntok, int g) {
+    // S^T = K . Q^T: 32 (d = 128) or 16 (d = 64) rank-4 steps, two accumulation chains.
+    f4 s0 = {0.f, 0.f, 0.f, 0.f};
+    f4 s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (j & 1)
+                s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(pr.k[j][i], q[j][i], s1, 0, 0, 0);
+            else
+                s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(pr.k[j][i], q[j][i], s0, 0, 0, 0);
+        }
+    }
+    f4 s = s0 + s1;  // lane: S[head n][token 4g + r]
+    if (ntok < kBlockSize) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (4 * g + r >= ntok) s[r] = -INFINITY;
+    }
+    float mp = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mp = fmaxf(mp, __shfl_xor(mp, 16));
+    mp = fmaxf(mp, __shfl_xor(mp, 32));
+    const float mn = fmaxf(st.m, mp);
+    const float alpha = fast_exp2(st.m - mn);  // 0 on the first page (m = -inf)
+    st.m = mn;
+    f4 p;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(s[r] - mn);
+    st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    // O rows are heads 4g + r; their alphas live in lanes 4g + r.
+    if (__any(alpha != 1.0f)) {
+        const int lane = threadIdx.x & 63;
+        const int src = 4 * (lane >> 4);
+        f4 ar;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, src + r);
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) st.o[b] *= ar;
+    }
+    // O += P . V: 4 token steps x D/16 output blocks.
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int c = 0; c < D / 64; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                st.o[4 * c + i] =
+                    __builtin_amdgcn_mfma_f32_16x16x4f32(p[kk], pr.v[kk][c][i], st.o[4 * c + i], 0, 0, 0);
+}
+
+template <int D, typename KT>
+__global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(DecodeArgs a) {
+    __shared__ float sh_o[kDecodeWaves][kMaxGroupMfma][D];
+    __shared__ float sh_m[kDecodeWaves][kMaxGroupMfma];
+    __shared__ float sh_l[kDecodeWaves][kMaxGroupMfma];
+
+    const DecodeUnit u = a.units[blockIdx.x];
+    const int kvh = blockIdx.y;
+    const int G = a.n_heads / a.n_kv;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int h0 = kvh * G;
+
+    // Q^T operand: q[j][i] = Q[h0 + n][16j + 4g + i] * scale * log2(e); padded heads are 0.
+    f4 q[D / 16];
+    {
+        const bool live = n < G;
+        const float* qrow = a.q + ((int64_t)u.qi * a.n_heads + h0 + (live ? n : 0)) * D;
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) {
+            f4 x = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
+            q[j] = live ? x * a.scale_log2 : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    WaveState<D> st;
+#pragma unroll
+    for (int b = 0; b < D / 16; ++b) st.o[b] = f4{0.f, 0.f, 0.f, 0.f};
+    st.m = -INFINITY;
+    st.l = 0.f;
+
+    const KT* kbase = static_cast<const KT*>(a.k_pool) + a.layer_offset + (int64_t)kvh * a.head_stride;
+    const KT* vbase = static_cast<const KT*>(a.v_pool) + a.layer_offset + (int64_t)kvh * a.head_stride;
+    const int32_t* bt = a.bt_ids + u.bt_base;
+
+    // Two page buffers in flight: load page p + kDecodeWaves while computing page p.
+    PageRegs<D> ra, rb;
+    int p = u.page_begin + wave;
+    if (p < u.page_end) {
+        const int64_t blk = bt[p];
+        load_page<D, KT>(ra, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
+                         min(kBlockSize, u.ctx - p * kBlockSize), n, g);
+    }
+    while (p < u.page_end) {
+        const int pn = p + kDecodeWaves;
+        if (pn < u.page_end) {
+            const int64_t blk = bt[pn];
+            load_page<D, KT>(rb, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
+                             min(kBlockSize, u.ctx - pn * kBlockSize), n, g);
+        }
+        compute_page<D>(st, ra, q, min(kBlockSize, u.ctx - p * kBlockSize), g);
+        if (pn >= u.page_end) break;
+        const int pnn = pn + kDecodeWaves;
+        if (pnn < u.page_end) {
+            const int64_t blk = bt[pnn];
+            load_page<D, KT>(ra, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
+                             min(kBlockSize, u.ctx - pnn * kBlockSize), n, g);
+        }
+        compute_page<D>(st, rb, q, min(kBlockSize, u.ctx - pn * kBlockSize), g);
+        p = pnn;
+    }
+
+    // Per-head sums over the four lane groups; m is uniform per head already.
+    st.l += __shfl_xor(st.l, 16);
+    st.l += __shfl_xor(st.l, 32);
+    if (g == 0 && n < G) {
+        sh_m[wave][n] = st.m;
+        sh_l[wave][n] = st.l;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int h = 4 * g + r;
+        if (h < G) {
+#pragma unroll
+            for (int c = 0; c < D / 64; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sh_o[wave][h][64 * c + 4 * n + i] = st.o[4 * c + i][r];
+        }
+    }
+    __syncthreads();
+
+    const bool single = (u.nsplit == 1);
+    const int64_t slot = (int64_t)u.slot + u.split;
+    for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
+        const int hh = idx / D;
+        const int e = idx - hh * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, sh_m[w][hh]);
+        float L = 0.f;
+        float O = 0.f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+            const float f = fast_exp2(sh_m[w][hh] - M);  // waves without pages: m = -inf -> 0
+            L = fmaf(sh_l[w][hh], f, L);
+            O = fmaf(sh_o[w][hh][e], f, O);
+        }
+        const int h = h0 + hh;
+        if (single) {
+            a.out[((int64_t)u.qi * a.n_heads + h) * D + e] = O / L;
+        } else {
+            a.part_o[(slot * a.n_heads + h) * D + e] = O;
+            if (e == 0) {
+                a.part_ml[(slot * a.n_heads + h) * 2 + 0] = M;
+                a.part_ml[(slot * a.n_heads + h) * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void merge_partials_kernel(MergeArgs a) {
+    const MergeItem it = a.items[blockIdx.x];
+    const int kvh = blockIdx.y;
+    const int G = a.n_heads / a.n_kv;
+    for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+        const int h = kvh * G + idx / D;
+        const int e = idx % D;
+        float M = -INFINITY;
+        for (int s = 0; s < it.nsplit; ++s) M = fmaxf(M, a.part_ml[(((int64_t)it.slot + s) * a.n_heads + h) * 2]);
+        float L = 0.f;
+        float O = 0.f;
+        for (int s = 0; s < it.nsplit; ++s) {
+            const int64_t si = ((int64_t)it.slot + s) * a.n_heads + h;
+            const float f = fast_exp2(a.part_ml[si * 2] - M);
+            L = fmaf(a.part_ml[si * 2 + 1], f, L);
+            O = fmaf(a.part_o[si * D + e], f, O);
+        }
+        a.out[((int64_t)it.qi * a.n_heads + h) * D + e] = O / L;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_decode_mfma(int head_dim, int kv_f16, int num_units, const DecodeArgs& a, hipStream_t stream) {
+    if (num_units <= 0) return hipSuccess;
+    dim3 grid(num_units, a.n_kv);
+    if (head_dim == 128) {
+        if (kv_f16)
+            hipLaunchKernelGGL((paged_decode_mfma_kernel<128, _Float16>), grid, dim3(kDecodeThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL((paged_decode_mfma_kernel<128, float>), grid, dim3(kDecodeThreads), 0, stream, a);
+    } else if (head_dim == 64) {
+        if (kv_f16)
+            hipLaunchKernelGGL((paged_decode_mfma_kernel<64, _Float16>), grid, dim3(kDecodeThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL((paged_decode_mfma_kernel<64, float>), grid, dim3(kDecodeThreads), 0, stream, a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_merge(int head_dim, int num_items, const MergeArgs& a, hipStream_t stream) {
+    if (num_items <= 0) return hipSuccess;
+    dim3 grid(num_items, a.n_kv);
+    if (head_dim == 128)
+        hipLaunchKernelGGL(merge_partials_kernel<128>, grid, dim3(256), 0, stream, a);
+    else if (head_dim == 64)
+        hipLaunchKernelGGL(merge_partials_kernel<64>, grid, dim3(256), 0, stream, a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace gsp

@@ -11,7 +11,8 @@ namespace gsp {
 constexpr int kBlockSize = 16;    // tokens per KV page (PagedBlockPool.DefaultBlockSize)
 constexpr int kDecodeWaves = 4;   // wave64s per decode workgroup
 constexpr int kDecodeThreads = kDecodeWaves * 64;
-constexpr int kMaxGroup = 8;      // query heads per KV head handled by one workgroup
+constexpr int kMaxGroup = 8;      // query heads per KV head of the DPP decode kernel
+constexpr int kMaxGroupMfma = 16; // query heads per KV head of the MFMA decode kernel (M/N tile)
 
 // One split-KV work unit of the decode kernel: a contiguous range of logical
 // pages of one query token.  The grid is (units, heads_kv); 32 bytes each.
@@ -39,15 +40,38 @@ struct DecodeArgs {
     float* out;            // [total_q][n_heads][head_dim]
     float* part_o;         // [slot][n_heads][head_dim] unnormalised partial outputs
     float* part_ml;        // [slot][n_heads][2] running max (log2 units) and sum
-    int32_t* counters;     // [total_q][heads_kv] splits finished; reset by the last one
     int32_t n_heads;
     int32_t n_kv;
     float scale_log2;      // attn_scale * log2(e)
 };
 
-// Launches the decode kernel instantiated for (head_dim, kv dtype, group).
+// A query token whose pages were split over several units: its partials
+// occupy slots [slot, slot + nsplit).  16 bytes each.
+struct MergeItem {
+    int32_t qi;
+    int32_t slot;
+    int32_t nsplit;
+    int32_t pad;
+};
+static_assert(sizeof(MergeItem) == 16, "MergeItem is packed as 4 int32");
+
+struct MergeArgs {
+    const MergeItem* items;
+    const float* part_o;
+    const float* part_ml;
+    float* out;
+    int32_t n_heads;
+    int32_t n_kv;
+};
+
+// Launches the DPP decode kernel instantiated for (head_dim, kv dtype, group <= 8).
 hipError_t launch_decode(int head_dim, int kv_f16, int group, int num_units,
                          const DecodeArgs& a, hipStream_t stream);
+// Launches the MFMA decode kernel for (head_dim, kv dtype); group <= 16.
+hipError_t launch_decode_mfma(int head_dim, int kv_f16, int num_units, const DecodeArgs& a,
+                              hipStream_t stream);
+// Combines split partials into out, one workgroup per (item, KV head).
+hipError_t launch_merge(int head_dim, int num_items, const MergeArgs& a, hipStream_t stream);
 
 struct WriteTokensArgs {
     void* k_pool;

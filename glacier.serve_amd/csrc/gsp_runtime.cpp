@@ -15,6 +15,7 @@
 #include "gsp_status.h"
 
 using gsp::DecodeUnit;
+using gsp::MergeItem;
 
 namespace {
 
@@ -27,6 +28,7 @@ enum : int {
     kHdrSplitPages,
     kHdrSlots,
     kHdrMaxId,
+    kHdrMerges,
     kHdrWords = 16
 };
 
@@ -64,20 +66,21 @@ struct gsp_ctx {
     bool step_valid = false;
     gsp_step_info info{};
     int32_t max_id = -1;
-    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_units = 0;
+    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_units = 0, off_merge = 0;
 
     // Split-KV workspace.
     float* part = nullptr;
     size_t part_floats = 0;
-    int32_t* counters = nullptr;
-    size_t counter_words = 0;
 
     int32_t split_pages_override = 0;
-    int32_t num_slots = 0;  // partial slots of the packed step
+    int32_t decode_path = GSP_DECODE_AUTO;
+    int32_t num_slots = 0;   // partial slots of the packed step
+    int32_t num_merges = 0;  // query tokens whose partials need merging
 
     // Host scratch reused across steps.
     std::vector<DecodeUnit> units;
-    std::vector<int32_t> q_row, q_ctx;
+    std::vector<MergeItem> merges;
+    std::vector<int32_t> q_ctx;
 };
 
 struct gsp_pool {
@@ -249,7 +252,6 @@ void gsp_shutdown(gsp_ctx* ctx) {
     if (ctx->d_step) (void)hipFree(ctx->d_step);
     if (ctx->d_aux) (void)hipFree(ctx->d_aux);
     if (ctx->part) (void)hipFree(ctx->part);
-    if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->staging_done) (void)hipEventDestroy(ctx->staging_done);
     if (ctx->aux_done) (void)hipEventDestroy(ctx->aux_done);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -286,6 +288,15 @@ int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages) {
     if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
     if (pages < 0) return gsp::fail(GSP_E_INVALID_ARG, "split pages must be >= 0 (got %d)", pages);
     ctx->split_pages_override = pages;
+    return GSP_OK;
+}
+
+int gsp_set_decode_path(gsp_ctx* ctx, int32_t path) {
+    gsp::clear_error();
+    if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
+    if (path != GSP_DECODE_AUTO && path != GSP_DECODE_DPP && path != GSP_DECODE_MFMA)
+        return gsp::fail(GSP_E_INVALID_ARG, "unknown decode path %d", path);
+    ctx->decode_path = path;
     return GSP_OK;
 }
 
@@ -511,6 +522,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
     // Pass 2: per-query contexts and split-KV units.
     const int32_t pps = choose_split_pages(ctx, unit_pages);
     ctx->units.clear();
+    ctx->merges.clear();
     ctx->q_ctx.assign((size_t)total_q, 0);
     int64_t slots = 0;
     {
@@ -538,7 +550,10 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
                     u.slot = nsplit > 1 ? (int32_t)slots : 0;
                     ctx->units.push_back(u);
                 }
-                if (nsplit > 1) slots += nsplit;
+                if (nsplit > 1) {
+                    ctx->merges.push_back(MergeItem{(int32_t)qi, (int32_t)slots, nsplit, 0});
+                    slots += nsplit;
+                }
             }
             bt_base += (total_last + gsp::kBlockSize - 1) / gsp::kBlockSize;
         }
@@ -560,6 +575,9 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
     off = align_up(off, 8);
     const size_t off_units = off;
     off += n_units * (sizeof(DecodeUnit) / sizeof(int32_t));
+    const size_t n_merges = ctx->merges.size();
+    const size_t off_merge = off;
+    off += n_merges * (sizeof(MergeItem) / sizeof(int32_t));
     const size_t words = off;
 
     int rc = set_device(ctx);
@@ -591,6 +609,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
     }
     if (total_q) std::memcpy(st + off_ctx, ctx->q_ctx.data(), (size_t)total_q * sizeof(int32_t));
     if (n_units) std::memcpy(st + off_units, ctx->units.data(), n_units * sizeof(DecodeUnit));
+    if (n_merges) std::memcpy(st + off_merge, ctx->merges.data(), n_merges * sizeof(MergeItem));
     st[kHdrRows] = B;
     st[kHdrTotalQ] = (int32_t)total_q;
     st[kHdrPages] = (int32_t)packed_pages;
@@ -598,6 +617,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
     st[kHdrSplitPages] = pps;
     st[kHdrSlots] = (int32_t)slots;
     st[kHdrMaxId] = max_id;
+    st[kHdrMerges] = (int32_t)n_merges;
 
     rc = check_hip(hipMemcpyAsync(ctx->d_step, st, words * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream),
                    "hipMemcpyAsync(step)");
@@ -609,8 +629,10 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
     ctx->off_ids = off_ids;
     ctx->off_ctx = off_ctx;
     ctx->off_units = off_units;
+    ctx->off_merge = off_merge;
     ctx->max_id = max_id;
     ctx->num_slots = (int32_t)slots;
+    ctx->num_merges = (int32_t)n_merges;
     ctx->info.num_rows = B;
     ctx->info.total_q = (int32_t)total_q;
     ctx->info.packed_pages = (int32_t)packed_pages;
@@ -671,8 +693,13 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     if (n_heads < 1 || n_heads % d.heads_kv != 0)
         return gsp::fail(GSP_E_INVALID_ARG, "nHeads (%d) must be a positive multiple of nHeadsKv (%d)", n_heads, d.heads_kv);
     const int group = n_heads / d.heads_kv;
-    if (group > gsp::kMaxGroup)
-        return gsp::fail(GSP_E_UNSUPPORTED, "GQA group %d exceeds %d query heads per KV head", group, gsp::kMaxGroup);
+    // The matrix-core kernel serves groups up to its 16-wide tile; the DPP
+    // kernel is kept for explicit selection (groups up to 8).
+    const bool use_mfma = ctx->decode_path == GSP_DECODE_MFMA ||
+                          (ctx->decode_path == GSP_DECODE_AUTO && group <= gsp::kMaxGroupMfma);
+    const int max_group = use_mfma ? gsp::kMaxGroupMfma : gsp::kMaxGroup;
+    if (group > max_group)
+        return gsp::fail(GSP_E_UNSUPPORTED, "GQA group %d exceeds %d query heads per KV head", group, max_group);
     if (ctx->max_id >= d.total_blocks)
         return gsp::fail(GSP_E_INVALID_ARG, "block id %d out of range [0, %d)", ctx->max_id, d.total_blocks);
     const gsp_step_info& in = ctx->info;
@@ -685,7 +712,6 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     if (slots > 0) {
         const size_t per_slot = (size_t)n_heads * (d.head_dim + 2);
         rc = ensure_device(ctx, &ctx->part, &ctx->part_floats, (size_t)slots * per_slot, false);
-        if (!rc) rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, (size_t)in.total_q * d.heads_kv, true);
         if (rc) return rc;
     }
 
@@ -701,12 +727,23 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     a.out = out_dev;
     a.part_o = ctx->part;
     a.part_ml = ctx->part ? ctx->part + (size_t)slots * n_heads * d.head_dim : nullptr;
-    a.counters = ctx->counters;
     a.n_heads = n_heads;
     a.n_kv = d.heads_kv;
     a.scale_log2 = attn_scale * 1.4426950408889634f;
-    return check_hip(gsp::launch_decode(d.head_dim, d.kv_dtype == GSP_KV_F16, group, in.decode_units, a, ctx->stream),
-                     "decode launch");
+    const int f16 = d.kv_dtype == GSP_KV_F16;
+    rc = use_mfma ? check_hip(gsp::launch_decode_mfma(d.head_dim, f16, in.decode_units, a, ctx->stream),
+                              "decode (mfma) launch")
+                  : check_hip(gsp::launch_decode(d.head_dim, f16, group, in.decode_units, a, ctx->stream),
+                              "decode (dpp) launch");
+    if (rc || ctx->num_merges == 0) return rc;
+    gsp::MergeArgs m;
+    m.items = reinterpret_cast<const MergeItem*>(ctx->d_step + ctx->off_merge);
+    m.part_o = a.part_o;
+    m.part_ml = a.part_ml;
+    m.out = out_dev;
+    m.n_heads = n_heads;
+    m.n_kv = d.heads_kv;
+    return check_hip(gsp::launch_merge(d.head_dim, ctx->num_merges, m, ctx->stream), "merge launch");
 }
 
 int gsp_compute_attention(gsp_ctx* ctx, const gsp_pool* pool, int32_t stage_layer, int32_t model_layer, int32_t pos,

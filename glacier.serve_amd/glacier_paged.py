@@ -41,6 +41,10 @@ GSP_E_STATE = 5
 
 KV_F32 = 0
 KV_F16 = 1
+
+DECODE_AUTO = 0
+DECODE_DPP = 1
+DECODE_MFMA = 2
 BLOCK_SIZE = 16
 
 
@@ -160,6 +164,7 @@ _SIGNATURES = {
     "gsp_step_get_info": (ctypes.c_int, [vp, ctypes.POINTER(StepInfo)]),
     "gsp_step_download": (ctypes.c_int, [vp, i32p, i32p, i32p]),
     "gsp_set_split_pages": (ctypes.c_int, [vp, i32]),
+    "gsp_set_decode_path": (ctypes.c_int, [vp, i32]),
     "gsp_attention_step": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, ctypes.c_float, fp]),
     "gsp_compute_attention": (
         ctypes.c_int,
@@ -263,6 +268,9 @@ class Context:
 
     def set_split_pages(self, pages: int) -> None:
         _check(self._lib.gsp_set_split_pages(self._h, int(pages)))
+
+    def set_decode_path(self, path: int) -> None:
+        _check(self._lib.gsp_set_decode_path(self._h, int(path)))
 
     # ---- step packing -------------------------------------------------
     def pack_step(

@@ -66,8 +66,10 @@ class Step:
         return 2 if self.kv_dtype == "f16" else 4
 
     def row_ctx(self) -> np.ndarray:
-        """Tokens each row reads: min(TokenCount, pos + q_len) (its last query's total)."""
-        return np.minimum(self.token_counts.astype(np.int64), self.positions.astype(np.int64) + self.lens)
+        """Tokens each row reads: min(TokenCount, pos + q_len) (its last query's total); 0 without queries."""
+        lens = self.lens.astype(np.int64)
+        ctx = np.minimum(self.token_counts.astype(np.int64), self.positions.astype(np.int64) + lens)
+        return np.where(lens > 0, ctx, 0)
 
     def kv_tokens(self) -> int:
         return int(self.row_ctx().sum())

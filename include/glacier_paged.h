@@ -212,6 +212,14 @@ int gsp_step_download(gsp_ctx* ctx, int32_t* row_offsets, int32_t* ids, int32_t*
  * size and the device's CU count; > 0 forces that many pages (for tests). */
 int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages);
 
+/* Decode kernel selection (tuning and tests): GSP_DECODE_AUTO picks the
+ * matrix-core kernel; GSP_DECODE_DPP forces the VALU/DPP kernel (GQA groups up
+ * to 8); GSP_DECODE_MFMA forces the matrix-core kernel (groups up to 16). */
+#define GSP_DECODE_AUTO 0
+#define GSP_DECODE_DPP 1
+#define GSP_DECODE_MFMA 2
+int gsp_set_decode_path(gsp_ctx* ctx, int32_t path);
+
 /* ------------------------------------------------------------------------ */
 /* Attention                                                                 */
 /* ------------------------------------------------------------------------ */
@@ -225,7 +233,7 @@ int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages);
  * out = sum p_t v_t (:73-370).  sink_logit must be NULL: attention sinks are
  * unsupported on the GPU path, as in CudaPagedTransformerRunner.cs:431.
  * Supported: head_dim == v_head_dim in {64, 128}; n_heads % heads_kv == 0 and
- * n_heads / heads_kv <= 8; block_size 16. */
+ * n_heads / heads_kv <= 16; block_size 16. */
 int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t n_heads,
                        const float* q_dev, float* out_dev, float attn_scale,
                        const float* sink_logit);

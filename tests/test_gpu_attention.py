@@ -28,23 +28,58 @@ GEOMS = [
     (12, 2, 64, "f32"),
     (4, 2, 128, "f16"),
     (8, 8, 64, "f16"),
+    (32, 2, 128, "f32"),  # group 16: the matrix-core tile exactly
+    (24, 2, 64, "f16"),   # group 12
 ]
 
+PATHS = {"mfma": 2, "dpp": 1}
 
+
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("geom", GEOMS, ids=lambda g: f"{g[0]}q{g[1]}kv_d{g[2]}_{g[3]}")
 @pytest.mark.parametrize("split_pages", [0, 1, 3, 8])
-def test_decode_matches_oracle(torch_mod, gsp, ctx, geom, split_pages):
+def test_decode_matches_oracle(torch_mod, gsp, ctx, geom, split_pages, path):
     nh, nkv, d, dt = geom
-    print(f"case decode {geom} split={split_pages}", flush=True)
+    if path == "dpp" and nh // nkv > 8:
+        pytest.skip("the DPP kernel serves GQA groups up to 8")
+    print(f"case decode {geom} split={split_pages} path={path}", flush=True)
     step = workloads.small_step(seed=nh * 131 + d + nkv, rows=11, n_heads=nh, n_kv=nkv, head_dim=d, kv_dtype=dt,
                                 ctx_lo=1, ctx_hi=300, total_blocks=256)
     q, k, v = workloads.host_values(step)
     pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
-    got = gpu_step(torch_mod, gsp, ctx, step, q, pool, split_pages=split_pages)
+    ctx.set_decode_path(PATHS[path])
+    try:
+        got = gpu_step(torch_mod, gsp, ctx, step, q, pool, split_pages=split_pages)
+    finally:
+        ctx.set_decode_path(0)
     ref = oracle_step(step, q, k, v, threads=threads())
     pool.destroy()
     assert not np.isnan(got).any()
     assert max_err(got, ref) <= TOL[dt]
+
+
+def test_stale_nan_slots_do_not_leak(torch_mod, gsp, ctx):
+    """Slots past a row's context may hold anything (a wrapped pool is caller memory): NaN there is ignored."""
+    step = workloads.small_step(seed=91, rows=8, n_heads=28, n_kv=4, head_dim=128, ctx_lo=1, ctx_hi=90,
+                                total_blocks=64)
+    q, k, v = workloads.host_values(step)
+    kn, vn = k.copy(), v.copy()
+    for b in range(step.num_rows):
+        tot = int(step.token_counts[b])
+        tbl = step.table(b)
+        last, used = tbl[(tot - 1) // 16], (tot - 1) % 16 + 1
+        kn[last, :, :, used:] = np.nan
+        vn[last, :, :, used:] = np.inf
+    pool, keep = to_device_pool(torch_mod, gsp, ctx, step, kn, vn)
+    for path in (2, 1):
+        ctx.set_decode_path(path)
+        try:
+            got = gpu_step(torch_mod, gsp, ctx, step, q, pool)
+        finally:
+            ctx.set_decode_path(0)
+        ref = oracle_step(step, q, k, v)
+        assert max_err(got, ref) <= 1e-4
+    pool.destroy()
 
 
 @pytest.mark.parametrize("dt", ["f32", "f16"])

@@ -76,8 +76,14 @@ def test_attention_rejects_ids_outside_the_pool(torch_mod, gsp, ctx):
     with pytest.raises(gsp.InvalidArgument):  # layer outside the pool
         ctx.pack_step([0], [1], [0, 1], [3], 16)
         ctx.attention_step(pool, 1, 1, q.data_ptr(), q.data_ptr(), 0.125)
-    with pytest.raises(gsp.Unsupported):  # GQA group above 8
-        ctx.attention_step(pool, 0, 9, q.data_ptr(), q.data_ptr(), 0.125)
+    with pytest.raises(gsp.Unsupported):  # GQA group above 16 is rejected before any launch
+        ctx.attention_step(pool, 0, 17, q.data_ptr(), q.data_ptr(), 0.125)
+    ctx.set_decode_path(gsp.DECODE_DPP)
+    try:
+        with pytest.raises(gsp.Unsupported):  # the DPP kernel stops at 8
+            ctx.attention_step(pool, 0, 9, q.data_ptr(), q.data_ptr(), 0.125)
+    finally:
+        ctx.set_decode_path(gsp.DECODE_AUTO)
     pool.destroy()
 
 
