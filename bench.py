@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "paged-attn decode KV GB/s (% HBM peak) + seq-steps/sec, Qwen2.5-7B shape"
 WORKLOADS = ["qwen05b_decode", "qwen7b_decode", "llama8b_decode", "qwen7b_mixed", "longctx_decode"]
 DEFAULT_WORKLOAD = "qwen7b_decode"
-KERNEL_NAME = "paged_decode_kernel"
+KERNEL_NAME = "paged_decode_mfma_kernel"
 
 
 def cpu_threads() -> int:
@@ -100,7 +100,7 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     out = torch.empty((step.total_q, step.n_heads, step.head_dim), device="cuda", dtype=torch.float32)
 
     def pack():
-        return ctx.pack_step(step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
+        return ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
                              q_lens=step.q_lens)
 
     def attend():
@@ -169,7 +169,8 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         "seq_steps_per_s_incl_pack_upload": round(step.num_rows / (t_step_ms * 1e-3), 1),
         "kv_gbs_incl_pack_upload": round(kv_bytes / (t_step_ms * 1e-3) / 1e9, 1),
         "wall_ms_timed_region": round(wall_ms, 3),
-        "step_info": {"decode_units": info.decode_units, "pages_per_split": info.pages_per_split,
+        "step_info": {"decode_units": info.decode_units, "split_pairs": info.split_pairs,
+                      "partial_slots": info.partial_slots, "pages_per_split": info.pages_per_split,
                       "packed_pages": info.packed_pages, "staging_bytes": int(info.staging_bytes)},
         "roofline": {
             "bound": "hbm",

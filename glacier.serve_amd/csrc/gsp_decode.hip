@@ -1,4 +1,4 @@
-// Split-KV decode kernel of the paged-attention step, written for gfx950
+// DPP (VALU) decode kernel of the paged-attention step, written for gfx950
 // (CDNA4, wave64).
 //
 // It computes PagedAttentionKernel.ComputeAttention
@@ -20,11 +20,10 @@
 // for fp16 at head_dim 128).  QK dot products are reduced across the 16 lanes
 // of a row with DPP row rotations; the page maximum is reduced across the four
 // rows with lane shuffles.  Each wave walks every kDecodeWaves-th page of the
-// unit; the four waves of a workgroup merge through LDS.  A query token whose
-// pages were cut into several units (split-KV, FlashDecoding style) writes
-// (max, sum, unnormalised out) partials that the merge kernel combines with
-// the log-sum-exp rescale.
-#include "gsp_internal.h"
+// unit; the four waves merge through LDS and split units merge in the
+// epilogue (gsp_epilogue.h).  The matrix-core kernel is the default; this one
+// is kept for explicit selection and as an independent second implementation.
+#include "gsp_epilogue.h"
 
 namespace gsp {
 namespace {
@@ -60,8 +59,6 @@ __device__ __forceinline__ float row_allsum16(float x) {
     return x;
 }
 
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
 template <int D, typename KT, int G>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs a) {
     constexpr int S = D / 16;                                          // elements per lane
@@ -70,12 +67,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
     constexpr int CH = 16 * VEC;                                       // distance between chunks
     typedef typename VecOf<KT, VEC>::T VT;
 
-    __shared__ float sh_o[kDecodeWaves][G][D];
-    __shared__ float sh_m[kDecodeWaves][G];
-    __shared__ float sh_l[kDecodeWaves][G];
+    __shared__ EpilogueLds<D, G> sh;
 
     const DecodeUnit u = a.units[blockIdx.x];
-    const int kvh = blockIdx.y;
+    const int kvh = u.kvh;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -194,50 +189,22 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
 #pragma unroll
             for (int c = 0; c < NCH; ++c)
 #pragma unroll
-                for (int j = 0; j < VEC; ++j) sh_o[wave][g][c * CH + lane_off + j] = o[g][c * VEC + j];
+                for (int j = 0; j < VEC; ++j) sh.o[wave][g][c * CH + lane_off + j] = o[g][c * VEC + j];
     }
     if (lane == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            sh_m[wave][g] = m[g];
-            sh_l[wave][g] = l[g];
+            sh.m[wave][g] = m[g];
+            sh.l[wave][g] = l[g];
         }
     }
     __syncthreads();
-
-    const bool single = (u.nsplit == 1);
-    const int64_t slot = (int64_t)u.slot + u.split;
-    for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
-        const int g = idx / D;
-        const int e = idx - g * D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, sh_m[w][g]);
-        float L = 0.f;
-        float O = 0.f;
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) {
-            const float f = fast_exp2(sh_m[w][g] - M);
-            L = fmaf(sh_l[w][g], f, L);
-            O = fmaf(sh_o[w][g][e], f, O);
-        }
-        const int h = h0 + g;
-        if (single) {
-            a.out[((int64_t)u.qi * a.n_heads + h) * D + e] = O / L;
-        } else {
-            a.part_o[(slot * a.n_heads + h) * D + e] = O;
-            if (e == 0) {
-                a.part_ml[(slot * a.n_heads + h) * 2 + 0] = M;
-                a.part_ml[(slot * a.n_heads + h) * 2 + 1] = L;
-            }
-        }
-    }
+    finish_unit<D, G>(a, u, G, sh);
 }
 
 template <int D, typename KT, int G>
 hipError_t launch_one(int num_units, const DecodeArgs& a, hipStream_t stream) {
-    dim3 grid(num_units, a.n_kv);
-    hipLaunchKernelGGL((paged_decode_kernel<D, KT, G>), grid, dim3(kDecodeThreads), 0, stream, a);
+    hipLaunchKernelGGL((paged_decode_kernel<D, KT, G>), dim3(num_units), dim3(kDecodeThreads), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -258,9 +225,9 @@ hipError_t launch_group(int group, int num_units, const DecodeArgs& a, hipStream
 
 }  // namespace
 
-hipError_t launch_decode(int head_dim, int kv_f16, int group, int num_units, const DecodeArgs& a,
-                         hipStream_t stream) {
+hipError_t launch_decode(int head_dim, int kv_f16, int num_units, const DecodeArgs& a, hipStream_t stream) {
     if (num_units <= 0) return hipSuccess;
+    const int group = a.group;
     if (head_dim == 128)
         return kv_f16 ? launch_group<128, _Float16>(group, num_units, a, stream)
                       : launch_group<128, float>(group, num_units, a, stream);

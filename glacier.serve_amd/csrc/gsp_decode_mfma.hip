@@ -21,18 +21,14 @@
 // as zero in hardware (no fetch, no NaN from stale slots reaches P.V).  Each
 // wave streams every kDecodeWaves-th page of its unit with the next page's
 // loads in flight while the current one is computed; the four waves merge
-// through LDS.  Split units write (max, sum, unnormalised out) partials that
-// merge_partials_kernel combines in a second launch.
-#include "gsp_internal.h"
+// through LDS and split units merge in the epilogue (gsp_epilogue.h).
+#include "gsp_epilogue.h"
 
 namespace gsp {
 namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef int i4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const void* base, int bytes) {
     // Raw buffer (stride 0) of `bytes` bytes; offsets at or past the end read 0.
@@ -85,7 +81,7 @@ struct WaveState {
 
 template <int D>
 __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D>& pr, const f4 (&q)[D / 16],
-                                             int ntok, int g) {
+                                             float scale, int ntok, int g) {
     // S^T = K . Q^T: 32 (d = 128) or 16 (d = 64) rank-4 steps, two accumulation chains.
     f4 s0 = {0.f, 0.f, 0.f, 0.f};
     f4 s1 = {0.f, 0.f, 0.f, 0.f};
@@ -99,7 +95,7 @@ __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D>
                 s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(pr.k[j][i], q[j][i], s0, 0, 0, 0);
         }
     }
-    f4 s = s0 + s1;  // lane: S[head n][token 4g + r]
+    f4 s = (s0 + s1) * scale;  // lane: S[head n][token 4g + r] in log2 units
     if (ntok < kBlockSize) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -138,21 +134,24 @@ __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D>
 
 template <int D, typename KT>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(DecodeArgs a) {
-    __shared__ float sh_o[kDecodeWaves][kMaxGroupMfma][D];
-    __shared__ float sh_m[kDecodeWaves][kMaxGroupMfma];
-    __shared__ float sh_l[kDecodeWaves][kMaxGroupMfma];
+    __shared__ EpilogueLds<D, kMaxGroupMfma> sh;
 
     const DecodeUnit u = a.units[blockIdx.x];
-    const int kvh = blockIdx.y;
-    const int G = a.n_heads / a.n_kv;
+    const int G = a.group;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15;
     const int g = lane >> 4;
-    const int h0 = kvh * G;
+    const int h0 = u.kvh * G;
 
-    // Q^T operand: q[j][i] = Q[h0 + n][16j + 4g + i] * scale * log2(e); padded heads are 0.
+    // The first page's block comes with the unit record, so its loads can go
+    // out together with the Q loads.
+    const int first_blk = a.units[blockIdx.x].first_blk[wave];
+
+    // Q^T operand: q[j][i] = Q[h0 + n][16j + 4g + i]; padded heads are 0.  The
+    // scale (times log2 e) multiplies S after the MFMA, as the reference
+    // multiplies the finished dot (PagedAttentionKernel.cs:65).
     f4 q[D / 16];
     {
         const bool live = n < G;
@@ -160,7 +159,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
 #pragma unroll
         for (int j = 0; j < D / 16; ++j) {
             f4 x = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
-            q[j] = live ? x * a.scale_log2 : f4{0.f, 0.f, 0.f, 0.f};
+            q[j] = live ? x : f4{0.f, 0.f, 0.f, 0.f};
         }
     }
 
@@ -170,15 +169,16 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
     st.m = -INFINITY;
     st.l = 0.f;
 
-    const KT* kbase = static_cast<const KT*>(a.k_pool) + a.layer_offset + (int64_t)kvh * a.head_stride;
-    const KT* vbase = static_cast<const KT*>(a.v_pool) + a.layer_offset + (int64_t)kvh * a.head_stride;
+    const KT* kbase = static_cast<const KT*>(a.k_pool) + a.layer_offset + (int64_t)u.kvh * a.head_stride;
+    const KT* vbase = static_cast<const KT*>(a.v_pool) + a.layer_offset + (int64_t)u.kvh * a.head_stride;
     const int32_t* bt = a.bt_ids + u.bt_base;
 
     // Two page buffers in flight: load page p + kDecodeWaves while computing page p.
+    const float scale = a.scale_log2;
     PageRegs<D> ra, rb;
     int p = u.page_begin + wave;
     if (p < u.page_end) {
-        const int64_t blk = bt[p];
+        const int64_t blk = first_blk;
         load_page<D, KT>(ra, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
                          min(kBlockSize, u.ctx - p * kBlockSize), n, g);
     }
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
             load_page<D, KT>(rb, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
                              min(kBlockSize, u.ctx - pn * kBlockSize), n, g);
         }
-        compute_page<D>(st, ra, q, min(kBlockSize, u.ctx - p * kBlockSize), g);
+        compute_page<D>(st, ra, q, scale, min(kBlockSize, u.ctx - p * kBlockSize), g);
         if (pn >= u.page_end) break;
         const int pnn = pn + kDecodeWaves;
         if (pnn < u.page_end) {
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
             load_page<D, KT>(ra, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
                              min(kBlockSize, u.ctx - pnn * kBlockSize), n, g);
         }
-        compute_page<D>(st, rb, q, min(kBlockSize, u.ctx - pn * kBlockSize), g);
+        compute_page<D>(st, rb, q, scale, min(kBlockSize, u.ctx - pn * kBlockSize), g);
         p = pnn;
     }
 
@@ -205,8 +205,8 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
     st.l += __shfl_xor(st.l, 16);
     st.l += __shfl_xor(st.l, 32);
     if (g == 0 && n < G) {
-        sh_m[wave][n] = st.m;
-        sh_l[wave][n] = st.l;
+        sh.m[wave][n] = st.m;
+        sh.l[wave][n] = st.l;
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -215,67 +215,18 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
 #pragma unroll
             for (int c = 0; c < D / 64; ++c)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sh_o[wave][h][64 * c + 4 * n + i] = st.o[4 * c + i][r];
+                for (int i = 0; i < 4; ++i) sh.o[wave][h][64 * c + 4 * n + i] = st.o[4 * c + i][r];
         }
     }
     __syncthreads();
-
-    const bool single = (u.nsplit == 1);
-    const int64_t slot = (int64_t)u.slot + u.split;
-    for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
-        const int hh = idx / D;
-        const int e = idx - hh * D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, sh_m[w][hh]);
-        float L = 0.f;
-        float O = 0.f;
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) {
-            const float f = fast_exp2(sh_m[w][hh] - M);  // waves without pages: m = -inf -> 0
-            L = fmaf(sh_l[w][hh], f, L);
-            O = fmaf(sh_o[w][hh][e], f, O);
-        }
-        const int h = h0 + hh;
-        if (single) {
-            a.out[((int64_t)u.qi * a.n_heads + h) * D + e] = O / L;
-        } else {
-            a.part_o[(slot * a.n_heads + h) * D + e] = O;
-            if (e == 0) {
-                a.part_ml[(slot * a.n_heads + h) * 2 + 0] = M;
-                a.part_ml[(slot * a.n_heads + h) * 2 + 1] = L;
-            }
-        }
-    }
-}
-
-template <int D>
-__global__ __launch_bounds__(256) void merge_partials_kernel(MergeArgs a) {
-    const MergeItem it = a.items[blockIdx.x];
-    const int kvh = blockIdx.y;
-    const int G = a.n_heads / a.n_kv;
-    for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-        const int h = kvh * G + idx / D;
-        const int e = idx % D;
-        float M = -INFINITY;
-        for (int s = 0; s < it.nsplit; ++s) M = fmaxf(M, a.part_ml[(((int64_t)it.slot + s) * a.n_heads + h) * 2]);
-        float L = 0.f;
-        float O = 0.f;
-        for (int s = 0; s < it.nsplit; ++s) {
-            const int64_t si = ((int64_t)it.slot + s) * a.n_heads + h;
-            const float f = fast_exp2(a.part_ml[si * 2] - M);
-            L = fmaf(a.part_ml[si * 2 + 1], f, L);
-            O = fmaf(a.part_o[si * D + e], f, O);
-        }
-        a.out[((int64_t)it.qi * a.n_heads + h) * D + e] = O / L;
-    }
+    finish_unit<D, kMaxGroupMfma>(a, u, G, sh);
 }
 
 }  // namespace
 
 hipError_t launch_decode_mfma(int head_dim, int kv_f16, int num_units, const DecodeArgs& a, hipStream_t stream) {
     if (num_units <= 0) return hipSuccess;
-    dim3 grid(num_units, a.n_kv);
+    dim3 grid(num_units);
     if (head_dim == 128) {
         if (kv_f16)
             hipLaunchKernelGGL((paged_decode_mfma_kernel<128, _Float16>), grid, dim3(kDecodeThreads), 0, stream, a);
@@ -289,18 +240,6 @@ hipError_t launch_decode_mfma(int head_dim, int kv_f16, int num_units, const Dec
     } else {
         return hipErrorInvalidValue;
     }
-    return hipGetLastError();
-}
-
-hipError_t launch_merge(int head_dim, int num_items, const MergeArgs& a, hipStream_t stream) {
-    if (num_items <= 0) return hipSuccess;
-    dim3 grid(num_items, a.n_kv);
-    if (head_dim == 128)
-        hipLaunchKernelGGL(merge_partials_kernel<128>, grid, dim3(256), 0, stream, a);
-    else if (head_dim == 64)
-        hipLaunchKernelGGL(merge_partials_kernel<64>, grid, dim3(256), 0, stream, a);
-    else
-        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

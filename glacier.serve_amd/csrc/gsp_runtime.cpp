@@ -15,8 +15,6 @@
 #include "gsp_status.h"
 
 using gsp::DecodeUnit;
-using gsp::MergeItem;
-
 namespace {
 
 // Packed step layout, in int32 elements from the start of the staging buffer.
@@ -25,12 +23,53 @@ enum : int {
     kHdrTotalQ,
     kHdrPages,
     kHdrUnits,
-    kHdrSplitPages,
+    kHdrTarget,
     kHdrSlots,
     kHdrMaxId,
-    kHdrMerges,
+    kHdrPairsSplit,
+    kHdrHeadsKv,
     kHdrWords = 16
 };
+
+// Split sizing.  The decode grid runs two 256-thread workgroups per CU (the
+// kernels' register use); units are dispatched longest first, i.e. LPT list
+// scheduling onto those slots.  Each candidate split size is scored by
+// simulating that schedule with a unit costing its pages plus a fixed
+// start-up (unit record, first page round trip, partial write), measured on
+// MI355X as about eight pages' worth; the cheapest candidate wins.
+constexpr int kDecodeBlocksPerCu = 2;
+constexpr int64_t kUnitStartupPages = 8;
+constexpr int32_t kSplitCandidates[] = {16, 24, 32, 48, 64, 96, 128, 192, 256, 384, 512, 768, 1024, 2048};
+
+// Makespan (in pages) of LPT-scheduling the units that `target` produces from
+// the per-query page counts onto `slots` identical workgroup slots.
+int64_t simulate_split(const std::vector<int32_t>& pages, int32_t heads_kv, int32_t target, int64_t slots,
+                       std::vector<int64_t>& count, std::vector<int64_t>& heap) {
+    count.assign((size_t)target + 1, 0);
+    for (int32_t P : pages) {
+        const int32_t ns = std::min((P + target - 1) / target, gsp::kMaxSplits);
+        const int32_t base = P / ns, extra = P % ns;
+        count[(size_t)base + 1] += (int64_t)extra * heads_kv;
+        count[(size_t)base] += (int64_t)(ns - extra) * heads_kv;
+    }
+    heap.clear();
+    for (int32_t s = target; s >= 1; --s) {
+        for (int64_t c = count[(size_t)s]; c > 0; --c) {
+            const int64_t cost = s + kUnitStartupPages;
+            if ((int64_t)heap.size() < slots) {
+                heap.push_back(-cost);  // min-heap through negated loads
+                std::push_heap(heap.begin(), heap.end());
+            } else {
+                std::pop_heap(heap.begin(), heap.end());
+                heap.back() -= cost;
+                std::push_heap(heap.begin(), heap.end());
+            }
+        }
+    }
+    int64_t worst = 0;
+    for (int64_t x : heap) worst = std::max(worst, -x);
+    return worst;
+}
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -66,21 +105,32 @@ struct gsp_ctx {
     bool step_valid = false;
     gsp_step_info info{};
     int32_t max_id = -1;
-    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_units = 0, off_merge = 0;
+    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_units = 0;
+    int32_t num_units = 0;      // decode workgroups of the packed step
+    int32_t num_slots = 0;      // partial slots of the packed step
+    int32_t step_heads_kv = 0;  // pool geometry the step was packed for
+    int32_t step_blocks = 0;
 
-    // Split-KV workspace.
+    // Split-KV workspace: partials and per-(query, KV head) split counters.
     float* part = nullptr;
     size_t part_floats = 0;
+    int32_t* counters = nullptr;
+    size_t counter_words = 0;
 
     int32_t split_pages_override = 0;
     int32_t decode_path = GSP_DECODE_AUTO;
-    int32_t num_slots = 0;   // partial slots of the packed step
-    int32_t num_merges = 0;  // query tokens whose partials need merging
+
+    // Split size chosen for the last step shape (reused while the work drifts < 3%).
+    int32_t cached_target = 0;
+    int64_t cached_tasks = 0;
+    int32_t cached_heads_kv = 0;
+    int64_t cached_queries = 0;
 
     // Host scratch reused across steps.
     std::vector<DecodeUnit> units;
-    std::vector<MergeItem> merges;
     std::vector<int32_t> q_ctx;
+    std::vector<int32_t> query_pages;
+    std::vector<int64_t> sim_count, sim_heap;
 };
 
 struct gsp_pool {
@@ -146,17 +196,6 @@ int ensure_device(gsp_ctx* ctx, T** buf, size_t* cap, size_t count, bool zero) {
     }
     *cap = n;
     return GSP_OK;
-}
-
-// Pages per split-KV unit: enough units to give every CU about one
-// workgroup per KV head, never fewer than one page per wave.
-int32_t choose_split_pages(const gsp_ctx* ctx, int64_t total_pages) {
-    if (ctx->split_pages_override > 0) return ctx->split_pages_override;
-    int64_t cus = std::max(1, ctx->num_cus);
-    int64_t pps = (total_pages + cus - 1) / cus;
-    pps = (pps + gsp::kDecodeWaves - 1) / gsp::kDecodeWaves * gsp::kDecodeWaves;
-    pps = std::max<int64_t>(gsp::kDecodeWaves, std::min<int64_t>(pps, 256));
-    return static_cast<int32_t>(pps);
 }
 
 int validate_pool_desc(const gsp_pool_desc* d) {
@@ -252,6 +291,7 @@ void gsp_shutdown(gsp_ctx* ctx) {
     if (ctx->d_step) (void)hipFree(ctx->d_step);
     if (ctx->d_aux) (void)hipFree(ctx->d_aux);
     if (ctx->part) (void)hipFree(ctx->part);
+    if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->staging_done) (void)hipEventDestroy(ctx->staging_done);
     if (ctx->aux_done) (void)hipEventDestroy(ctx->aux_done);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -471,10 +511,11 @@ int gsp_pool_download(gsp_ctx* ctx, gsp_pool* pool, int32_t which, size_t offset
 
 /* ---------------------------------------------------------------- steps */
 
-int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
+int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc) {
     gsp::clear_error();
-    if (!ctx || !desc) return gsp::fail(GSP_E_INVALID_ARG, "ctx/desc is NULL");
+    if (!ctx || !pool || !desc) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool/desc is NULL");
     ctx->step_valid = false;
+    const gsp_pool_desc& pd = pool->desc;
     const int32_t B = desc->num_rows;
     if (B < 0) return gsp::fail(GSP_E_INVALID_ARG, "num_rows must be >= 0 (got %d)", B);
     if (desc->max_seq_len <= 0)
@@ -482,9 +523,11 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
     if (B > 0 && (!desc->positions || !desc->token_counts || !desc->bt_offsets || !desc->bt_ids))
         return gsp::fail(GSP_E_INVALID_ARG, "positions/token_counts/bt_offsets/bt_ids must not be NULL");
     const int32_t L = desc->max_seq_len;
+    const int32_t H = pd.heads_kv;
 
-    // Pass 1: validate rows and size the packed arrays.
-    int64_t total_q = 0, packed_pages = 0, kv_tokens = 0, unit_pages = 0;
+    // Pass 1: validate rows (the reference's throws, PagedAttentionKernel.cs:34-39,
+    // plus the table and pool bounds) and size the packed arrays.
+    int64_t total_q = 0, packed_pages = 0, kv_tokens = 0, pair_pages = 0, max_pages = 0;
     if (B > 0 && desc->bt_offsets[0] < 0)
         return gsp::fail(GSP_E_INVALID_ARG, "bt_offsets[0] must be >= 0");
     for (int32_t b = 0; b < B; ++b) {
@@ -507,24 +550,65 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
                              (long long)total_last, (long long)pages, span);
         const int32_t* ids = desc->bt_ids + desc->bt_offsets[b];
         for (int64_t i = 0; i < pages; ++i)
-            if (ids[i] < 0) return gsp::fail(GSP_E_INVALID_ARG, "row %d: block id %d is negative", b, ids[i]);
+            if (ids[i] < 0 || ids[i] >= pd.total_blocks)
+                return gsp::fail(GSP_E_INVALID_ARG, "row %d: block id %d out of range [0, %d)", b, ids[i],
+                                 pd.total_blocks);
         total_q += ql;
         packed_pages += pages;
         kv_tokens += total_last;
+        max_pages = std::max(max_pages, pages);
         for (int32_t i = 0; i < ql; ++i) {
             const int64_t tot = std::min<int64_t>(tc, (int64_t)pos + i + 1);
-            unit_pages += (tot + gsp::kBlockSize - 1) / gsp::kBlockSize;
+            pair_pages += (tot + gsp::kBlockSize - 1) / gsp::kBlockSize;
         }
     }
-    if (total_q > INT32_MAX / 4 || packed_pages > INT32_MAX / 4)
+    if (total_q > INT32_MAX / 4 || packed_pages > INT32_MAX / 4 || pair_pages * H > INT32_MAX / 2)
         return gsp::fail(GSP_E_INVALID_ARG, "step too large");
 
-    // Pass 2: per-query contexts and split-KV units.
-    const int32_t pps = choose_split_pages(ctx, unit_pages);
+    // Pass 2: split-KV units.  Each query token is cut into nsplit near-equal
+    // page ranges of at most `target` pages; a unit is one (query token, KV
+    // head, page range) and one workgroup.  Units are sorted longest first, so
+    // in-order dispatch schedules them longest-processing-time first.
+    const int64_t T = pair_pages * H;
+    // A pair may not be cut into more pieces than the merge LDS holds.
+    const int64_t min_target = std::max<int64_t>(1, (max_pages + gsp::kMaxSplits - 1) / gsp::kMaxSplits);
+    int64_t target = 1;
+    if (T > 0) {
+        if (ctx->split_pages_override > 0) {
+            target = std::max<int64_t>(ctx->split_pages_override, min_target);
+        } else if (ctx->cached_target > 0 && ctx->cached_heads_kv == H && ctx->cached_queries == total_q &&
+                   T * 100 >= ctx->cached_tasks * 97 && T * 100 <= ctx->cached_tasks * 103) {
+            target = std::max<int64_t>(ctx->cached_target, min_target);  // engine steps drift slowly
+        } else {
+            ctx->query_pages.clear();
+            for (int32_t b = 0; b < B; ++b) {
+                const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
+                for (int32_t i = 0; i < ql; ++i) {
+                    const int64_t tot = std::min<int64_t>(desc->token_counts[b], (int64_t)desc->positions[b] + i + 1);
+                    if (tot > 0) ctx->query_pages.push_back((int32_t)((tot + gsp::kBlockSize - 1) / gsp::kBlockSize));
+                }
+            }
+            const int64_t slots_dev = (int64_t)std::max(1, ctx->num_cus) * kDecodeBlocksPerCu;
+            int64_t best_cost = INT64_MAX;
+            for (int32_t cand : kSplitCandidates) {
+                if (cand < min_target) continue;
+                if (T / cand > 16 * slots_dev) continue;  // far too many units to be competitive
+                const int64_t c = simulate_split(ctx->query_pages, H, cand, slots_dev, ctx->sim_count, ctx->sim_heap);
+                if (c <= best_cost) {  // ties go to the larger split (fewer units)
+                    best_cost = c;
+                    target = cand;
+                }
+                if (cand >= max_pages) break;  // larger candidates give the same units
+            }
+            ctx->cached_target = (int32_t)target;
+            ctx->cached_tasks = T;
+            ctx->cached_heads_kv = H;
+            ctx->cached_queries = total_q;
+        }
+    }
     ctx->units.clear();
-    ctx->merges.clear();
     ctx->q_ctx.assign((size_t)total_q, 0);
-    int64_t slots = 0;
+    int64_t slots = 0, pairs_split = 0;
     {
         int64_t qi = 0, bt_base = 0;
         for (int32_t b = 0; b < B; ++b) {
@@ -537,33 +621,40 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
                 ctx->q_ctx[qi] = tot;
                 if (tot <= 0) continue;
                 const int32_t pages = (tot + gsp::kBlockSize - 1) / gsp::kBlockSize;
-                const int32_t nsplit = (pages + pps - 1) / pps;
-                for (int32_t s = 0; s < nsplit; ++s) {
-                    DecodeUnit u;
-                    u.qi = (int32_t)qi;
-                    u.bt_base = (int32_t)bt_base;
-                    u.page_begin = s * pps;
-                    u.page_end = std::min(pages, (s + 1) * pps);
-                    u.ctx = tot;
-                    u.split = s;
-                    u.nsplit = nsplit;
-                    u.slot = nsplit > 1 ? (int32_t)slots : 0;
-                    ctx->units.push_back(u);
-                }
-                if (nsplit > 1) {
-                    ctx->merges.push_back(MergeItem{(int32_t)qi, (int32_t)slots, nsplit, 0});
-                    slots += nsplit;
+                const int32_t nsplit = (int32_t)std::min<int64_t>((pages + target - 1) / target, gsp::kMaxSplits);
+                const int32_t base = pages / nsplit, extra = pages % nsplit;
+                for (int32_t kvh = 0; kvh < H; ++kvh) {
+                    for (int32_t s = 0; s < nsplit; ++s) {
+                        DecodeUnit u;
+                        u.qi = (int32_t)qi;
+                        u.bt_base = (int32_t)bt_base;
+                        u.page_begin = s * base + std::min(s, extra);
+                        u.page_end = u.page_begin + base + (s < extra ? 1 : 0);
+                        u.ctx = tot;
+                        u.kvh = kvh;
+                        u.slot = nsplit > 1 ? (int32_t)slots : -1;
+                        u.split_info = s | (nsplit << 16);
+                        const int32_t* row_ids = desc->bt_ids + desc->bt_offsets[b];
+                        for (int w = 0; w < gsp::kDecodeWaves; ++w) {
+                            const int32_t p = u.page_begin + w;
+                            u.first_blk[w] = p < u.page_end ? row_ids[p] : -1;
+                        }
+                        ctx->units.push_back(u);
+                    }
+                    if (nsplit > 1) {
+                        slots += nsplit;
+                        ++pairs_split;
+                    }
                 }
             }
             bt_base += (total_last + gsp::kBlockSize - 1) / gsp::kBlockSize;
         }
     }
-    // Longest units first so the tail of the grid is made of short ones.
     std::stable_sort(ctx->units.begin(), ctx->units.end(), [](const DecodeUnit& x, const DecodeUnit& y) {
         return (x.page_end - x.page_begin) > (y.page_end - y.page_begin);
     });
 
-    // Pass 3: write the staging buffer.
+    // Pass 3: write the staging buffer and upload it with one copy.
     const size_t n_units = ctx->units.size();
     size_t off = kHdrWords;
     const size_t off_rows = off;
@@ -575,9 +666,6 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
     off = align_up(off, 8);
     const size_t off_units = off;
     off += n_units * (sizeof(DecodeUnit) / sizeof(int32_t));
-    const size_t n_merges = ctx->merges.size();
-    const size_t off_merge = off;
-    off += n_merges * (sizeof(MergeItem) / sizeof(int32_t));
     const size_t words = off;
 
     int rc = set_device(ctx);
@@ -609,15 +697,15 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
     }
     if (total_q) std::memcpy(st + off_ctx, ctx->q_ctx.data(), (size_t)total_q * sizeof(int32_t));
     if (n_units) std::memcpy(st + off_units, ctx->units.data(), n_units * sizeof(DecodeUnit));
-    if (n_merges) std::memcpy(st + off_merge, ctx->merges.data(), n_merges * sizeof(MergeItem));
     st[kHdrRows] = B;
     st[kHdrTotalQ] = (int32_t)total_q;
     st[kHdrPages] = (int32_t)packed_pages;
     st[kHdrUnits] = (int32_t)n_units;
-    st[kHdrSplitPages] = pps;
+    st[kHdrTarget] = (int32_t)target;
     st[kHdrSlots] = (int32_t)slots;
     st[kHdrMaxId] = max_id;
-    st[kHdrMerges] = (int32_t)n_merges;
+    st[kHdrPairsSplit] = (int32_t)pairs_split;
+    st[kHdrHeadsKv] = H;
 
     rc = check_hip(hipMemcpyAsync(ctx->d_step, st, words * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream),
                    "hipMemcpyAsync(step)");
@@ -629,16 +717,19 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc) {
     ctx->off_ids = off_ids;
     ctx->off_ctx = off_ctx;
     ctx->off_units = off_units;
-    ctx->off_merge = off_merge;
     ctx->max_id = max_id;
     ctx->num_slots = (int32_t)slots;
-    ctx->num_merges = (int32_t)n_merges;
+    ctx->num_units = (int32_t)n_units;
+    ctx->step_heads_kv = H;
+    ctx->step_blocks = pd.total_blocks;
     ctx->info.num_rows = B;
     ctx->info.total_q = (int32_t)total_q;
     ctx->info.packed_pages = (int32_t)packed_pages;
+    ctx->info.heads_kv = H;
     ctx->info.decode_units = (int32_t)n_units;
-    ctx->info.prefill_tiles = 0;
-    ctx->info.pages_per_split = pps;
+    ctx->info.split_pairs = (int32_t)pairs_split;
+    ctx->info.partial_slots = (int32_t)slots;
+    ctx->info.pages_per_split = (int32_t)target;
     ctx->info.kv_tokens = kv_tokens;
     ctx->info.staging_bytes = (int64_t)(words * sizeof(int32_t));
     ctx->step_valid = true;
@@ -692,6 +783,9 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     if (layer < 0 || layer >= d.layers) return gsp::fail(GSP_E_INVALID_ARG, "layer %d out of range [0, %d)", layer, d.layers);
     if (n_heads < 1 || n_heads % d.heads_kv != 0)
         return gsp::fail(GSP_E_INVALID_ARG, "nHeads (%d) must be a positive multiple of nHeadsKv (%d)", n_heads, d.heads_kv);
+    if (d.heads_kv != ctx->step_heads_kv || d.total_blocks < ctx->step_blocks)
+        return gsp::fail(GSP_E_INVALID_ARG, "the step was packed for a pool with %d KV heads and %d blocks",
+                         ctx->step_heads_kv, ctx->step_blocks);
     const int group = n_heads / d.heads_kv;
     // The matrix-core kernel serves groups up to its 16-wide tile; the DPP
     // kernel is kept for explicit selection (groups up to 8).
@@ -702,16 +796,17 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
         return gsp::fail(GSP_E_UNSUPPORTED, "GQA group %d exceeds %d query heads per KV head", group, max_group);
     if (ctx->max_id >= d.total_blocks)
         return gsp::fail(GSP_E_INVALID_ARG, "block id %d out of range [0, %d)", ctx->max_id, d.total_blocks);
-    const gsp_step_info& in = ctx->info;
-    if (in.decode_units == 0) return GSP_OK;
+    if (ctx->num_units == 0) return GSP_OK;
     if (!q_dev || !out_dev) return gsp::fail(GSP_E_INVALID_ARG, "q/out must not be NULL");
     int rc = set_device(ctx);
     if (rc) return rc;
 
     const int32_t slots = ctx->num_slots;
     if (slots > 0) {
-        const size_t per_slot = (size_t)n_heads * (d.head_dim + 2);
+        const size_t per_slot = (size_t)group * (d.head_dim + 2);
         rc = ensure_device(ctx, &ctx->part, &ctx->part_floats, (size_t)slots * per_slot, false);
+        // Counters start at zero and every launch leaves them at zero.
+        if (!rc) rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, (size_t)ctx->info.total_q * d.heads_kv, true);
         if (rc) return rc;
     }
 
@@ -726,24 +821,17 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     a.q = q_dev;
     a.out = out_dev;
     a.part_o = ctx->part;
-    a.part_ml = ctx->part ? ctx->part + (size_t)slots * n_heads * d.head_dim : nullptr;
+    a.part_ml = ctx->part ? ctx->part + (size_t)slots * group * d.head_dim : nullptr;
+    a.counters = ctx->counters;
     a.n_heads = n_heads;
     a.n_kv = d.heads_kv;
+    a.group = group;
     a.scale_log2 = attn_scale * 1.4426950408889634f;
     const int f16 = d.kv_dtype == GSP_KV_F16;
-    rc = use_mfma ? check_hip(gsp::launch_decode_mfma(d.head_dim, f16, in.decode_units, a, ctx->stream),
-                              "decode (mfma) launch")
-                  : check_hip(gsp::launch_decode(d.head_dim, f16, group, in.decode_units, a, ctx->stream),
-                              "decode (dpp) launch");
-    if (rc || ctx->num_merges == 0) return rc;
-    gsp::MergeArgs m;
-    m.items = reinterpret_cast<const MergeItem*>(ctx->d_step + ctx->off_merge);
-    m.part_o = a.part_o;
-    m.part_ml = a.part_ml;
-    m.out = out_dev;
-    m.n_heads = n_heads;
-    m.n_kv = d.heads_kv;
-    return check_hip(gsp::launch_merge(d.head_dim, ctx->num_merges, m, ctx->stream), "merge launch");
+    return use_mfma ? check_hip(gsp::launch_decode_mfma(d.head_dim, f16, ctx->num_units, a, ctx->stream),
+                                "decode (mfma) launch")
+                    : check_hip(gsp::launch_decode(d.head_dim, f16, ctx->num_units, a, ctx->stream),
+                                "decode (dpp) launch");
 }
 
 int gsp_compute_attention(gsp_ctx* ctx, const gsp_pool* pool, int32_t stage_layer, int32_t model_layer, int32_t pos,
@@ -772,7 +860,7 @@ int gsp_compute_attention(gsp_ctx* ctx, const gsp_pool* pool, int32_t stage_laye
     s.token_counts = &token_count;
     s.bt_offsets = offsets;
     s.bt_ids = n_block_ids ? block_ids : empty_ids;
-    int rc = gsp_step_pack(ctx, &s);
+    int rc = gsp_step_pack(ctx, pool, &s);
     if (rc) return rc;
     return gsp_attention_step(ctx, pool, stage_layer, n_heads, q_dev, out_dev, attn_scale, sink_logit);
 }

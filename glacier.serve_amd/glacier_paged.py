@@ -117,8 +117,10 @@ class StepInfo(ctypes.Structure):
         ("num_rows", i32),
         ("total_q", i32),
         ("packed_pages", i32),
+        ("heads_kv", i32),
         ("decode_units", i32),
-        ("prefill_tiles", i32),
+        ("split_pairs", i32),
+        ("partial_slots", i32),
         ("pages_per_split", i32),
         ("kv_tokens", ctypes.c_int64),
         ("staging_bytes", ctypes.c_int64),
@@ -160,7 +162,7 @@ _SIGNATURES = {
     "gsp_pool_copy_block": (ctypes.c_int, [vp, vp, i32, i32, i32]),
     "gsp_pool_upload": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
     "gsp_pool_download": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
-    "gsp_step_pack": (ctypes.c_int, [vp, ctypes.POINTER(StepDesc)]),
+    "gsp_step_pack": (ctypes.c_int, [vp, vp, ctypes.POINTER(StepDesc)]),
     "gsp_step_get_info": (ctypes.c_int, [vp, ctypes.POINTER(StepInfo)]),
     "gsp_step_download": (ctypes.c_int, [vp, i32p, i32p, i32p]),
     "gsp_set_split_pages": (ctypes.c_int, [vp, i32]),
@@ -267,6 +269,7 @@ class Context:
         _check(self._lib.gsp_sync(self._h))
 
     def set_split_pages(self, pages: int) -> None:
+        """Largest split-KV unit in pages for the next pack (0: sized from the step and device)."""
         _check(self._lib.gsp_set_split_pages(self._h, int(pages)))
 
     def set_decode_path(self, path: int) -> None:
@@ -275,6 +278,7 @@ class Context:
     # ---- step packing -------------------------------------------------
     def pack_step(
         self,
+        pool: "Pool",
         positions: Sequence[int],
         token_counts: Sequence[int],
         bt_offsets: Sequence[int],
@@ -295,7 +299,7 @@ class Context:
         d.token_counts = _ptr(tc)
         d.bt_offsets = _ptr(off)
         d.bt_ids = _ptr(ids)
-        _check(self._lib.gsp_step_pack(self._h, ctypes.byref(d)))
+        _check(self._lib.gsp_step_pack(self._h, pool.handle, ctypes.byref(d)))
         return self.step_info()
 
     def step_info(self) -> StepInfo:

@@ -175,9 +175,10 @@ typedef struct gsp_step_desc {
     const int32_t* bt_ids;       /* concatenated BlockTable.AsSpan() of each row */
 } gsp_step_desc;
 
-/* Validates and packs one engine step and uploads it with a single
- * host-to-device copy on the context's stream.  Query token i of row b sits at
- * pos = positions[b] + i and attends to
+/* Validates and packs one engine step for `pool` (its KV-head count and
+ * block count) and uploads it with a single host-to-device copy on the
+ * context's stream; the packed step serves every layer of that pool.  Query
+ * token i of row b sits at pos = positions[b] + i and attends to
  *     total = min(token_counts[b], pos + 1)           (PagedAttentionKernel.cs:41)
  * tokens (causal for q_lens[b] > 1, PagedTransformerRunner.cs:454-474); a row
  * whose every query token has total == 0 is skipped and its out rows are left
@@ -185,20 +186,21 @@ typedef struct gsp_step_desc {
  * entries of a row are packed.  Errors (GSP_E_INVALID_ARG):
  *   max_seq_len <= 0; pos < 0 or pos + q_len - 1 >= max_seq_len
  *   (PagedAttentionKernel.cs:34-37); token_counts[b] > max_seq_len (:38-39);
- *   a row's table shorter than ceil(total/16); a block id outside the pool
- *   (checked by gsp_attention_step against the pool). */
-int gsp_step_pack(gsp_ctx* ctx, const gsp_step_desc* desc);
+ *   a row's table shorter than ceil(total/16); a block id outside the pool. */
+int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc);
 
 /* Sizes of the packed step (for tests and the bench). */
 typedef struct gsp_step_info {
     int32_t num_rows;
-    int32_t total_q;         /* query tokens in the step = sum of q_lens */
-    int32_t packed_pages;    /* bt entries actually packed */
-    int32_t decode_units;    /* work units of the split-KV decode kernel */
-    int32_t prefill_tiles;   /* work tiles of the MFMA prefill kernel */
-    int32_t pages_per_split; /* split size chosen for this step */
-    int64_t kv_tokens;       /* sum over rows of the longest total (KV tokens read once) */
-    int64_t staging_bytes;   /* bytes of the single host-to-device upload */
+    int32_t total_q;             /* query tokens in the step = sum of q_lens */
+    int32_t packed_pages;        /* bt entries actually packed */
+    int32_t heads_kv;            /* KV heads of the pool the step was packed for */
+    int32_t decode_units;        /* (query, KV head, page range) units = decode workgroups */
+    int32_t split_pairs;         /* (query, KV head) pairs cut into several units */
+    int32_t partial_slots;       /* split partials written and merged */
+    int32_t pages_per_split;     /* largest unit, in pages */
+    int64_t kv_tokens;           /* sum over rows of the longest total (KV tokens read once) */
+    int64_t staging_bytes;       /* bytes of the single host-to-device upload */
 } gsp_step_info;
 
 int gsp_step_get_info(const gsp_ctx* ctx, gsp_step_info* out);
@@ -208,8 +210,10 @@ int gsp_step_get_info(const gsp_ctx* ctx, gsp_step_info* out);
  * `total` of each query token).  Any output may be NULL.  Synchronous. */
 int gsp_step_download(gsp_ctx* ctx, int32_t* row_offsets, int32_t* ids, int32_t* ctx_lens);
 
-/* Pages per split-KV unit: 0 (default) lets the library choose from the step's
- * size and the device's CU count; > 0 forces that many pages (for tests). */
+/* Largest split-KV unit, in pages, for the next gsp_step_pack: 0 (default)
+ * sizes units from the step's page count and the device's CU count; > 0
+ * forces it (tuning and tests, e.g. 1 cuts every query token into one-page
+ * splits).  A query token is never cut into more than 256 splits. */
 int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages);
 
 /* Decode kernel selection (tuning and tests): GSP_DECODE_AUTO picks the

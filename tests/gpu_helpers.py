@@ -23,7 +23,7 @@ def to_device_pool(torch, gsp, ctx, step, k, v):
 def gpu_step(torch, gsp, ctx, step, q, pool, layer=0, split_pages=0, fill=np.nan):
     """Packs the step, runs gsp_attention_step and returns out [total_q, nH, d] on the host."""
     ctx.set_split_pages(split_pages)
-    ctx.pack_step(step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
+    ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
                   q_lens=step.q_lens)
     qd = torch.from_numpy(np.ascontiguousarray(q, dtype=np.float32)).cuda()
     out = torch.full((step.total_q, step.n_heads, step.head_dim), float(fill), dtype=torch.float32, device="cuda")

@@ -24,7 +24,7 @@ def test_full_size_config_matches_oracle(torch_mod, gsp, ctx, cfg):
     pool = gsp.Pool.wrap(ctx, k.data_ptr(), v.data_ptr(), step.total_blocks, 1, step.n_kv, step.head_dim,
                          gsp.KV_F16 if step.kv_dtype == "f16" else gsp.KV_F32)
     out = torch.full((step.total_q, step.n_heads, step.head_dim), float("nan"), device="cuda")
-    ctx.pack_step(step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
+    ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
                   q_lens=step.q_lens)
     torch.cuda.synchronize()
     ctx.attention_step(pool, 0, step.n_heads, q.data_ptr(), out.data_ptr(), step.scale)

@@ -35,8 +35,11 @@ def test_packing_is_bit_exact(gsp, ctx, which):
                                     q_lens=np.array([1, 9, 1, 33, 0, 2, 16], np.int32))
     else:
         step = workloads.llama8b_decode(steps=300)
-    info = ctx.pack_step(step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
+    # Packing reads only the pool's geometry; a thin pool of the same block count will do.
+    pool = gsp.Pool.create(ctx, total_blocks=step.total_blocks, layers=1, heads_kv=step.n_kv, head_dim=4)
+    info = ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
                          q_lens=step.q_lens)
+    pool.destroy()
     rows, ids, ctxs = ctx.download_step()
     er, ei, ec = expected_packing(step)
     assert np.array_equal(rows, er)
@@ -47,35 +50,41 @@ def test_packing_is_bit_exact(gsp, ctx, which):
 
 
 def test_pack_rejects_what_the_reference_throws_on(gsp, ctx):
+    pool = gsp.Pool.create(ctx, total_blocks=4, layers=1, heads_kv=1, head_dim=4)
     ok = dict(positions=[3], token_counts=[4], bt_offsets=[0, 1], bt_ids=[0], max_seq_len=16)
 
     def pack(**kw):
         a = dict(ok)
         a.update(kw)
-        ctx.pack_step(**a)
+        ctx.pack_step(pool, **a)
 
     pack()
     for bad in (dict(positions=[16]), dict(positions=[-1]), dict(max_seq_len=0), dict(token_counts=[17]),
                 dict(token_counts=[-1]), dict(positions=[40], token_counts=[41], max_seq_len=64),
-                dict(bt_ids=[-3]), dict(positions=[10], q_lens=[7])):
+                dict(bt_ids=[-3]), dict(bt_ids=[4]), dict(positions=[10], q_lens=[7])):
         with pytest.raises(gsp.InvalidArgument):
             pack(**bad)
     # After a failed pack there is no step to run.
     with pytest.raises(gsp.StateError):
         ctx.step_info()
+    pool.destroy()
 
 
 def test_attention_rejects_ids_outside_the_pool(torch_mod, gsp, ctx):
     torch = torch_mod
     k = torch.zeros((4, 1, 1, 16, 64), device="cuda")
     pool = gsp.Pool.wrap(ctx, k.data_ptr(), k.data_ptr(), 4, 1, 1, 64)
-    ctx.pack_step([0], [1], [0, 1], [4], 16)
-    q = torch.zeros((1, 1, 64), device="cuda")
-    with pytest.raises(gsp.InvalidArgument):
-        ctx.attention_step(pool, 0, 1, q.data_ptr(), q.data_ptr(), 0.125)
+    k2 = torch.zeros((2, 1, 2, 16, 64), device="cuda")
+    pool2 = gsp.Pool.wrap(ctx, k2.data_ptr(), k2.data_ptr(), 2, 1, 2, 64)
+    with pytest.raises(gsp.InvalidArgument):  # block id 4 of a 4-block pool
+        ctx.pack_step(pool, [0], [1], [0, 1], [4], 16)
+    q = torch.zeros((1, 2, 64), device="cuda")
+    ctx.pack_step(pool, [0], [1], [0, 1], [3], 16)
     with pytest.raises(gsp.InvalidArgument):  # layer outside the pool
-        ctx.pack_step([0], [1], [0, 1], [3], 16)
         ctx.attention_step(pool, 1, 1, q.data_ptr(), q.data_ptr(), 0.125)
+    with pytest.raises(gsp.InvalidArgument):  # packed for another pool geometry
+        ctx.attention_step(pool2, 0, 2, q.data_ptr(), q.data_ptr(), 0.125)
+    pool2.destroy()
     with pytest.raises(gsp.Unsupported):  # GQA group above 16 is rejected before any launch
         ctx.attention_step(pool, 0, 17, q.data_ptr(), q.data_ptr(), 0.125)
     ctx.set_decode_path(gsp.DECODE_DPP)
