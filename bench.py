@@ -52,6 +52,19 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def profiled_traffic(workload: str):
+    """HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary of this workload (profiles/), or None when none has been recorded."""
+    path = ROOT / "profiles" / f"{KERNEL_NAME}_{workload}.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def describe(step) -> dict:
     import numpy as np
 
@@ -179,7 +192,7 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(name),
             "algorithmic_bytes_per_launch": kv_bytes,
             "mean_launch_ms": round(kernel_ms, 5),
         },
@@ -251,6 +264,9 @@ def main() -> int:
     ap.add_argument("--all", action="store_true", help="one line per workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline timing")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run a device copy of this many MiB (a known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this path is not sharded across GPUs "
@@ -260,6 +276,17 @@ def main() -> int:
     for name in names:
         res = run_workload(name, args.steps, args.warmup, cpu=not args.no_cpu, cpu_budget_s=args.cpu_budget)
         print(json.dumps(res), flush=True)
+    if args.copy_calibration > 0:
+        import torch
+
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, device="cuda", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}),
+              file=sys.stderr, flush=True)
     return 0
 
 
