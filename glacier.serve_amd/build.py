@@ -20,6 +20,7 @@ LIB = PKG / "libglacier_paged.so"
 SOURCES = [
     CSRC / "gsp_decode.hip",
     CSRC / "gsp_decode_mfma.hip",
+    CSRC / "gsp_prefill_mfma.hip",
     CSRC / "gsp_pool_ops.hip",
     CSRC / "gsp_runtime.cpp",
     CSRC / "gsp_host_meta.cpp",

@@ -51,6 +51,43 @@ struct DecodeArgs {
     float scale_log2;      // attn_scale * log2(e)
 };
 
+// One prefill tile, one workgroup per (tile, group of up to 8 query heads):
+// up to 16 consecutive query tokens of one row against one KV head.  Query
+// token j of the tile attends to min(token_count, pos0 + j + 1) tokens.
+struct PrefillTile {
+    int32_t qi0;          // first query token of the tile (row of q / out)
+    int32_t bt_base;      // offset of the row's table inside the packed ids
+    int32_t pos0;         // position of the first query token
+    int32_t ntok;         // query tokens in the tile, 1..16
+    int32_t token_count;  // the row's BlockTable.TokenCount
+    int32_t pages;        // ceil(min(token_count, pos0 + ntok) / 16): pages the tile reads
+    int32_t kvh;          // KV head
+    int32_t reserved;
+};
+static_assert(sizeof(PrefillTile) == 32, "PrefillTile is packed as 8 int32");
+
+constexpr int kPrefillTileTokens = 16;  // query tokens per tile (MFMA N dimension)
+constexpr int kPrefillHeads = 8;        // query heads per prefill workgroup (two per wave)
+
+struct PrefillArgs {
+    const void* k_pool;
+    const void* v_pool;
+    int64_t block_stride;
+    int64_t layer_offset;
+    int64_t head_stride;
+    const PrefillTile* tiles;
+    const int32_t* bt_ids;
+    const float* q;        // [total_q][n_heads][head_dim]
+    float* out;            // [total_q][n_heads][head_dim]
+    int32_t n_heads;
+    int32_t n_kv;
+    int32_t group;         // query heads per KV head (any; grid.y covers them 8 at a time)
+    float scale_log2;
+};
+
+// Launches the MFMA prefill kernel for (head_dim, kv dtype).
+hipError_t launch_prefill_mfma(int head_dim, int kv_f16, int num_tiles, const PrefillArgs& a, hipStream_t stream);
+
 // Launches the DPP decode kernel instantiated for (head_dim, kv dtype, group <= 8).
 hipError_t launch_decode(int head_dim, int kv_f16, int num_units, const DecodeArgs& a, hipStream_t stream);
 // Launches the MFMA decode kernel for (head_dim, kv dtype); group <= 16.

@@ -15,6 +15,7 @@
 #include "gsp_status.h"
 
 using gsp::DecodeUnit;
+using gsp::PrefillTile;
 namespace {
 
 // Packed step layout, in int32 elements from the start of the staging buffer.
@@ -28,6 +29,7 @@ enum : int {
     kHdrMaxId,
     kHdrPairsSplit,
     kHdrHeadsKv,
+    kHdrTiles,
     kHdrWords = 16
 };
 
@@ -73,6 +75,16 @@ int64_t simulate_split(const std::vector<int32_t>& pages, int32_t heads_kv, int3
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Rows of at least this many query tokens run as prefill tiles by default:
+// a tile reads each K/V page once for 16 query tokens, while shorter rows keep
+// the decode kernel's split-KV parallelism over long prefixes.
+constexpr int32_t kPrefillAutoMinQ = 16;
+
+bool row_is_tiled(int32_t path, int32_t q_len) {
+    if (path == GSP_PREFILL_PER_TOKEN || q_len < 2) return false;
+    return path == GSP_PREFILL_TILES || q_len >= kPrefillAutoMinQ;
+}
+
 bool is_oom(hipError_t e) { return e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation; }
 
 }  // namespace
@@ -105,8 +117,9 @@ struct gsp_ctx {
     bool step_valid = false;
     gsp_step_info info{};
     int32_t max_id = -1;
-    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_units = 0;
+    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_units = 0, off_tiles = 0;
     int32_t num_units = 0;      // decode workgroups of the packed step
+    int32_t num_tiles = 0;      // prefill tiles of the packed step
     int32_t num_slots = 0;      // partial slots of the packed step
     int32_t step_heads_kv = 0;  // pool geometry the step was packed for
     int32_t step_blocks = 0;
@@ -119,6 +132,7 @@ struct gsp_ctx {
 
     int32_t split_pages_override = 0;
     int32_t decode_path = GSP_DECODE_AUTO;
+    int32_t prefill_path = GSP_PREFILL_AUTO;
 
     // Split size chosen for the last step shape (reused while the work drifts < 3%).
     int32_t cached_target = 0;
@@ -128,6 +142,7 @@ struct gsp_ctx {
 
     // Host scratch reused across steps.
     std::vector<DecodeUnit> units;
+    std::vector<PrefillTile> tiles;
     std::vector<int32_t> q_ctx;
     std::vector<int32_t> query_pages;
     std::vector<int64_t> sim_count, sim_heap;
@@ -337,6 +352,15 @@ int gsp_set_decode_path(gsp_ctx* ctx, int32_t path) {
     if (path != GSP_DECODE_AUTO && path != GSP_DECODE_DPP && path != GSP_DECODE_MFMA)
         return gsp::fail(GSP_E_INVALID_ARG, "unknown decode path %d", path);
     ctx->decode_path = path;
+    return GSP_OK;
+}
+
+int gsp_set_prefill_path(gsp_ctx* ctx, int32_t path) {
+    gsp::clear_error();
+    if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
+    if (path != GSP_PREFILL_AUTO && path != GSP_PREFILL_TILES && path != GSP_PREFILL_PER_TOKEN)
+        return gsp::fail(GSP_E_INVALID_ARG, "unknown prefill path %d", path);
+    ctx->prefill_path = path;
     return GSP_OK;
 }
 
@@ -556,6 +580,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         total_q += ql;
         packed_pages += pages;
         kv_tokens += total_last;
+        if (row_is_tiled(ctx->prefill_path, ql)) continue;  // tiles, not split-KV units
         max_pages = std::max(max_pages, pages);
         for (int32_t i = 0; i < ql; ++i) {
             const int64_t tot = std::min<int64_t>(tc, (int64_t)pos + i + 1);
@@ -583,6 +608,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
             ctx->query_pages.clear();
             for (int32_t b = 0; b < B; ++b) {
                 const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
+                if (row_is_tiled(ctx->prefill_path, ql)) continue;
                 for (int32_t i = 0; i < ql; ++i) {
                     const int64_t tot = std::min<int64_t>(desc->token_counts[b], (int64_t)desc->positions[b] + i + 1);
                     if (tot > 0) ctx->query_pages.push_back((int32_t)((tot + gsp::kBlockSize - 1) / gsp::kBlockSize));
@@ -607,8 +633,9 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         }
     }
     ctx->units.clear();
+    ctx->tiles.clear();
     ctx->q_ctx.assign((size_t)total_q, 0);
-    int64_t slots = 0, pairs_split = 0;
+    int64_t slots = 0, pairs_split = 0, tiled_queries = 0, tiled_pairs = 0;
     {
         int64_t qi = 0, bt_base = 0;
         for (int32_t b = 0; b < B; ++b) {
@@ -616,6 +643,34 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
             const int32_t pos = desc->positions[b];
             const int32_t tc = desc->token_counts[b];
             const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
+            if (row_is_tiled(ctx->prefill_path, ql)) {
+                // Causal tiles of 16 query tokens; a row with TokenCount 0 has
+                // total 0 for every token and gets none (out left untouched).
+                for (int32_t i = 0; i < ql; ++i)
+                    ctx->q_ctx[qi + i] = (int32_t)std::min<int64_t>(tc, (int64_t)pos + i + 1);
+                if (tc > 0) {
+                    for (int32_t t0 = 0; t0 < ql; t0 += gsp::kPrefillTileTokens) {
+                        PrefillTile t;
+                        t.qi0 = (int32_t)(qi + t0);
+                        t.bt_base = (int32_t)bt_base;
+                        t.pos0 = pos + t0;
+                        t.ntok = std::min(gsp::kPrefillTileTokens, ql - t0);
+                        t.token_count = tc;
+                        const int64_t last = std::min<int64_t>(tc, (int64_t)t.pos0 + t.ntok);
+                        t.pages = (int32_t)((last + gsp::kBlockSize - 1) / gsp::kBlockSize);
+                        t.reserved = 0;
+                        for (int32_t kvh = 0; kvh < H; ++kvh) {
+                            t.kvh = kvh;
+                            ctx->tiles.push_back(t);
+                        }
+                    }
+                    for (int32_t i = 0; i < ql; ++i) tiled_pairs += ctx->q_ctx[qi + i];
+                    tiled_queries += ql;
+                }
+                qi += ql;
+                bt_base += (total_last + gsp::kBlockSize - 1) / gsp::kBlockSize;
+                continue;
+            }
             for (int32_t i = 0; i < ql; ++i, ++qi) {
                 const int32_t tot = (int32_t)std::min<int64_t>(tc, (int64_t)pos + i + 1);
                 ctx->q_ctx[qi] = tot;
@@ -653,9 +708,12 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     std::stable_sort(ctx->units.begin(), ctx->units.end(), [](const DecodeUnit& x, const DecodeUnit& y) {
         return (x.page_end - x.page_begin) > (y.page_end - y.page_begin);
     });
+    std::stable_sort(ctx->tiles.begin(), ctx->tiles.end(),
+                     [](const PrefillTile& x, const PrefillTile& y) { return x.pages > y.pages; });
 
     // Pass 3: write the staging buffer and upload it with one copy.
     const size_t n_units = ctx->units.size();
+    const size_t n_tiles = ctx->tiles.size();
     size_t off = kHdrWords;
     const size_t off_rows = off;
     off += (size_t)B + 1;
@@ -666,6 +724,8 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     off = align_up(off, 8);
     const size_t off_units = off;
     off += n_units * (sizeof(DecodeUnit) / sizeof(int32_t));
+    const size_t off_tiles = off;
+    off += n_tiles * (sizeof(PrefillTile) / sizeof(int32_t));
     const size_t words = off;
 
     int rc = set_device(ctx);
@@ -697,6 +757,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     }
     if (total_q) std::memcpy(st + off_ctx, ctx->q_ctx.data(), (size_t)total_q * sizeof(int32_t));
     if (n_units) std::memcpy(st + off_units, ctx->units.data(), n_units * sizeof(DecodeUnit));
+    if (n_tiles) std::memcpy(st + off_tiles, ctx->tiles.data(), n_tiles * sizeof(PrefillTile));
     st[kHdrRows] = B;
     st[kHdrTotalQ] = (int32_t)total_q;
     st[kHdrPages] = (int32_t)packed_pages;
@@ -706,6 +767,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     st[kHdrMaxId] = max_id;
     st[kHdrPairsSplit] = (int32_t)pairs_split;
     st[kHdrHeadsKv] = H;
+    st[kHdrTiles] = (int32_t)n_tiles;
 
     rc = check_hip(hipMemcpyAsync(ctx->d_step, st, words * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream),
                    "hipMemcpyAsync(step)");
@@ -717,9 +779,11 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->off_ids = off_ids;
     ctx->off_ctx = off_ctx;
     ctx->off_units = off_units;
+    ctx->off_tiles = off_tiles;
     ctx->max_id = max_id;
     ctx->num_slots = (int32_t)slots;
     ctx->num_units = (int32_t)n_units;
+    ctx->num_tiles = (int32_t)n_tiles;
     ctx->step_heads_kv = H;
     ctx->step_blocks = pd.total_blocks;
     ctx->info.num_rows = B;
@@ -732,6 +796,9 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->info.pages_per_split = (int32_t)target;
     ctx->info.kv_tokens = kv_tokens;
     ctx->info.staging_bytes = (int64_t)(words * sizeof(int32_t));
+    ctx->info.prefill_tiles = (int32_t)n_tiles;
+    ctx->info.prefill_queries = (int32_t)tiled_queries;
+    ctx->info.prefill_pairs = tiled_pairs;
     ctx->step_valid = true;
     return GSP_OK;
 }
@@ -791,12 +858,13 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     // kernel is kept for explicit selection (groups up to 8).
     const bool use_mfma = ctx->decode_path == GSP_DECODE_MFMA ||
                           (ctx->decode_path == GSP_DECODE_AUTO && group <= gsp::kMaxGroupMfma);
-    const int max_group = use_mfma ? gsp::kMaxGroupMfma : gsp::kMaxGroup;
-    if (group > max_group)
+    const int max_group = ctx->decode_path == GSP_DECODE_DPP ? gsp::kMaxGroup : gsp::kMaxGroupMfma;
+    // Prefill tiles take any group (eight heads per workgroup); decode units do not.
+    if (ctx->num_units > 0 && group > max_group)
         return gsp::fail(GSP_E_UNSUPPORTED, "GQA group %d exceeds %d query heads per KV head", group, max_group);
     if (ctx->max_id >= d.total_blocks)
         return gsp::fail(GSP_E_INVALID_ARG, "block id %d out of range [0, %d)", ctx->max_id, d.total_blocks);
-    if (ctx->num_units == 0) return GSP_OK;
+    if (ctx->num_units == 0 && ctx->num_tiles == 0) return GSP_OK;
     if (!q_dev || !out_dev) return gsp::fail(GSP_E_INVALID_ARG, "q/out must not be NULL");
     int rc = set_device(ctx);
     if (rc) return rc;
@@ -828,10 +896,31 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     a.group = group;
     a.scale_log2 = attn_scale * 1.4426950408889634f;
     const int f16 = d.kv_dtype == GSP_KV_F16;
-    return use_mfma ? check_hip(gsp::launch_decode_mfma(d.head_dim, f16, ctx->num_units, a, ctx->stream),
-                                "decode (mfma) launch")
-                    : check_hip(gsp::launch_decode(d.head_dim, f16, ctx->num_units, a, ctx->stream),
-                                "decode (dpp) launch");
+    if (ctx->num_units > 0) {
+        rc = use_mfma ? check_hip(gsp::launch_decode_mfma(d.head_dim, f16, ctx->num_units, a, ctx->stream),
+                                  "decode (mfma) launch")
+                      : check_hip(gsp::launch_decode(d.head_dim, f16, ctx->num_units, a, ctx->stream),
+                                  "decode (dpp) launch");
+        if (rc) return rc;
+    }
+    if (ctx->num_tiles > 0) {
+        gsp::PrefillArgs p;
+        p.k_pool = a.k_pool;
+        p.v_pool = a.v_pool;
+        p.block_stride = a.block_stride;
+        p.layer_offset = a.layer_offset;
+        p.head_stride = a.head_stride;
+        p.tiles = reinterpret_cast<const PrefillTile*>(ctx->d_step + ctx->off_tiles);
+        p.bt_ids = a.bt_ids;
+        p.q = q_dev;
+        p.out = out_dev;
+        p.n_heads = n_heads;
+        p.n_kv = d.heads_kv;
+        p.group = group;
+        p.scale_log2 = a.scale_log2;
+        rc = check_hip(gsp::launch_prefill_mfma(d.head_dim, f16, ctx->num_tiles, p, ctx->stream), "prefill launch");
+    }
+    return rc;
 }
 
 int gsp_compute_attention(gsp_ctx* ctx, const gsp_pool* pool, int32_t stage_layer, int32_t model_layer, int32_t pos,

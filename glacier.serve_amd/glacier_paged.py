@@ -45,6 +45,9 @@ KV_F16 = 1
 DECODE_AUTO = 0
 DECODE_DPP = 1
 DECODE_MFMA = 2
+PREFILL_AUTO = 0
+PREFILL_TILES = 1
+PREFILL_PER_TOKEN = 2
 BLOCK_SIZE = 16
 
 
@@ -124,6 +127,9 @@ class StepInfo(ctypes.Structure):
         ("pages_per_split", i32),
         ("kv_tokens", ctypes.c_int64),
         ("staging_bytes", ctypes.c_int64),
+        ("prefill_tiles", i32),
+        ("prefill_queries", i32),
+        ("prefill_pairs", ctypes.c_int64),
     ]
 
 
@@ -167,6 +173,7 @@ _SIGNATURES = {
     "gsp_step_download": (ctypes.c_int, [vp, i32p, i32p, i32p]),
     "gsp_set_split_pages": (ctypes.c_int, [vp, i32]),
     "gsp_set_decode_path": (ctypes.c_int, [vp, i32]),
+    "gsp_set_prefill_path": (ctypes.c_int, [vp, i32]),
     "gsp_attention_step": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, ctypes.c_float, fp]),
     "gsp_compute_attention": (
         ctypes.c_int,
@@ -274,6 +281,10 @@ class Context:
 
     def set_decode_path(self, path: int) -> None:
         _check(self._lib.gsp_set_decode_path(self._h, int(path)))
+
+    def set_prefill_path(self, path: int) -> None:
+        """Route prefill rows for the next pack_step (PREFILL_AUTO / TILES / PER_TOKEN)."""
+        _check(self._lib.gsp_set_prefill_path(self._h, int(path)))
 
     # ---- step packing -------------------------------------------------
     def pack_step(

@@ -40,7 +40,7 @@ extern "C" {
 #pragma GCC visibility push(default)
 #endif
 
-#define GSP_ABI_VERSION 1
+#define GSP_ABI_VERSION 2
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
 
 typedef enum gsp_status {
@@ -201,6 +201,9 @@ typedef struct gsp_step_info {
     int32_t pages_per_split;     /* largest unit, in pages */
     int64_t kv_tokens;           /* sum over rows of the longest total (KV tokens read once) */
     int64_t staging_bytes;       /* bytes of the single host-to-device upload */
+    int32_t prefill_tiles;       /* (16 query tokens, KV head) tiles of prefill rows */
+    int32_t prefill_queries;     /* query tokens served by those tiles */
+    int64_t prefill_pairs;       /* sum over tiled query tokens of total (causal key count) */
 } gsp_step_info;
 
 int gsp_step_get_info(const gsp_ctx* ctx, gsp_step_info* out);
@@ -223,6 +226,16 @@ int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages);
 #define GSP_DECODE_DPP 1
 #define GSP_DECODE_MFMA 2
 int gsp_set_decode_path(gsp_ctx* ctx, int32_t path);
+
+/* Prefill-row routing for the next gsp_step_pack (tuning and tests).
+ * GSP_PREFILL_AUTO runs rows with q_len >= 16 as matrix-core tiles of 16 query
+ * tokens x one KV head, which read each K/V page once per tile; shorter rows
+ * go through the decode kernel one query token at a time.  GSP_PREFILL_TILES
+ * tiles every row with q_len >= 2; GSP_PREFILL_PER_TOKEN tiles none. */
+#define GSP_PREFILL_AUTO 0
+#define GSP_PREFILL_TILES 1
+#define GSP_PREFILL_PER_TOKEN 2
+int gsp_set_prefill_path(gsp_ctx* ctx, int32_t path);
 
 /* ------------------------------------------------------------------------ */
 /* Attention                                                                 */

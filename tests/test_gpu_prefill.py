@@ -1,0 +1,154 @@
+"""GPU parity of the matrix-core prefill tiles (rows with q_len > 1) against the CPU oracle.
+
+Query token i of a prefill row attends to min(TokenCount, pos + i + 1) tokens
+(PagedAttentionKernel.cs:41, PagedTransformerRunner.cs:454-474).  The tiles
+cover 16 query tokens x one KV head x up to 8 query heads; these cases pin the
+ragged last tile (q_len % 16), tiles that straddle page boundaries, the first
+chunk of a sequence (pos 0), token counts below pos + q_len, rows with
+TokenCount 0, GQA groups above 8 (several head chunks per tile) and steps that
+mix decode units with tiles.  Bar: max abs error <= 1e-4 (fp32 KV), <= 2e-3 (fp16 KV).
+"""
+import numpy as np
+import pytest
+
+import workloads
+from conftest import threads
+from gpu_helpers import TOL, max_err, oracle_step, to_device_pool
+
+pytestmark = pytest.mark.gpu
+
+PREFILL_PATHS = {"tiles": 1, "auto": 0, "per_token": 2}
+
+GEOMS = [
+    (28, 4, 128, "f32"),  # group 7
+    (14, 2, 64, "f32"),   # group 7, d64
+    (32, 8, 128, "f16"),  # group 4
+    (8, 1, 128, "f32"),   # group 8: one full head chunk
+    (1, 1, 64, "f32"),    # MHA, group 1
+    (32, 2, 128, "f32"),  # group 16: two head chunks
+    (24, 2, 64, "f16"),   # group 12: a full and a partial head chunk
+    (40, 2, 64, "f32"),   # group 20: three chunks (tiles only; decode units stop at 16)
+]
+
+
+def run_step(torch, gsp, ctx, step, q, pool, prefill_path, layer=0, split_pages=0, fill=np.nan):
+    ctx.set_split_pages(split_pages)
+    ctx.set_prefill_path(prefill_path)
+    try:
+        ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
+                      q_lens=step.q_lens)
+        info = ctx.step_info()
+        qd = torch.from_numpy(np.ascontiguousarray(q, dtype=np.float32)).cuda()
+        out = torch.full((step.total_q, step.n_heads, step.head_dim), float(fill), dtype=torch.float32,
+                         device="cuda")
+        torch.cuda.synchronize()
+        ctx.attention_step(pool, layer, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
+        ctx.sync()
+        return out.cpu().numpy(), info
+    finally:
+        ctx.set_split_pages(0)
+        ctx.set_prefill_path(0)
+
+
+def expected_tiles(step, min_q):
+    lens = step.lens
+    return sum(-(-int(ql) // 16) * step.n_kv for ql, tc in zip(lens, step.token_counts) if ql >= min_q and tc > 0)
+
+
+@pytest.mark.parametrize("geom", GEOMS, ids=lambda g: f"{g[0]}q{g[1]}kv_d{g[2]}_{g[3]}")
+@pytest.mark.parametrize("path", list(PREFILL_PATHS))
+def test_prefill_tiles_match_oracle(torch_mod, gsp, ctx, geom, path):
+    nh, nkv, d, dt = geom
+    if path != "tiles" and nh // nkv > 16:
+        pytest.skip("decode units serve GQA groups up to 16")
+    print(f"case prefill {geom} path={path}", flush=True)
+    q_lens = np.array([2, 15, 16, 17, 33, 64, 1, 5, 48, 31], np.int32)
+    if nh // nkv > 16:
+        q_lens[q_lens == 1] = 3  # no decode units: they reject groups above 16
+    step = workloads.small_step(seed=nh * 17 + nkv * 3 + d, rows=len(q_lens), n_heads=nh, n_kv=nkv, head_dim=d,
+                                kv_dtype=dt, ctx_lo=0, ctx_hi=150, total_blocks=256, q_lens=q_lens)
+    q, k, v = workloads.host_values(step)
+    pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
+    got, info = run_step(torch_mod, gsp, ctx, step, q, pool, PREFILL_PATHS[path])
+    ref = oracle_step(step, q, k, v, threads=threads())
+    pool.destroy()
+    min_q = {"tiles": 2, "auto": 16, "per_token": 1 << 30}[path]
+    assert info.prefill_tiles == expected_tiles(step, min_q)
+    assert not np.isnan(got).any()
+    assert max_err(got, ref) <= TOL[dt]
+
+
+def test_first_chunk_and_clamped_token_counts(torch_mod, gsp, ctx):
+    """pos 0 chunks, TokenCount below pos + q_len (later tokens see TokenCount keys) and TokenCount 0."""
+    rng = np.random.default_rng(5)
+    q_lens = np.array([16, 40, 23, 18, 32], np.int32)
+    positions = np.array([0, 0, 30, 100, 7], np.int32)
+    token_counts = np.array([16, 25, 41, 0, 39], np.int32)  # row 3 empty; rows 1, 2, 4 clamp
+    pages = [max(1, -(-int(min(tc, p + ql)) // 16)) for tc, p, ql in zip(token_counts, positions, q_lens)]
+    offsets = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    ids = rng.permutation(64)[: offsets[-1]].astype(np.int32)
+    step = workloads.Step("clamp", 28, 4, 128, "f32", 64, 4096, positions=positions, token_counts=token_counts,
+                          bt_offsets=offsets, bt_ids=ids, q_lens=q_lens, seed=5)
+    q, k, v = workloads.host_values(step)
+    pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
+    got, info = run_step(torch_mod, gsp, ctx, step, q, pool, 1, fill=1234.5)
+    ref = oracle_step(step, q, k, v, fill=1234.5)
+    pool.destroy()
+    r3 = slice(int(q_lens[:3].sum()), int(q_lens[:4].sum()))
+    assert np.all(got[r3] == 1234.5)  # TokenCount 0: every query token has total 0, out untouched
+    assert info.prefill_tiles == (1 + 3 + 2 + 2) * 4
+    assert max_err(got, ref) <= 1e-4
+
+
+def test_stale_slots_past_token_count_do_not_leak(torch_mod, gsp, ctx):
+    """Slots past a prefill row's TokenCount may hold NaN / Inf; tiles never read them."""
+    q_lens = np.array([20, 37, 16], np.int32)
+    step = workloads.small_step(seed=44, rows=3, n_heads=28, n_kv=4, head_dim=128, ctx_lo=0, ctx_hi=60,
+                                total_blocks=64, q_lens=q_lens)
+    q, k, v = workloads.host_values(step)
+    kn, vn = k.copy(), v.copy()
+    for b in range(step.num_rows):
+        tot = int(step.token_counts[b])
+        last, used = step.table(b)[(tot - 1) // 16], (tot - 1) % 16 + 1
+        kn[last, :, :, used:] = np.nan
+        vn[last, :, :, used:] = np.inf
+    pool, keep = to_device_pool(torch_mod, gsp, ctx, step, kn, vn)
+    got, _ = run_step(torch_mod, gsp, ctx, step, q, pool, 1)
+    pool.destroy()
+    assert max_err(got, oracle_step(step, q, k, v)) <= 1e-4
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_mixed_decode_and_prefill_step(torch_mod, gsp, ctx, dt):
+    """Decode units (split-KV) and prefill tiles of one packed step, over two layers."""
+    rng = np.random.default_rng(12)
+    q_lens = np.array([1, 1, 96, 1, 19, 1, 1, 250, 1], np.int32)
+    step = workloads.small_step(seed=12, rows=len(q_lens), n_heads=28, n_kv=4, head_dim=128, kv_dtype=dt,
+                                ctx_lo=0, ctx_hi=500, total_blocks=512, q_lens=q_lens)
+    q, _, _ = workloads.host_values(step)
+    shape = (512, 2, 4, 16, 128)
+    k = rng.standard_normal(shape, dtype=np.float32)
+    v = rng.standard_normal(shape, dtype=np.float32)
+    if dt == "f16":
+        k, v = k.astype(np.float16), v.astype(np.float16)
+    pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
+    for layer, sp in ((0, 0), (1, 3)):
+        got, info = run_step(torch_mod, gsp, ctx, step, q, pool, 0, layer=layer, split_pages=sp)
+        assert info.prefill_tiles == expected_tiles(step, 16) and info.decode_units > 0
+        ref = oracle_step(step, q, k.astype(np.float32), v.astype(np.float32), layer=layer, threads=threads())
+        assert max_err(got, ref) <= TOL[dt]
+    pool.destroy()
+
+
+def test_tiles_equal_per_token_path(torch_mod, gsp, ctx):
+    """The two prefill routes agree with each other to the fp32 bar on a long causal chunk."""
+    q_lens = np.array([300, 129], np.int32)
+    step = workloads.small_step(seed=8, rows=2, n_heads=32, n_kv=8, head_dim=128, ctx_lo=0, ctx_hi=900,
+                                total_blocks=256, q_lens=q_lens)
+    q, k, v = workloads.host_values(step)
+    pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
+    tiles, _ = run_step(torch_mod, gsp, ctx, step, q, pool, 1)
+    per_token, _ = run_step(torch_mod, gsp, ctx, step, q, pool, 2)
+    pool.destroy()
+    assert max_err(tiles, per_token) <= 1e-4
+    assert max_err(tiles, oracle_step(step, q, k, v, threads=threads())) <= 1e-4
