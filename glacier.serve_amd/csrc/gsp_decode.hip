@@ -60,16 +60,13 @@ __device__ __forceinline__ float row_allsum16(float x) {
 }
 
 template <int D, typename KT, int G>
-__global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_unit(const DecodeArgs& a, const DecodeUnit& u, EpilogueLds<D, G>& sh) {
     constexpr int S = D / 16;                                          // elements per lane
     constexpr int VEC = (sizeof(KT) == 4) ? 4 : (S >= 8 ? 8 : 4);      // elements per load
     constexpr int NCH = S / VEC;                                       // loads per token row
     constexpr int CH = 16 * VEC;                                       // distance between chunks
     typedef typename VecOf<KT, VEC>::T VT;
 
-    __shared__ EpilogueLds<D, G> sh;
-
-    const DecodeUnit u = a.units[blockIdx.x];
     const int kvh = u.kvh;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -202,38 +199,50 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
     finish_unit<D, G>(a, u, G, sh);
 }
 
+// One workgroup per bin; the bin's units run back to back.
 template <int D, typename KT, int G>
-hipError_t launch_one(int num_units, const DecodeArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL((paged_decode_kernel<D, KT, G>), dim3(num_units), dim3(kDecodeThreads), 0, stream, a);
+__global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs a) {
+    __shared__ EpilogueLds<D, G> sh;
+    const int rb = a.bin_rest[blockIdx.x];
+    const int re = a.bin_rest[blockIdx.x + 1];
+    for (int k = rb - 1; k < re; ++k) {  // k = rb - 1: the bin's first unit, at index blockIdx.x
+        decode_unit<D, KT, G>(a, a.units[k < rb ? (int)blockIdx.x : k], sh);
+        __syncthreads();  // the epilogue LDS is reused by the next unit
+    }
+}
+
+template <int D, typename KT, int G>
+hipError_t launch_one(int num_bins, const DecodeArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL((paged_decode_kernel<D, KT, G>), dim3(num_bins), dim3(kDecodeThreads), 0, stream, a);
     return hipGetLastError();
 }
 
 template <int D, typename KT>
-hipError_t launch_group(int group, int num_units, const DecodeArgs& a, hipStream_t stream) {
+hipError_t launch_group(int group, int num_bins, const DecodeArgs& a, hipStream_t stream) {
     switch (group) {
-        case 1: return launch_one<D, KT, 1>(num_units, a, stream);
-        case 2: return launch_one<D, KT, 2>(num_units, a, stream);
-        case 3: return launch_one<D, KT, 3>(num_units, a, stream);
-        case 4: return launch_one<D, KT, 4>(num_units, a, stream);
-        case 5: return launch_one<D, KT, 5>(num_units, a, stream);
-        case 6: return launch_one<D, KT, 6>(num_units, a, stream);
-        case 7: return launch_one<D, KT, 7>(num_units, a, stream);
-        case 8: return launch_one<D, KT, 8>(num_units, a, stream);
+        case 1: return launch_one<D, KT, 1>(num_bins, a, stream);
+        case 2: return launch_one<D, KT, 2>(num_bins, a, stream);
+        case 3: return launch_one<D, KT, 3>(num_bins, a, stream);
+        case 4: return launch_one<D, KT, 4>(num_bins, a, stream);
+        case 5: return launch_one<D, KT, 5>(num_bins, a, stream);
+        case 6: return launch_one<D, KT, 6>(num_bins, a, stream);
+        case 7: return launch_one<D, KT, 7>(num_bins, a, stream);
+        case 8: return launch_one<D, KT, 8>(num_bins, a, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
 
-hipError_t launch_decode(int head_dim, int kv_f16, int num_units, const DecodeArgs& a, hipStream_t stream) {
-    if (num_units <= 0) return hipSuccess;
+hipError_t launch_decode(int head_dim, int kv_f16, int num_bins, const DecodeArgs& a, hipStream_t stream) {
+    if (num_bins <= 0) return hipSuccess;
     const int group = a.group;
     if (head_dim == 128)
-        return kv_f16 ? launch_group<128, _Float16>(group, num_units, a, stream)
-                      : launch_group<128, float>(group, num_units, a, stream);
+        return kv_f16 ? launch_group<128, _Float16>(group, num_bins, a, stream)
+                      : launch_group<128, float>(group, num_bins, a, stream);
     if (head_dim == 64)
-        return kv_f16 ? launch_group<64, _Float16>(group, num_units, a, stream)
-                      : launch_group<64, float>(group, num_units, a, stream);
+        return kv_f16 ? launch_group<64, _Float16>(group, num_bins, a, stream)
+                      : launch_group<64, float>(group, num_bins, a, stream);
     return hipErrorInvalidValue;
 }
 

@@ -38,7 +38,11 @@ struct DecodeArgs {
     int64_t block_stride;  // elements per block over all layers and heads
     int64_t layer_offset;  // layer * heads_kv * 16 * head_dim
     int64_t head_stride;   // 16 * head_dim
+    // Workgroup b runs unit b first, then units [bin_rest[b], bin_rest[b + 1]):
+    // the first unit of every bin sits at the bin's own index, so a workgroup
+    // can fetch it without waiting for the offsets.
     const DecodeUnit* units;
+    const int32_t* bin_rest;     // [num_bins + 1], bin_rest[0] == num_bins
     const int32_t* bt_ids;
     const float* q;        // [total_q][n_heads][head_dim]
     float* out;            // [total_q][n_heads][head_dim]
@@ -88,11 +92,11 @@ struct PrefillArgs {
 // Launches the MFMA prefill kernel for (head_dim, kv dtype).
 hipError_t launch_prefill_mfma(int head_dim, int kv_f16, int num_tiles, const PrefillArgs& a, hipStream_t stream);
 
-// Launches the DPP decode kernel instantiated for (head_dim, kv dtype, group <= 8).
-hipError_t launch_decode(int head_dim, int kv_f16, int num_units, const DecodeArgs& a, hipStream_t stream);
+// Launches the DPP decode kernel instantiated for (head_dim, kv dtype, group <= 8),
+// one workgroup per bin.
+hipError_t launch_decode(int head_dim, int kv_f16, int num_bins, const DecodeArgs& a, hipStream_t stream);
 // Launches the MFMA decode kernel for (head_dim, kv dtype); group <= 16.
-hipError_t launch_decode_mfma(int head_dim, int kv_f16, int num_units, const DecodeArgs& a,
-                              hipStream_t stream);
+hipError_t launch_decode_mfma(int head_dim, int kv_f16, int num_bins, const DecodeArgs& a, hipStream_t stream);
 
 struct WriteTokensArgs {
     void* k_pool;

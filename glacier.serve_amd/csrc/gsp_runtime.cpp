@@ -7,7 +7,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/glacier_paged.h"
@@ -30,41 +32,55 @@ enum : int {
     kHdrPairsSplit,
     kHdrHeadsKv,
     kHdrTiles,
+    kHdrBins,
     kHdrWords = 16
 };
 
-// Split sizing.  The decode grid runs two 256-thread workgroups per CU (the
-// kernels' register use); units are dispatched longest first, i.e. LPT list
-// scheduling onto those slots.  Each candidate split size is scored by
-// simulating that schedule with a unit costing its pages plus a fixed
-// start-up (unit record, first page round trip, partial write), measured on
-// MI355X as about eight pages' worth; the cheapest candidate wins.
-constexpr int kDecodeBlocksPerCu = 2;
-constexpr int64_t kUnitStartupPages = 8;
-constexpr int32_t kSplitCandidates[] = {16, 24, 32, 48, 64, 96, 128, 192, 256, 384, 512, 768, 1024, 2048};
+// Decode schedule.  The decode kernel is persistent: one workgroup per bin,
+// and each bin's units run back to back while the next unit's first pages
+// are already in flight.  The host packs units into bins longest first (LPT
+// list scheduling).  Within a bin, split pieces go first and whole pairs
+// last, so split merges finish while other work still streams rather than in
+// the kernel's tail.  Two bins per CU (the decode kernels' occupancy) keep a
+// second workgroup streaming while the first one is in a unit epilogue.  A
+// unit costs its pages plus a fixed transition; a split piece also pays for
+// publishing its partial and for its share of the merge.
+constexpr int kDecodeBinsPerCu = 2;
+constexpr int64_t kUnitCostPages = 1;
+constexpr int64_t kSplitCostPages = 3;
+constexpr int32_t kSplitCandidates[] = {8,   12,  16,  20,  24,  32,  40,  48,  64,  80,   96,
+                                        128, 160, 192, 256, 384, 512, 768, 1024, 1536, 2048};
 
-// Makespan (in pages) of LPT-scheduling the units that `target` produces from
-// the per-query page counts onto `slots` identical workgroup slots.
-int64_t simulate_split(const std::vector<int32_t>& pages, int32_t heads_kv, int32_t target, int64_t slots,
+int64_t unit_cost(int64_t pages, bool split) { return pages + kUnitCostPages + (split ? kSplitCostPages : 0); }
+
+// Makespan (in pages) of LPT-packing the units that `target` produces from
+// the per-query page counts into `bins` bins.
+int64_t simulate_split(const std::vector<int32_t>& pages, int32_t heads_kv, int32_t target, int64_t bins,
                        std::vector<int64_t>& count, std::vector<int64_t>& heap) {
-    count.assign((size_t)target + 1, 0);
+    // count[2s] whole pairs of s pages, count[2s + 1] split pieces of s pages.
+    count.assign(2 * ((size_t)target + 1), 0);
+    int32_t longest = 0;
     for (int32_t P : pages) {
         const int32_t ns = std::min((P + target - 1) / target, gsp::kMaxSplits);
         const int32_t base = P / ns, extra = P % ns;
-        count[(size_t)base + 1] += (int64_t)extra * heads_kv;
-        count[(size_t)base] += (int64_t)(ns - extra) * heads_kv;
+        const int sp = ns > 1 ? 1 : 0;
+        count[2 * ((size_t)base + 1) + sp] += (int64_t)extra * heads_kv;
+        count[2 * (size_t)base + sp] += (int64_t)(ns - extra) * heads_kv;
+        longest = std::max(longest, base + (extra ? 1 : 0));
     }
     heap.clear();
-    for (int32_t s = target; s >= 1; --s) {
-        for (int64_t c = count[(size_t)s]; c > 0; --c) {
-            const int64_t cost = s + kUnitStartupPages;
-            if ((int64_t)heap.size() < slots) {
-                heap.push_back(-cost);  // min-heap through negated loads
-                std::push_heap(heap.begin(), heap.end());
-            } else {
-                std::pop_heap(heap.begin(), heap.end());
-                heap.back() -= cost;
-                std::push_heap(heap.begin(), heap.end());
+    for (int32_t s = longest; s >= 1; --s) {
+        for (int sp = 1; sp >= 0; --sp) {
+            const int64_t cost = unit_cost(s, sp == 1);
+            for (int64_t c = count[2 * (size_t)s + sp]; c > 0; --c) {
+                if ((int64_t)heap.size() < bins) {
+                    heap.push_back(-cost);  // min-heap through negated loads
+                    std::push_heap(heap.begin(), heap.end());
+                } else {
+                    std::pop_heap(heap.begin(), heap.end());
+                    heap.back() -= cost;
+                    std::push_heap(heap.begin(), heap.end());
+                }
             }
         }
     }
@@ -117,8 +133,9 @@ struct gsp_ctx {
     bool step_valid = false;
     gsp_step_info info{};
     int32_t max_id = -1;
-    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_units = 0, off_tiles = 0;
-    int32_t num_units = 0;      // decode workgroups of the packed step
+    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_units = 0, off_tiles = 0, off_bins = 0;
+    int32_t num_units = 0;      // decode units of the packed step
+    int32_t num_bins = 0;       // decode workgroups (bins of units) of the packed step
     int32_t num_tiles = 0;      // prefill tiles of the packed step
     int32_t num_slots = 0;      // partial slots of the packed step
     int32_t step_heads_kv = 0;  // pool geometry the step was packed for
@@ -131,6 +148,7 @@ struct gsp_ctx {
     size_t counter_words = 0;
 
     int32_t split_pages_override = 0;
+    int32_t decode_bins_override = 0;
     int32_t decode_path = GSP_DECODE_AUTO;
     int32_t prefill_path = GSP_PREFILL_AUTO;
 
@@ -139,9 +157,15 @@ struct gsp_ctx {
     int64_t cached_tasks = 0;
     int32_t cached_heads_kv = 0;
     int64_t cached_queries = 0;
+    int64_t cached_bins = 0;
 
     // Host scratch reused across steps.
     std::vector<DecodeUnit> units;
+    std::vector<DecodeUnit> units_binned;
+    std::vector<int32_t> bin_units;   // [num_bins + 1] offsets of each bin's units after its first
+    std::vector<int32_t> unit_bin;
+    std::vector<std::pair<int64_t, int32_t>> bin_heap;
+    std::vector<int32_t> bin_cursor;
     std::vector<PrefillTile> tiles;
     std::vector<int32_t> q_ctx;
     std::vector<int32_t> query_pages;
@@ -355,6 +379,14 @@ int gsp_set_decode_path(gsp_ctx* ctx, int32_t path) {
     return GSP_OK;
 }
 
+int gsp_set_decode_bins(gsp_ctx* ctx, int32_t bins) {
+    gsp::clear_error();
+    if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
+    if (bins < 0) return gsp::fail(GSP_E_INVALID_ARG, "decode bins must be >= 0 (got %d)", bins);
+    ctx->decode_bins_override = bins;
+    return GSP_OK;
+}
+
 int gsp_set_prefill_path(gsp_ctx* ctx, int32_t path) {
     gsp::clear_error();
     if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
@@ -535,6 +567,59 @@ int gsp_pool_download(gsp_ctx* ctx, gsp_pool* pool, int32_t which, size_t offset
 
 /* ---------------------------------------------------------------- steps */
 
+// Packs the longest-first units into at most `bins_max` bins (LPT: each unit
+// goes to the least-loaded bin; ties to the lowest bin).  Within a bin, split
+// pieces run first and whole pairs last, each group keeping the longest-first
+// order.  The first bins_max units land in distinct empty bins, so no bin is
+// empty.  Layout: units[b] is bin b's first unit; the other units follow, bin
+// by bin, with bin b's at [bin_units[b], bin_units[b + 1]).  Returns the bin
+// count.
+static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max) {
+    const size_t n = ctx->units.size();
+    const int32_t nb = (int32_t)std::min<int64_t>(bins_max, (int64_t)n);
+    ctx->bin_units.assign((size_t)nb + 1, 0);
+    if (nb == 0) return 0;
+    auto& heap = ctx->bin_heap;
+    heap.clear();
+    for (int32_t b = 0; b < nb; ++b) heap.emplace_back(0, b);
+    const std::greater<std::pair<int64_t, int32_t>> later;
+    std::make_heap(heap.begin(), heap.end(), later);
+    ctx->unit_bin.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+        const DecodeUnit& u = ctx->units[i];
+        std::pop_heap(heap.begin(), heap.end(), later);
+        const int32_t b = heap.back().second;
+        ctx->unit_bin[i] = b;
+        ctx->bin_units[(size_t)b + 1] += 1;
+        heap.back().first += unit_cost(u.page_end - u.page_begin, (u.split_info >> 16) > 1);
+        std::push_heap(heap.begin(), heap.end(), later);
+    }
+    // bin_units[b + 1] holds bin b's unit count: its first unit goes to slot b,
+    // the rest to the bin's run after the nb first units.
+    ctx->bin_units[0] = nb;
+    for (int32_t b = 0; b < nb; ++b) ctx->bin_units[(size_t)b + 1] += ctx->bin_units[(size_t)b] - 1;
+    ctx->bin_cursor.resize((size_t)nb);
+    for (int32_t b = 0; b < nb; ++b) ctx->bin_cursor[(size_t)b] = -1;  // -1: the first unit is still to place
+    ctx->units_binned.resize(n);
+    for (int pass = 0; pass < 2; ++pass) {
+        const bool want_split = pass == 0;
+        for (size_t i = 0; i < n; ++i) {
+            const DecodeUnit& u = ctx->units[i];
+            if (((u.split_info >> 16) > 1) != want_split) continue;
+            const int32_t b = ctx->unit_bin[i];
+            int32_t& cur = ctx->bin_cursor[(size_t)b];
+            if (cur < 0) {
+                ctx->units_binned[(size_t)b] = u;
+                cur = ctx->bin_units[(size_t)b];
+            } else {
+                ctx->units_binned[(size_t)cur++] = u;
+            }
+        }
+    }
+    std::swap(ctx->units, ctx->units_binned);
+    return nb;
+}
+
 int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc) {
     gsp::clear_error();
     if (!ctx || !pool || !desc) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool/desc is NULL");
@@ -597,12 +682,15 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     const int64_t T = pair_pages * H;
     // A pair may not be cut into more pieces than the merge LDS holds.
     const int64_t min_target = std::max<int64_t>(1, (max_pages + gsp::kMaxSplits - 1) / gsp::kMaxSplits);
+    const int64_t bins_max = ctx->decode_bins_override > 0 ? ctx->decode_bins_override
+                                                           : (int64_t)kDecodeBinsPerCu * std::max(1, ctx->num_cus);
     int64_t target = 1;
     if (T > 0) {
         if (ctx->split_pages_override > 0) {
             target = std::max<int64_t>(ctx->split_pages_override, min_target);
         } else if (ctx->cached_target > 0 && ctx->cached_heads_kv == H && ctx->cached_queries == total_q &&
-                   T * 100 >= ctx->cached_tasks * 97 && T * 100 <= ctx->cached_tasks * 103) {
+                   ctx->cached_bins == bins_max && T * 100 >= ctx->cached_tasks * 97 &&
+                   T * 100 <= ctx->cached_tasks * 103) {
             target = std::max<int64_t>(ctx->cached_target, min_target);  // engine steps drift slowly
         } else {
             ctx->query_pages.clear();
@@ -614,12 +702,11 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                     if (tot > 0) ctx->query_pages.push_back((int32_t)((tot + gsp::kBlockSize - 1) / gsp::kBlockSize));
                 }
             }
-            const int64_t slots_dev = (int64_t)std::max(1, ctx->num_cus) * kDecodeBlocksPerCu;
             int64_t best_cost = INT64_MAX;
             for (int32_t cand : kSplitCandidates) {
                 if (cand < min_target) continue;
-                if (T / cand > 16 * slots_dev) continue;  // far too many units to be competitive
-                const int64_t c = simulate_split(ctx->query_pages, H, cand, slots_dev, ctx->sim_count, ctx->sim_heap);
+                if (T / cand > 16 * bins_max) continue;  // far too many units to be competitive
+                const int64_t c = simulate_split(ctx->query_pages, H, cand, bins_max, ctx->sim_count, ctx->sim_heap);
                 if (c <= best_cost) {  // ties go to the larger split (fewer units)
                     best_cost = c;
                     target = cand;
@@ -630,6 +717,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
             ctx->cached_tasks = T;
             ctx->cached_heads_kv = H;
             ctx->cached_queries = total_q;
+            ctx->cached_bins = bins_max;
         }
     }
     ctx->units.clear();
@@ -710,6 +798,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     });
     std::stable_sort(ctx->tiles.begin(), ctx->tiles.end(),
                      [](const PrefillTile& x, const PrefillTile& y) { return x.pages > y.pages; });
+    const int32_t n_bins = assign_bins(ctx, bins_max);
 
     // Pass 3: write the staging buffer and upload it with one copy.
     const size_t n_units = ctx->units.size();
@@ -726,6 +815,8 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     off += n_units * (sizeof(DecodeUnit) / sizeof(int32_t));
     const size_t off_tiles = off;
     off += n_tiles * (sizeof(PrefillTile) / sizeof(int32_t));
+    const size_t off_bins = off;
+    off += (size_t)n_bins + 1;
     const size_t words = off;
 
     int rc = set_device(ctx);
@@ -758,6 +849,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     if (total_q) std::memcpy(st + off_ctx, ctx->q_ctx.data(), (size_t)total_q * sizeof(int32_t));
     if (n_units) std::memcpy(st + off_units, ctx->units.data(), n_units * sizeof(DecodeUnit));
     if (n_tiles) std::memcpy(st + off_tiles, ctx->tiles.data(), n_tiles * sizeof(PrefillTile));
+    std::memcpy(st + off_bins, ctx->bin_units.data(), ((size_t)n_bins + 1) * sizeof(int32_t));
     st[kHdrRows] = B;
     st[kHdrTotalQ] = (int32_t)total_q;
     st[kHdrPages] = (int32_t)packed_pages;
@@ -768,6 +860,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     st[kHdrPairsSplit] = (int32_t)pairs_split;
     st[kHdrHeadsKv] = H;
     st[kHdrTiles] = (int32_t)n_tiles;
+    st[kHdrBins] = n_bins;
 
     rc = check_hip(hipMemcpyAsync(ctx->d_step, st, words * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream),
                    "hipMemcpyAsync(step)");
@@ -780,6 +873,8 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->off_ctx = off_ctx;
     ctx->off_units = off_units;
     ctx->off_tiles = off_tiles;
+    ctx->off_bins = off_bins;
+    ctx->num_bins = n_bins;
     ctx->max_id = max_id;
     ctx->num_slots = (int32_t)slots;
     ctx->num_units = (int32_t)n_units;
@@ -799,6 +894,8 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->info.prefill_tiles = (int32_t)n_tiles;
     ctx->info.prefill_queries = (int32_t)tiled_queries;
     ctx->info.prefill_pairs = tiled_pairs;
+    ctx->info.decode_bins = n_bins;
+    ctx->info.reserved = 0;
     ctx->step_valid = true;
     return GSP_OK;
 }
@@ -885,6 +982,7 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     a.layer_offset = (int64_t)layer * pool->layer_stride_k;
     a.head_stride = pool->head_stride_k;
     a.units = reinterpret_cast<const DecodeUnit*>(ctx->d_step + ctx->off_units);
+    a.bin_rest = ctx->d_step + ctx->off_bins;
     a.bt_ids = ctx->d_step + ctx->off_ids;
     a.q = q_dev;
     a.out = out_dev;
@@ -897,9 +995,9 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     a.scale_log2 = attn_scale * 1.4426950408889634f;
     const int f16 = d.kv_dtype == GSP_KV_F16;
     if (ctx->num_units > 0) {
-        rc = use_mfma ? check_hip(gsp::launch_decode_mfma(d.head_dim, f16, ctx->num_units, a, ctx->stream),
+        rc = use_mfma ? check_hip(gsp::launch_decode_mfma(d.head_dim, f16, ctx->num_bins, a, ctx->stream),
                                   "decode (mfma) launch")
-                      : check_hip(gsp::launch_decode(d.head_dim, f16, ctx->num_units, a, ctx->stream),
+                      : check_hip(gsp::launch_decode(d.head_dim, f16, ctx->num_bins, a, ctx->stream),
                                   "decode (dpp) launch");
         if (rc) return rc;
     }

@@ -130,6 +130,8 @@ class StepInfo(ctypes.Structure):
         ("prefill_tiles", i32),
         ("prefill_queries", i32),
         ("prefill_pairs", ctypes.c_int64),
+        ("decode_bins", i32),
+        ("reserved", i32),
     ]
 
 
@@ -174,6 +176,7 @@ _SIGNATURES = {
     "gsp_set_split_pages": (ctypes.c_int, [vp, i32]),
     "gsp_set_decode_path": (ctypes.c_int, [vp, i32]),
     "gsp_set_prefill_path": (ctypes.c_int, [vp, i32]),
+    "gsp_set_decode_bins": (ctypes.c_int, [vp, i32]),
     "gsp_attention_step": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, ctypes.c_float, fp]),
     "gsp_compute_attention": (
         ctypes.c_int,
@@ -281,6 +284,10 @@ class Context:
 
     def set_decode_path(self, path: int) -> None:
         _check(self._lib.gsp_set_decode_path(self._h, int(path)))
+
+    def set_decode_bins(self, bins: int) -> None:
+        """Most decode workgroups for the next pack_step (0: two per CU)."""
+        _check(self._lib.gsp_set_decode_bins(self._h, int(bins)))
 
     def set_prefill_path(self, path: int) -> None:
         """Route prefill rows for the next pack_step (PREFILL_AUTO / TILES / PER_TOKEN)."""

@@ -40,7 +40,7 @@ extern "C" {
 #pragma GCC visibility push(default)
 #endif
 
-#define GSP_ABI_VERSION 2
+#define GSP_ABI_VERSION 3
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
 
 typedef enum gsp_status {
@@ -204,6 +204,8 @@ typedef struct gsp_step_info {
     int32_t prefill_tiles;       /* (16 query tokens, KV head) tiles of prefill rows */
     int32_t prefill_queries;     /* query tokens served by those tiles */
     int64_t prefill_pairs;       /* sum over tiled query tokens of total (causal key count) */
+    int32_t decode_bins;         /* decode workgroups: each runs one bin of units back to back */
+    int32_t reserved;
 } gsp_step_info;
 
 int gsp_step_get_info(const gsp_ctx* ctx, gsp_step_info* out);
@@ -218,6 +220,12 @@ int gsp_step_download(gsp_ctx* ctx, int32_t* row_offsets, int32_t* ids, int32_t*
  * forces it (tuning and tests, e.g. 1 cuts every query token into one-page
  * splits).  A query token is never cut into more than 256 splits. */
 int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages);
+
+/* Most decode workgroups for the next gsp_step_pack: 0 (default) uses two
+ * per CU; > 0 forces the count (tuning and tests).  Units are packed into that
+ * many bins longest first, and each workgroup runs its bin's units back to
+ * back. */
+int gsp_set_decode_bins(gsp_ctx* ctx, int32_t bins);
 
 /* Decode kernel selection (tuning and tests): GSP_DECODE_AUTO picks the
  * matrix-core kernel; GSP_DECODE_DPP forces the VALU/DPP kernel (GQA groups up

@@ -20,19 +20,22 @@ def to_device_pool(torch, gsp, ctx, step, k, v):
     return pool, (kd, vd)
 
 
-def gpu_step(torch, gsp, ctx, step, q, pool, layer=0, split_pages=0, fill=np.nan):
+def gpu_step(torch, gsp, ctx, step, q, pool, layer=0, split_pages=0, fill=np.nan, bins=0):
     """Packs the step, runs gsp_attention_step and returns out [total_q, nH, d] on the host."""
     ctx.set_split_pages(split_pages)
-    ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
-                  q_lens=step.q_lens)
+    ctx.set_decode_bins(bins)
+    try:
+        ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
+                      q_lens=step.q_lens)
+    finally:
+        ctx.set_split_pages(0)
+        ctx.set_decode_bins(0)
     qd = torch.from_numpy(np.ascontiguousarray(q, dtype=np.float32)).cuda()
     out = torch.full((step.total_q, step.n_heads, step.head_dim), float(fill), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     ctx.attention_step(pool, layer, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
     ctx.sync()
-    res = out.cpu().numpy()
-    ctx.set_split_pages(0)
-    return res
+    return out.cpu().numpy()
 
 
 def oracle_step(step, q, k, v, layer=0, threads=8, fill=np.nan):

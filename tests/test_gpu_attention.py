@@ -58,6 +58,33 @@ def test_decode_matches_oracle(torch_mod, gsp, ctx, geom, split_pages, path):
     assert max_err(got, ref) <= TOL[dt]
 
 
+@pytest.mark.parametrize("path", list(PATHS))
+@pytest.mark.parametrize("bins", [1, 3, 64, 1000])
+@pytest.mark.parametrize("split_pages", [0, 2])
+def test_decode_bins_match_oracle(torch_mod, gsp, ctx, bins, split_pages, path):
+    """Persistent bins: one workgroup runs a bin's units back to back (bins=1 runs every unit,
+    merging its own split pieces; bins above the unit count leave one unit per workgroup)."""
+    print(f"case bins={bins} split={split_pages} path={path}", flush=True)
+    step = workloads.small_step(seed=400 + bins, rows=13, n_heads=28, n_kv=4, head_dim=128, ctx_lo=1, ctx_hi=400,
+                                total_blocks=512)
+    q, k, v = workloads.host_values(step)
+    pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
+    ctx.set_decode_path(PATHS[path])
+    try:
+        ctx.set_decode_bins(bins)
+        info = ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids,
+                             step.max_seq_len)
+        ctx.set_decode_bins(0)
+        assert info.decode_bins == min(bins, info.decode_units)
+        got = gpu_step(torch_mod, gsp, ctx, step, q, pool, split_pages=split_pages, bins=bins)
+    finally:
+        ctx.set_decode_path(0)
+        ctx.set_decode_bins(0)
+    ref = oracle_step(step, q, k, v, threads=threads())
+    pool.destroy()
+    assert max_err(got, ref) <= 1e-4
+
+
 def test_stale_nan_slots_do_not_leak(torch_mod, gsp, ctx):
     """Slots past a row's context may hold anything (a wrapped pool is caller memory): NaN there is ignored."""
     step = workloads.small_step(seed=91, rows=8, n_heads=28, n_kv=4, head_dim=128, ctx_lo=1, ctx_hi=90,
