@@ -8,20 +8,24 @@
 //   O[head][e]      += P[16 heads x 16 tokens] . V_page[16 x d]          (v_mfma_f32_16x16x4f32, M = heads, K = tokens)
 //
 // Heads of the group beyond G are zero padding (G <= 16).  MFMA operand
-// layouts (lane l, n = l % 16, g = l / 16):
+// layouts for fp32 pages (lane l, n = l % 16, g = l / 16):
 //   QK step kk = 4j + i uses d = 16j + 4g + i:  A = K[token n][d],  B = Q[head n][d]
 //   result: lane holds S[head n][token 4g + r], r = 0..3
 //   PV step kk uses token 4g + kk:  A = P[head n][token 4g + kk] (the lane's own r = kk),
 //   B = V[token 4g + kk][e], e = 64c + 4n + i for output block 4c + i
 //   result: lane holds O[head 4g + r][e].
-// So each lane reads 16-byte pieces of K rows and V rows straight into MFMA
-// operands; the softmax needs one max-reduction across the four lane groups
-// per page and four exp2 per lane.  Page loads are raw buffer loads whose
-// descriptor covers only the page's valid tokens: slots past the context read
-// as zero in hardware (no fetch, no NaN from stale slots reaches P.V).  Each
-// wave streams every kDecodeWaves-th page of its unit with the next page's
-// loads in flight while the current one is computed; the four waves merge
-// through LDS and split units merge in the epilogue (gsp_epilogue.h).
+// fp16 pages run the same contractions on v_mfma_f32_16x16x16f16 from the
+// same registers (one rank-16 step covers d = 16j + 4g + 0..3, or tokens
+// 4g + 0..3): K and V are exact in fp16, Q and P enter as hi + lo fp16 pairs,
+// accumulation is fp32.  So each lane reads 16-byte (8-byte for fp16) pieces
+// of K rows and V rows straight into MFMA operands; the softmax needs one
+// max-reduction across the four lane groups per page and four exp2 per lane.
+// Page loads are raw buffer loads whose descriptor covers only the page's
+// valid tokens: slots past the context read as zero in hardware (no fetch,
+// no NaN from stale slots reaches P.V).  Each wave streams every
+// kDecodeWaves-th page of its unit with the next page's loads in flight
+// while the current one is computed; the four waves merge through LDS and
+// split units merge in the epilogue (gsp_epilogue.h).
 #include "gsp_epilogue.h"
 
 namespace gsp {
@@ -35,41 +39,122 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const void* base, in
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-// 4 consecutive elements of a K/V row at element offset `off`, as fp32.
-template <typename KT>
-__device__ __forceinline__ f4 load4(__amdgpu_buffer_rsrc_t r, int off);
-
-template <>
-__device__ __forceinline__ f4 load4<float>(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4, 0, 0));
-}
-
-template <>
-__device__ __forceinline__ f4 load4<_Float16>(__amdgpu_buffer_rsrc_t r, int off) {
-    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
-    const u2 raw = __builtin_amdgcn_raw_buffer_load_b64(r, off * 2, 0, 0);
-    const h4 h = __builtin_bit_cast(h4, raw);
-    return f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
-}
+// Page operands in registers, as stored in the pool (fp16 pages stay fp16).
+//   k[j]     = K[token n][16j + 4g .. +3]
+//   v[kk][c] = V[token 4g + kk][64c + 4n .. +3]
+template <int D, typename KT>
+struct PageRegs;
 
 template <int D>
-struct PageRegs {
-    f4 k[D / 16];          // K[token n][16j + 4g .. +3]
-    f4 v[4][D / 64];       // V[token 4g + kk][64c + 4n .. +3]
+struct PageRegs<D, float> {
+    f4 k[D / 16];
+    f4 v[4][D / 64];
+};
+
+template <int D>
+struct PageRegs<D, _Float16> {
+    h4 k[D / 16];
+    h4 v[4][D / 64];
+};
+
+template <typename KT>
+struct Raw4;
+template <>
+struct Raw4<float> {
+    typedef f4 T;
+    __device__ static f4 load(__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4, 0, 0));
+    }
+};
+template <>
+struct Raw4<_Float16> {
+    typedef h4 T;
+    __device__ static h4 load(__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, off * 2, 0, 0));
+    }
 };
 
 template <int D, typename KT>
-__device__ __forceinline__ void load_page(PageRegs<D>& pr, const KT* kpage, const KT* vpage, int ntok, int n,
+__device__ __forceinline__ void load_page(PageRegs<D, KT>& pr, const KT* kpage, const KT* vpage, int ntok, int n,
                                           int g) {
     const int bytes = ntok * D * (int)sizeof(KT);
     const __amdgpu_buffer_rsrc_t rk = page_rsrc(kpage, bytes);
     const __amdgpu_buffer_rsrc_t rv = page_rsrc(vpage, bytes);
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) pr.k[j] = load4<KT>(rk, n * D + 16 * j + 4 * g);
+    for (int j = 0; j < D / 16; ++j) pr.k[j] = Raw4<KT>::load(rk, n * D + 16 * j + 4 * g);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int c = 0; c < D / 64; ++c) pr.v[kk][c] = load4<KT>(rv, (4 * g + kk) * D + 64 * c + 4 * n);
+        for (int c = 0; c < D / 64; ++c) pr.v[kk][c] = Raw4<KT>::load(rv, (4 * g + kk) * D + 64 * c + 4 * n);
+}
+
+// Q^T operand of a unit, q[j] = Q[head n][16j + 4g .. +3] (padded heads 0),
+// and `sc`, the factor that turns the lane's S column (head n) into log2
+// units.  The attention scale multiplies the finished dot, as in the
+// reference (PagedAttentionKernel.cs:65).
+//  - fp32 pages: q in fp32, sc = scale * log2 e.
+//  - fp16 pages: the matrix cores take fp16 operands.  K is exact in fp16;
+//    Q is cut into q_hi + q_lo fp16 halves after scaling head n by 2^s_n so
+//    that its largest |element| lies in [2^12, 2^13): q_hi + q_lo then
+//    carries ~22 significant bits of every element, and sc folds 2^-s_n back.
+template <int D, typename KT>
+struct QRegs;
+
+template <int D>
+struct QRegs<D, float> {
+    f4 q[D / 16];
+    float sc;
+};
+
+template <int D>
+struct QRegs<D, _Float16> {
+    h4 hi[D / 16];
+    h4 lo[D / 16];
+    float sc;
+};
+
+template <int D>
+__device__ __forceinline__ void load_q_f32(f4 (&q)[D / 16], const DecodeArgs& a, int qi, int kvh, int G, int n,
+                                           int g) {
+    const bool live = n < G;
+    const float* qrow = a.q + ((int64_t)qi * a.n_heads + kvh * G + (live ? n : 0)) * D;
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+        const f4 x = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
+        q[j] = live ? x : f4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void load_q(QRegs<D, float>& qr, const DecodeArgs& a, int qi, int kvh, int G, int n,
+                                       int g) {
+    load_q_f32<D>(qr.q, a, qi, kvh, G, n, g);
+    qr.sc = a.scale_log2;
+}
+
+template <int D>
+__device__ __forceinline__ void load_q(QRegs<D, _Float16>& qr, const DecodeArgs& a, int qi, int kvh, int G, int n,
+                                       int g) {
+    f4 q[D / 16];
+    load_q_f32<D>(q, a, qi, kvh, G, n, g);
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(q[j][0]), fabsf(q[j][1])), fmaxf(fabsf(q[j][2]), fabsf(q[j][3]))));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));  // head n's elements live in lanes n + 16g
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    int ex = 0;
+    if (mx > 0.f) (void)frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
+    const int sh = 13 - ex;               // scaled max in [2^12, 2^13)
+    const float up = ldexpf(1.0f, sh);
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+        const f4 x = q[j] * up;
+        const h4 hi = __builtin_convertvector(x, h4);
+        qr.hi[j] = hi;
+        qr.lo[j] = __builtin_convertvector(x - __builtin_convertvector(hi, f4), h4);
+    }
+    qr.sc = ldexpf(a.scale_log2, -sh);
 }
 
 template <int D>
@@ -79,10 +164,10 @@ struct WaveState {
     float l;       // partial sum of head n over this lane's tokens
 };
 
+// S^T = K . Q^T for one page; returns the lane's S[head n][token 4g + r] in log2 units.
 template <int D>
-__device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D>& pr, const f4 (&q)[D / 16],
-                                             float scale, int ntok, int g) {
-    // S^T = K . Q^T: 32 (d = 128) or 16 (d = 64) rank-4 steps, two accumulation chains.
+__device__ __forceinline__ f4 page_scores(const PageRegs<D, float>& pr, const QRegs<D, float>& qr) {
+    // 32 (d = 128) or 16 (d = 64) rank-4 steps, two accumulation chains.
     f4 s0 = {0.f, 0.f, 0.f, 0.f};
     f4 s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -90,12 +175,62 @@ __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D>
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             if (j & 1)
-                s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(pr.k[j][i], q[j][i], s1, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(pr.k[j][i], qr.q[j][i], s1, 0, 0, 0);
             else
-                s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(pr.k[j][i], q[j][i], s0, 0, 0, 0);
+                s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(pr.k[j][i], qr.q[j][i], s0, 0, 0, 0);
         }
     }
-    f4 s = (s0 + s1) * scale;  // lane: S[head n][token 4g + r] in log2 units
+    return (s0 + s1) * qr.sc;
+}
+
+template <int D>
+__device__ __forceinline__ f4 page_scores(const PageRegs<D, _Float16>& pr, const QRegs<D, _Float16>& qr) {
+    // K . (q_hi + q_lo): one rank-16 step per 16 dims and half, fp32 accumulation.
+    f4 s0 = {0.f, 0.f, 0.f, 0.f};
+    f4 s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x16f16(pr.k[j], qr.hi[j], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x16f16(pr.k[j], qr.lo[j], s1, 0, 0, 0);
+    }
+    return (s0 + s1) * qr.sc;
+}
+
+// O += P . V for one page; p = the lane's P[head n][token 4g + r].
+template <int D>
+__device__ __forceinline__ void page_pv(WaveState<D>& st, const PageRegs<D, float>& pr, const f4& p) {
+    // 4 token steps x D/16 output blocks.
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int c = 0; c < D / 64; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                st.o[4 * c + i] =
+                    __builtin_amdgcn_mfma_f32_16x16x4f32(p[kk], pr.v[kk][c][i], st.o[4 * c + i], 0, 0, 0);
+}
+
+template <int D>
+__device__ __forceinline__ void page_pv(WaveState<D>& st, const PageRegs<D, _Float16>& pr, const f4& p) {
+    // P = p_hi + p_lo in fp16 (P is in [0, 1]); V is exact in fp16.  Output
+    // block 4c + i takes B[token 4g + kk][col] = V[4g + kk][64c + 4n + i],
+    // i.e. element i of the lane's four V pieces.
+    const h4 ph = __builtin_convertvector(p, h4);
+    const h4 pl = __builtin_convertvector(p - __builtin_convertvector(ph, f4), h4);
+#pragma unroll
+    for (int c = 0; c < D / 64; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const h4 b = {pr.v[0][c][i], pr.v[1][c][i], pr.v[2][c][i], pr.v[3][c][i]};
+            st.o[4 * c + i] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, b, st.o[4 * c + i], 0, 0, 0);
+            st.o[4 * c + i] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, b, st.o[4 * c + i], 0, 0, 0);
+        }
+}
+
+template <int D, typename KT>
+__device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D, KT>& pr, const QRegs<D, KT>& qr,
+                                             int ntok, int g) {
+    f4 s = page_scores<D>(pr, qr);
     if (ntok < kBlockSize) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -121,15 +256,7 @@ __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D>
 #pragma unroll
         for (int b = 0; b < D / 16; ++b) st.o[b] *= ar;
     }
-    // O += P . V: 4 token steps x D/16 output blocks.
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int c = 0; c < D / 64; ++c)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                st.o[4 * c + i] =
-                    __builtin_amdgcn_mfma_f32_16x16x4f32(p[kk], pr.v[kk][c][i], st.o[4 * c + i], 0, 0, 0);
+    page_pv<D>(st, pr, p);
 }
 
 // Step metadata (unit records, bin offsets, block table) is read-only while
@@ -156,21 +283,6 @@ __device__ __forceinline__ DecodeUnit read_unit(const DecodeArgs& a, int ui) {
     return u;
 }
 
-// Q^T operand of a unit: q[j][i] = Q[kvh * G + n][16j + 4g + i]; padded heads
-// are 0.  The scale (times log2 e) multiplies S after the MFMA, as the
-// reference multiplies the finished dot (PagedAttentionKernel.cs:65).
-template <int D>
-__device__ __forceinline__ void load_q(f4 (&q)[D / 16], const DecodeArgs& a, const DecodeUnit& u, int G, int n,
-                                       int g) {
-    const bool live = n < G;
-    const float* qrow = a.q + ((int64_t)u.qi * a.n_heads + u.kvh * G + (live ? n : 0)) * D;
-#pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
-        const f4 x = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
-        q[j] = live ? x : f4{0.f, 0.f, 0.f, 0.f};
-    }
-}
-
 // The block id of this wave's first page of unit `ui` (page_begin + wave),
 // which travels in the unit record so the first load needs no table lookup.
 // It is read from the record in memory with wave-uniform indices: a local
@@ -181,7 +293,7 @@ __device__ __forceinline__ int first_block(const DecodeArgs& a, int ui, int wave
 }
 
 template <int D, typename KT>
-__device__ __forceinline__ void load_first_page(PageRegs<D>& pr, const DecodeArgs& a, const DecodeUnit& u, int blk,
+__device__ __forceinline__ void load_first_page(PageRegs<D, KT>& pr, const DecodeArgs& a, const DecodeUnit& u, int blk,
                                                 int wave, int n, int g) {
     const int p = u.page_begin + wave;
     if (p < u.page_end) {
@@ -205,19 +317,19 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15;
     const int g = lane >> 4;
-    const float scale = a.scale_log2;
     const int first = blockIdx.x;
 
-    f4 q[D / 16];
-    PageRegs<D> ra, rb;
+    QRegs<D, KT> q;
+    PageRegs<D, KT> ra, rb;
     {
         const DecodeUnit u0 = read_unit(a, first);
         const int blk0 = first_block(a, first, wave);
-        load_q<D>(q, a, u0, G, n, g);
+        load_q<D>(q, a, u0.qi, u0.kvh, G, n, g);
         load_first_page<D, KT>(ra, a, u0, blk0, wave, n, g);
     }
     const int rb0 = ld_meta(a.bin_rest + first);
     const int re = ld_meta(a.bin_rest + first + 1);
+    bool rb_ready = false;  // rb already holds page p + kDecodeWaves (prefetched across a boundary)
 
     // The unit record is re-read from memory in every iteration (wave-uniform
     // address), never carried across iterations, so every field stays scalar.
@@ -225,9 +337,13 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
         const int ui = k < rb0 ? first : k;
         const DecodeUnit u = read_unit(a, ui);
         const bool has_next = k + 1 < re;
-        // The next record is fetched now; its latency hides behind this unit.
+        // The next record and its first two page ids are fetched now; their
+        // latency hides behind this unit.
         const DecodeUnit un = read_unit(a, has_next ? k + 1 : ui);
         const int blkn = first_block(a, has_next ? k + 1 : ui, wave);
+        const int pn2 = un.page_begin + wave + kDecodeWaves;  // the next unit's second page of this wave
+        const bool has_n2 = has_next && pn2 < un.page_end;
+        const int blkn2 = has_n2 ? ld_meta(a.bt_ids + un.bt_base + pn2) : 0;
 
         WaveState<D> st;
 #pragma unroll
@@ -243,12 +359,13 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
         int p = u.page_begin + wave;
         while (p < u.page_end) {
             const int pn = p + kDecodeWaves;
-            if (pn < u.page_end) {
+            if (pn < u.page_end && !rb_ready) {
                 const int64_t blk = ld_meta(bt + pn);
                 load_page<D, KT>(rb, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
                                  min(kBlockSize, u.ctx - pn * kBlockSize), n, g);
             }
-            compute_page<D>(st, ra, q, scale, min(kBlockSize, u.ctx - p * kBlockSize), g);
+            rb_ready = false;
+            compute_page<D, KT>(st, ra, q, min(kBlockSize, u.ctx - p * kBlockSize), g);
             if (pn >= u.page_end) break;
             const int pnn = pn + kDecodeWaves;
             if (pnn < u.page_end) {
@@ -256,14 +373,23 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
                 load_page<D, KT>(ra, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
                                  min(kBlockSize, u.ctx - pnn * kBlockSize), n, g);
             }
-            compute_page<D>(st, rb, q, scale, min(kBlockSize, u.ctx - pn * kBlockSize), g);
+            compute_page<D, KT>(st, rb, q, min(kBlockSize, u.ctx - pn * kBlockSize), g);
             p = pnn;
         }
 
-        // Both page buffers and q are free now: request the next unit's inputs.
+        // Both page buffers and q are free now: request the next unit's Q and
+        // first two pages of this wave, so the epilogue runs with two pages
+        // per wave in flight.
+        rb_ready = false;
         if (has_next) {
-            load_q<D>(q, a, un, G, n, g);
+            load_q<D>(q, a, un.qi, un.kvh, G, n, g);
             load_first_page<D, KT>(ra, a, un, blkn, wave, n, g);
+            if (has_n2) {
+                const int64_t off = a.layer_offset + (int64_t)un.kvh * a.head_stride + (int64_t)blkn2 * a.block_stride;
+                load_page<D, KT>(rb, static_cast<const KT*>(a.k_pool) + off, static_cast<const KT*>(a.v_pool) + off,
+                                 min(kBlockSize, un.ctx - pn2 * kBlockSize), n, g);
+                rb_ready = true;
+            }
         }
 
         // Per-head sums over the four lane groups; m is uniform per head already.

@@ -30,17 +30,17 @@ __device__ __forceinline__ float coherent_load(const float* p) {
 // this wave, stores included, has completed.
 __device__ __forceinline__ void wait_vm_complete() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// LDS of the epilogue.  `o`, `m`, `l` hold the four waves' states; `w` holds
-// the per-split merge weights of the last split.
+// LDS of the epilogue: the four waves' states.
 template <int D, int GMAX>
 struct EpilogueLds {
     float o[kDecodeWaves][GMAX][D];
     float m[kDecodeWaves][GMAX];
     float l[kDecodeWaves][GMAX];
-    float w[kMaxSplits][GMAX];
-    float lsum[kMaxSplits][GMAX];
     int last;
 };
+
+// Splits merged per round trip by the last split of a pair.
+constexpr int kMergeChunk = 8;
 
 template <int D, int GMAX>
 __device__ __forceinline__ void finish_unit(const DecodeArgs& a, const DecodeUnit& u, int G,
@@ -89,44 +89,43 @@ __device__ __forceinline__ void finish_unit(const DecodeArgs& a, const DecodeUni
     __syncthreads();
     if (!sh.last) return;
 
-    // Last split of the pair: weights w_s = 2^(m_s - M) / sum_s' 2^(m_s' - M) l_s'.
-    for (int idx = tid; idx < nsplit * G; idx += kDecodeThreads) {
-        const int s = idx / G;
-        const int g = idx - s * G;
-        const int64_t ps = (pair + s) * G + g;
-        sh.w[s][g] = coherent_load(a.part_ml + ps * 2 + 0);
-        sh.lsum[s][g] = coherent_load(a.part_ml + ps * 2 + 1);
-    }
-    __syncthreads();
-    if (tid < G) {
-        const int g = tid;
-        float M = -INFINITY;
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, sh.w[s][g]);
-        float L = 0.f;
-        for (int s = 0; s < nsplit; ++s) {
-            const float f = fast_exp2(sh.w[s][g] - M);
-            sh.w[s][g] = f;
-            L = fmaf(sh.lsum[s][g], f, L);
-        }
-        const float inv = 1.0f / L;
-        for (int s = 0; s < nsplit; ++s) sh.w[s][g] *= inv;
-    }
-    __syncthreads();
+    // Last split of the pair: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+    // Each thread loads the (m, l) and O of up to kMergeChunk splits at once
+    // (one round trip for pairs cut into at most that many pieces) and folds
+    // chunks together with a running max, as the online softmax does.
+    const int64_t stride = (int64_t)G * D;
     for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
         const int g = idx / D;
         const int e = idx - g * D;
         const float* po = a.part_o + (pair * G + g) * D + e;
-        const int64_t stride = (int64_t)G * D;
-        float O0 = 0.f, O1 = 0.f, O2 = 0.f, O3 = 0.f;
-        int s = 0;
-        for (; s + 4 <= nsplit; s += 4) {
-            O0 = fmaf(coherent_load(po + (s + 0) * stride), sh.w[s + 0][g], O0);
-            O1 = fmaf(coherent_load(po + (s + 1) * stride), sh.w[s + 1][g], O1);
-            O2 = fmaf(coherent_load(po + (s + 2) * stride), sh.w[s + 2][g], O2);
-            O3 = fmaf(coherent_load(po + (s + 3) * stride), sh.w[s + 3][g], O3);
+        const float* pml = a.part_ml + (pair * G + g) * 2;
+        float M = -INFINITY, L = 0.f, O = 0.f;
+        for (int s0 = 0; s0 < nsplit; s0 += kMergeChunk) {
+            float ms[kMergeChunk], ls[kMergeChunk], os[kMergeChunk];
+#pragma unroll
+            for (int i = 0; i < kMergeChunk; ++i) {
+                const bool in = s0 + i < nsplit;
+                const int s = in ? s0 + i : s0;
+                ms[i] = coherent_load(pml + (int64_t)s * G * 2 + 0);
+                ls[i] = coherent_load(pml + (int64_t)s * G * 2 + 1);
+                os[i] = coherent_load(po + s * stride);
+                if (!in) ms[i] = -INFINITY;
+            }
+            float Mc = M;
+#pragma unroll
+            for (int i = 0; i < kMergeChunk; ++i) Mc = fmaxf(Mc, ms[i]);
+            const float r = fast_exp2(M - Mc);  // 0 on the first chunk (M = -inf)
+            L *= r;
+            O *= r;
+#pragma unroll
+            for (int i = 0; i < kMergeChunk; ++i) {
+                const float f = ms[i] == -INFINITY ? 0.f : fast_exp2(ms[i] - Mc);
+                L = fmaf(ls[i], f, L);
+                O = fmaf(os[i], f, O);
+            }
+            M = Mc;
         }
-        for (; s < nsplit; ++s) O0 = fmaf(coherent_load(po + s * stride), sh.w[s][g], O0);
-        a.out[((int64_t)u.qi * a.n_heads + h0 + g) * D + e] = (O0 + O1) + (O2 + O3);
+        a.out[((int64_t)u.qi * a.n_heads + h0 + g) * D + e] = O / L;
     }
     if (tid == 0) {
         __hip_atomic_store(a.counters + (int64_t)u.qi * a.n_kv + u.kvh, 0, __ATOMIC_RELAXED,

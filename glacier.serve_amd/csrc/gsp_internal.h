@@ -13,7 +13,7 @@ constexpr int kDecodeWaves = 4;   // wave64s per decode workgroup
 constexpr int kDecodeThreads = kDecodeWaves * 64;
 constexpr int kMaxGroup = 8;      // query heads per KV head of the DPP decode kernel
 constexpr int kMaxGroupMfma = 16; // query heads per KV head of the MFMA decode kernel (M/N tile)
-constexpr int kMaxSplits = 256;   // split-KV units per query token (merge kernel LDS)
+constexpr int kMaxSplits = 256;   // split-KV units per (query token, KV head) pair
 
 // One unit of decode work, one workgroup each: a contiguous range of logical
 // pages of one (query token, KV head) pair.  Units are ordered longest first
