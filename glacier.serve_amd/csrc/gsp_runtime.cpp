@@ -42,9 +42,11 @@ enum : int {
 // list scheduling).  Within a bin, split pieces go first and whole pairs
 // last, so split merges finish while other work still streams rather than in
 // the kernel's tail.  Two bins per CU (the decode kernels' occupancy) keep a
-// second workgroup streaming while the first one is in a unit epilogue.  A
-// unit costs its pages plus a fixed transition; a split piece also pays for
-// publishing its partial and for its share of the merge.
+// second workgroup streaming while the first one is in a unit epilogue; one
+// workgroup alone can draw the CU's full share of HBM bandwidth, so the split
+// size is scored per CU.  A unit costs its pages plus a fixed transition; a
+// split piece also pays for publishing its partial and for its share of the
+// merge.
 constexpr int kDecodeBinsPerCu = 2;
 constexpr int64_t kUnitCostPages = 1;
 constexpr int64_t kSplitCostPages = 3;
@@ -166,6 +168,7 @@ struct gsp_ctx {
     std::vector<int32_t> unit_bin;
     std::vector<std::pair<int64_t, int32_t>> bin_heap;
     std::vector<int32_t> bin_cursor;
+    std::vector<int64_t> bin_load;
     std::vector<PrefillTile> tiles;
     std::vector<int32_t> q_ctx;
     std::vector<int32_t> query_pages;
@@ -567,39 +570,68 @@ int gsp_pool_download(gsp_ctx* ctx, gsp_pool* pool, int32_t which, size_t offset
 
 /* ---------------------------------------------------------------- steps */
 
-// Packs the longest-first units into at most `bins_max` bins (LPT: each unit
-// goes to the least-loaded bin; ties to the lowest bin).  Within a bin, split
-// pieces run first and whole pairs last, each group keeping the longest-first
-// order.  The first bins_max units land in distinct empty bins, so no bin is
-// empty.  Layout: units[b] is bin b's first unit; the other units follow, bin
-// by bin, with bin b's at [bin_units[b], bin_units[b + 1]).  Returns the bin
-// count.
-static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max) {
+// Packs the longest-first units into bins, one decode workgroup each.
+//  - LPT: each unit goes to the least-loaded bin (ties to the lowest).  With
+//    `pair` (a grid of two workgroups per CU) the LPT runs over `nb / 2` CU
+//    bins and each CU bin's units are then dealt to its workgroups c and
+//    c + nb / 2, each unit to the lighter of the two.  In-order dispatch puts
+//    those two workgroups on one CU, where they share its bandwidth, so what
+//    must balance is their sum; should they land apart, each still holds
+//    about half of a balanced CU bin.  Pairing needs two units per CU bin.
+//  - Within a bin, split pieces run first and whole pairs last, each group
+//    keeping the longest-first order, so merges finish before the tail.
+// Layout: units[b] is bin b's first unit; the other units follow, bin by
+// bin, with bin b's at [bin_units[b], bin_units[b + 1]).  No bin is empty.
+// Returns the bin count.
+static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max, bool pair) {
     const size_t n = ctx->units.size();
     const int32_t nb = (int32_t)std::min<int64_t>(bins_max, (int64_t)n);
     ctx->bin_units.assign((size_t)nb + 1, 0);
     if (nb == 0) return 0;
+    pair = pair && nb == bins_max && nb % 2 == 0;
+    const int32_t nl = pair ? nb / 2 : nb;  // bins of the LPT
     auto& heap = ctx->bin_heap;
     heap.clear();
-    for (int32_t b = 0; b < nb; ++b) heap.emplace_back(0, b);
+    for (int32_t b = 0; b < nl; ++b) heap.emplace_back(0, b);
     const std::greater<std::pair<int64_t, int32_t>> later;
     std::make_heap(heap.begin(), heap.end(), later);
     ctx->unit_bin.resize(n);
+    auto& count = ctx->bin_cursor;
+    count.assign((size_t)nl, 0);
     for (size_t i = 0; i < n; ++i) {
         const DecodeUnit& u = ctx->units[i];
         std::pop_heap(heap.begin(), heap.end(), later);
         const int32_t b = heap.back().second;
         ctx->unit_bin[i] = b;
-        ctx->bin_units[(size_t)b + 1] += 1;
+        count[(size_t)b] += 1;
         heap.back().first += unit_cost(u.page_end - u.page_begin, (u.split_info >> 16) > 1);
         std::push_heap(heap.begin(), heap.end(), later);
+    }
+    if (pair) {
+        for (int32_t b = 0; b < nl; ++b)
+            if (count[(size_t)b] < 2) return assign_bins(ctx, bins_max, false);
+        auto& load = ctx->bin_load;
+        load.assign((size_t)nb, 0);
+        for (int pass = 0; pass < 2; ++pass)
+            for (size_t i = 0; i < n; ++i) {
+                const DecodeUnit& u = ctx->units[i];
+                const bool split = (u.split_info >> 16) > 1;
+                if (split != (pass == 0)) continue;
+                const int32_t c = ctx->unit_bin[i];
+                const int32_t w = load[(size_t)c] <= load[(size_t)(c + nl)] ? c : c + nl;
+                ctx->unit_bin[i] = w;
+                load[(size_t)w] += unit_cost(u.page_end - u.page_begin, split);
+            }
+        for (size_t i = 0; i < n; ++i) ctx->bin_units[(size_t)ctx->unit_bin[i] + 1] += 1;
+    } else {
+        for (int32_t b = 0; b < nb; ++b) ctx->bin_units[(size_t)b + 1] = count[(size_t)b];
     }
     // bin_units[b + 1] holds bin b's unit count: its first unit goes to slot b,
     // the rest to the bin's run after the nb first units.
     ctx->bin_units[0] = nb;
     for (int32_t b = 0; b < nb; ++b) ctx->bin_units[(size_t)b + 1] += ctx->bin_units[(size_t)b] - 1;
-    ctx->bin_cursor.resize((size_t)nb);
-    for (int32_t b = 0; b < nb; ++b) ctx->bin_cursor[(size_t)b] = -1;  // -1: the first unit is still to place
+    auto& cursor = ctx->bin_cursor;
+    cursor.assign((size_t)nb, -1);  // -1: the bin's first unit is still to place
     ctx->units_binned.resize(n);
     for (int pass = 0; pass < 2; ++pass) {
         const bool want_split = pass == 0;
@@ -607,7 +639,7 @@ static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max) {
             const DecodeUnit& u = ctx->units[i];
             if (((u.split_info >> 16) > 1) != want_split) continue;
             const int32_t b = ctx->unit_bin[i];
-            int32_t& cur = ctx->bin_cursor[(size_t)b];
+            int32_t& cur = cursor[(size_t)b];
             if (cur < 0) {
                 ctx->units_binned[(size_t)b] = u;
                 cur = ctx->bin_units[(size_t)b];
@@ -680,10 +712,13 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     // head, page range) and one workgroup.  Units are sorted longest first, so
     // in-order dispatch schedules them longest-processing-time first.
     const int64_t T = pair_pages * H;
-    // A pair may not be cut into more pieces than the merge LDS holds.
+    // A pair is cut into at most kMaxSplits pieces.
     const int64_t min_target = std::max<int64_t>(1, (max_pages + gsp::kMaxSplits - 1) / gsp::kMaxSplits);
-    const int64_t bins_max = ctx->decode_bins_override > 0 ? ctx->decode_bins_override
-                                                           : (int64_t)kDecodeBinsPerCu * std::max(1, ctx->num_cus);
+    // Default grid: two workgroups per CU, bins balanced per CU (assign_bins).
+    const bool pair_cus = ctx->decode_bins_override <= 0;
+    const int64_t bins_max = pair_cus ? (int64_t)kDecodeBinsPerCu * std::max(1, ctx->num_cus)
+                                      : (int64_t)ctx->decode_bins_override;
+    const int64_t sim_bins = pair_cus ? bins_max / kDecodeBinsPerCu : bins_max;
     int64_t target = 1;
     if (T > 0) {
         if (ctx->split_pages_override > 0) {
@@ -706,7 +741,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
             for (int32_t cand : kSplitCandidates) {
                 if (cand < min_target) continue;
                 if (T / cand > 16 * bins_max) continue;  // far too many units to be competitive
-                const int64_t c = simulate_split(ctx->query_pages, H, cand, bins_max, ctx->sim_count, ctx->sim_heap);
+                const int64_t c = simulate_split(ctx->query_pages, H, cand, sim_bins, ctx->sim_count, ctx->sim_heap);
                 if (c <= best_cost) {  // ties go to the larger split (fewer units)
                     best_cost = c;
                     target = cand;
@@ -798,7 +833,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     });
     std::stable_sort(ctx->tiles.begin(), ctx->tiles.end(),
                      [](const PrefillTile& x, const PrefillTile& y) { return x.pages > y.pages; });
-    const int32_t n_bins = assign_bins(ctx, bins_max);
+    const int32_t n_bins = assign_bins(ctx, bins_max, pair_cus);
 
     // Pass 3: write the staging buffer and upload it with one copy.
     const size_t n_units = ctx->units.size();
