@@ -8,8 +8,12 @@ rows), with Q, the KV pool and the packed tables already resident in HBM.
 Prints ONE JSON line (per workload with --all):
   value        KV GB/s = algorithmic KV bytes / ms_per_step (every valid K/V
                element counted once), unit GB/s
-  roofline     the decode kernel's algorithmic bytes / its mean launch time
-               (HIP events around each launch on the launch stream) vs 8 TB/s
+  roofline     the dominant kernel: decode = algorithmic KV bytes / its mean
+               launch time (K launches back to back between HIP events on the
+               launch stream) vs 8 TB/s; for steps with prefill rows each kernel is
+               also timed alone on its rows (roofline_decode, roofline_prefill;
+               prefill = 4*d*nH FLOPs per causal (query, key) pair vs the
+               157.3 TFLOP/s fp32 matrix peak)
   cpu_baseline the CPU oracle (C++ restatement of the reference kernel) timed
                on this host on the same inputs
 """
@@ -32,6 +36,9 @@ METRIC = "paged-attn decode KV GB/s (% HBM peak) + seq-steps/sec, Qwen2.5-7B sha
 WORKLOADS = ["qwen05b_decode", "qwen7b_decode", "llama8b_decode", "qwen7b_mixed", "longctx_decode"]
 DEFAULT_WORKLOAD = "qwen7b_decode"
 KERNEL_NAME = "paged_decode_mfma_kernel"
+PREFILL_KERNEL_NAME = "paged_prefill_mfma_kernel"
+FP32_MFMA_PEAK_TFS = 157.3  # MI355X dense fp32 matrix peak
+PREFILL_TILE_MIN_Q = 16     # rows the library runs as prefill tiles by default
 
 
 def cpu_threads() -> int:
@@ -52,10 +59,32 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def profiled_traffic(workload: str):
-    """HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary of this workload (profiles/), or None when none has been recorded."""
-    path = ROOT / "profiles" / f"{KERNEL_NAME}_{workload}.md"
+def time_substep(gsp, torch, ctx, stream, pool, sub, q, q_index, steps: int) -> float:
+    """Mean ms of one gsp_attention_step over `sub` (a subset of the step's rows,
+    same pool; one kernel launch per step): `steps` steps back to back between
+    two HIP events on the launch stream."""
+    idx = torch.from_numpy(q_index).to(q.device)
+    qs = q.index_select(0, idx).contiguous()
+    out = torch.empty((sub.total_q, sub.n_heads, sub.head_dim), device=q.device, dtype=torch.float32)
+    ctx.pack_step(pool, sub.positions, sub.token_counts, sub.bt_offsets, sub.bt_ids, sub.max_seq_len,
+                  q_lens=sub.q_lens)
+    for _ in range(3):
+        ctx.attention_step(pool, 0, sub.n_heads, qs.data_ptr(), out.data_ptr(), sub.scale)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        ctx.attention_step(pool, 0, sub.n_heads, qs.data_ptr(), out.data_ptr(), sub.scale)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def profiled_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary of this workload (profiles/), or None when none is recorded."""
+    path = ROOT / "profiles" / f"{kernel}_{workload}.md"
     try:
         for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch:"):
@@ -137,15 +166,11 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     wall_ms = (time.perf_counter() - t0) * 1e3
     ms_per_step = e0.elapsed_time(e1) / steps
 
-    # Mean duration of one decode-kernel launch (one launch per step).
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for a, b in evs:
-        a.record(stream)
-        attend()
-        b.record(stream)
-    torch.cuda.synchronize()
-    launch_ms = [a.elapsed_time(b) for a, b in evs]
-    kernel_ms = statistics.mean(launch_ms)
+    # A decode-only step is one launch of the decode kernel, so its mean launch
+    # duration over the timed region is ms_per_step.  (Events around every
+    # launch would add their own gaps; rocprofv3's kernel trace agrees with
+    # ms_per_step to about 1%.)
+    kernel_ms = ms_per_step
 
     # Engine-step time: pinned pack + one H2D copy + kernel, host-synchronous per step.
     n_step = max(10, steps // 4)
@@ -161,6 +186,52 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     gbs = kv_bytes / (ms_per_step * 1e-3) / 1e9
     kernel_gbs = kv_bytes / (kernel_ms * 1e-3) / 1e9
     got = out.cpu().numpy()
+
+    decode_roof = {
+        "bound": "hbm",
+        "kernel": KERNEL_NAME,
+        "achieved": round(kernel_gbs, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+        "traffic": profiled_traffic(name, KERNEL_NAME),
+        "algorithmic_bytes_per_launch": kv_bytes,
+        "mean_launch_ms": round(kernel_ms, 5),
+    }
+    roofline = decode_roof
+    extra = {}
+    tiled = np.nonzero(step.lens >= PREFILL_TILE_MIN_Q)[0]
+    if len(tiled):
+        # Rows of both kinds: time each kernel alone on its rows' sub-step
+        # (one launch of one kernel per step), and report the longer one.
+        rows_d = np.nonzero(step.lens < PREFILL_TILE_MIN_Q)[0]
+        sub_p, qi_p = step.subset(tiled)
+        pre_ms = time_substep(gsp, torch, ctx, stream, pool, sub_p, q, qi_p, steps)
+        flops = sub_p.prefill_flops()
+        tfs = flops / (pre_ms * 1e-3) / 1e12
+        prefill_roof = {
+            "bound": "mfma",
+            "kernel": PREFILL_KERNEL_NAME,
+            "achieved": round(tfs, 2),
+            "peak": FP32_MFMA_PEAK_TFS,
+            "unit": "TFLOP/s",
+            "frac": round(tfs / FP32_MFMA_PEAK_TFS, 4),
+            "traffic": profiled_traffic(name, PREFILL_KERNEL_NAME),
+            "algorithmic_flops_per_launch": int(flops),
+            "mean_launch_ms": round(pre_ms, 5),
+        }
+        if len(rows_d):
+            sub_d, qi_d = step.subset(rows_d)
+            dec_ms = time_substep(gsp, torch, ctx, stream, pool, sub_d, q, qi_d, steps)
+            dgbs = sub_d.kv_bytes() / (dec_ms * 1e-3) / 1e9
+            decode_roof.update({"achieved": round(dgbs, 1), "frac": round(dgbs / HBM_PEAK_GBS, 4),
+                                "algorithmic_bytes_per_launch": sub_d.kv_bytes(), "mean_launch_ms": round(dec_ms, 5),
+                                "rows": "decode rows alone"})
+        else:
+            dec_ms = 0.0
+        extra["roofline_decode"] = decode_roof
+        extra["roofline_prefill"] = prefill_roof
+        roofline = prefill_roof if pre_ms >= dec_ms else decode_roof
 
     result = {
         "metric": METRIC,
@@ -185,18 +256,9 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         "step_info": {"decode_units": info.decode_units, "split_pairs": info.split_pairs,
                       "partial_slots": info.partial_slots, "pages_per_split": info.pages_per_split,
                       "packed_pages": info.packed_pages, "staging_bytes": int(info.staging_bytes)},
-        "roofline": {
-            "bound": "hbm",
-            "kernel": KERNEL_NAME,
-            "achieved": round(kernel_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic(name),
-            "algorithmic_bytes_per_launch": kv_bytes,
-            "mean_launch_ms": round(kernel_ms, 5),
-        },
+        "roofline": roofline,
     }
+    result.update(extra)
 
     if cpu:
         result["cpu_baseline"], ref = cpu_baseline(step, q, k, v, cpu_budget_s)

@@ -94,6 +94,24 @@ class Step:
     def table(self, b: int) -> np.ndarray:
         return self.bt_ids[self.bt_offsets[b]:self.bt_offsets[b + 1]]
 
+    def subset(self, rows) -> Tuple["Step", np.ndarray]:
+        """The step restricted to `rows` (same pool and seed), and the indices of
+        its query tokens within this step's q / out rows."""
+        rows = np.asarray(rows, np.int64)
+        lens = self.lens.astype(np.int64)
+        starts = np.concatenate([[0], np.cumsum(lens)])
+        q_index = np.concatenate([np.arange(starts[b], starts[b + 1]) for b in rows]) if len(rows) else \
+            np.zeros(0, np.int64)
+        spans = [self.table(int(b)) for b in rows]
+        offsets = np.concatenate([[0], np.cumsum([len(t) for t in spans])]).astype(np.int32)
+        ids = np.concatenate(spans).astype(np.int32) if spans else np.zeros(0, np.int32)
+        q_lens = None if self.q_lens is None else self.q_lens[rows].astype(np.int32)
+        sub = Step(self.name, self.n_heads, self.n_kv, self.head_dim, self.kv_dtype, self.total_blocks,
+                   self.max_seq_len, positions=self.positions[rows].astype(np.int32),
+                   token_counts=self.token_counts[rows].astype(np.int32), bt_offsets=offsets, bt_ids=ids,
+                   q_lens=q_lens, seed=self.seed, notes=dict(self.notes))
+        return sub, q_index
+
 
 def _slices(rng: np.random.Generator, total_blocks: int, pages: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
     """Fisher-Yates permutation of the pool, cut into consecutive per-row slices."""
