@@ -145,7 +145,8 @@ __device__ __forceinline__ void load_q(QRegs<D, _Float16>& qr, const DecodeArgs&
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     int ex = 0;
     if (mx > 0.f) (void)frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
-    const int sh = 13 - ex;               // scaled max in [2^12, 2^13)
+    // Scaled max in [2^12, 2^13); clamped so that 2^sh and 2^-sh stay normal floats.
+    const int sh = mx > 0.f ? min(100, max(-100, 13 - ex)) : 0;
     const float up = ldexpf(1.0f, sh);
 #pragma unroll
     for (int j = 0; j < D / 16; ++j) {
@@ -215,6 +216,8 @@ __device__ __forceinline__ void page_pv(WaveState<D>& st, const PageRegs<D, _Flo
     // P = p_hi + p_lo in fp16 (P is in [0, 1]); V is exact in fp16.  Output
     // block 4c + i takes B[token 4g + kk][col] = V[4g + kk][64c + 4n + i],
     // i.e. element i of the lane's four V pieces.
+    // P arrives times 2^12 (compute_page), so p_lo of a typical probability is a
+    // normal fp16 number: the matrix cores flush fp16 subnormals.
     const h4 ph = __builtin_convertvector(p, h4);
     const h4 pl = __builtin_convertvector(p - __builtin_convertvector(ph, f4), h4);
 #pragma unroll
@@ -245,6 +248,10 @@ __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D,
     f4 p;
 #pragma unroll
     for (int r = 0; r < 4; ++r) p[r] = fast_exp2(s[r] - mn);
+    // fp16 pages feed P to the matrix cores times 2^12 (page_pv); O and l then
+    // carry the same factor, which cancels in O / l.
+    const float pscale = sizeof(KT) == 2 ? 4096.0f : 1.0f;
+    p *= pscale;
     st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
     // O rows are heads 4g + r; their alphas live in lanes 4g + r.
     if (__any(alpha != 1.0f)) {

@@ -5,21 +5,44 @@
 // min(TokenCount, pos + i + 1) tokens (PagedTransformerRunner.cs:425-474,
 // PagedAttentionKernel.cs:41).  Its queries share every K/V page of the prefix,
 // so the work is a dense causal contraction; one workgroup owns a tile of 16
-// consecutive query tokens of one row and one KV head, for all G <= 8 query
-// heads of the GQA group, and walks the row's pages in order:
+// consecutive query tokens of one row and one KV head, for up to 8 query heads
+// of the GQA group (grid.y covers larger groups), and walks the row's pages in
+// order:
 //
 //   per page (16 keys, staged once in LDS and shared by the group's heads):
-//     S^T[key][token] = K_page . Q_head^T   v_mfma_f32_16x16x4f32 (M = keys, N = tokens)
-//     O_head[token][e] += P . V_page          v_mfma_f32_16x16x4f32 (M = tokens, K = keys)
+//     S^T[key][token] = K_page . Q_head^T   (M = keys, N = tokens, K = head dim)
+//     O_head[token][e] += P . V_page          (M = tokens, N = head dim, K = keys)
 //
-// Row-tile T of the workgroup is query head kvh*G + T over the 16 tokens; wave
-// w owns tiles w and w + 4.  The operand layouts are those of the decode
-// kernel with "head" replaced by "query token", so each lane holds the scores
-// of one token for four keys and the online softmax costs four exp2 per lane
-// per page.  The causal limit is per row (token); padding rows past the
-// tile's tokens keep finite scores and are never written.  Pages are staged
-// through two LDS buffers (register-prefetched one page ahead) with one
-// barrier per page.  The roofline of these rows is FP32 matrix throughput.
+// both on v_mfma_f32_16x16x16f16 with fp32 accumulation.  Operands enter as
+// fp16 pairs x = x_hi + x_lo, each side scaled by a power of two so that its
+// largest element lies in [2^12, 2^13) (the pair then carries ~22
+// significant bits and nothing overflows or flushes):
+//   - Q: per query token (the lane's S column), at load;
+//   - fp32 K, V pages: per key row, while the page is staged into LDS;
+//     fp16 pages are exact in fp16 and enter as they are (x_lo = 0);
+//   - P in [0, 1]: times 2^12, so that p_lo stays a normal fp16 number
+//     (the matrix cores flush fp16 subnormals; an unscaled p_lo of a typical
+//     probability would be one, and P would keep only 11 bits).
+// S = K_hi.Q_hi + K_hi.Q_lo + K_lo.Q_hi (the K_lo.Q_lo term is ~2^-22
+// relative), times 2^(e_key + e_token) * scale.  The V scales fold into P:
+// the accumulator O is kept in units of 2^(eO - 12), eO the largest V
+// exponent seen so far, so P' = P * 2^(e_v(key) - eO + 12) <= 2^12, and O is
+// rescaled (like the softmax's alpha) when a page raises eO.  Precision bound
+// of that fold: a key whose V row is more than ~2^14 smaller than the row's
+// largest V row gets a subnormal P' and keeps fewer bits (none beyond ~2^26);
+// its absolute error stays below ~2^-25 of the largest |V| element.
+//
+// Row tile T of the workgroup is query head hc + T over the 16 tokens; wave w
+// owns tiles w and w + 4.  The MFMA operand layouts are the decode kernel's
+// with "head" replaced by "query token" (lane l, n = l % 16, g = l / 16):
+//   QK A = K[key n][16j + 4g .. +3], B = Q[token n][16j + 4g .. +3]
+//   result: lane holds S[token n][key 4g + r]
+//   PV A = P'[token n][keys 4g .. 4g+3] (the lane's own four), B = V[keys 4g .. 4g+3][col],
+//   col = 64c + 4n + i for output block 4c + i; result: lane holds O[token 4g + r][col].
+// The causal limit is per row (token); padding rows past the tile's tokens
+// keep finite scores and are never written.  Pages are staged through two LDS
+// buffers (register-prefetched one page ahead) with one barrier per page.
+// The roofline of these rows is the matrix peak.
 #include "gsp_epilogue.h"
 
 namespace gsp {
@@ -29,74 +52,218 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPrefillTiles = kPrefillHeads / kDecodeWaves;  // row tiles (query heads) per wave
+constexpr int kPScaleLog2 = 12;  // P enters the matrix cores times 2^12 (p_lo stays normal)
 static_assert(kPrefillTileTokens == kBlockSize, "the tile's token and key dimensions are both 16");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t prefill_rsrc(const void* base, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-template <typename KT>
-__device__ __forceinline__ f4 pload4(__amdgpu_buffer_rsrc_t r, int off);
-
-template <>
-__device__ __forceinline__ f4 pload4<float>(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4, 0, 0));
+// Exponent e such that x * 2^-e has its largest |element| `mx` in [2^12, 2^13).
+// Clamped to [-100, 100] so that 2^-e and 2^e stay normal floats (inputs below
+// 2^-87 then keep their absolute fp16 rounding only).  An all-zero vector
+// (such as the slots past a page's valid tokens, which load as 0) gets the
+// floor -100, so it never raises the largest V exponent of a page.
+constexpr int kPairExpFloor = -100;
+__device__ __forceinline__ int pair_exponent(float mx) {
+    int ex = 0;
+    if (mx > 0.f) (void)frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
+    return mx > 0.f ? min(100, max(kPairExpFloor, ex - 13)) : kPairExpFloor;
 }
 
-template <>
-__device__ __forceinline__ f4 pload4<_Float16>(__amdgpu_buffer_rsrc_t r, int off) {
-    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
-    const u2 raw = __builtin_amdgcn_raw_buffer_load_b64(r, off * 2, 0, 0);
-    const h4 h = __builtin_bit_cast(h4, raw);
-    return f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+__device__ __forceinline__ void split_pair(const f4& x, h4& hi, h4& lo) {
+    hi = __builtin_convertvector(x, h4);
+    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f4), h4);
 }
 
-template <int D>
-struct PrefillLds {
-    static constexpr int kRow = D + 4;  // padded row: 16-byte skew between keys
-    float k[2][kBlockSize * kRow];
-    float v[2][kBlockSize * kRow];
-};
+__device__ __forceinline__ float max_abs4(const f4& x) {
+    return fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+}
 
-// Each of the 256 threads moves (16 * D / 4) / 256 four-element chunks of K and of V.
+// Page staging: each of the 256 threads moves (16 * D / 4) / 256 four-element
+// chunks of K and of V; chunk c is key c / (D/4), elements 4 * (c % (D/4)).
 template <int D>
-struct StageRegs {
-    f4 k[(kBlockSize * D / 4) / kDecodeThreads];
-    f4 v[(kBlockSize * D / 4) / kDecodeThreads];
-};
+constexpr int kStageChunks = (kBlockSize * D / 4) / kDecodeThreads;
 
 template <int D, typename KT>
-__device__ __forceinline__ void stage_load(StageRegs<D>& sr, const KT* kpage, const KT* vpage, int ntok) {
-    constexpr int NC = (kBlockSize * D / 4) / kDecodeThreads;
-    const int bytes = ntok * D * (int)sizeof(KT);
+struct PfStage;
+
+template <int D>
+struct PfStage<D, float> {
+    f4 k[kStageChunks<D>];
+    f4 v[kStageChunks<D>];
+};
+
+template <int D>
+struct PfStage<D, _Float16> {
+    h4 k[kStageChunks<D>];
+    h4 v[kStageChunks<D>];
+};
+
+// LDS page buffers (two).  Rows are padded by 8 halves (16 bytes).
+template <int D, typename KT>
+struct PfLds;
+
+template <int D>
+struct alignas(16) PfLds<D, float> {
+    static constexpr int kRow = D + 8;
+    _Float16 kh[2][kBlockSize * kRow], kl[2][kBlockSize * kRow];
+    _Float16 vh[2][kBlockSize * kRow], vl[2][kBlockSize * kRow];
+    int ek[2][kBlockSize], ev[2][kBlockSize];  // per-key exponents of the K and V pairs
+};
+
+template <int D>
+struct alignas(16) PfLds<D, _Float16> {
+    static constexpr int kRow = D + 8;
+    _Float16 k[2][kBlockSize * kRow];
+    _Float16 v[2][kBlockSize * kRow];
+};
+
+template <int D>
+__device__ __forceinline__ void stage_load(PfStage<D, float>& sr, const float* kpage, const float* vpage, int ntok) {
+    const int bytes = ntok * D * 4;
     const __amdgpu_buffer_rsrc_t rk = prefill_rsrc(kpage, bytes);
     const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(vpage, bytes);
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-        const int c = threadIdx.x + i * kDecodeThreads;  // chunk: key c / (D/4), elements 4 * (c % (D/4))
-        sr.k[i] = pload4<KT>(rk, 4 * c);
-        sr.v[i] = pload4<KT>(rv, 4 * c);
+    for (int i = 0; i < kStageChunks<D>; ++i) {
+        const int c = threadIdx.x + i * kDecodeThreads;
+        sr.k[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rk, 16 * c, 0, 0));
+        sr.v[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rv, 16 * c, 0, 0));
     }
 }
 
 template <int D>
-__device__ __forceinline__ void stage_store(const StageRegs<D>& sr, float* lk, float* lv) {
-    constexpr int NC = (kBlockSize * D / 4) / kDecodeThreads;
-    constexpr int kRow = PrefillLds<D>::kRow;
+__device__ __forceinline__ void stage_load(PfStage<D, _Float16>& sr, const _Float16* kpage, const _Float16* vpage,
+                                           int ntok) {
+    const int bytes = ntok * D * 2;
+    const __amdgpu_buffer_rsrc_t rk = prefill_rsrc(kpage, bytes);
+    const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(vpage, bytes);
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
+    for (int i = 0; i < kStageChunks<D>; ++i) {
+        const int c = threadIdx.x + i * kDecodeThreads;
+        sr.k[i] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rk, 8 * c, 0, 0));
+        sr.v[i] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rv, 8 * c, 0, 0));
+    }
+}
+
+// Max of |x| over the D/4 threads of one key row: they are D/4 consecutive
+// lanes of one wave (32 for d = 128, 16 for d = 64), aligned to D/4.
+template <int D>
+__device__ __forceinline__ float key_row_max(float x) {
+#pragma unroll
+    for (int s = 1; s < D / 4; s <<= 1) x = fmaxf(x, __shfl_xor(x, s));
+    return x;
+}
+
+template <int D>
+__device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D, float>& sh, int buf) {
+    constexpr int kRow = PfLds<D, float>::kRow;
+#pragma unroll
+    for (int i = 0; i < kStageChunks<D>; ++i) {
         const int c = threadIdx.x + i * kDecodeThreads;
         const int key = c / (D / 4);
         const int col = 4 * (c % (D / 4));
-        *reinterpret_cast<f4*>(lk + key * kRow + col) = sr.k[i];
-        *reinterpret_cast<f4*>(lv + key * kRow + col) = sr.v[i];
+        const int ek = pair_exponent(key_row_max<D>(max_abs4(sr.k[i])));
+        const int ev = pair_exponent(key_row_max<D>(max_abs4(sr.v[i])));
+        h4 hi, lo;
+        split_pair(sr.k[i] * ldexpf(1.0f, -ek), hi, lo);
+        *reinterpret_cast<h4*>(&sh.kh[buf][key * kRow + col]) = hi;
+        *reinterpret_cast<h4*>(&sh.kl[buf][key * kRow + col]) = lo;
+        split_pair(sr.v[i] * ldexpf(1.0f, -ev), hi, lo);
+        *reinterpret_cast<h4*>(&sh.vh[buf][key * kRow + col]) = hi;
+        *reinterpret_cast<h4*>(&sh.vl[buf][key * kRow + col]) = lo;
+        if (col == 0) {
+            sh.ek[buf][key] = ek;
+            sh.ev[buf][key] = ev;
+        }
     }
+}
+
+template <int D>
+__device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLds<D, _Float16>& sh, int buf) {
+    constexpr int kRow = PfLds<D, _Float16>::kRow;
+#pragma unroll
+    for (int i = 0; i < kStageChunks<D>; ++i) {
+        const int c = threadIdx.x + i * kDecodeThreads;
+        const int key = c / (D / 4);
+        const int col = 4 * (c % (D / 4));
+        *reinterpret_cast<h4*>(&sh.k[buf][key * kRow + col]) = sr.k[i];
+        *reinterpret_cast<h4*>(&sh.v[buf][key * kRow + col]) = sr.v[i];
+    }
+}
+
+// Q operands of one tile, q[j] = Q[token n][16j + 4g .. +3] as a scaled fp16
+// pair, and the lane's score factor 2^e_token * scale (log2 units).
+template <int D>
+struct TileQ {
+    h4 hi[D / 16];
+    h4 lo[D / 16];
+    float sc;
+};
+
+template <int D>
+__device__ __forceinline__ void load_tile_q(TileQ<D>& tq, const float* qrow, bool live, int g, float scale) {
+    f4 x[D / 16];
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+        const f4 v = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
+        x[j] = live ? v : f4{0.f, 0.f, 0.f, 0.f};
+        mx = fmaxf(mx, max_abs4(x[j]));
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));  // token n's elements live in lanes n + 16g
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const int e = pair_exponent(mx);
+    const float down = ldexpf(1.0f, -e);
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) split_pair(x[j] * down, tq.hi[j], tq.lo[j]);
+    tq.sc = ldexpf(scale, e);
+}
+
+// Per-tile softmax state: O in units of 2^eo, running max m (log2 units) of
+// token n, partial sum l of token n over this lane's keys.
+template <int D>
+struct TileState {
+    f4 o[D / 16];
+    float m;
+    float l;
+    int eo;
+};
+
+// Causal mask and online softmax of one page's scores; returns P, and in
+// `alpha_rows` the factors that the lane's O rows (tokens 4g + r) must take,
+// fetched from the lanes that own those tokens (`rescale` false: all 1).
+template <int D>
+__device__ __forceinline__ f4 page_softmax(TileState<D>& st, f4 s, bool diag, int key0, int row_ctx, int g,
+                                           f4& alpha_rows, bool& rescale) {
+    if (diag) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (key0 + r >= row_ctx) s[r] = -INFINITY;
+    }
+    float mp = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mp = fmaxf(mp, __shfl_xor(mp, 16));
+    mp = fmaxf(mp, __shfl_xor(mp, 32));
+    const float mn = fmaxf(st.m, mp);  // finite: page 0 holds key 0 for every row
+    const float alpha = fast_exp2(st.m - mn);
+    st.m = mn;
+    f4 p;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(s[r] - mn);
+    st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    rescale = __any(alpha != 1.0f);
+    if (rescale) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) alpha_rows[r] = __shfl(alpha, 4 * g + r);
+    }
+    return p;
 }
 
 template <int D, typename KT>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(PrefillArgs a) {
-    constexpr int kRow = PrefillLds<D>::kRow;
-    __shared__ PrefillLds<D> sh;
+    constexpr int kRow = PfLds<D, KT>::kRow;
+    constexpr bool kSplitKV = sizeof(KT) == 4;  // fp32 pages enter as hi + lo pairs
+    __shared__ PfLds<D, KT> sh;
 
     const PrefillTile t = a.tiles[blockIdx.x];
     const int hc = blockIdx.y * kPrefillHeads;  // first head of this workgroup within the group
@@ -111,25 +278,19 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
     // whole page range so their scores stay finite.
     const bool row_live = n < t.ntok;
     const int row_ctx = row_live ? min(t.token_count, t.pos0 + n + 1) : 0x7fffffff;
-    const float scale = a.scale_log2;
 
-    // Q^T operands and accumulators of this wave's tiles (tile T = head T).
-    f4 q[kPrefillTiles][D / 16];
-    f4 o[kPrefillTiles][D / 16];
-    float m[kPrefillTiles], l[kPrefillTiles];
+    TileQ<D> q[kPrefillTiles];
+    TileState<D> st[kPrefillTiles];
 #pragma unroll
     for (int s = 0; s < kPrefillTiles; ++s) {
         const int T = wave + 4 * s;
-        const bool live = T < G && row_live;
         const float* qrow = a.q + ((int64_t)(t.qi0 + (row_live ? n : 0)) * a.n_heads + h0 + (T < G ? T : 0)) * D;
+        load_tile_q<D>(q[s], qrow, T < G && row_live, g, a.scale_log2);
 #pragma unroll
-        for (int j = 0; j < D / 16; ++j) {
-            const f4 x = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
-            q[s][j] = live ? x : f4{0.f, 0.f, 0.f, 0.f};
-            o[s][j] = f4{0.f, 0.f, 0.f, 0.f};
-        }
-        m[s] = -INFINITY;
-        l[s] = 0.f;
+        for (int j = 0; j < D / 16; ++j) st[s].o[j] = f4{0.f, 0.f, 0.f, 0.f};
+        st[s].m = -INFINITY;
+        st[s].l = 0.f;
+        st[s].eo = -1000;  // below any page's V exponent: the first page sets it
     }
 
     const KT* kbase = static_cast<const KT*>(a.k_pool) + a.layer_offset + (int64_t)t.kvh * a.head_stride;
@@ -137,12 +298,11 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
     const int32_t* bt = a.bt_ids + t.bt_base;
     const int ctx_last = min(t.token_count, t.pos0 + t.ntok);
 
-    StageRegs<D> sr;
+    PfStage<D, KT> sr;
     {
         const int64_t blk = bt[0];
-        stage_load<D, KT>(sr, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
-                          min(kBlockSize, ctx_last));
-        stage_store<D>(sr, sh.k[0], sh.v[0]);
+        stage_load<D>(sr, kbase + blk * a.block_stride, vbase + blk * a.block_stride, min(kBlockSize, ctx_last));
+        stage_store<D>(sr, sh, 0);
     }
     __syncthreads();
 
@@ -150,71 +310,105 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
         const int buf = p & 1;
         if (p + 1 < t.pages) {
             const int64_t blk = bt[p + 1];
-            stage_load<D, KT>(sr, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
-                              min(kBlockSize, ctx_last - (p + 1) * kBlockSize));
+            stage_load<D>(sr, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
+                          min(kBlockSize, ctx_last - (p + 1) * kBlockSize));
         }
-        // K operand: K[key n][16j + 4g ..]; V operand: V[key 4g + kk][64c + 4n ..].
-        const float* lk = sh.k[buf];
-        const float* lv = sh.v[buf];
-        f4 kop[D / 16];
-#pragma unroll
-        for (int j = 0; j < D / 16; ++j) kop[j] = *reinterpret_cast<const f4*>(lk + n * kRow + 16 * j + 4 * g);
-        f4 vop[4][D / 64];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-            for (int c = 0; c < D / 64; ++c)
-                vop[kk][c] = *reinterpret_cast<const f4*>(lv + (4 * g + kk) * kRow + 64 * c + 4 * n);
-
         const int key0 = p * kBlockSize + 4 * g;
         const bool diag = (p + 1) * kBlockSize > min(t.pos0 + 1, t.token_count);  // some row may stop here
+
+        // Page scales (fp32 pages): 2^e_k and e_v of keys 4g + r, and the page's largest e_v.
+        f4 kscale = {1.f, 1.f, 1.f, 1.f};
+        int evk[4] = {0, 0, 0, 0};
+        int evmax = 0;
+        if constexpr (kSplitKV) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                kscale[r] = ldexpf(1.0f, sh.ek[buf][4 * g + r]);
+                evk[r] = sh.ev[buf][4 * g + r];
+            }
+            evmax = sh.ev[buf][0];
+#pragma unroll
+            for (int k = 1; k < kBlockSize; ++k) evmax = max(evmax, sh.ev[buf][k]);
+        }
+
 #pragma unroll
         for (int s = 0; s < kPrefillTiles; ++s) {
             if (wave + 4 * s >= G) continue;  // uniform per wave
+            TileState<D>& ts = st[s];
+            // S^T = K . Q^T (hi/lo products; two accumulation chains).  The K
+            // operands come from LDS per tile (re-read by the wave's second tile).
             f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < D / 16; ++j)
+            for (int j = 0; j < D / 16; ++j) {
+                const int at = n * kRow + 16 * j + 4 * g;
+                if constexpr (kSplitKV) {
+                    const h4 kh = *reinterpret_cast<const h4*>(&sh.kh[buf][at]);
+                    const h4 kl = *reinterpret_cast<const h4*>(&sh.kl[buf][at]);
+                    s0 = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].hi[j], s0, 0, 0, 0);
+                    s1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].lo[j], s1, 0, 0, 0);
+                    s1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, q[s].hi[j], s1, 0, 0, 0);
+                } else {
+                    const h4 kx = *reinterpret_cast<const h4*>(&sh.k[buf][at]);
+                    s0 = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].hi[j], s0, 0, 0, 0);
+                    s1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].lo[j], s1, 0, 0, 0);
+                }
+            }
+            f4 sc = (s0 + s1) * q[s].sc;  // lane: S[token n][keys key0 .. key0 + 3], log2 units
+            if constexpr (kSplitKV) sc *= kscale;
+
+            f4 alpha_rows = {1.f, 1.f, 1.f, 1.f};
+            bool rescale = false;
+            f4 pr = page_softmax<D>(ts, sc, diag, key0, row_ctx, g, alpha_rows, rescale);
+
+            if constexpr (kSplitKV) {
+                // O in units of 2^eo: a page with larger V exponents raises eo first.
+                if (evmax > ts.eo) {
+                    const float down = ldexpf(1.0f, ts.eo - evmax);  // 0 on the first page
+                    alpha_rows *= down;
+                    rescale = true;
+                    ts.eo = evmax;
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) pr[r] = ldexpf(pr[r], evk[r] - ts.eo + kPScaleLog2);
+            } else {
+                pr *= (float)(1 << kPScaleLog2);
+            }
+            if (rescale) {
+#pragma unroll
+                for (int b = 0; b < D / 16; ++b) ts.o[b] *= alpha_rows;
+            }
+            h4 ph, pl;
+            split_pair(pr, ph, pl);
+            // O += P' . V: output block 4c + i takes B = V[keys 4g + kk][64c + 4n + i],
+            // element i of the lane's four V pieces of keys 4g .. 4g + 3.
+#pragma unroll
+            for (int c = 0; c < D / 64; ++c) {
+                h4 vh[4], vl[4];
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const int at = (4 * g + kk) * kRow + 64 * c + 4 * n;
+                    if constexpr (kSplitKV) {
+                        vh[kk] = *reinterpret_cast<const h4*>(&sh.vh[buf][at]);
+                        vl[kk] = *reinterpret_cast<const h4*>(&sh.vl[buf][at]);
+                    } else {
+                        vh[kk] = *reinterpret_cast<const h4*>(&sh.v[buf][at]);
+                    }
+                }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    if (j & 1)
-                        s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kop[j][i], q[s][j][i], s1, 0, 0, 0);
-                    else
-                        s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kop[j][i], q[s][j][i], s0, 0, 0, 0);
+                    const h4 bh = {vh[0][i], vh[1][i], vh[2][i], vh[3][i]};
+                    f4 acc = ts.o[4 * c + i];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bh, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, bh, acc, 0, 0, 0);
+                    if constexpr (kSplitKV) {
+                        const h4 bl = {vl[0][i], vl[1][i], vl[2][i], vl[3][i]};
+                        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bl, acc, 0, 0, 0);
+                    }
+                    ts.o[4 * c + i] = acc;
                 }
-            f4 sc = (s0 + s1) * scale;  // lane: S[token n][keys key0 .. key0 + 3]
-            if (diag) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (key0 + r >= row_ctx) sc[r] = -INFINITY;
             }
-            float mp = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-            mp = fmaxf(mp, __shfl_xor(mp, 16));
-            mp = fmaxf(mp, __shfl_xor(mp, 32));
-            const float mn = fmaxf(m[s], mp);  // finite: page 0 holds key 0 for every row
-            const float alpha = fast_exp2(m[s] - mn);
-            m[s] = mn;
-            f4 pr;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sc[r] - mn);
-            l[s] = l[s] * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-            if (__any(alpha != 1.0f)) {
-                const int src = 4 * g;
-                f4 ar;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, src + r);
-#pragma unroll
-                for (int b = 0; b < D / 16; ++b) o[s][b] *= ar;
-            }
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-                for (int c = 0; c < D / 64; ++c)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        o[s][4 * c + i] =
-                            __builtin_amdgcn_mfma_f32_16x16x4f32(pr[kk], vop[kk][c][i], o[s][4 * c + i], 0, 0, 0);
         }
-        if (p + 1 < t.pages) stage_store<D>(sr, sh.k[buf ^ 1], sh.v[buf ^ 1]);
+        if (p + 1 < t.pages) stage_store<D>(sr, sh, buf ^ 1);
         __syncthreads();
     }
 
@@ -223,12 +417,13 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
     for (int s = 0; s < kPrefillTiles; ++s) {
         const int T = wave + 4 * s;
         if (T >= G) continue;
-        float ls = l[s];
+        float ls = st[s].l;
         ls += __shfl_xor(ls, 16);
         ls += __shfl_xor(ls, 32);
+        const float unit = ldexpf(1.0f, (kSplitKV ? st[s].eo : 0) - kPScaleLog2);
         f4 inv;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) inv[r] = 1.0f / __shfl(ls, 4 * g + r);
+        for (int r = 0; r < 4; ++r) inv[r] = unit / __shfl(ls, 4 * g + r);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int tok = 4 * g + r;
@@ -238,7 +433,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
                 for (int c = 0; c < D / 64; ++c) {
                     f4 v;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) v[i] = o[s][4 * c + i][r] * inv[r];
+                    for (int i = 0; i < 4; ++i) v[i] = st[s].o[4 * c + i][r] * inv[r];
                     *reinterpret_cast<f4*>(orow + 64 * c + 4 * n) = v;
                 }
             }

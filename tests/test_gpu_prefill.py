@@ -152,3 +152,53 @@ def test_tiles_equal_per_token_path(torch_mod, gsp, ctx):
     pool.destroy()
     assert max_err(tiles, per_token) <= 1e-4
     assert max_err(tiles, oracle_step(step, q, k, v, threads=threads())) <= 1e-4
+
+
+def fp64_reference(step, q, k, v):
+    """Exact-arithmetic (float64) attention of every query token, from the oracle's fp64 path."""
+    import glacier_oracle as orc
+
+    pool = orc.HostPool(k, v)
+    out = np.zeros((step.total_q, step.n_heads, step.head_dim), np.float64)
+    qi = 0
+    for b in range(step.num_rows):
+        for i in range(int(step.lens[b])):
+            pos = int(step.positions[b]) + i
+            out[qi] = orc.attention_fp64(pool, step.table(b), int(step.token_counts[b]), 0, pos, q[qi], step.n_heads,
+                                         step.scale, step.max_seq_len).reshape(step.n_heads, step.head_dim)
+            qi += 1
+    return out
+
+
+@pytest.mark.parametrize("case", ["peaked_scores", "mixed_v_pages", "beyond_fp16_range", "small_v", "tiny_values"])
+def test_prefill_tiles_hold_fp32_range(torch_mod, gsp, ctx, case):
+    """fp32 pages enter the fp16 matrix cores as scaled hi + lo pairs.  Values far outside fp16's
+    range, pages whose V magnitudes differ by 1e9, tiny values and near-one-hot softmaxes stay
+    within 4x of fp32 arithmetic's own error against float64 (the fp32 oracle's error; for
+    peaked scores |S| ~ 1e3 it is ~1e-4 relative), plus 1e-6 of the output's magnitude."""
+    q_lens = np.array([40, 16, 23], np.int32)
+    step = workloads.small_step(seed=321, rows=3, n_heads=14, n_kv=2, head_dim=128, ctx_lo=0, ctx_hi=90,
+                                total_blocks=64, q_lens=q_lens)
+    q, k, v = workloads.host_values(step)
+    rng = np.random.default_rng(9)
+    if case == "peaked_scores":
+        q, k = q * 40.0, k * 25.0
+    elif case == "mixed_v_pages":
+        page_scale = 10.0 ** rng.uniform(-4, 5, size=(k.shape[0], 1, 1, 1, 1))
+        v = v * page_scale
+    elif case == "beyond_fp16_range":
+        q, k, v = q * 3e4, k * 2e5, v * 1e7
+    elif case == "small_v":
+        v = v * 1e-20  # the zero slots of a partial last page must not set the V scale
+    else:
+        q, k, v = q * 1e-6, k * 1e-7, v * 1e-30
+    q, k, v = q.astype(np.float32), k.astype(np.float32), v.astype(np.float32)
+    pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
+    got, info = run_step(torch_mod, gsp, ctx, step, q, pool, 1)
+    pool.destroy()
+    assert info.prefill_tiles > 0
+    exact = fp64_reference(step, q, k, v)
+    fp32_err = max_err(oracle_step(step, q, k, v), exact)
+    mag = float(np.abs(exact).max())
+    assert np.isfinite(got).all()
+    assert max_err(got, exact) <= 4.0 * fp32_err + 1e-6 * mag
