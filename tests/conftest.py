@@ -5,7 +5,7 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
-for sub in ("glacier.serve_amd", "oracle"):
+for sub in ("glacier.serve_amd", "oracle", "tests/golden"):
     p = str(ROOT / sub)
     if p not in sys.path:
         sys.path.insert(0, p)
