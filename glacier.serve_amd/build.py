@@ -30,7 +30,12 @@ SOURCES = [
 ARCH = "gfx950"
 
 # Packed FP32 (v_pk_*_f32) is switched off for all device code.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# The atomic optimizer is off too: it turns the decode kernels' one-lane queue
+# ticket into a wave-wide scan whose result is waited for at once, which
+# drains every page load in flight.  Without it the wait lands where the
+# ticket is used, as a count that leaves the prefetched pages in flight.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]
 
 
 def hipcc() -> str:

@@ -88,15 +88,24 @@ __device__ __forceinline__ void load_page(PageRegs<D, KT>& pr, const KT* kpage, 
         for (int c = 0; c < D / 64; ++c) pr.v[kk][c] = Raw4<KT>::load(rv, (4 * g + kk) * D + 64 * c + 4 * n);
 }
 
-// Q^T operand of a unit, q[j] = Q[head n][16j + 4g .. +3] (padded heads 0),
-// and `sc`, the factor that turns the lane's S column (head n) into log2
-// units.  The attention scale multiplies the finished dot, as in the
-// reference (PagedAttentionKernel.cs:65).
+// Q^T operand of a unit, q[j] = Q[head n][16j + 4g .. +3], and `sc`, the
+// factor that turns the lane's S column (head n) into log2 units.  The
+// attention scale multiplies the finished dot, as in the reference
+// (PagedAttentionKernel.cs:65).  Heads n >= G of the 16-wide tile read the
+// group's head 0: their S, P and O columns stay finite and are never stored.
 //  - fp32 pages: q in fp32, sc = scale * log2 e.
 //  - fp16 pages: the matrix cores take fp16 operands.  K is exact in fp16;
 //    Q is cut into q_hi + q_lo fp16 halves after scaling head n by 2^s_n so
 //    that its largest |element| lies in [2^12, 2^13): q_hi + q_lo then
 //    carries ~22 significant bits of every element, and sc folds 2^-s_n back.
+// The raw fp32 rows are loaded into QRaw ahead of the unit (load_q, no
+// arithmetic on the loaded values, so nothing waits for them there) and
+// turned into the operand when the unit starts (prepare_q).
+template <int D>
+struct QRaw {
+    f4 q[D / 16];
+};
+
 template <int D, typename KT>
 struct QRegs;
 
@@ -114,33 +123,26 @@ struct QRegs<D, _Float16> {
 };
 
 template <int D>
-__device__ __forceinline__ void load_q_f32(f4 (&q)[D / 16], const DecodeArgs& a, int qi, int kvh, int G, int n,
-                                           int g) {
-    const bool live = n < G;
-    const float* qrow = a.q + ((int64_t)qi * a.n_heads + kvh * G + (live ? n : 0)) * D;
+__device__ __forceinline__ void load_q(QRaw<D>& qr, const DecodeArgs& a, int qi, int kvh, int G, int n, int g) {
+    const float* qrow = a.q + ((int64_t)qi * a.n_heads + kvh * G + (n < G ? n : 0)) * D;
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
-        const f4 x = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
-        q[j] = live ? x : f4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int j = 0; j < D / 16; ++j) qr.q[j] = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
 }
 
 template <int D>
-__device__ __forceinline__ void load_q(QRegs<D, float>& qr, const DecodeArgs& a, int qi, int kvh, int G, int n,
-                                       int g) {
-    load_q_f32<D>(qr.q, a, qi, kvh, G, n, g);
+__device__ __forceinline__ void prepare_q(QRegs<D, float>& qr, const QRaw<D>& raw, const DecodeArgs& a) {
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) qr.q[j] = raw.q[j];
     qr.sc = a.scale_log2;
 }
 
 template <int D>
-__device__ __forceinline__ void load_q(QRegs<D, _Float16>& qr, const DecodeArgs& a, int qi, int kvh, int G, int n,
-                                       int g) {
-    f4 q[D / 16];
-    load_q_f32<D>(q, a, qi, kvh, G, n, g);
+__device__ __forceinline__ void prepare_q(QRegs<D, _Float16>& qr, const QRaw<D>& raw, const DecodeArgs& a) {
     float mx = 0.f;
 #pragma unroll
     for (int j = 0; j < D / 16; ++j)
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(q[j][0]), fabsf(q[j][1])), fmaxf(fabsf(q[j][2]), fabsf(q[j][3]))));
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(raw.q[j][0]), fabsf(raw.q[j][1])),
+                             fmaxf(fabsf(raw.q[j][2]), fabsf(raw.q[j][3]))));
     mx = fmaxf(mx, __shfl_xor(mx, 16));  // head n's elements live in lanes n + 16g
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     int ex = 0;
@@ -150,7 +152,7 @@ __device__ __forceinline__ void load_q(QRegs<D, _Float16>& qr, const DecodeArgs&
     const float up = ldexpf(1.0f, sh);
 #pragma unroll
     for (int j = 0; j < D / 16; ++j) {
-        const f4 x = q[j] * up;
+        const f4 x = raw.q[j] * up;
         const h4 hi = __builtin_convertvector(x, h4);
         qr.hi[j] = hi;
         qr.lo[j] = __builtin_convertvector(x - __builtin_convertvector(hi, f4), h4);
@@ -311,9 +313,19 @@ __device__ __forceinline__ void load_first_page(PageRegs<D, KT>& pr, const Decod
 }
 
 // One workgroup per bin: unit blockIdx.x, then units [bin_rest[b], bin_rest[b + 1]),
-// back to back.  Before a unit's epilogue (wave merge, partial publish, split
-// merge) the next unit's Q and first pages are already requested, so the
-// CU's load stream keeps going across unit boundaries.
+// back to back.  Before a unit's epilogue (wave merge, output or partial) the
+// next unit's Q and first pages are already requested, so the CU's load
+// stream keeps going across unit boundaries.
+//
+// A split piece's partial is published without waiting for it.  The split
+// counter protocol then runs at points where waiting is free: at the end of
+// the next unit's page loop every wave has no load outstanding, so its wait
+// for the partial's stores costs nothing; after the epilogue's barrier (all
+// waves' stores complete) lane 0 bumps the pair's counter, behind the next
+// unit's prefetch.  The counter's answer is read at the end of the following
+// page loop, again with nothing else in flight, and the last split of a pair
+// merges it in that unit's epilogue.  A workgroup's last one or two pieces settle after its
+// final unit.
 template <int D, typename KT>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(DecodeArgs a) {
     __shared__ EpilogueLds<D, kMaxGroupMfma> sh;
@@ -326,23 +338,29 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
     const int g = lane >> 4;
     const int first = blockIdx.x;
 
-    QRegs<D, KT> q;
+    QRaw<D> qraw;
     PageRegs<D, KT> ra, rb;
     {
         const DecodeUnit u0 = read_unit(a, first);
         const int blk0 = first_block(a, first, wave);
-        load_q<D>(q, a, u0.qi, u0.kvh, G, n, g);
+        load_q<D>(qraw, a, u0.qi, u0.kvh, G, n, g);
         load_first_page<D, KT>(ra, a, u0, blk0, wave, n, g);
     }
     const int rb0 = ld_meta(a.bin_rest + first);
     const int re = ld_meta(a.bin_rest + first + 1);
     bool rb_ready = false;  // rb already holds page p + kDecodeWaves (prefetched across a boundary)
 
+    int pub = -1;      // split unit whose partial is stored but not yet counted
+    int cnt = -1;      // split unit whose count is in flight (answer in `counted`, lane 0 of wave 0)
+    int counted = 0;
+
     // The unit record is re-read from memory in every iteration (wave-uniform
     // address), never carried across iterations, so every field stays scalar.
     for (int k = rb0 - 1; k < re; ++k) {
         const int ui = k < rb0 ? first : k;
         const DecodeUnit u = read_unit(a, ui);
+        QRegs<D, KT> q;
+        prepare_q<D>(q, qraw, a);
         const bool has_next = k + 1 < re;
         // The next record and its first two page ids are fetched now; their
         // latency hides behind this unit.
@@ -384,12 +402,18 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
             p = pnn;
         }
 
+        // No page load is outstanding here, so these waits are free: the
+        // count in flight comes back (read by every lane, so that on every
+        // path it is done here), and this wave's stores of `pub` complete.
+        const int prev = __builtin_amdgcn_readfirstlane(counted);
+        if (pub >= 0) wait_vm_complete();
+
         // Both page buffers and q are free now: request the next unit's Q and
         // first two pages of this wave, so the epilogue runs with two pages
         // per wave in flight.
         rb_ready = false;
         if (has_next) {
-            load_q<D>(q, a, un.qi, un.kvh, G, n, g);
+            load_q<D>(qraw, a, un.qi, un.kvh, G, n, g);
             load_first_page<D, KT>(ra, a, un, blkn, wave, n, g);
             if (has_n2) {
                 const int64_t off = a.layer_offset + (int64_t)un.kvh * a.head_stride + (int64_t)blkn2 * a.block_stride;
@@ -416,9 +440,33 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
                     for (int i = 0; i < 4; ++i) sh.o[wave][h][64 * c + 4 * n + i] = st.o[4 * c + i][r];
             }
         }
+        if (cnt >= 0 && tid == 0) sh.last = prev == (read_unit(a, cnt).split_info >> 16) - 1;
         __syncthreads();
-        finish_unit<D, kMaxGroupMfma>(a, u, G, sh);
+        // Every wave has waited for its part of `pub`'s partial: count it.
+        // The answer is read at the end of the next page loop.
+        if (pub >= 0 && tid == 0) counted = count_split(a, read_unit(a, pub));
+        const bool merge_cnt = cnt >= 0 && sh.last;
+        publish_unit<D, kMaxGroupMfma>(a, u, G, sh);
+        if (merge_cnt) merge_pair<D>(a, read_unit(a, cnt), G);
+        cnt = pub;
+        pub = (u.split_info >> 16) > 1 ? ui : -1;
         __syncthreads();  // the epilogue LDS is reused by the next unit
+    }
+
+    // Settle the last pieces: `cnt` has a count in flight, `pub` none yet.
+    if (cnt >= 0 || pub >= 0) {
+        const int prev = __builtin_amdgcn_readfirstlane(counted);
+        wait_vm_complete();
+        __syncthreads();
+        int prev_pub = 0;
+        if (pub >= 0 && tid == 0) prev_pub = count_split(a, read_unit(a, pub));
+        if (tid == 0) {
+            sh.last = cnt >= 0 && prev == (read_unit(a, cnt).split_info >> 16) - 1;
+            sh.last_pub = pub >= 0 && prev_pub == (read_unit(a, pub).split_info >> 16) - 1;
+        }
+        __syncthreads();
+        if (sh.last) merge_pair<D>(a, read_unit(a, cnt), G);
+        if (sh.last_pub) merge_pair<D>(a, read_unit(a, pub), G);
     }
 }
 

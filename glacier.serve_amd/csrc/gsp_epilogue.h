@@ -36,22 +36,27 @@ struct EpilogueLds {
     float o[kDecodeWaves][GMAX][D];
     float m[kDecodeWaves][GMAX];
     float l[kDecodeWaves][GMAX];
-    int last;
+    int last;      // the pair counted last is complete: merge it
+    int last_pub;  // the same, for a second pair settled after a workgroup's final unit
 };
 
 // Splits merged per round trip by the last split of a pair.
 constexpr int kMergeChunk = 8;
 
+// Merges the four waves' states (LDS) of unit u and writes the result: the
+// normalised output of an unsplit unit, or the (max, sum, unnormalised out)
+// partial of a split piece, stored coherently.  Nothing here waits for the
+// stores; the caller orders them before the pair's counter is bumped.
 template <int D, int GMAX>
-__device__ __forceinline__ void finish_unit(const DecodeArgs& a, const DecodeUnit& u, int G,
-                                            EpilogueLds<D, GMAX>& sh) {
+__device__ __forceinline__ void publish_unit(const DecodeArgs& a, const DecodeUnit& u, int G,
+                                             EpilogueLds<D, GMAX>& sh) {
     const int tid = threadIdx.x;
     const int h0 = u.kvh * G;
     const int split = u.split_info & 0xFFFF;
     const int nsplit = u.split_info >> 16;
     const int64_t pair = (int64_t)u.slot;  // first partial slot of the pair (-1: unsplit)
 
-    // Merge the four waves; a wave without pages has m = -inf and weighs 0.
+    // A wave without pages has m = -inf and weighs 0.
     for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
         const int g = idx / D;
         const int e = idx - g * D;
@@ -77,22 +82,29 @@ __device__ __forceinline__ void finish_unit(const DecodeArgs& a, const DecodeUni
             }
         }
     }
-    if (nsplit == 1) return;
+}
 
-    wait_vm_complete();
-    __syncthreads();
-    if (tid == 0) {
-        int* ctr = a.counters + (int64_t)u.qi * a.n_kv + u.kvh;
-        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sh.last = (prev == nsplit - 1);
-    }
-    __syncthreads();
-    if (!sh.last) return;
+__device__ __forceinline__ int* pair_counter(const DecodeArgs& a, const DecodeUnit& u) {
+    return a.counters + (int64_t)u.qi * a.n_kv + u.kvh;
+}
 
-    // Last split of the pair: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
-    // Each thread loads the (m, l) and O of up to kMergeChunk splits at once
-    // (one round trip for pairs cut into at most that many pieces) and folds
-    // chunks together with a running max, as the online softmax does.
+// Counts one finished split of u's pair; returns the count before it.  The
+// split's partial must be complete (stored and waited for by every wave).
+__device__ __forceinline__ int count_split(const DecodeArgs& a, const DecodeUnit& u) {
+    return __hip_atomic_fetch_add(pair_counter(a, u), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The last split of u's pair to finish: out = sum_s 2^(m_s - M) O_s / sum_s
+// 2^(m_s - M) l_s over all partials of the pair, then the counter goes back
+// to zero.  Each thread loads the (m, l) and O of up to kMergeChunk splits at
+// once (one round trip for pairs cut into at most that many pieces) and folds
+// chunks together with a running max, as the online softmax does.
+template <int D>
+__device__ __forceinline__ void merge_pair(const DecodeArgs& a, const DecodeUnit& u, int G) {
+    const int tid = threadIdx.x;
+    const int h0 = u.kvh * G;
+    const int nsplit = u.split_info >> 16;
+    const int64_t pair = (int64_t)u.slot;
     const int64_t stride = (int64_t)G * D;
     for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
         const int g = idx / D;
@@ -127,10 +139,22 @@ __device__ __forceinline__ void finish_unit(const DecodeArgs& a, const DecodeUni
         }
         a.out[((int64_t)u.qi * a.n_heads + h0 + g) * D + e] = O / L;
     }
-    if (tid == 0) {
-        __hip_atomic_store(a.counters + (int64_t)u.qi * a.n_kv + u.kvh, 0, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (tid == 0) __hip_atomic_store(pair_counter(a, u), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// publish_unit, then for a split piece the counter protocol on the spot:
+// wait for the partial, count it, and merge the pair if it was the last one.
+template <int D, int GMAX>
+__device__ __forceinline__ void finish_unit(const DecodeArgs& a, const DecodeUnit& u, int G,
+                                            EpilogueLds<D, GMAX>& sh) {
+    publish_unit<D, GMAX>(a, u, G, sh);
+    const int nsplit = u.split_info >> 16;
+    if (nsplit == 1) return;
+    wait_vm_complete();
+    __syncthreads();
+    if (threadIdx.x == 0) sh.last = (count_split(a, u) == nsplit - 1);
+    __syncthreads();
+    if (sh.last) merge_pair<D>(a, u, G);
 }
 
 }  // namespace gsp
