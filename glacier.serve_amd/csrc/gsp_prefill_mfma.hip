@@ -20,13 +20,15 @@
 //   - Q: per query token (the lane's S column), at load;
 //   - fp32 K, V pages: per key row, while the page is staged into LDS;
 //     fp16 pages are exact in fp16 and enter as they are (x_lo = 0);
-//   - P in [0, 1]: times 2^12, so that p_lo stays a normal fp16 number
-//     (the matrix cores flush fp16 subnormals; an unscaled p_lo of a typical
-//     probability would be one, and P would keep only 11 bits).
+//   - P: times 2^12, so that p_lo stays a normal fp16 number (the matrix
+//     cores flush fp16 subnormals; an unscaled p_lo of a typical probability
+//     would be one, and P would keep only 11 bits).  P = 2^(s - m) is taken
+//     against a max m that lags the running max by at most 2^3 (the O
+//     rescale is skipped until a row grows further), so P' < 2^15.
 // S = K_hi.Q_hi + K_hi.Q_lo + K_lo.Q_hi (the K_lo.Q_lo term is ~2^-22
 // relative), times 2^(e_key + e_token) * scale.  The V scales fold into P:
 // the accumulator O is kept in units of 2^(eO - 12), eO the largest V
-// exponent seen so far, so P' = P * 2^(e_v(key) - eO + 12) <= 2^12, and O is
+// exponent seen so far, so P' = P * 2^(e_v(key) - eO + 12) < 2^15, and O is
 // rescaled (like the softmax's alpha) when a page raises eO.  Precision bound
 // of that fold: a key whose V row is more than ~2^14 smaller than the row's
 // largest V row gets a subnormal P' and keeps fewer bits (none beyond ~2^26);
@@ -80,10 +82,12 @@ __device__ __forceinline__ float max_abs4(const f4& x) {
     return fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
 }
 
-// Page staging: each of the 256 threads moves (16 * D / 4) / 256 four-element
-// chunks of K and of V; chunk c is key c / (D/4), elements 4 * (c % (D/4)).
+// Page staging: key row tid / 16 is moved by the 16 lanes of one DPP row;
+// lane part = tid % 16 moves the D / 64 four-element chunks at columns
+// 64 j + 4 part (each load instruction reads 256 contiguous bytes per row).
 template <int D>
-constexpr int kStageChunks = (kBlockSize * D / 4) / kDecodeThreads;
+constexpr int kStageChunks = D / 64;
+static_assert(kBlockSize * 16 == kDecodeThreads, "one 16-lane row per key of the page");
 
 template <int D, typename KT>
 struct PfStage;
@@ -110,6 +114,7 @@ struct alignas(16) PfLds<D, float> {
     _Float16 kh[2][kBlockSize * kRow], kl[2][kBlockSize * kRow];
     _Float16 vh[2][kBlockSize * kRow], vl[2][kBlockSize * kRow];
     int ek[2][kBlockSize], ev[2][kBlockSize];  // per-key exponents of the K and V pairs
+    int evw[2][kDecodeWaves];                   // largest V exponent of each wave's four keys
 };
 
 template <int D>
@@ -119,6 +124,12 @@ struct alignas(16) PfLds<D, _Float16> {
     _Float16 v[2][kBlockSize * kRow];
 };
 
+// Element offset of lane tid's chunk j in a page (key row tid / 16).
+template <int D>
+__device__ __forceinline__ int stage_offset(int j) {
+    return (threadIdx.x >> 4) * D + 64 * j + 4 * (threadIdx.x & 15);
+}
+
 template <int D>
 __device__ __forceinline__ void stage_load(PfStage<D, float>& sr, const float* kpage, const float* vpage, int ntok) {
     const int bytes = ntok * D * 4;
@@ -126,9 +137,9 @@ __device__ __forceinline__ void stage_load(PfStage<D, float>& sr, const float* k
     const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(vpage, bytes);
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
-        const int c = threadIdx.x + i * kDecodeThreads;
-        sr.k[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rk, 16 * c, 0, 0));
-        sr.v[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rv, 16 * c, 0, 0));
+        const int off = 4 * stage_offset<D>(i);
+        sr.k[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+        sr.v[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
     }
 }
 
@@ -140,55 +151,81 @@ __device__ __forceinline__ void stage_load(PfStage<D, _Float16>& sr, const _Floa
     const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(vpage, bytes);
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
-        const int c = threadIdx.x + i * kDecodeThreads;
-        sr.k[i] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rk, 8 * c, 0, 0));
-        sr.v[i] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rv, 8 * c, 0, 0));
+        const int off = 2 * stage_offset<D>(i);
+        sr.k[i] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rk, off, 0, 0));
+        sr.v[i] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0));
     }
 }
 
-// Max of |x| over the D/4 threads of one key row: they are D/4 consecutive
-// lanes of one wave (32 for d = 128, 16 for d = 64), aligned to D/4.
-template <int D>
-__device__ __forceinline__ float key_row_max(float x) {
-#pragma unroll
-    for (int s = 1; s < D / 4; s <<= 1) x = fmaxf(x, __shfl_xor(x, s));
-    return x;
+// DPP lane moves within a row of 16 lanes (bound_ctrl off: every source lane is in the row).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+
+// Max over the 16 lanes of the caller's DPP row (one key row of the page):
+// lane swaps within quads, then rotations by 4 and 8.
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_mov<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+    x = fmaxf(x, dpp_mov<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+    x = fmaxf(x, dpp_mov<0x124>(x));  // row_ror:4
+    return fmaxf(x, dpp_mov<0x128>(x));  // row_ror:8
+}
+
+// Max of x over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four rows of a wave),
+// with the row swaps of gfx950: max of the swapped pair is the max across the
+// exchanged rows.
+__device__ __forceinline__ float cross_row_max(float x) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
 template <int D>
 __device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D, float>& sh, int buf) {
     constexpr int kRow = PfLds<D, float>::kRow;
+    const int key = threadIdx.x >> 4;
+    const int part = threadIdx.x & 15;
+    float mk = 0.f, mv = 0.f;
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
-        const int c = threadIdx.x + i * kDecodeThreads;
-        const int key = c / (D / 4);
-        const int col = 4 * (c % (D / 4));
-        const int ek = pair_exponent(key_row_max<D>(max_abs4(sr.k[i])));
-        const int ev = pair_exponent(key_row_max<D>(max_abs4(sr.v[i])));
-        h4 hi, lo;
-        split_pair(sr.k[i] * ldexpf(1.0f, -ek), hi, lo);
-        *reinterpret_cast<h4*>(&sh.kh[buf][key * kRow + col]) = hi;
-        *reinterpret_cast<h4*>(&sh.kl[buf][key * kRow + col]) = lo;
-        split_pair(sr.v[i] * ldexpf(1.0f, -ev), hi, lo);
-        *reinterpret_cast<h4*>(&sh.vh[buf][key * kRow + col]) = hi;
-        *reinterpret_cast<h4*>(&sh.vl[buf][key * kRow + col]) = lo;
-        if (col == 0) {
-            sh.ek[buf][key] = ek;
-            sh.ev[buf][key] = ev;
-        }
+        mk = fmaxf(mk, max_abs4(sr.k[i]));
+        mv = fmaxf(mv, max_abs4(sr.v[i]));
     }
+    const int ek = pair_exponent(row16_max(mk));
+    const int ev = pair_exponent(row16_max(mv));
+    const float dk = ldexpf(1.0f, -ek), dv = ldexpf(1.0f, -ev);
+#pragma unroll
+    for (int i = 0; i < kStageChunks<D>; ++i) {
+        const int at = key * kRow + 64 * i + 4 * part;
+        h4 hi, lo;
+        split_pair(sr.k[i] * dk, hi, lo);
+        *reinterpret_cast<h4*>(&sh.kh[buf][at]) = hi;
+        *reinterpret_cast<h4*>(&sh.kl[buf][at]) = lo;
+        split_pair(sr.v[i] * dv, hi, lo);
+        *reinterpret_cast<h4*>(&sh.vh[buf][at]) = hi;
+        *reinterpret_cast<h4*>(&sh.vl[buf][at]) = lo;
+    }
+    if (part == 0) {
+        sh.ek[buf][key] = ek;
+        sh.ev[buf][key] = ev;
+    }
+    // The page's largest V exponent: this wave's four keys, then one slot per wave.
+    const float evw = cross_row_max((float)ev);
+    if ((threadIdx.x & 63) == 0) sh.evw[buf][threadIdx.x >> 6] = (int)evw;
 }
 
 template <int D>
 __device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLds<D, _Float16>& sh, int buf) {
     constexpr int kRow = PfLds<D, _Float16>::kRow;
+    const int key = threadIdx.x >> 4;
+    const int part = threadIdx.x & 15;
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
-        const int c = threadIdx.x + i * kDecodeThreads;
-        const int key = c / (D / 4);
-        const int col = 4 * (c % (D / 4));
-        *reinterpret_cast<h4*>(&sh.k[buf][key * kRow + col]) = sr.k[i];
-        *reinterpret_cast<h4*>(&sh.v[buf][key * kRow + col]) = sr.v[i];
+        const int at = key * kRow + 64 * i + 4 * part;
+        *reinterpret_cast<h4*>(&sh.k[buf][at]) = sr.k[i];
+        *reinterpret_cast<h4*>(&sh.v[buf][at]) = sr.v[i];
     }
 }
 
@@ -220,8 +257,9 @@ __device__ __forceinline__ void load_tile_q(TileQ<D>& tq, const float* qrow, boo
     tq.sc = ldexpf(scale, e);
 }
 
-// Per-tile softmax state: O in units of 2^eo, running max m (log2 units) of
-// token n, partial sum l of token n over this lane's keys.
+// Per-tile softmax state: O in units of 2^eo, the max m (log2 units) that
+// token n's probabilities are taken against, partial sum l of token n over
+// this lane's keys.
 template <int D>
 struct TileState {
     f4 o[D / 16];
@@ -230,9 +268,16 @@ struct TileState {
     int eo;
 };
 
+// A row's running max may grow this much (log2 units) before O and l are
+// rescaled: until then P = 2^(s - m) stays below 2^kLazyLog2, and P' (P times
+// at most 2^kPScaleLog2, see below) below 2^15, inside fp16's range.
+constexpr float kLazyLog2 = 3.0f;
+
 // Causal mask and online softmax of one page's scores; returns P, and in
 // `alpha_rows` the factors that the lane's O rows (tokens 4g + r) must take,
-// fetched from the lanes that own those tokens (`rescale` false: all 1).
+// fetched from the lanes that own those tokens (`rescale` false: all 1).  m
+// only moves when some row of the tile has grown by more than kLazyLog2, which
+// after the first pages is rare, so most pages skip the O rescale.
 template <int D>
 __device__ __forceinline__ f4 page_softmax(TileState<D>& st, f4 s, bool diag, int key0, int row_ctx, int g,
                                            f4& alpha_rows, bool& rescale) {
@@ -241,21 +286,21 @@ __device__ __forceinline__ f4 page_softmax(TileState<D>& st, f4 s, bool diag, in
         for (int r = 0; r < 4; ++r)
             if (key0 + r >= row_ctx) s[r] = -INFINITY;
     }
-    float mp = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    mp = fmaxf(mp, __shfl_xor(mp, 16));
-    mp = fmaxf(mp, __shfl_xor(mp, 32));
-    const float mn = fmaxf(st.m, mp);  // finite: page 0 holds key 0 for every row
-    const float alpha = fast_exp2(st.m - mn);
-    st.m = mn;
-    f4 p;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(s[r] - mn);
-    st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    rescale = __any(alpha != 1.0f);
+    // Token n's page max: its keys live in lanes n + 16g.
+    const float mp = cross_row_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+    rescale = __any(mp > st.m + kLazyLog2);  // true on the first page (m = -inf)
     if (rescale) {
+        const float mn = fmaxf(st.m, mp);  // finite: page 0 holds key 0 for every row
+        const float alpha = fast_exp2(st.m - mn);
+        st.m = mn;
+        st.l *= alpha;
 #pragma unroll
         for (int r = 0; r < 4; ++r) alpha_rows[r] = __shfl(alpha, 4 * g + r);
     }
+    f4 p;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(s[r] - st.m);
+    st.l += (p[0] + p[1]) + (p[2] + p[3]);
     return p;
 }
 
@@ -326,34 +371,52 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
                 kscale[r] = ldexpf(1.0f, sh.ek[buf][4 * g + r]);
                 evk[r] = sh.ev[buf][4 * g + r];
             }
-            evmax = sh.ev[buf][0];
+            evmax = sh.evw[buf][0];
 #pragma unroll
-            for (int k = 1; k < kBlockSize; ++k) evmax = max(evmax, sh.ev[buf][k]);
+            for (int w = 1; w < kDecodeWaves; ++w) evmax = max(evmax, sh.evw[buf][w]);
         }
 
+        // The wave's tiles share the page, so each K operand read from LDS and
+        // each V operand assembled below serves all of them.
+        bool live[kPrefillTiles];
 #pragma unroll
-        for (int s = 0; s < kPrefillTiles; ++s) {
-            if (wave + 4 * s >= G) continue;  // uniform per wave
-            TileState<D>& ts = st[s];
-            // S^T = K . Q^T (hi/lo products; two accumulation chains).  The K
-            // operands come from LDS per tile (re-read by the wave's second tile).
-            f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < kPrefillTiles; ++s) live[s] = wave + 4 * s < G;  // uniform per wave
+
+        // S^T = K . Q^T (hi/lo products; two accumulation chains per tile).
+        f4 s0[kPrefillTiles], s1[kPrefillTiles];
 #pragma unroll
-            for (int j = 0; j < D / 16; ++j) {
-                const int at = n * kRow + 16 * j + 4 * g;
-                if constexpr (kSplitKV) {
-                    const h4 kh = *reinterpret_cast<const h4*>(&sh.kh[buf][at]);
-                    const h4 kl = *reinterpret_cast<const h4*>(&sh.kl[buf][at]);
-                    s0 = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].hi[j], s0, 0, 0, 0);
-                    s1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].lo[j], s1, 0, 0, 0);
-                    s1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, q[s].hi[j], s1, 0, 0, 0);
-                } else {
-                    const h4 kx = *reinterpret_cast<const h4*>(&sh.k[buf][at]);
-                    s0 = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].hi[j], s0, 0, 0, 0);
-                    s1 = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].lo[j], s1, 0, 0, 0);
+        for (int s = 0; s < kPrefillTiles; ++s) s0[s] = s1[s] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) {
+            const int at = n * kRow + 16 * j + 4 * g;
+            if constexpr (kSplitKV) {
+                const h4 kh = *reinterpret_cast<const h4*>(&sh.kh[buf][at]);
+                const h4 kl = *reinterpret_cast<const h4*>(&sh.kl[buf][at]);
+#pragma unroll
+                for (int s = 0; s < kPrefillTiles; ++s) {
+                    if (!live[s]) continue;
+                    s0[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].hi[j], s0[s], 0, 0, 0);
+                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].lo[j], s1[s], 0, 0, 0);
+                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, q[s].hi[j], s1[s], 0, 0, 0);
+                }
+            } else {
+                const h4 kx = *reinterpret_cast<const h4*>(&sh.k[buf][at]);
+#pragma unroll
+                for (int s = 0; s < kPrefillTiles; ++s) {
+                    if (!live[s]) continue;
+                    s0[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].hi[j], s0[s], 0, 0, 0);
+                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].lo[j], s1[s], 0, 0, 0);
                 }
             }
-            f4 sc = (s0 + s1) * q[s].sc;  // lane: S[token n][keys key0 .. key0 + 3], log2 units
+        }
+
+        // Softmax of each tile, and its P' as an fp16 pair.
+        h4 ph[kPrefillTiles], pl[kPrefillTiles];
+#pragma unroll
+        for (int s = 0; s < kPrefillTiles; ++s) {
+            if (!live[s]) continue;
+            TileState<D>& ts = st[s];
+            f4 sc = (s0[s] + s1[s]) * q[s].sc;  // lane: S[token n][keys key0 .. key0 + 3], log2 units
             if constexpr (kSplitKV) sc *= kscale;
 
             f4 alpha_rows = {1.f, 1.f, 1.f, 1.f};
@@ -377,34 +440,37 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
 #pragma unroll
                 for (int b = 0; b < D / 16; ++b) ts.o[b] *= alpha_rows;
             }
-            h4 ph, pl;
-            split_pair(pr, ph, pl);
-            // O += P' . V: output block 4c + i takes B = V[keys 4g + kk][64c + 4n + i],
-            // element i of the lane's four V pieces of keys 4g .. 4g + 3.
+            split_pair(pr, ph[s], pl[s]);
+        }
+
+        // O += P' . V: output block 4c + i takes B = V[keys 4g + kk][64c + 4n + i],
+        // element i of the lane's four V pieces of keys 4g .. 4g + 3.
 #pragma unroll
-            for (int c = 0; c < D / 64; ++c) {
-                h4 vh[4], vl[4];
+        for (int c = 0; c < D / 64; ++c) {
+            h4 vh[4], vl[4];
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk) {
-                    const int at = (4 * g + kk) * kRow + 64 * c + 4 * n;
-                    if constexpr (kSplitKV) {
-                        vh[kk] = *reinterpret_cast<const h4*>(&sh.vh[buf][at]);
-                        vl[kk] = *reinterpret_cast<const h4*>(&sh.vl[buf][at]);
-                    } else {
-                        vh[kk] = *reinterpret_cast<const h4*>(&sh.v[buf][at]);
-                    }
+            for (int kk = 0; kk < 4; ++kk) {
+                const int at = (4 * g + kk) * kRow + 64 * c + 4 * n;
+                if constexpr (kSplitKV) {
+                    vh[kk] = *reinterpret_cast<const h4*>(&sh.vh[buf][at]);
+                    vl[kk] = *reinterpret_cast<const h4*>(&sh.vl[buf][at]);
+                } else {
+                    vh[kk] = *reinterpret_cast<const h4*>(&sh.v[buf][at]);
                 }
+            }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const h4 bh = {vh[0][i], vh[1][i], vh[2][i], vh[3][i]};
-                    f4 acc = ts.o[4 * c + i];
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bh, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, bh, acc, 0, 0, 0);
-                    if constexpr (kSplitKV) {
-                        const h4 bl = {vl[0][i], vl[1][i], vl[2][i], vl[3][i]};
-                        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, bl, acc, 0, 0, 0);
-                    }
-                    ts.o[4 * c + i] = acc;
+            for (int i = 0; i < 4; ++i) {
+                const h4 bh = {vh[0][i], vh[1][i], vh[2][i], vh[3][i]};
+                h4 bl;
+                if constexpr (kSplitKV) bl = h4{vl[0][i], vl[1][i], vl[2][i], vl[3][i]};
+#pragma unroll
+                for (int s = 0; s < kPrefillTiles; ++s) {
+                    if (!live[s]) continue;
+                    f4 acc = st[s].o[4 * c + i];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[s], bh, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[s], bh, acc, 0, 0, 0);
+                    if constexpr (kSplitKV) acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[s], bl, acc, 0, 0, 0);
+                    st[s].o[4 * c + i] = acc;
                 }
             }
         }
