@@ -85,7 +85,7 @@ struct PrefillArgs {
     float* out;            // [total_q][n_heads][head_dim]
     int32_t n_heads;
     int32_t n_kv;
-    int32_t group;         // query heads per KV head (any; grid.y covers them 8 at a time)
+    int32_t group;         // query heads per KV head (any; grid.y covers them 8, or for groups up to 4, 4 at a time)
     float scale_log2;
 };
 

@@ -6,7 +6,8 @@
 // PagedAttentionKernel.cs:41).  Its queries share every K/V page of the prefix,
 // so the work is a dense causal contraction; one workgroup owns a tile of 16
 // consecutive query tokens of one row and one KV head, for up to 8 query heads
-// of the GQA group (grid.y covers larger groups), and walks the row's pages in
+// of the GQA group (4 when the group has at most 4; grid.y covers larger
+// groups), and walks the row's pages in
 // order:
 //
 //   per page (16 keys, staged once in LDS and shared by the group's heads):
@@ -35,7 +36,7 @@
 // its absolute error stays below ~2^-25 of the largest |V| element.
 //
 // Row tile T of the workgroup is query head hc + T over the 16 tokens; wave w
-// owns tiles w and w + 4.  The MFMA operand layouts are the decode kernel's
+// owns tiles w and w + 4 (or tile w alone, for groups of at most 4).  The MFMA operand layouts are the decode kernel's
 // with "head" replaced by "query token" (lane l, n = l % 16, g = l / 16):
 //   QK A = K[key n][16j + 4g .. +3], B = Q[token n][16j + 4g .. +3]
 //   result: lane holds S[token n][key 4g + r]
@@ -53,7 +54,6 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPrefillTiles = kPrefillHeads / kDecodeWaves;  // row tiles (query heads) per wave
 constexpr int kPScaleLog2 = 12;  // P enters the matrix cores times 2^12 (p_lo stays normal)
 static_assert(kPrefillTileTokens == kBlockSize, "the tile's token and key dimensions are both 16");
 
@@ -304,15 +304,20 @@ __device__ __forceinline__ f4 page_softmax(TileState<D>& st, f4 s, bool diag, in
     return p;
 }
 
-template <int D, typename KT>
+// TILES query heads per wave (heads wave + 4 s, s < TILES): 2 for groups above
+// 4 heads, else 1.  Every tile of a wave is computed on every page, so the
+// hot loop has no branches; a tile past the group (zero Q) is simply not
+// stored.  It costs no time: the page barrier waits for the busiest wave.
+template <int D, typename KT, int TILES>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(PrefillArgs a) {
+    constexpr int kPrefillTiles = TILES;
     constexpr int kRow = PfLds<D, KT>::kRow;
     constexpr bool kSplitKV = sizeof(KT) == 4;  // fp32 pages enter as hi + lo pairs
     __shared__ PfLds<D, KT> sh;
 
     const PrefillTile t = a.tiles[blockIdx.x];
-    const int hc = blockIdx.y * kPrefillHeads;  // first head of this workgroup within the group
-    const int G = min(kPrefillHeads, a.group - hc);
+    const int hc = blockIdx.y * kDecodeWaves * TILES;  // first head of this workgroup within the group
+    const int G = min(kDecodeWaves * TILES, a.group - hc);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -378,9 +383,6 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
 
         // The wave's tiles share the page, so each K operand read from LDS and
         // each V operand assembled below serves all of them.
-        bool live[kPrefillTiles];
-#pragma unroll
-        for (int s = 0; s < kPrefillTiles; ++s) live[s] = wave + 4 * s < G;  // uniform per wave
 
         // S^T = K . Q^T (hi/lo products; two accumulation chains per tile).
         f4 s0[kPrefillTiles], s1[kPrefillTiles];
@@ -394,7 +396,6 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
                 const h4 kl = *reinterpret_cast<const h4*>(&sh.kl[buf][at]);
 #pragma unroll
                 for (int s = 0; s < kPrefillTiles; ++s) {
-                    if (!live[s]) continue;
                     s0[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].hi[j], s0[s], 0, 0, 0);
                     s1[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].lo[j], s1[s], 0, 0, 0);
                     s1[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, q[s].hi[j], s1[s], 0, 0, 0);
@@ -403,7 +404,6 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
                 const h4 kx = *reinterpret_cast<const h4*>(&sh.k[buf][at]);
 #pragma unroll
                 for (int s = 0; s < kPrefillTiles; ++s) {
-                    if (!live[s]) continue;
                     s0[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].hi[j], s0[s], 0, 0, 0);
                     s1[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].lo[j], s1[s], 0, 0, 0);
                 }
@@ -414,7 +414,6 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
         h4 ph[kPrefillTiles], pl[kPrefillTiles];
 #pragma unroll
         for (int s = 0; s < kPrefillTiles; ++s) {
-            if (!live[s]) continue;
             TileState<D>& ts = st[s];
             f4 sc = (s0[s] + s1[s]) * q[s].sc;  // lane: S[token n][keys key0 .. key0 + 3], log2 units
             if constexpr (kSplitKV) sc *= kscale;
@@ -465,7 +464,6 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
                 if constexpr (kSplitKV) bl = h4{vl[0][i], vl[1][i], vl[2][i], vl[3][i]};
 #pragma unroll
                 for (int s = 0; s < kPrefillTiles; ++s) {
-                    if (!live[s]) continue;
                     f4 acc = st[s].o[4 * c + i];
                     acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[s], bh, acc, 0, 0, 0);
                     acc = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[s], bh, acc, 0, 0, 0);
@@ -507,26 +505,29 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
     }
 }
 
+template <int D, typename KT>
+hipError_t launch_tiles(int num_tiles, const PrefillArgs& a, hipStream_t stream) {
+    const int tiles = a.group > kDecodeWaves ? 2 : 1;
+    const int per_wg = kDecodeWaves * tiles;
+    static_assert(kPrefillHeads == 2 * kDecodeWaves, "a workgroup covers at most kPrefillHeads heads");
+    const dim3 grid(num_tiles, (a.group + per_wg - 1) / per_wg);
+    if (tiles == 2)
+        hipLaunchKernelGGL((paged_prefill_mfma_kernel<D, KT, 2>), grid, dim3(kDecodeThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((paged_prefill_mfma_kernel<D, KT, 1>), grid, dim3(kDecodeThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_prefill_mfma(int head_dim, int kv_f16, int num_tiles, const PrefillArgs& a, hipStream_t stream) {
     if (num_tiles <= 0) return hipSuccess;
     if (a.group < 1) return hipErrorInvalidValue;
-    dim3 grid(num_tiles, (a.group + kPrefillHeads - 1) / kPrefillHeads);
-    if (head_dim == 128) {
-        if (kv_f16)
-            hipLaunchKernelGGL((paged_prefill_mfma_kernel<128, _Float16>), grid, dim3(kDecodeThreads), 0, stream, a);
-        else
-            hipLaunchKernelGGL((paged_prefill_mfma_kernel<128, float>), grid, dim3(kDecodeThreads), 0, stream, a);
-    } else if (head_dim == 64) {
-        if (kv_f16)
-            hipLaunchKernelGGL((paged_prefill_mfma_kernel<64, _Float16>), grid, dim3(kDecodeThreads), 0, stream, a);
-        else
-            hipLaunchKernelGGL((paged_prefill_mfma_kernel<64, float>), grid, dim3(kDecodeThreads), 0, stream, a);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    if (head_dim == 128) return kv_f16 ? launch_tiles<128, _Float16>(num_tiles, a, stream)
+                                       : launch_tiles<128, float>(num_tiles, a, stream);
+    if (head_dim == 64) return kv_f16 ? launch_tiles<64, _Float16>(num_tiles, a, stream)
+                                      : launch_tiles<64, float>(num_tiles, a, stream);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace gsp
