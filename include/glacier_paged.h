@@ -222,9 +222,11 @@ int gsp_step_download(gsp_ctx* ctx, int32_t* row_offsets, int32_t* ids, int32_t*
 int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages);
 
 /* Most decode workgroups for the next gsp_step_pack: 0 (default) uses two
- * per CU; > 0 forces the count (tuning and tests).  Units are packed into that
- * many bins longest first, and each workgroup runs its bin's units back to
- * back. */
+ * per CU, or one per two CUs when the step also has prefill tiles (those run
+ * beside the decode units, on a second stream forked from and joined back
+ * into the context's stream); > 0 forces the count (tuning and tests).  Units
+ * are packed into that many bins longest first, and each workgroup runs its
+ * bin's units back to back. */
 int gsp_set_decode_bins(gsp_ctx* ctx, int32_t bins);
 
 /* Decode kernel selection (tuning and tests): GSP_DECODE_AUTO picks the
@@ -258,7 +260,11 @@ int gsp_set_prefill_path(gsp_ctx* ctx, int32_t path);
  * out = sum p_t v_t (:73-370).  sink_logit must be NULL: attention sinks are
  * unsupported on the GPU path, as in CudaPagedTransformerRunner.cs:431.
  * Supported: head_dim == v_head_dim in {64, 128}; n_heads % heads_kv == 0 and
- * n_heads / heads_kv <= 16; block_size 16. */
+ * n_heads / heads_kv <= 16 (any group for a step of prefill tiles only);
+ * block_size 16.  Work is enqueued on the context's stream.  A step with both
+ * decode units and prefill tiles runs the tiles on a second stream of the
+ * context, forked from and joined back into that stream, so the call is still
+ * ordered as a whole on the context's stream (and can be captured). */
 int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t n_heads,
                        const float* q_dev, float* out_dev, float attn_scale,
                        const float* sink_logit);
