@@ -270,6 +270,7 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         "roofline": roofline,
     }
     result.update(extra)
+    result["host_prefix_cache"] = host_prefix_cache(gsp, step)
 
     if cpu:
         result["cpu_baseline"], ref = cpu_baseline(step, q, k, v, cpu_budget_s)
@@ -279,6 +280,33 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     pool.destroy()
     ctx.close()
     return result
+
+
+def host_prefix_cache(gsp, step) -> dict:
+    """Host cost of the prefix cache for this step's rows: the XXH3 hash chain
+    over every full 16-token block of every row (what admitting those prompts
+    costs, ContinuousBatchEngine.cs:223-263), and a cache lookup per block."""
+    import numpy as np
+
+    rng = np.random.default_rng(step.seed)
+    blocks = int(sum(int(t) // 16 for t in step.token_counts))
+    tokens = rng.integers(0, 150000, size=max(16, blocks * 16), dtype=np.int64).astype(np.int32)
+    alloc = gsp.BlockAllocator(max(1, blocks), 16)
+    gsp.prefix_hash_chain(0, tokens[:16])  # load and warm
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        hashes = gsp.prefix_hash_chain(0, tokens[:blocks * 16])  # one call per step's worth of blocks
+    t1 = time.perf_counter()
+    for h in hashes[:2000]:
+        alloc.try_find_prefix_block(int(h))
+    t2 = time.perf_counter()
+    alloc.close()
+    n = max(1, blocks)
+    return {"blocks": blocks, "hash_ns_per_block": round((t1 - t0) / (reps * n) * 1e9, 1),
+            "hash_gbs": round(reps * n * 64 / (t1 - t0) / 1e9, 2),
+            "find_us_per_call": round((t2 - t1) / max(1, min(2000, len(hashes))) * 1e6, 3),
+            "note": "one host thread; the chain is one C call, finds go through the Python binding per call"}
 
 
 def cpu_baseline(step, q, k, v, budget_s: float):

@@ -1,15 +1,19 @@
 // Host-side block metadata: the free-stack / refcount half of PagedBlockPool
-// (PagedBlockPool.cs:112-121,178-299,332-353) and BlockTable
+// (PagedBlockPool.cs:112-121,178-299,332-353), its prefix cache
+// (:163-234: the XXH3 hash chain over full blocks' token ids and the map from
+// a prefix hash to the block that holds it) and BlockTable
 // (BlockTable.cs:13-117).  Pages themselves live in a device pool; an attached
 // pool receives the copy-on-write page copies.
 #include <algorithm>
 #include <atomic>
 #include <memory>
 #include <mutex>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/glacier_paged.h"
 #include "gsp_status.h"
+#include "gsp_xxh3.h"
 
 struct gsp_block_allocator {
     int32_t total = 0;
@@ -18,6 +22,9 @@ struct gsp_block_allocator {
     std::vector<int32_t> free_stack;  // back() is the top of the LIFO stack
     std::unique_ptr<std::atomic<int32_t>[]> allocated;
     std::unique_ptr<std::atomic<int32_t>[]> refs;
+    std::unique_ptr<std::atomic<uint64_t>[]> hashes;  // prefix hash bound to each block (0: none)
+    std::mutex map_mu;
+    std::unordered_map<uint64_t, int32_t> prefix_map;  // prefix hash -> block
     gsp_ctx* ctx = nullptr;
     gsp_pool* pool = nullptr;
 
@@ -34,6 +41,7 @@ struct gsp_block_allocator {
         }
         allocated[b].store(1);
         refs[b].store(1);
+        hashes[b].store(0);
         *id = b;
         return true;
     }
@@ -46,6 +54,17 @@ struct gsp_block_allocator {
             return 0;
         }
         if (remaining == 0) {
+            // A freed block leaves the prefix cache, unless its hash has since
+            // been bound to another block (:263-271).
+            const uint64_t h = hashes[id].load();
+            if (h != 0) {
+                {
+                    std::lock_guard<std::mutex> lk(map_mu);
+                    const auto it = prefix_map.find(h);
+                    if (it != prefix_map.end() && it->second == id) prefix_map.erase(it);
+                }
+                hashes[id].store(0);
+            }
             int32_t expected = 1;
             if (allocated[id].compare_exchange_strong(expected, 0)) {
                 std::lock_guard<std::mutex> lk(stack_mu);
@@ -75,11 +94,13 @@ int gsp_block_allocator_create(int32_t total_blocks, int32_t block_size, gsp_blo
     a->block_size = block_size;
     a->allocated.reset(new std::atomic<int32_t>[total_blocks]);
     a->refs.reset(new std::atomic<int32_t>[total_blocks]);
+    a->hashes.reset(new std::atomic<uint64_t>[total_blocks]);
     a->free_stack.reserve(total_blocks);
     // Pushing total-1 .. 0 leaves 0 on top: the first pop returns block 0.
     for (int32_t i = total_blocks - 1; i >= 0; --i) {
         a->allocated[i].store(0);
         a->refs[i].store(0);
+        a->hashes[i].store(0);
         a->free_stack.push_back(i);
     }
     *out = a;
@@ -135,6 +156,68 @@ int gsp_block_allocator_free_count(const gsp_block_allocator* a) {
 }
 
 int gsp_block_allocator_total(const gsp_block_allocator* a) { return a ? a->total : 0; }
+
+uint64_t gsp_prefix_hash(uint64_t parent_hash, const int32_t* tokens, int32_t n) {
+    gsp::clear_error();
+    if (n < 0 || (n > 0 && !tokens)) {
+        gsp::fail(GSP_E_INVALID_ARG, "token span is invalid");
+        return 0;
+    }
+    // The token ids' bytes as stored (little-endian int32), seeded with the parent.
+    return gsp::xxh3::hash64(tokens, (size_t)n * sizeof(int32_t), parent_hash);
+}
+
+int gsp_prefix_hash_chain(uint64_t parent_hash, const int32_t* tokens, int32_t n_blocks, int32_t block_size,
+                          uint64_t* out) {
+    gsp::clear_error();
+    if (n_blocks < 0 || block_size < 1 || (n_blocks > 0 && (!tokens || !out)))
+        return gsp::fail(GSP_E_INVALID_ARG, "token blocks or output are invalid");
+    uint64_t h = parent_hash;
+    for (int32_t b = 0; b < n_blocks; ++b) {
+        h = gsp::xxh3::hash64(tokens + (int64_t)b * block_size, (size_t)block_size * sizeof(int32_t), h);
+        out[b] = h;
+    }
+    return GSP_OK;
+}
+
+int gsp_block_allocator_find_prefix(gsp_block_allocator* a, uint64_t prefix_hash, int32_t* block_id) {
+    gsp::clear_error();
+    if (!a || !block_id) return gsp::fail(GSP_E_INVALID_ARG, "allocator/block_id is NULL"), 0;
+    *block_id = -1;
+    if (prefix_hash == 0) return 0;
+    int32_t b;
+    {
+        std::lock_guard<std::mutex> lk(a->map_mu);
+        const auto it = a->prefix_map.find(prefix_hash);
+        if (it == a->prefix_map.end()) return 0;
+        b = it->second;
+    }
+    // Take a reference only while the block is live, then check that it still
+    // holds this prefix (it may have been freed and reused meanwhile).
+    int32_t cur = a->refs[b].load();
+    while (true) {
+        if (cur <= 0) return 0;
+        if (a->refs[b].compare_exchange_weak(cur, cur + 1)) break;
+    }
+    if (a->hashes[b].load() != prefix_hash) {
+        a->release(b);
+        return 0;
+    }
+    *block_id = b;
+    return 1;
+}
+
+int gsp_block_allocator_bind_prefix(gsp_block_allocator* a, uint64_t prefix_hash, int32_t block_id) {
+    gsp::clear_error();
+    if (!a) return gsp::fail(GSP_E_INVALID_ARG, "allocator is NULL");
+    if (block_id < 0 || block_id >= a->total)
+        return gsp::fail(GSP_E_INVALID_ARG, "physicalBlockId %d out of range [0, %d)", block_id, a->total);
+    if (prefix_hash == 0) return gsp::fail(GSP_E_INVALID_ARG, "Prefix hash cannot be 0.");
+    a->hashes[block_id].store(prefix_hash);
+    std::lock_guard<std::mutex> lk(a->map_mu);
+    a->prefix_map[prefix_hash] = block_id;
+    return GSP_OK;
+}
 
 int gsp_block_table_create(gsp_block_allocator* a, gsp_block_table** out) {
     gsp::clear_error();

@@ -191,6 +191,10 @@ _SIGNATURES = {
     "gsp_block_allocator_ref_count": (ctypes.c_int, [vp, i32]),
     "gsp_block_allocator_free_count": (ctypes.c_int, [vp]),
     "gsp_block_allocator_total": (ctypes.c_int, [vp]),
+    "gsp_prefix_hash": (ctypes.c_uint64, [ctypes.c_uint64, i32p, i32]),
+    "gsp_prefix_hash_chain": (ctypes.c_int, [ctypes.c_uint64, i32p, i32, i32, ctypes.POINTER(ctypes.c_uint64)]),
+    "gsp_block_allocator_find_prefix": (ctypes.c_int, [vp, ctypes.c_uint64, i32p]),
+    "gsp_block_allocator_bind_prefix": (ctypes.c_int, [vp, ctypes.c_uint64, i32]),
     "gsp_block_table_create": (ctypes.c_int, [vp, ctypes.POINTER(vp)]),
     "gsp_block_table_destroy": (None, [vp]),
     "gsp_block_table_attach_prefix": (ctypes.c_int, [vp, i32p, i32, i32]),
@@ -451,6 +455,28 @@ class Pool:
         _check(load().gsp_pool_copy_block(self._ctx.handle, self._h, int(src), int(dst), int(valid_tokens)))
 
 
+def prefix_hash(parent_hash: int, tokens) -> int:
+    """PagedBlockPool.ComputePrefixHash (PagedBlockPool.cs:168-172): XXH3-64 of the
+    token ids' little-endian bytes, seeded with the parent block's hash."""
+    t = _i32(tokens)
+    h = load().gsp_prefix_hash(int(parent_hash) & 0xFFFFFFFFFFFFFFFF, _ptr(t) if len(t) else None, len(t))
+    if h == 0:
+        err = load().gsp_last_error()
+        if err:
+            _check(GSP_E_INVALID_ARG)
+    return h
+
+
+def prefix_hash_chain(parent_hash: int, tokens, block_size: int = BLOCK_SIZE) -> np.ndarray:
+    """The hash of every full block of `tokens`, each seeded with the previous one (uint64 array)."""
+    t = _i32(tokens)
+    n = len(t) // block_size
+    out = np.zeros(max(1, n), np.uint64)
+    _check(load().gsp_prefix_hash_chain(int(parent_hash) & 0xFFFFFFFFFFFFFFFF, _ptr(t) if len(t) else None, n,
+                                        int(block_size), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))))
+    return out[:n]
+
+
 class BlockAllocator:
     """Block-id half of PagedBlockPool: LIFO free stack with refcounts."""
 
@@ -509,6 +535,16 @@ class BlockAllocator:
     @property
     def free_blocks_count(self) -> int:
         return load().gsp_block_allocator_free_count(self._h)
+
+    def try_find_prefix_block(self, prefix_hash: int):
+        """TryFindPrefixBlock (PagedBlockPool.cs:194-220): (found, block id); a hit holds one more reference."""
+        b = i32()
+        ok = load().gsp_block_allocator_find_prefix(self._h, int(prefix_hash), ctypes.byref(b))
+        return bool(ok), b.value
+
+    def bind_prefix_block(self, prefix_hash: int, block_id: int) -> None:
+        """BindPrefixBlock (PagedBlockPool.cs:225-234)."""
+        _check(load().gsp_block_allocator_bind_prefix(self._h, int(prefix_hash), int(block_id)))
 
     @property
     def allocated_blocks_count(self) -> int:

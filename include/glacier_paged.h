@@ -40,7 +40,7 @@ extern "C" {
 #pragma GCC visibility push(default)
 #endif
 
-#define GSP_ABI_VERSION 3
+#define GSP_ABI_VERSION 4
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
 
 typedef enum gsp_status {
@@ -308,6 +308,28 @@ int gsp_block_allocator_release(gsp_block_allocator* a, int32_t block_id);
 int gsp_block_allocator_ref_count(const gsp_block_allocator* a, int32_t block_id);
 int gsp_block_allocator_free_count(const gsp_block_allocator* a);
 int gsp_block_allocator_total(const gsp_block_allocator* a);
+
+/* Prefix cache (PagedBlockPool.cs:163-234).
+ * gsp_prefix_hash: ComputePrefixHash (:168-172), the 64-bit XXH3 hash of the
+ * n token ids' little-endian bytes seeded with the parent block's hash (0 for
+ * the first block): the cumulative Merkle chain over full blocks.  Returns 0
+ * with GSP_E_INVALID_ARG set for an invalid span.
+ * gsp_block_allocator_find_prefix: TryFindPrefixBlock (:194-220).  1 and
+ * *block_id, with the block's refcount raised by one, if a live block holds
+ * the hash; 0 and -1 otherwise (also for hash 0).
+ * gsp_block_allocator_bind_prefix: BindPrefixBlock (:225-234), the last
+ * binding of a hash wins.  GSP_E_INVALID_ARG for an id outside the pool or a
+ * zero hash.  Allocating a block clears its hash; freeing it removes its map
+ * entry if the hash still maps to it (:263-271). */
+uint64_t gsp_prefix_hash(uint64_t parent_hash, const int32_t* tokens, int32_t n);
+/* The chain over n_blocks consecutive full blocks of block_size tokens, in one
+ * call: out[i] = gsp_prefix_hash(i ? out[i-1] : parent_hash, block i), what
+ * ContinuousBatchEngine.cs:223-263 computes block by block when it admits a
+ * prompt. */
+int gsp_prefix_hash_chain(uint64_t parent_hash, const int32_t* tokens, int32_t n_blocks, int32_t block_size,
+                          uint64_t* out);
+int gsp_block_allocator_find_prefix(gsp_block_allocator* a, uint64_t prefix_hash, int32_t* block_id);
+int gsp_block_allocator_bind_prefix(gsp_block_allocator* a, uint64_t prefix_hash, int32_t block_id);
 
 int gsp_block_table_create(gsp_block_allocator* a, gsp_block_table** out);
 void gsp_block_table_destroy(gsp_block_table* t);

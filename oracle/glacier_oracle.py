@@ -86,6 +86,8 @@ def load():
         "orc_alloc_release": (ctypes.c_int, [vp, i32]),
         "orc_alloc_ref_count": (ctypes.c_int, [vp, i32]),
         "orc_alloc_free_count": (ctypes.c_int, [vp]),
+        "orc_alloc_find_prefix": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.POINTER(i32)]),
+        "orc_alloc_bind_prefix": (ctypes.c_int, [vp, ctypes.c_uint64, i32]),
         "orc_btab_create": (vp, [vp]),
         "orc_btab_destroy": (None, [vp]),
         "orc_btab_attach_prefix": (None, [vp, i32p, i32, i32]),
@@ -240,6 +242,15 @@ class Alloc:
     @property
     def free_blocks_count(self) -> int:
         return load().orc_alloc_free_count(self._h)
+
+    def try_find_prefix_block(self, prefix_hash: int):
+        b = i32()
+        ok = load().orc_alloc_find_prefix(self._h, prefix_hash, ctypes.byref(b))
+        return bool(ok), b.value
+
+    def bind_prefix_block(self, prefix_hash: int, bid: int) -> None:
+        if load().orc_alloc_bind_prefix(self._h, prefix_hash, bid) < 0:
+            raise ArgumentOutOfRange("physicalBlockId or prefixHash")
 
 
 class BTab:

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <vector>
 
 namespace {
@@ -343,6 +344,8 @@ struct orc_alloc {
     int32_t total, block_size;
     std::vector<int32_t> stack;  // back() = top
     std::vector<int32_t> allocated, refs;
+    std::vector<uint64_t> hashes;              // _blockPrefixHashes
+    std::map<uint64_t, int32_t> prefix_map;    // _prefixHashMap
 };
 
 struct orc_btab {
@@ -358,6 +361,7 @@ orc_alloc* orc_alloc_create(int32_t total_blocks, int32_t block_size) {
     a->block_size = block_size;
     a->allocated.assign(total_blocks, 0);
     a->refs.assign(total_blocks, 0);
+    a->hashes.assign(total_blocks, 0);
     for (int32_t i = total_blocks - 1; i >= 0; --i) a->stack.push_back(i);  // :116-120
     return a;
 }
@@ -373,6 +377,7 @@ int orc_alloc_try_allocate(orc_alloc* a, int32_t* id) {  // :178-189
     a->stack.pop_back();
     a->allocated[*id] = 1;
     a->refs[*id] = 1;
+    a->hashes[*id] = 0;
     return 1;
 }
 
@@ -388,11 +393,42 @@ int orc_alloc_release(orc_alloc* a, int32_t id) {  // :251-279
         a->refs[id] = 0;
         return 0;
     }
-    if (remaining == 0 && a->allocated[id] == 1) {
-        a->allocated[id] = 0;
-        a->stack.push_back(id);
+    if (remaining == 0) {
+        const uint64_t h = a->hashes[id];  // :265-270: drop the map entry only if it is still this block's
+        if (h != 0) {
+            const auto it = a->prefix_map.find(h);
+            if (it != a->prefix_map.end() && it->second == id) a->prefix_map.erase(it);
+            a->hashes[id] = 0;
+        }
+        if (a->allocated[id] == 1) {  // :272-275
+            a->allocated[id] = 0;
+            a->stack.push_back(id);
+        }
     }
     return remaining;
+}
+
+int orc_alloc_find_prefix(orc_alloc* a, uint64_t hash, int32_t* id) {  // :194-220
+    *id = -1;
+    if (hash == 0) return 0;
+    const auto it = a->prefix_map.find(hash);
+    if (it == a->prefix_map.end()) return 0;
+    const int32_t b = it->second;
+    if (a->refs[b] <= 0) return 0;
+    ++a->refs[b];
+    if (a->hashes[b] != hash) {
+        orc_alloc_release(a, b);
+        return 0;
+    }
+    *id = b;
+    return 1;
+}
+
+int orc_alloc_bind_prefix(orc_alloc* a, uint64_t hash, int32_t id) {  // :225-234; -1 where the reference throws
+    if (id < 0 || id >= a->total || hash == 0) return -1;
+    a->hashes[id] = hash;
+    a->prefix_map[hash] = id;
+    return 0;
 }
 
 int orc_alloc_ref_count(const orc_alloc* a, int32_t id) {

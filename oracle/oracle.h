@@ -96,6 +96,11 @@ int orc_alloc_retain(orc_alloc* a, int32_t id); /* -1 where the reference throws
 int orc_alloc_release(orc_alloc* a, int32_t id);
 int orc_alloc_ref_count(const orc_alloc* a, int32_t id);
 int orc_alloc_free_count(const orc_alloc* a);
+/* Prefix cache (PagedBlockPool.cs:194-234): find returns 1 and raises the
+ * refcount when a live block holds the hash; bind returns -1 where the
+ * reference throws (id outside the pool, hash 0). */
+int orc_alloc_find_prefix(orc_alloc* a, uint64_t hash, int32_t* id);
+int orc_alloc_bind_prefix(orc_alloc* a, uint64_t hash, int32_t id);
 
 orc_btab* orc_btab_create(orc_alloc* a);
 void orc_btab_destroy(orc_btab* t);

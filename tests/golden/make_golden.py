@@ -20,6 +20,15 @@ attention_cases.npz
     (PagedAttentionTests.cs:111-179).  Its closed-form value is checked here
     before it is written.
 
+xxh3_vectors.npz
+    PagedBlockPool.ComputePrefixHash (PagedBlockPool.cs:168-172) is the 64-bit
+    XXH3 hash of a block's token ids (little-endian int32 bytes), seeded with
+    the parent block's hash.  The expected values come from the `xxhash`
+    module (the reference implementation of the published XXH3 algorithm):
+    every length path of XXH3 (0 to 4000 bytes), seeds 0, chained parents and
+    random 64-bit seeds, and the token blocks of the reference's own tests
+    (PrefixHashKvCacheTests.cs:11-51, PrefixHashKvCacheAdversarialTests.cs:143-177).
+
 block_tables.npz
     A seeded admit / grow / share / evict log replayed on a plain-Python
     restatement of the LIFO free stack with refcounts (PagedBlockPool.cs:
@@ -317,6 +326,56 @@ def block_table_log(total_blocks=96, n_ops=400):
     }
 
 
+# --------------------------------------------------------------------------
+# XXH3 prefix hashes
+
+REFERENCE_TOKEN_BLOCKS = [
+    [101, 2054, 2003, 1037, 3231, 102] + [0] * 10,                 # PrefixHashKvCacheTests.cs:14
+    list(range(1, 17)),                                             # :27, :44
+    list(range(1, 16)) + [99],                                      # :28
+    list(range(100, 116)),                                          # :30
+    list(range(16, 0, -1)),                                         # :45
+    [10, 20, 30, 40, 50, 60, 70, 80, 90, 100, 110, 120, 130, 140, 150, 160],  # Adversarial :167
+]
+
+
+def xxh3_vectors():
+    import xxhash  # only this generator needs it
+
+    rng = np.random.default_rng(SEED + 2)
+    token_sets, seeds = [], []
+    for n in list(range(0, 71)) + [100, 300, 1000]:  # 0 .. 280 bytes, then the long path
+        toks = rng.integers(-2**31, 2**31, size=n, dtype=np.int64).astype(np.int32)
+        for seed in (0, int(rng.integers(0, 2**63, dtype=np.int64)) * 2 + 1, 2**64 - 1):
+            token_sets.append(toks)
+            seeds.append(seed)
+    # A Merkle chain over a prompt's full blocks, as ContinuousBatchEngine.cs:223-263 walks it.
+    prompt = rng.integers(0, 150000, size=16 * 6, dtype=np.int64).astype(np.int32)
+    parent = 0
+    for b in range(6):
+        token_sets.append(prompt[16 * b:16 * (b + 1)])
+        seeds.append(parent)
+        parent = xxhash.xxh3_64_intdigest(prompt[16 * b:16 * (b + 1)].astype("<i4").tobytes(), seed=parent)
+    for blk in REFERENCE_TOKEN_BLOCKS:
+        token_sets.append(np.array(blk, np.int32))
+        seeds.append(0)
+    offsets = np.zeros(len(token_sets) + 1, np.int64)
+    offsets[1:] = np.cumsum([len(t) for t in token_sets])
+    expected = [xxhash.xxh3_64_intdigest(t.astype("<i4").tobytes(), seed=sd) for t, sd in zip(token_sets, seeds)]
+    return {
+        "tokens": np.concatenate(token_sets).astype(np.int32),
+        "offsets": offsets,
+        "seeds": np.array(seeds, np.uint64),
+        "expected": np.array(expected, np.uint64),
+        "chain_first": np.array([len(token_sets) - 6 - len(REFERENCE_TOKEN_BLOCKS)], np.int64),
+    }
+
+
+def load_xxh3_vectors(path: Path = HERE / "xxh3_vectors.npz"):
+    with np.load(path) as z:
+        return {k: z[k] for k in z.files}
+
+
 def write(out_dir: Path = HERE) -> None:
     flat = {}
     for name, case in attention_cases().items():
@@ -324,6 +383,7 @@ def write(out_dir: Path = HERE) -> None:
             flat[f"{name}__{key}"] = arr
     np.savez_compressed(out_dir / "attention_cases.npz", **flat)
     np.savez_compressed(out_dir / "block_tables.npz", **block_table_log())
+    np.savez_compressed(out_dir / "xxh3_vectors.npz", **xxh3_vectors())
 
 
 def load_attention_cases(path: Path = HERE / "attention_cases.npz"):

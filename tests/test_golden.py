@@ -22,7 +22,7 @@ TABLES = make_golden.load_block_tables()
 def test_fixtures_regenerate_identically(tmp_path):
     """The committed files are exactly what the committed script writes."""
     make_golden.write(tmp_path)
-    for name in ("attention_cases.npz", "block_tables.npz"):
+    for name in ("attention_cases.npz", "block_tables.npz", "xxh3_vectors.npz"):
         with np.load(make_golden.HERE / name) as a, np.load(tmp_path / name) as b:
             assert sorted(a.files) == sorted(b.files)
             for key in a.files:
