@@ -80,12 +80,19 @@ __device__ __forceinline__ void load_page(PageRegs<D, KT>& pr, const KT* kpage, 
     const int bytes = ntok * D * (int)sizeof(KT);
     const __amdgpu_buffer_rsrc_t rk = page_rsrc(kpage, bytes);
     const __amdgpu_buffer_rsrc_t rv = page_rsrc(vpage, bytes);
+    // The lane's K and V offsets are formed here at every call (the empty asm
+    // keeps them from being hoisted out of the page loop), so each load takes
+    // its constant part in the instruction's immediate offset.  Hoisted, the
+    // sixteen offsets would each hold a register across the loop.
+    int kl = n * D + 4 * g;
+    int vl = 4 * g * D + 4 * n;
+    asm volatile("" : "+v"(kl), "+v"(vl));
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) pr.k[j] = Raw4<KT>::load(rk, n * D + 16 * j + 4 * g);
+    for (int j = 0; j < D / 16; ++j) pr.k[j] = Raw4<KT>::load(rk, kl + 16 * j);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int c = 0; c < D / 64; ++c) pr.v[kk][c] = Raw4<KT>::load(rv, (4 * g + kk) * D + 64 * c + 4 * n);
+        for (int c = 0; c < D / 64; ++c) pr.v[kk][c] = Raw4<KT>::load(rv, vl + kk * D + 64 * c);
 }
 
 // Q^T operand of a unit, q[j] = Q[head n][16j + 4g .. +3], and `sc`, the
@@ -277,7 +284,7 @@ typedef __attribute__((address_space(4))) const int32_t const_i32;
 
 __device__ __forceinline__ int ld_meta(const int32_t* p) { return *(const_i32*)p; }
 
-// The scalar fields of unit `ui`; first_blk is read separately (first_block).
+// The scalar fields of unit `ui`; the block ids are read separately (first_block).
 __device__ __forceinline__ DecodeUnit read_unit(const DecodeArgs& a, int ui) {
     const int32_t* src = reinterpret_cast<const int32_t*>(a.units + ui);
     DecodeUnit u;
@@ -299,6 +306,11 @@ __device__ __forceinline__ DecodeUnit read_unit(const DecodeArgs& a, int ui) {
 // address divergent.
 __device__ __forceinline__ int first_block(const DecodeArgs& a, int ui, int wave) {
     return ld_meta(reinterpret_cast<const int32_t*>(a.units + ui) + 8 + wave);
+}
+
+// The same for the wave's second page (page_begin + wave + kDecodeWaves).
+__device__ __forceinline__ int second_block(const DecodeArgs& a, int ui, int wave) {
+    return ld_meta(reinterpret_cast<const int32_t*>(a.units + ui) + 12 + wave);
 }
 
 template <int D, typename KT>
@@ -368,7 +380,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
         const int blkn = first_block(a, has_next ? k + 1 : ui, wave);
         const int pn2 = un.page_begin + wave + kDecodeWaves;  // the next unit's second page of this wave
         const bool has_n2 = has_next && pn2 < un.page_end;
-        const int blkn2 = has_n2 ? ld_meta(a.bt_ids + un.bt_base + pn2) : 0;
+        const int blkn2 = second_block(a, has_next ? k + 1 : ui, wave);
 
         WaveState<D> st;
 #pragma unroll

@@ -17,7 +17,7 @@ constexpr int kMaxSplits = 256;   // split-KV units per (query token, KV head) p
 
 // One unit of decode work, one workgroup each: a contiguous range of logical
 // pages of one (query token, KV head) pair.  Units are ordered longest first
-// so the hardware's in-order dispatch schedules them like LPT.  32 bytes each.
+// so the hardware's in-order dispatch schedules them like LPT.  64 bytes each.
 struct DecodeUnit {
     int32_t qi;          // query token (row of q / out)
     int32_t bt_base;     // offset of the token's row table inside the packed ids
@@ -27,10 +27,11 @@ struct DecodeUnit {
     int32_t kvh;         // KV head
     int32_t slot;        // first partial slot of the pair (-1 when nsplit == 1)
     int32_t split_info;  // split index | nsplit << 16
-    int32_t first_blk[kDecodeWaves];  // block of each wave's first page (-1: none), so
-                                      // the first page loads need no table lookup
+    int32_t first_blk[kDecodeWaves];   // block of each wave's first page (-1: none) and of
+    int32_t second_blk[kDecodeWaves];  // its second, so a unit's first two page loads per
+                                       // wave need no table lookup
 };
-static_assert(sizeof(DecodeUnit) == 48, "DecodeUnit is packed as 12 int32");
+static_assert(sizeof(DecodeUnit) == 64, "DecodeUnit is packed as 16 int32");
 
 struct DecodeArgs {
     const void* k_pool;

@@ -836,7 +836,9 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                         const int32_t* row_ids = desc->bt_ids + desc->bt_offsets[b];
                         for (int w = 0; w < gsp::kDecodeWaves; ++w) {
                             const int32_t p = u.page_begin + w;
+                            const int32_t p2 = p + gsp::kDecodeWaves;
                             u.first_blk[w] = p < u.page_end ? row_ids[p] : -1;
+                            u.second_blk[w] = p2 < u.page_end ? row_ids[p2] : -1;
                         }
                         ctx->units.push_back(u);
                     }
