@@ -271,6 +271,7 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     }
     result.update(extra)
     result["host_prefix_cache"] = host_prefix_cache(gsp, step)
+    result["rope_write"] = rope_write_timing(gsp, torch, ctx, stream, step)
 
     if cpu:
         result["cpu_baseline"], ref = cpu_baseline(step, q, k, v, cpu_budget_s)
@@ -280,6 +281,45 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     pool.destroy()
     ctx.close()
     return result
+
+
+def rope_write_timing(gsp, torch, ctx, stream, step, calls: int = 100) -> dict:
+    """Device cost of the step's K/V write with RoPE (QuantKernels.RoPE then
+    PagedBlockPool.Store, PagedTransformerRunner.cs:620-634, fused): one new token
+    per decode row and the chunk's tokens for prefill rows, into a scratch pool of
+    the step's geometry.  Each call restages positions, blocks and slots from the
+    host, as an engine tick does."""
+    import numpy as np
+
+    n = step.total_q
+    pos = np.concatenate([int(p) + np.arange(int(l)) for p, l in zip(step.positions, step.lens)]).astype(np.int32)
+    blocks = (np.arange(n) // 16).astype(np.int32)
+    slots = (np.arange(n) % 16).astype(np.int32)
+    pool = gsp.Pool.create(ctx, total_blocks=int(blocks[-1]) + 1, layers=1, heads_kv=step.n_kv, head_dim=step.head_dim,
+                           kv_dtype=gsp.KV_F16 if step.kv_dtype == "f16" else gsp.KV_F32)
+    gen = torch.Generator(device="cuda").manual_seed(step.seed)
+    q = torch.randn((n, step.n_heads, step.head_dim), device="cuda", generator=gen)
+    k = torch.randn((n, step.n_kv, step.head_dim), device="cuda", generator=gen)
+    v = torch.randn((n, step.n_kv, step.head_dim), device="cuda", generator=gen)
+    args = (0, pos, blocks, slots, step.n_heads, 1000000.0, gsp.ROPE_HALVES, q.data_ptr(), k.data_ptr(), v.data_ptr())
+    with torch.cuda.stream(stream):
+        for _ in range(5):
+            pool.rope_write_tokens(*args)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(calls):
+            pool.rope_write_tokens(*args)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / calls * 1e3
+    elem = 2 if step.kv_dtype == "f16" else 4
+    moved = n * (2 * step.n_heads * step.head_dim * 4 + 2 * step.n_kv * step.head_dim * 4
+                 + 2 * step.n_kv * step.head_dim * elem)
+    pool.destroy()
+    return {"tokens": n, "us_per_call": round(us, 2), "bytes_per_call": moved,
+            "gbs": round(moved / (us * 1e-6) / 1e9, 1),
+            "note": "Q rotated in place, K rotated and stored, V stored; includes the per-call host staging"}
 
 
 def host_prefix_cache(gsp, step) -> dict:

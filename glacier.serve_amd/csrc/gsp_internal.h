@@ -116,6 +116,30 @@ struct WriteTokensArgs {
 
 hipError_t launch_write_tokens(int kv_f16, const WriteTokensArgs& a, hipStream_t stream);
 
+constexpr int kRopeMaxHalf = 128;  // head_dim <= 256
+
+struct RopeWriteArgs {
+    void* k_pool;
+    void* v_pool;
+    int64_t block_stride;
+    int64_t layer_offset;
+    int64_t head_stride;
+    const int32_t* positions;  // [n]
+    const int32_t* block_ids;  // [n]
+    const int32_t* slots;      // [n]
+    float* q;                  // [n][n_heads][d], rotated in place (n_heads 0: none)
+    const float* k;            // [n][n_kv][d], rotated into the pool
+    const float* v;            // [n][n_kv][d], stored as is
+    double log2_base;          // log2(freq_base)
+    int32_t n;
+    int32_t n_heads;
+    int32_t n_kv;
+    int32_t head_dim;
+    int32_t style;             // GSP_ROPE_PAIRS or GSP_ROPE_HALVES
+};
+
+hipError_t launch_rope_write(int kv_f16, const RopeWriteArgs& a, hipStream_t stream);
+
 struct CopyBlockArgs {
     void* k_pool;
     void* v_pool;

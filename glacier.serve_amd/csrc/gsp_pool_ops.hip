@@ -1,6 +1,8 @@
-// Device page operations on the KV pool (gfx950): the batched Store scatter
-// and the copy-on-write page copy.  Both are plain HBM-bound copies.
+// Device page operations on the KV pool (gfx950): the batched Store scatter,
+// the same scatter with the rotary embedding applied on the way, and the
+// copy-on-write page copy.  All are small HBM-bound copies.
 #include "gsp_internal.h"
+#include "../../include/glacier_paged.h"
 
 namespace gsp {
 namespace {
@@ -20,6 +22,61 @@ __global__ __launch_bounds__(128) void write_tokens_kernel(WriteTokensArgs a) {
     for (int e = threadIdx.x; e < a.head_dim; e += blockDim.x) {
         kd[e] = static_cast<KT>(a.k[src + e]);
         vd[e] = static_cast<KT>(a.v[src + e]);
+    }
+}
+
+// QuantKernels.RoPE then PagedBlockPool.Store for n tokens
+// (PagedTransformerRunner.cs:253-267, 437-452, 620-634), one workgroup per
+// token.  Pair j of every head turns by pos * base^(-2j/d) (Su et al.,
+// RoFormer): the angle is formed and reduced to [-pi, pi] in fp64, so it
+// stays exact at long positions, and its cosine and sine are taken once per
+// token in fp32.  Q heads are rotated in place, K heads are rotated into the
+// pool slot and V is stored as is; fp16 pools round to nearest even.
+template <typename KT>
+__global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
+    __shared__ float cs[kRopeMaxHalf][2];
+    const int i = blockIdx.x;
+    const int d = a.head_dim;
+    const int half = d >> 1;
+    const double pos = (double)a.positions[i];
+    for (int j = threadIdx.x; j < half; j += blockDim.x) {
+        const double ang = pos * exp2(-(2.0 * j / d) * a.log2_base);
+        const double r = ang - 6.283185307179586 * rint(ang * 0.15915494309189535);
+        float s, c;
+        sincosf((float)r, &s, &c);
+        cs[j][0] = c;
+        cs[j][1] = s;
+    }
+    __syncthreads();
+    const int64_t dst = (int64_t)a.block_ids[i] * a.block_stride + a.layer_offset + (int64_t)a.slots[i] * d;
+    const bool pairs = a.style == GSP_ROPE_PAIRS;
+    const int heads = a.n_heads + a.n_kv;
+    for (int idx = threadIdx.x; idx < heads * half; idx += blockDim.x) {
+        const int h = idx / half;
+        const int j = idx - h * half;
+        const int e0 = pairs ? 2 * j : j;
+        const int e1 = pairs ? 2 * j + 1 : j + half;
+        const float c = cs[j][0];
+        const float s = cs[j][1];
+        if (h < a.n_heads) {
+            float* q = a.q + ((int64_t)i * a.n_heads + h) * d;
+            const float x0 = q[e0], x1 = q[e1];
+            q[e0] = x0 * c - x1 * s;
+            q[e1] = x0 * s + x1 * c;
+        } else {
+            const int hk = h - a.n_heads;
+            const float* k = a.k + ((int64_t)i * a.n_kv + hk) * d;
+            KT* kd = static_cast<KT*>(a.k_pool) + dst + (int64_t)hk * a.head_stride;
+            const float x0 = k[e0], x1 = k[e1];
+            kd[e0] = static_cast<KT>(x0 * c - x1 * s);
+            kd[e1] = static_cast<KT>(x0 * s + x1 * c);
+        }
+    }
+    for (int idx = threadIdx.x; idx < a.n_kv * d; idx += blockDim.x) {
+        const int hk = idx / d;
+        const int e = idx - hk * d;
+        static_cast<KT*>(a.v_pool)[dst + (int64_t)hk * a.head_stride + e] =
+            static_cast<KT>(a.v[((int64_t)i * a.n_kv + hk) * d + e]);
     }
 }
 
@@ -49,6 +106,16 @@ hipError_t launch_write_tokens(int kv_f16, const WriteTokensArgs& a, hipStream_t
         hipLaunchKernelGGL(write_tokens_kernel<_Float16>, grid, dim3(128), 0, stream, a);
     else
         hipLaunchKernelGGL(write_tokens_kernel<float>, grid, dim3(128), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_write(int kv_f16, const RopeWriteArgs& a, hipStream_t stream) {
+    if (a.n <= 0) return hipSuccess;
+    if (a.head_dim > 2 * kRopeMaxHalf || (a.head_dim & 1)) return hipErrorInvalidValue;
+    if (kv_f16)
+        hipLaunchKernelGGL(rope_write_kernel<_Float16>, dim3(a.n), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(rope_write_kernel<float>, dim3(a.n), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -525,6 +526,67 @@ int gsp_pool_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
     a.n_kv = d.heads_kv;
     a.head_dim = d.head_dim;
     return check_hip(gsp::launch_write_tokens(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "write_tokens launch");
+}
+
+int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const int32_t* positions,
+                          const int32_t* block_ids, const int32_t* slots, int32_t n_heads, float freq_base,
+                          int32_t style, float* q_dev, const float* k_dev, const float* v_dev) {
+    gsp::clear_error();
+    if (!ctx || !pool) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool is NULL");
+    if (n < 0) return gsp::fail(GSP_E_INVALID_ARG, "n must be >= 0 (got %d)", n);
+    if (n == 0) return GSP_OK;
+    if (!positions || !block_ids || !slots || !k_dev || !v_dev) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument");
+    if (n_heads < 0) return gsp::fail(GSP_E_INVALID_ARG, "nHeads must be >= 0 (got %d)", n_heads);
+    if (n_heads > 0 && !q_dev) return gsp::fail(GSP_E_INVALID_ARG, "q is NULL with nHeads %d", n_heads);
+    if (style != GSP_ROPE_PAIRS && style != GSP_ROPE_HALVES)
+        return gsp::fail(GSP_E_INVALID_ARG, "unknown RoPE pairing %d", style);
+    if (!(freq_base > 0.0f) || !std::isfinite(freq_base))
+        return gsp::fail(GSP_E_INVALID_ARG, "RoPE frequency base must be positive and finite");
+    const gsp_pool_desc& d = pool->desc;
+    if (d.v_head_dim != d.head_dim) return gsp::fail(GSP_E_UNSUPPORTED, "vHeadDim != headDim is not supported on the device pool");
+    if (d.head_dim % 2 != 0 || d.head_dim > 2 * gsp::kRopeMaxHalf)
+        return gsp::fail(GSP_E_UNSUPPORTED, "RoPE needs an even headDim <= %d (got %d)", 2 * gsp::kRopeMaxHalf, d.head_dim);
+    if (layer < 0 || layer >= d.layers) return gsp::fail(GSP_E_INVALID_ARG, "layer %d out of range [0, %d)", layer, d.layers);
+    for (int32_t i = 0; i < n; ++i) {
+        if (positions[i] < 0) return gsp::fail(GSP_E_INVALID_ARG, "token %d: position %d is negative", i, positions[i]);
+        if (block_ids[i] < 0 || block_ids[i] >= d.total_blocks)
+            return gsp::fail(GSP_E_INVALID_ARG, "block id %d out of range [0, %d)", block_ids[i], d.total_blocks);
+        if (slots[i] < 0 || slots[i] >= d.block_size)
+            return gsp::fail(GSP_E_INVALID_ARG, "slot %d out of range [0, %d)", slots[i], d.block_size);
+    }
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    const size_t words = 3 * (size_t)n;
+    rc = ensure_pinned(&ctx->aux, &ctx->aux_words, words, ctx->aux_done, &ctx->aux_pending);
+    if (!rc) rc = ensure_device(ctx, &ctx->d_aux, &ctx->d_aux_words, words, false);
+    if (rc) return rc;
+    std::memcpy(ctx->aux, positions, n * sizeof(int32_t));
+    std::memcpy(ctx->aux + n, block_ids, n * sizeof(int32_t));
+    std::memcpy(ctx->aux + 2 * (size_t)n, slots, n * sizeof(int32_t));
+    rc = check_hip(hipMemcpyAsync(ctx->d_aux, ctx->aux, words * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream),
+                   "hipMemcpyAsync(rope ids)");
+    if (!rc) rc = check_hip(hipEventRecord(ctx->aux_done, ctx->stream), "hipEventRecord");
+    if (rc) return rc;
+    ctx->aux_pending = true;
+    gsp::RopeWriteArgs a;
+    a.k_pool = pool->k;
+    a.v_pool = pool->v;
+    a.block_stride = pool->block_stride_k;
+    a.layer_offset = (int64_t)layer * pool->layer_stride_k;
+    a.head_stride = pool->head_stride_k;
+    a.positions = ctx->d_aux;
+    a.block_ids = ctx->d_aux + n;
+    a.slots = ctx->d_aux + 2 * (size_t)n;
+    a.q = q_dev;
+    a.k = k_dev;
+    a.v = v_dev;
+    a.log2_base = std::log2((double)freq_base);
+    a.n = n;
+    a.n_heads = n_heads;
+    a.n_kv = d.heads_kv;
+    a.head_dim = d.head_dim;
+    a.style = style;
+    return check_hip(gsp::launch_rope_write(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "rope_write launch");
 }
 
 int gsp_pool_copy_block(gsp_ctx* ctx, gsp_pool* pool, int32_t src, int32_t dst, int32_t valid_tokens) {

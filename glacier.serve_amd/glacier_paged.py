@@ -48,6 +48,8 @@ DECODE_MFMA = 2
 PREFILL_AUTO = 0
 PREFILL_TILES = 1
 PREFILL_PER_TOKEN = 2
+ROPE_PAIRS = 0
+ROPE_HALVES = 1
 BLOCK_SIZE = 16
 
 
@@ -167,6 +169,7 @@ _SIGNATURES = {
         [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     ),
     "gsp_pool_write_tokens": (ctypes.c_int, [vp, vp, i32, i32, i32p, i32p, vp, vp]),
+    "gsp_rope_write_tokens": (ctypes.c_int, [vp, vp, i32, i32, i32p, i32p, i32p, i32, ctypes.c_float, i32, vp, vp, vp]),
     "gsp_pool_copy_block": (ctypes.c_int, [vp, vp, i32, i32, i32]),
     "gsp_pool_upload": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
     "gsp_pool_download": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
@@ -449,6 +452,19 @@ class Pool:
             raise ValueError("block_ids and slots differ in length")
         _check(load().gsp_pool_write_tokens(self._ctx.handle, self._h, int(layer), len(b), _ptr(b), _ptr(s),
                                             vp(k_ptr), vp(v_ptr)))
+
+    def rope_write_tokens(self, layer: int, positions, block_ids, slots, n_heads: int, freq_base: float,
+                          style: int, q_ptr: int, k_ptr: int, v_ptr: int) -> None:
+        """QuantKernels.RoPE then PagedBlockPool.Store for a batch of tokens
+        (PagedTransformerRunner.cs:253-267): Q rotated in place, K rotated into the pool, V stored."""
+        p = _i32(positions)
+        b = _i32(block_ids)
+        s = _i32(slots)
+        if not (len(p) == len(b) == len(s)):
+            raise ValueError("positions, block_ids and slots differ in length")
+        _check(load().gsp_rope_write_tokens(self._ctx.handle, self._h, int(layer), len(b), _ptr(p), _ptr(b), _ptr(s),
+                                            int(n_heads), float(freq_base), int(style), vp(q_ptr), vp(k_ptr),
+                                            vp(v_ptr)))
 
     def copy_block_data(self, src: int, dst: int, valid_tokens: int) -> None:
         """PagedBlockPool.CopyBlockData (PagedBlockPool.cs:304-327) on the device."""

@@ -40,7 +40,7 @@ extern "C" {
 #pragma GCC visibility push(default)
 #endif
 
-#define GSP_ABI_VERSION 4
+#define GSP_ABI_VERSION 5
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
 
 typedef enum gsp_status {
@@ -146,6 +146,27 @@ int gsp_pool_arenas(const gsp_pool* pool, void** k_dev, void** v_dev, size_t* k_
 int gsp_pool_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n,
                           const int32_t* block_ids, const int32_t* slots, const float* k_dev,
                           const float* v_dev);
+
+/* Pairings of gsp_rope_write_tokens. */
+#define GSP_ROPE_PAIRS 0   /* pair j is (x[2j], x[2j+1]) */
+#define GSP_ROPE_HALVES 1  /* pair j is (x[j], x[j + head_dim/2]) */
+
+/* QuantKernels.RoPE(q, k, nHeads, nHeadsKv, headDim, pos, freqBase) followed
+ * by PagedBlockPool.Store, fused and batched (PagedTransformerRunner.cs:253-267
+ * and :620-634 for decode, :437-452 for a prefill chunk).  Token i sits at
+ * position positions[i]; pair j of each of its heads turns by
+ * positions[i] * freq_base^(-2j/head_dim).  q_dev ([n][n_heads][head_dim]
+ * fp32, device) is rotated in place, or left alone with n_heads 0; k_dev is
+ * rotated and stored, and v_dev stored as is, exactly where
+ * gsp_pool_write_tokens stores them.  This is the domain of the reference's
+ * GPU runner: RoPE over the full head, no frequency table, no YaRN
+ * (CudaPagedTransformerRunner.cs:414-418); head_dim even and at most 256.  The
+ * reference's rotation lives in closed code, so `style` (GSP_ROPE_*) names the
+ * pairing.  positions, block_ids and slots are host arrays. */
+int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n,
+                          const int32_t* positions, const int32_t* block_ids,
+                          const int32_t* slots, int32_t n_heads, float freq_base, int32_t style,
+                          float* q_dev, const float* k_dev, const float* v_dev);
 
 /* PagedBlockPool.CopyBlockData (PagedBlockPool.cs:304-327): copies the first
  * min(valid_tokens, block_size) slots of every layer and KV head of block

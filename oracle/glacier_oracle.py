@@ -88,6 +88,7 @@ def load():
         "orc_alloc_free_count": (ctypes.c_int, [vp]),
         "orc_alloc_find_prefix": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.POINTER(i32)]),
         "orc_alloc_bind_prefix": (ctypes.c_int, [vp, ctypes.c_uint64, i32]),
+        "orc_rope": (None, [f32p, i32, i32, i32, ctypes.c_double, i32]),
         "orc_btab_create": (vp, [vp]),
         "orc_btab_destroy": (None, [vp]),
         "orc_btab_attach_prefix": (None, [vp, i32p, i32, i32]),
@@ -115,6 +116,18 @@ def _f32(a) -> np.ndarray:
 
 def _i32(a) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+ROPE_PAIRS, ROPE_HALVES = 0, 1
+
+
+def rope(x: np.ndarray, pos: int, freq_base: float, style: int = ROPE_PAIRS) -> np.ndarray:
+    """Rotary embedding of the vectors along x's last axis at position `pos` (a rotated copy);
+    textbook definition in fp64 (orc_rope)."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    dim = y.shape[-1]
+    load().orc_rope(y.ctypes.data_as(f32p), y.size // dim, dim, int(pos), float(freq_base), int(style))
+    return y
 
 
 class HostPool:

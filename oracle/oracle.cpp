@@ -502,3 +502,21 @@ void orc_btab_release_all(orc_btab* t) {  // BlockTable.cs:108-116
 }
 
 }  // extern "C"
+
+/* ------------------------------------------------------------------ RoPE */
+
+extern "C" void orc_rope(float* x, int32_t n_vec, int32_t dim, int32_t pos, double freq_base, int32_t style) {
+    const int32_t half = dim / 2;
+    for (int32_t j = 0; j < half; ++j) {
+        const double ang = (double)pos * std::pow(freq_base, -2.0 * j / dim);
+        const double c = std::cos(ang), s = std::sin(ang);
+        for (int32_t v = 0; v < n_vec; ++v) {
+            float* p = x + (size_t)v * dim;
+            float* a = style == ORC_ROPE_PAIRS ? p + 2 * j : p + j;
+            float* b = style == ORC_ROPE_PAIRS ? p + 2 * j + 1 : p + j + half;
+            const double x0 = *a, x1 = *b;
+            *a = (float)(x0 * c - x1 * s);
+            *b = (float)(x0 * s + x1 * c);
+        }
+    }
+}

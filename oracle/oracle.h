@@ -11,6 +11,7 @@
  *   PagedBlockPool free stack / refcounts   PagedBlockPool.cs:112-121,178-299,332-353
  *   BlockTable                              BlockTable.cs:13-117
  *   decode / prefill call order             PagedTransformerRunner.cs:521-656, 362-474
+ *   RoPE before the store                   PagedTransformerRunner.cs:253-267, 437-452, 620-634
  *
  * Parity status of each function is stated at its declaration.
  */
@@ -65,6 +66,18 @@ int orc_compute_attention(const orc_pool* pool, const orc_table* table, int32_t 
                           int32_t n_heads, int32_t n_heads_kv, int32_t head_dim, int32_t v_head_dim,
                           float attn_scale, float* head_scores, int32_t max_seq_len,
                           const float* sink_logit, int32_t n_threads, int32_t isa);
+
+/* Rotary position embedding as the reference applies it before the store
+ * (PagedTransformerRunner.cs:253-267: QuantKernels.RoPE(q, k, nHeads, nHeadsKv,
+ * headDim, pos, freqBase), then PagedBlockPool.Store).  Rotates n_vec vectors
+ * of `dim` floats in place: pair j < dim/2 turns by
+ * pos * freq_base^(-2j/dim), pairing (x[2j], x[2j+1]) for ORC_ROPE_PAIRS or
+ * (x[j], x[j + dim/2]) for ORC_ROPE_HALVES; angles, sines and products in
+ * fp64.  Parity: QuantKernels.RoPE is closed code; this is the textbook
+ * definition (Su et al., RoFormer, 2021), and which pairing the reference
+ * uses is unpinned. */
+enum { ORC_ROPE_PAIRS = 0, ORC_ROPE_HALVES = 1 };
+void orc_rope(float* x, int32_t n_vec, int32_t dim, int32_t pos, double freq_base, int32_t style);
 
 /* One engine step the way the reference runner drives the kernel: rows in
  * order (PagedTransformerRunner.cs:605-656), query token i of a row at

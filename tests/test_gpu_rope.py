@@ -1,0 +1,134 @@
+"""gsp_rope_write_tokens: RoPE on Q and K fused with the KV store, against the oracle.
+
+The oracle computes the textbook rotation in fp64 (orc_rope).  The device
+forms each angle in fp64 and takes its cosine and sine in fp32, so fp32
+results stay within a few 1e-7 of the oracle at any position (bar 2e-6 on
+N(0, 1) inputs); fp16 pools hold the rotated value rounded to fp16 (bar one
+fp16 ulp, 2e-3 at these magnitudes).  V is stored untouched, bit-exact.
+"""
+import numpy as np
+import pytest
+
+import glacier_oracle as orc
+import workloads
+from gpu_helpers import max_err, oracle_step, to_device_pool
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # (n_heads, n_kv, head_dim, kv dtype, freq base)
+    (28, 4, 128, "f32", 1000000.0),
+    (14, 2, 64, "f32", 10000.0),
+    (32, 8, 128, "f16", 500000.0),
+    (8, 8, 64, "f16", 10000.0),
+]
+
+
+def _tokens(rng, n, total_blocks):
+    blocks = rng.choice(total_blocks, size=n, replace=False).astype(np.int32)
+    slots = rng.integers(0, 16, size=n).astype(np.int32)
+    positions = rng.integers(0, 40000, size=n).astype(np.int32)
+    positions[:3] = [0, 1, 32767]
+    return positions, blocks, slots
+
+
+@pytest.mark.parametrize("style", [0, 1], ids=["pairs", "halves"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"{c[0]}q{c[1]}kv_d{c[2]}_{c[3]}")
+def test_rope_write_matches_oracle(torch_mod, gsp, ctx, case, style):
+    torch = torch_mod
+    nh, nkv, d, dt, base = case
+    print(f"case rope {case} style={style}", flush=True)
+    rng = np.random.default_rng(nh * 7 + d + style)
+    n, total_blocks = 37, 64
+    positions, blocks, slots = _tokens(rng, n, total_blocks)
+    q = rng.standard_normal((n, nh, d)).astype(np.float32)
+    k = rng.standard_normal((n, nkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, nkv, d)).astype(np.float32)
+    pool = gsp.Pool.create(ctx, total_blocks=total_blocks, layers=2, heads_kv=nkv, head_dim=d,
+                           kv_dtype=gsp.KV_F16 if dt == "f16" else gsp.KV_F32)
+    qd = torch.from_numpy(q).cuda()
+    kd = torch.from_numpy(k).cuda()
+    vd = torch.from_numpy(v).cuda()
+    torch.cuda.synchronize()
+    pool.rope_write_tokens(1, positions, blocks, slots, nh, base, style, qd.data_ptr(), kd.data_ptr(), vd.data_ptr())
+    ctx.sync()
+    npdt = np.float16 if dt == "f16" else np.float32
+    _, _, kb, vb = pool.arenas()
+    K = pool.download(0, kb).view(npdt).reshape(total_blocks, 2, nkv, 16, d)
+    V = pool.download(1, vb).view(npdt).reshape(total_blocks, 2, nkv, 16, d)
+    got_q = qd.cpu().numpy()
+    tol = 2e-3 if dt == "f16" else 2e-6
+    for i in range(n):
+        ref_q = orc.rope(q[i], int(positions[i]), base, style)
+        ref_k = orc.rope(k[i], int(positions[i]), base, style)
+        assert max_err(got_q[i], ref_q) <= 2e-6, f"q of token {i} at position {positions[i]}"
+        assert max_err(K[blocks[i], 1, :, slots[i]].astype(np.float32), ref_k) <= tol, f"k of token {i}"
+        assert np.array_equal(V[blocks[i], 1, :, slots[i]], v[i].astype(npdt)), f"v of token {i}"
+    # Nothing else in the pool was written (pools start zeroed).
+    mask = np.ones(K.shape, bool)
+    mask[blocks, 1, :, slots] = False
+    assert not K[mask].any() and not V[mask].any()
+    pool.destroy()
+
+
+def test_rope_write_without_q_and_errors(torch_mod, gsp, ctx):
+    torch = torch_mod
+    pool = gsp.Pool.create(ctx, total_blocks=8, layers=1, heads_kv=2, head_dim=64)
+    k = torch.ones((2, 2, 64), device="cuda")
+    q = torch.full((2, 4, 64), 5.0, device="cuda")
+    torch.cuda.synchronize()
+    pool.rope_write_tokens(0, [3, 4], [1, 2], [0, 0], 0, 10000.0, 0, 0, k.data_ptr(), k.data_ptr())
+    ctx.sync()
+    _, _, kb, _ = pool.arenas()
+    K = pool.download(0, kb).view(np.float32).reshape(8, 1, 2, 16, 64)
+    assert np.allclose(K[1, 0, 0, 0], orc.rope(np.ones(64, np.float32), 3, 10000.0), atol=2e-6)
+    for bad in (dict(positions=[-1]), dict(slots=[16]), dict(blocks=[8]), dict(style=2), dict(base=0.0),
+                dict(nh=4, qp=0)):
+        with pytest.raises(gsp.InvalidArgument):
+            pool.rope_write_tokens(0, bad.get("positions", [0]), bad.get("blocks", [0]), bad.get("slots", [0]),
+                                   bad.get("nh", 0), bad.get("base", 10000.0), bad.get("style", 0),
+                                   bad.get("qp", q.data_ptr()), k.data_ptr(), k.data_ptr())
+    ctx.sync()
+    pool.destroy()
+
+
+@pytest.mark.parametrize("style", [0, 1], ids=["pairs", "halves"])
+def test_rope_write_then_attention(torch_mod, gsp, ctx, style):
+    """The reference decode order (PagedTransformerRunner.cs:605-656): RoPE, Store, then attention
+    over the stored pages; the device path against the oracle's rotated Q and K."""
+    torch = torch_mod
+    print(f"case rope+attention style={style}", flush=True)
+    base = 1000000.0
+    step = workloads.small_step(seed=91 + style, rows=6, n_heads=28, n_kv=4, head_dim=128, ctx_lo=20, ctx_hi=200,
+                                total_blocks=256)
+    q, k, v = workloads.host_values(step)
+    pool, keep = to_device_pool(torch, gsp, ctx, step, k, v)
+    # Every row's newest token (position TokenCount - 1) gets fresh K/V through RoPE + Store.
+    rng = np.random.default_rng(5)
+    rows = step.num_rows
+    pos = (step.token_counts - 1).astype(np.int32)
+    blocks = np.array([step.table(b)[p // 16] for b, p in enumerate(pos)], np.int32)
+    slots = (pos % 16).astype(np.int32)
+    k_new = rng.standard_normal((rows, step.n_kv, step.head_dim)).astype(np.float32)
+    v_new = rng.standard_normal((rows, step.n_kv, step.head_dim)).astype(np.float32)
+    qd = torch.from_numpy(np.ascontiguousarray(q)).cuda()
+    kn = torch.from_numpy(k_new).cuda()
+    vn = torch.from_numpy(v_new).cuda()
+    torch.cuda.synchronize()
+    pool.rope_write_tokens(0, pos, blocks, slots, step.n_heads, base, style, qd.data_ptr(), kn.data_ptr(),
+                           vn.data_ptr())
+    ctx.pack_step(pool, pos, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len)
+    out = torch.full((rows, step.n_heads, step.head_dim), float("nan"), device="cuda")
+    ctx.attention_step(pool, 0, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
+    ctx.sync()
+    # Oracle: the same rotation and store on the host arenas, then the reference attention.
+    k2, v2 = k.copy(), v.copy()
+    qr = np.stack([orc.rope(q[b], int(pos[b]), base, style) for b in range(rows)])
+    for b in range(rows):
+        k2[blocks[b], 0, :, slots[b]] = orc.rope(k_new[b], int(pos[b]), base, style)
+        v2[blocks[b], 0, :, slots[b]] = v_new[b]
+    step2 = workloads.Step(step.name, step.n_heads, step.n_kv, step.head_dim, step.kv_dtype, step.total_blocks,
+                           step.max_seq_len, pos, step.token_counts, step.bt_offsets, step.bt_ids, None, step.seed)
+    ref = oracle_step(step2, qr, k2, v2)
+    assert max_err(out.cpu().numpy(), ref) <= 1e-4
+    pool.destroy()
