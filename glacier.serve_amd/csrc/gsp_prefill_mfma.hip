@@ -14,7 +14,9 @@
 //     S^T[key][token] = K_page . Q_head^T   (M = keys, N = tokens, K = head dim)
 //     O_head[token][e] += P . V_page          (M = tokens, N = head dim, K = keys)
 //
-// both on v_mfma_f32_16x16x16f16 with fp32 accumulation.  Operands enter as
+// with fp32 accumulation: QK on v_mfma_f32_16x16x32_f16 (32 head dims per
+// step; on gfx950 it does twice the work of v_mfma_f32_16x16x16f16 in the same
+// cycles), PV on v_mfma_f32_16x16x16f16 (a page holds 16 keys).  Operands enter as
 // fp16 pairs x = x_hi + x_lo, each side scaled by a power of two so that its
 // largest element lies in [2^12, 2^13) (the pair then carries ~22
 // significant bits and nothing overflows or flushes):
@@ -38,7 +40,7 @@
 // Row tile T of the workgroup is query head hc + T over the 16 tokens; wave w
 // owns tiles w and w + 4 (or tile w alone, for groups of at most 4).  The MFMA operand layouts are the decode kernel's
 // with "head" replaced by "query token" (lane l, n = l % 16, g = l / 16):
-//   QK A = K[key n][16j + 4g .. +3], B = Q[token n][16j + 4g .. +3]
+//   QK A = K[key n][32j + 8g .. +7], B = Q[token n][32j + 8g .. +7]
 //   result: lane holds S[token n][key 4g + r]
 //   PV A = P'[token n][keys 4g .. 4g+3] (the lane's own four), B = V[keys 4g .. 4g+3][col],
 //   col = 64c + 4n + i for output block 4c + i; result: lane holds O[token 4g + r][col].
@@ -53,6 +55,7 @@ namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int kPScaleLog2 = 12;  // P enters the matrix cores times 2^12 (p_lo stays normal)
 static_assert(kPrefillTileTokens == kBlockSize, "the tile's token and key dimensions are both 16");
@@ -229,22 +232,23 @@ __device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLd
     }
 }
 
-// Q operands of one tile, q[j] = Q[token n][16j + 4g .. +3] as a scaled fp16
-// pair, and the lane's score factor 2^e_token * scale (log2 units).
+// Q operands of one tile for the K = 32 matrix cores, q[j] = Q[token n][32j + 8g
+// .. +7] as a scaled fp16 pair, and the lane's score factor 2^e_token * scale
+// (log2 units).
 template <int D>
 struct TileQ {
-    h4 hi[D / 16];
-    h4 lo[D / 16];
+    h8 hi[D / 32];
+    h8 lo[D / 32];
     float sc;
 };
 
 template <int D>
 __device__ __forceinline__ void load_tile_q(TileQ<D>& tq, const float* qrow, bool live, int g, float scale) {
-    f4 x[D / 16];
+    f4 x[D / 16];  // x[2j + h] = Q[token n][32j + 8g + 4h .. +3]
     float mx = 0.f;
 #pragma unroll
     for (int j = 0; j < D / 16; ++j) {
-        const f4 v = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
+        const f4 v = *reinterpret_cast<const f4*>(qrow + 32 * (j >> 1) + 8 * g + 4 * (j & 1));
         x[j] = live ? v : f4{0.f, 0.f, 0.f, 0.f};
         mx = fmaxf(mx, max_abs4(x[j]));
     }
@@ -253,7 +257,13 @@ __device__ __forceinline__ void load_tile_q(TileQ<D>& tq, const float* qrow, boo
     const int e = pair_exponent(mx);
     const float down = ldexpf(1.0f, -e);
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) split_pair(x[j] * down, tq.hi[j], tq.lo[j]);
+    for (int j = 0; j < D / 32; ++j) {
+        h4 h0, l0, h1, l1;
+        split_pair(x[2 * j] * down, h0, l0);
+        split_pair(x[2 * j + 1] * down, h1, l1);
+        tq.hi[j] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+        tq.lo[j] = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
     tq.sc = ldexpf(scale, e);
 }
 
@@ -384,28 +394,29 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
         // The wave's tiles share the page, so each K operand read from LDS and
         // each V operand assembled below serves all of them.
 
-        // S^T = K . Q^T (hi/lo products; two accumulation chains per tile).
+        // S^T = K . Q^T (hi/lo products; two accumulation chains per tile), 32
+        // head dims per matrix-core step: A = K[key n][32j + 8g .. +7].
         f4 s0[kPrefillTiles], s1[kPrefillTiles];
 #pragma unroll
         for (int s = 0; s < kPrefillTiles; ++s) s0[s] = s1[s] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < D / 16; ++j) {
-            const int at = n * kRow + 16 * j + 4 * g;
+        for (int j = 0; j < D / 32; ++j) {
+            const int at = n * kRow + 32 * j + 8 * g;
             if constexpr (kSplitKV) {
-                const h4 kh = *reinterpret_cast<const h4*>(&sh.kh[buf][at]);
-                const h4 kl = *reinterpret_cast<const h4*>(&sh.kl[buf][at]);
+                const h8 kh = *reinterpret_cast<const h8*>(&sh.kh[buf][at]);
+                const h8 kl = *reinterpret_cast<const h8*>(&sh.kl[buf][at]);
 #pragma unroll
                 for (int s = 0; s < kPrefillTiles; ++s) {
-                    s0[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].hi[j], s0[s], 0, 0, 0);
-                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, q[s].lo[j], s1[s], 0, 0, 0);
-                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, q[s].hi[j], s1[s], 0, 0, 0);
+                    s0[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].hi[j], s0[s], 0, 0, 0);
+                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].lo[j], s1[s], 0, 0, 0);
+                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, q[s].hi[j], s1[s], 0, 0, 0);
                 }
             } else {
-                const h4 kx = *reinterpret_cast<const h4*>(&sh.k[buf][at]);
+                const h8 kx = *reinterpret_cast<const h8*>(&sh.k[buf][at]);
 #pragma unroll
                 for (int s = 0; s < kPrefillTiles; ++s) {
-                    s0[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].hi[j], s0[s], 0, 0, 0);
-                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(kx, q[s].lo[j], s1[s], 0, 0, 0);
+                    s0[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, q[s].hi[j], s0[s], 0, 0, 0);
+                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, q[s].lo[j], s1[s], 0, 0, 0);
                 }
             }
         }
