@@ -10,13 +10,13 @@
 // groups), and walks the row's pages in
 // order:
 //
-//   per page (16 keys, staged once in LDS and shared by the group's heads):
-//     S^T[key][token] = K_page . Q_head^T   (M = keys, N = tokens, K = head dim)
-//     O_head[token][e] += P . V_page          (M = tokens, N = head dim, K = keys)
+//   per pair of pages (32 keys, staged once in LDS and shared by the group's heads):
+//     S^T[key][token] = K_page . Q_head^T   (per page: M = keys, N = tokens, K = head dim)
+//     O_head[token][e] += P . V_pair          (M = tokens, N = head dim, K = 32 keys)
 //
-// with fp32 accumulation: QK on v_mfma_f32_16x16x32_f16 (32 head dims per
-// step; on gfx950 it does twice the work of v_mfma_f32_16x16x16f16 in the same
-// cycles), PV on v_mfma_f32_16x16x16f16 (a page holds 16 keys).  Operands enter as
+// with fp32 accumulation, on v_mfma_f32_16x16x32_f16 (on gfx950 it does twice
+// the work of v_mfma_f32_16x16x16f16 in the same cycles): QK takes 32 head
+// dims per step, and PV 32 keys, so pages go in pairs.  Operands enter as
 // fp16 pairs x = x_hi + x_lo, each side scaled by a power of two so that its
 // largest element lies in [2^12, 2^13) (the pair then carries ~22
 // significant bits and nothing overflows or flushes):
@@ -42,11 +42,12 @@
 // with "head" replaced by "query token" (lane l, n = l % 16, g = l / 16):
 //   QK A = K[key n][32j + 8g .. +7], B = Q[token n][32j + 8g .. +7]
 //   result: lane holds S[token n][key 4g + r]
-//   PV A = P'[token n][keys 4g .. 4g+3] (the lane's own four), B = V[keys 4g .. 4g+3][col],
-//   col = 64c + 4n + i for output block 4c + i; result: lane holds O[token 4g + r][col].
+//   PV A = P'[token n][the lane's own eight keys: 4g .. 4g+3 of each page of the pair],
+//   B = V[the same eight keys][col], col = 64c + 4n + i for output block 4c + i;
+//   result: lane holds O[token 4g + r][col].
 // The causal limit is per row (token); padding rows past the tile's tokens
-// keep finite scores and are never written.  Pages are staged through two LDS
-// buffers (register-prefetched one page ahead) with one barrier per page.
+// keep finite scores and are never written.  Page pairs are staged through two
+// LDS buffers (register-prefetched a page at a time) with one barrier per pair.
 // The roofline of these rows is the matrix peak.
 #include "gsp_epilogue.h"
 
@@ -107,24 +108,39 @@ struct PfStage<D, _Float16> {
     h4 v[kStageChunks<D>];
 };
 
-// LDS page buffers (two).  Rows are padded by 8 halves (16 bytes).
+// LDS buffers (two), each holding a pair of pages: keys 0..15 of the first
+// page, then 16..31 of the second.  Rows are padded by 8 halves (16 bytes).
+constexpr int kPairKeys = 2 * kBlockSize;
+
 template <int D, typename KT>
 struct PfLds;
+
+// Each buffer's arrays sit together, so every offset within a buffer fits the
+// 16-bit immediate of an LDS instruction.
+template <int D>
+struct alignas(16) PfLdsBuf32 {
+    _Float16 kh[kPairKeys * (D + 8)], kl[kPairKeys * (D + 8)];
+    _Float16 vh[kPairKeys * (D + 8)], vl[kPairKeys * (D + 8)];
+    int ek[kPairKeys], ev[kPairKeys];  // per-key exponents of the K and V pairs
+    int evw[2 * kDecodeWaves];          // largest V exponent of each wave's four keys, per page
+};
 
 template <int D>
 struct alignas(16) PfLds<D, float> {
     static constexpr int kRow = D + 8;
-    _Float16 kh[2][kBlockSize * kRow], kl[2][kBlockSize * kRow];
-    _Float16 vh[2][kBlockSize * kRow], vl[2][kBlockSize * kRow];
-    int ek[2][kBlockSize], ev[2][kBlockSize];  // per-key exponents of the K and V pairs
-    int evw[2][kDecodeWaves];                   // largest V exponent of each wave's four keys
+    PfLdsBuf32<D> b[2];
+};
+
+template <int D>
+struct alignas(16) PfLdsBuf16 {
+    _Float16 k[kPairKeys * (D + 8)];
+    _Float16 v[kPairKeys * (D + 8)];
 };
 
 template <int D>
 struct alignas(16) PfLds<D, _Float16> {
     static constexpr int kRow = D + 8;
-    _Float16 k[2][kBlockSize * kRow];
-    _Float16 v[2][kBlockSize * kRow];
+    PfLdsBuf16<D> b[2];
 };
 
 // Element offset of lane tid's chunk j in a page (key row tid / 16).
@@ -186,7 +202,7 @@ __device__ __forceinline__ float cross_row_max(float x) {
 }
 
 template <int D>
-__device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D, float>& sh, int buf) {
+__device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D, float>& sh, int buf, int slot) {
     constexpr int kRow = PfLds<D, float>::kRow;
     const int key = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
@@ -201,34 +217,34 @@ __device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D
     const float dk = ldexpf(1.0f, -ek), dv = ldexpf(1.0f, -ev);
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
-        const int at = key * kRow + 64 * i + 4 * part;
+        const int at = (slot * kBlockSize + key) * kRow + 64 * i + 4 * part;
         h4 hi, lo;
         split_pair(sr.k[i] * dk, hi, lo);
-        *reinterpret_cast<h4*>(&sh.kh[buf][at]) = hi;
-        *reinterpret_cast<h4*>(&sh.kl[buf][at]) = lo;
+        *reinterpret_cast<h4*>(&sh.b[buf].kh[at]) = hi;
+        *reinterpret_cast<h4*>(&sh.b[buf].kl[at]) = lo;
         split_pair(sr.v[i] * dv, hi, lo);
-        *reinterpret_cast<h4*>(&sh.vh[buf][at]) = hi;
-        *reinterpret_cast<h4*>(&sh.vl[buf][at]) = lo;
+        *reinterpret_cast<h4*>(&sh.b[buf].vh[at]) = hi;
+        *reinterpret_cast<h4*>(&sh.b[buf].vl[at]) = lo;
     }
     if (part == 0) {
-        sh.ek[buf][key] = ek;
-        sh.ev[buf][key] = ev;
+        sh.b[buf].ek[slot * kBlockSize + key] = ek;
+        sh.b[buf].ev[slot * kBlockSize + key] = ev;
     }
     // The page's largest V exponent: this wave's four keys, then one slot per wave.
     const float evw = cross_row_max((float)ev);
-    if ((threadIdx.x & 63) == 0) sh.evw[buf][threadIdx.x >> 6] = (int)evw;
+    if ((threadIdx.x & 63) == 0) sh.b[buf].evw[slot * kDecodeWaves + (threadIdx.x >> 6)] = (int)evw;
 }
 
 template <int D>
-__device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLds<D, _Float16>& sh, int buf) {
+__device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLds<D, _Float16>& sh, int buf, int slot) {
     constexpr int kRow = PfLds<D, _Float16>::kRow;
     const int key = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
-        const int at = key * kRow + 64 * i + 4 * part;
-        *reinterpret_cast<h4*>(&sh.k[buf][at]) = sr.k[i];
-        *reinterpret_cast<h4*>(&sh.v[buf][at]) = sr.v[i];
+        const int at = (slot * kBlockSize + key) * kRow + 64 * i + 4 * part;
+        *reinterpret_cast<h4*>(&sh.b[buf].k[at]) = sr.k[i];
+        *reinterpret_cast<h4*>(&sh.b[buf].v[at]) = sr.v[i];
     }
 }
 
@@ -314,6 +330,37 @@ __device__ __forceinline__ f4 page_softmax(TileState<D>& st, f4 s, bool diag, in
     return p;
 }
 
+// page_softmax over a pair of pages: the lane's eight scores are keys
+// key0 + r (first page, s0) and key0 + 16 + r (second page, s1).
+template <int D>
+__device__ __forceinline__ void pair_softmax(TileState<D>& st, f4& s0, f4& s1, bool diag, int key0, int row_ctx,
+                                             int g, f4& alpha_rows, bool& rescale) {
+    if (diag) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (key0 + r >= row_ctx) s0[r] = -INFINITY;
+            if (key0 + kBlockSize + r >= row_ctx) s1[r] = -INFINITY;
+        }
+    }
+    const float mp = cross_row_max(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                                         fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))));
+    rescale = __any(mp > st.m + kLazyLog2);  // true on the first pair (m = -inf)
+    if (rescale) {
+        const float mn = fmaxf(st.m, mp);  // finite: the first page holds key 0 for every row
+        const float alpha = fast_exp2(st.m - mn);
+        st.m = mn;
+        st.l *= alpha;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) alpha_rows[r] = __shfl(alpha, 4 * g + r);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        s0[r] = fast_exp2(s0[r] - st.m);
+        s1[r] = fast_exp2(s1[r] - st.m);
+    }
+    st.l += ((s0[0] + s0[1]) + (s0[2] + s0[3])) + ((s1[0] + s1[1]) + (s1[2] + s1[3]));
+}
+
 // TILES query heads per wave (heads wave + 4 s, s < TILES): 2 for groups above
 // 4 heads, else 1.  Every tile of a wave is computed on every page, so the
 // hot loop has no branches; a tile past the group (zero Q) is simply not
@@ -358,132 +405,187 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
     const int32_t* bt = a.bt_ids + t.bt_base;
     const int ctx_last = min(t.token_count, t.pos0 + t.ntok);
 
+    // Page p of the row into registers; pages past the row's last load as zeros
+    // (its keys are past every row's limit, so they are masked).
     PfStage<D, KT> sr;
-    {
-        const int64_t blk = bt[0];
-        stage_load<D>(sr, kbase + blk * a.block_stride, vbase + blk * a.block_stride, min(kBlockSize, ctx_last));
-        stage_store<D>(sr, sh, 0);
-    }
+    auto load_regs = [&](int pg) {
+        const bool have = pg < t.pages;
+        const int64_t blk = have ? bt[pg] : 0;
+        stage_load<D>(sr, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
+                      have ? min(kBlockSize, ctx_last - pg * kBlockSize) : 0);
+    };
+    load_regs(0);
+    stage_store<D>(sr, sh, 0, 0);
+    load_regs(1);
+    stage_store<D>(sr, sh, 0, 1);
     __syncthreads();
 
-    for (int p = 0; p < t.pages; ++p) {
-        const int buf = p & 1;
-        if (p + 1 < t.pages) {
-            const int64_t blk = bt[p + 1];
-            stage_load<D>(sr, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
-                          min(kBlockSize, ctx_last - (p + 1) * kBlockSize));
-        }
-        const int key0 = p * kBlockSize + 4 * g;
-        const bool diag = (p + 1) * kBlockSize > min(t.pos0 + 1, t.token_count);  // some row may stop here
+    // Pages go in pairs (32 keys, one v_mfma_f32_16x16x32_f16 step of P.V).
+    // The next pair is staged one page at a time: the first after this pair's
+    // scores, the second at the end.
+    const int pairs = (t.pages + 1) >> 1;
+    for (int i = 0; i < pairs; ++i) {
+        const int buf = i & 1;
+        const bool more = i + 1 < pairs;
+        if (more) load_regs(2 * i + 2);
+        const int key0 = i * kPairKeys + 4 * g;  // the lane's keys: key0 + r and key0 + 16 + r
+        const bool diag = (i + 1) * kPairKeys > min(t.pos0 + 1, t.token_count);  // some row may stop here
 
-        // Page scales (fp32 pages): 2^e_k and e_v of keys 4g + r, and the page's largest e_v.
-        f4 kscale = {1.f, 1.f, 1.f, 1.f};
-        int evk[4] = {0, 0, 0, 0};
+        // Page scales (fp32 pages): 2^e_k and e_v of the lane's keys, and the pair's largest e_v.
+        f4 ks0 = {1.f, 1.f, 1.f, 1.f}, ks1 = {1.f, 1.f, 1.f, 1.f};
+        int evk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         int evmax = 0;
         if constexpr (kSplitKV) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                kscale[r] = ldexpf(1.0f, sh.ek[buf][4 * g + r]);
-                evk[r] = sh.ev[buf][4 * g + r];
+                ks0[r] = ldexpf(1.0f, sh.b[buf].ek[4 * g + r]);
+                ks1[r] = ldexpf(1.0f, sh.b[buf].ek[kBlockSize + 4 * g + r]);
+                evk[r] = sh.b[buf].ev[4 * g + r];
+                evk[4 + r] = sh.b[buf].ev[kBlockSize + 4 * g + r];
             }
-            evmax = sh.evw[buf][0];
+            evmax = sh.b[buf].evw[0];
 #pragma unroll
-            for (int w = 1; w < kDecodeWaves; ++w) evmax = max(evmax, sh.evw[buf][w]);
+            for (int w = 1; w < 2 * kDecodeWaves; ++w) evmax = max(evmax, sh.b[buf].evw[w]);
         }
 
-        // The wave's tiles share the page, so each K operand read from LDS and
+        // S^T = K . Q^T for both pages (hi/lo products, one accumulation chain per
+        // page and tile), 32 head dims per matrix-core step: A = K[key n][32j + 8g .. +7].
+        // The wave's tiles share the pages, so each K operand read from LDS and
         // each V operand assembled below serves all of them.
-
-        // S^T = K . Q^T (hi/lo products; two accumulation chains per tile), 32
-        // head dims per matrix-core step: A = K[key n][32j + 8g .. +7].
-        f4 s0[kPrefillTiles], s1[kPrefillTiles];
+        // The lane's parts of the LDS addresses are formed here, in every
+        // iteration (the empty asm keeps them from being hoisted), so the
+        // constant parts go into the instructions' immediate offsets.
+        int kq = n * kRow + 8 * g;
+        int vq = 4 * g * kRow + 4 * n;
+        asm volatile("" : "+v"(kq), "+v"(vq));
+        f4 sc[2][kPrefillTiles];
 #pragma unroll
-        for (int s = 0; s < kPrefillTiles; ++s) s0[s] = s1[s] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int s = 0; s < kPrefillTiles; ++s) sc[h][s] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < D / 32; ++j) {
-            const int at = n * kRow + 32 * j + 8 * g;
-            if constexpr (kSplitKV) {
-                const h8 kh = *reinterpret_cast<const h8*>(&sh.kh[buf][at]);
-                const h8 kl = *reinterpret_cast<const h8*>(&sh.kl[buf][at]);
+            __builtin_amdgcn_sched_barrier(0);  // K reads one step at a time, as the V reads below
 #pragma unroll
-                for (int s = 0; s < kPrefillTiles; ++s) {
-                    s0[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].hi[j], s0[s], 0, 0, 0);
-                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].lo[j], s1[s], 0, 0, 0);
-                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, q[s].hi[j], s1[s], 0, 0, 0);
-                }
-            } else {
-                const h8 kx = *reinterpret_cast<const h8*>(&sh.k[buf][at]);
+            for (int h = 0; h < 2; ++h) {
+                const int at = kq + h * kBlockSize * kRow + 32 * j;
+                if constexpr (kSplitKV) {
+                    const h8 kh = *reinterpret_cast<const h8*>(&sh.b[buf].kh[at]);
+                    const h8 kl = *reinterpret_cast<const h8*>(&sh.b[buf].kl[at]);
 #pragma unroll
-                for (int s = 0; s < kPrefillTiles; ++s) {
-                    s0[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, q[s].hi[j], s0[s], 0, 0, 0);
-                    s1[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, q[s].lo[j], s1[s], 0, 0, 0);
+                    for (int s = 0; s < kPrefillTiles; ++s) {
+                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].hi[j], sc[h][s], 0, 0, 0);
+                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].lo[j], sc[h][s], 0, 0, 0);
+                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, q[s].hi[j], sc[h][s], 0, 0, 0);
+                    }
+                } else {
+                    const h8 kx = *reinterpret_cast<const h8*>(&sh.b[buf].k[at]);
+#pragma unroll
+                    for (int s = 0; s < kPrefillTiles; ++s) {
+                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, q[s].hi[j], sc[h][s], 0, 0, 0);
+                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, q[s].lo[j], sc[h][s], 0, 0, 0);
+                    }
                 }
             }
         }
 
-        // Softmax of each tile, and its P' as an fp16 pair.
-        h4 ph[kPrefillTiles], pl[kPrefillTiles];
+        // Softmax of each tile over the pair, and its P' as an fp16 pair in the
+        // A layout of the K = 32 step: elements 0..3 are the lane's keys of the
+        // first page, 4..7 those of the second.
+        h8 ph[kPrefillTiles], pl[kPrefillTiles];
 #pragma unroll
         for (int s = 0; s < kPrefillTiles; ++s) {
             TileState<D>& ts = st[s];
-            f4 sc = (s0[s] + s1[s]) * q[s].sc;  // lane: S[token n][keys key0 .. key0 + 3], log2 units
-            if constexpr (kSplitKV) sc *= kscale;
-
+            f4 p0 = sc[0][s] * q[s].sc;  // lane: S[token n][keys key0 .. key0 + 3], log2 units
+            f4 p1 = sc[1][s] * q[s].sc;
+            if constexpr (kSplitKV) {
+                p0 *= ks0;
+                p1 *= ks1;
+            }
             f4 alpha_rows = {1.f, 1.f, 1.f, 1.f};
             bool rescale = false;
-            f4 pr = page_softmax<D>(ts, sc, diag, key0, row_ctx, g, alpha_rows, rescale);
+            pair_softmax<D>(ts, p0, p1, diag, key0, row_ctx, g, alpha_rows, rescale);
 
             if constexpr (kSplitKV) {
-                // O in units of 2^eo: a page with larger V exponents raises eo first.
+                // O in units of 2^eo: a pair with larger V exponents raises eo first.
                 if (evmax > ts.eo) {
-                    const float down = ldexpf(1.0f, ts.eo - evmax);  // 0 on the first page
+                    const float down = ldexpf(1.0f, ts.eo - evmax);  // 0 on the first pair
                     alpha_rows *= down;
                     rescale = true;
                     ts.eo = evmax;
                 }
 #pragma unroll
-                for (int r = 0; r < 4; ++r) pr[r] = ldexpf(pr[r], evk[r] - ts.eo + kPScaleLog2);
+                for (int r = 0; r < 4; ++r) {
+                    p0[r] = ldexpf(p0[r], evk[r] - ts.eo + kPScaleLog2);
+                    p1[r] = ldexpf(p1[r], evk[4 + r] - ts.eo + kPScaleLog2);
+                }
             } else {
-                pr *= (float)(1 << kPScaleLog2);
+                p0 *= (float)(1 << kPScaleLog2);
+                p1 *= (float)(1 << kPScaleLog2);
             }
             if (rescale) {
 #pragma unroll
                 for (int b = 0; b < D / 16; ++b) ts.o[b] *= alpha_rows;
             }
-            split_pair(pr, ph[s], pl[s]);
+            h4 h0, l0, h1, l1;
+            split_pair(p0, h0, l0);
+            split_pair(p1, h1, l1);
+            ph[s] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+            pl[s] = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
         }
 
-        // O += P' . V: output block 4c + i takes B = V[keys 4g + kk][64c + 4n + i],
-        // element i of the lane's four V pieces of keys 4g .. 4g + 3.
+        // The first page of the next pair goes to the other buffer (free since
+        // the last barrier), and its second page starts loading.
+        if (more) {
+            stage_store<D>(sr, sh, buf ^ 1, 0);
+            load_regs(2 * i + 3);
+        }
+
+        // O += P' . V over the pair's 32 keys: output block 4c + i takes
+        // B = V[keys][64c + 4n + i] for the same eight keys as the lane's P'
+        // (keys 4g .. 4g + 3 of each page).
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 #pragma unroll
         for (int c = 0; c < D / 64; ++c) {
-            h4 vh[4], vl[4];
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int at = (4 * g + kk) * kRow + 64 * c + 4 * n;
-                if constexpr (kSplitKV) {
-                    vh[kk] = *reinterpret_cast<const h4*>(&sh.vh[buf][at]);
-                    vl[kk] = *reinterpret_cast<const h4*>(&sh.vl[buf][at]);
-                } else {
-                    vh[kk] = *reinterpret_cast<const h4*>(&sh.v[buf][at]);
-                }
-            }
+            for (int eh = 0; eh < 2; ++eh) {  // elements 2 eh and 2 eh + 1 of the lane's four columns
+                // One group of V reads at a time: hoisted together they would
+                // hold every group's operands at once.
+                __builtin_amdgcn_sched_barrier(0);
+                h2 vh[2][4], vl[2][4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const h4 bh = {vh[0][i], vh[1][i], vh[2][i], vh[3][i]};
-                h4 bl;
-                if constexpr (kSplitKV) bl = h4{vl[0][i], vl[1][i], vl[2][i], vl[3][i]};
+                for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int s = 0; s < kPrefillTiles; ++s) {
-                    f4 acc = st[s].o[4 * c + i];
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[s], bh, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[s], bh, acc, 0, 0, 0);
-                    if constexpr (kSplitKV) acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[s], bl, acc, 0, 0, 0);
-                    st[s].o[4 * c + i] = acc;
+                    for (int kk = 0; kk < 4; ++kk) {
+                        const int at = vq + (h * kBlockSize + kk) * kRow + 64 * c + 2 * eh;
+                        if constexpr (kSplitKV) {
+                            vh[h][kk] = *reinterpret_cast<const h2*>(&sh.b[buf].vh[at]);
+                            vl[h][kk] = *reinterpret_cast<const h2*>(&sh.b[buf].vl[at]);
+                        } else {
+                            vh[h][kk] = *reinterpret_cast<const h2*>(&sh.b[buf].v[at]);
+                        }
+                    }
+#pragma unroll
+                for (int e2 = 0; e2 < 2; ++e2) {
+                    const int e = 2 * eh + e2;
+                    const h8 bh = {vh[0][0][e2], vh[0][1][e2], vh[0][2][e2], vh[0][3][e2],
+                                   vh[1][0][e2], vh[1][1][e2], vh[1][2][e2], vh[1][3][e2]};
+                    h8 bl;
+                    if constexpr (kSplitKV)
+                        bl = h8{vl[0][0][e2], vl[0][1][e2], vl[0][2][e2], vl[0][3][e2],
+                                vl[1][0][e2], vl[1][1][e2], vl[1][2][e2], vl[1][3][e2]};
+#pragma unroll
+                    for (int s = 0; s < kPrefillTiles; ++s) {
+                        f4 acc = st[s].o[4 * c + e];
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bh, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s], bh, acc, 0, 0, 0);
+                        if constexpr (kSplitKV) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bl, acc, 0, 0, 0);
+                        st[s].o[4 * c + e] = acc;
+                    }
                 }
             }
         }
-        if (p + 1 < t.pages) stage_store<D>(sr, sh, buf ^ 1);
+        if (more) stage_store<D>(sr, sh, buf ^ 1, 1);
         __syncthreads();
     }
 
