@@ -795,12 +795,13 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     // Default grid: two workgroups per CU, bins balanced per CU (assign_bins).
     // A step that also has prefill tiles runs them beside the decode units
     // (gsp_attention_step): the HBM-bound decode grid then takes one
-    // workgroup per two CUs and leaves the other slots to the matrix-bound
-    // tiles (config 4 measured 461 us this way, against 491 us with one per CU).
+    // workgroup per four CUs and leaves the other slots to the matrix-bound
+    // tiles, which take several times longer (config 4 measured 428 us this
+    // way, against 452 us with one per two CUs and 487 us with one per CU).
     const bool pair_cus = ctx->decode_bins_override <= 0 && !any_tiles;
     const int64_t bins_max = ctx->decode_bins_override > 0 ? (int64_t)ctx->decode_bins_override
                              : pair_cus                    ? (int64_t)kDecodeBinsPerCu * std::max(1, ctx->num_cus)
-                                                           : (int64_t)std::max(1, ctx->num_cus / 2);
+                                                           : (int64_t)std::max(1, ctx->num_cus / 4);
     const int64_t sim_bins = pair_cus ? bins_max / kDecodeBinsPerCu : bins_max;
     int64_t target = 1;
     if (T > 0) {

@@ -243,7 +243,7 @@ int gsp_step_download(gsp_ctx* ctx, int32_t* row_offsets, int32_t* ids, int32_t*
 int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages);
 
 /* Most decode workgroups for the next gsp_step_pack: 0 (default) uses two
- * per CU, or one per two CUs when the step also has prefill tiles (those run
+ * per CU, or one per four CUs when the step also has prefill tiles (those run
  * beside the decode units, on a second stream forked from and joined back
  * into the context's stream); > 0 forces the count (tuning and tests).  Units
  * are packed into that many bins longest first, and each workgroup runs its
