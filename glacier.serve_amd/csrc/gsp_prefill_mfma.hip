@@ -47,7 +47,9 @@
 //   result: lane holds O[token 4g + r][col].
 // The causal limit is per row (token); padding rows past the tile's tokens
 // keep finite scores and are never written.  Page pairs are staged through two
-// LDS buffers (register-prefetched a page at a time) with one barrier per pair.
+// LDS buffers (register-prefetched a page at a time) with one barrier per pair;
+// V goes in transposed, so each PV B operand is one 16-byte LDS read, and the
+// K and V operands of the next matrix step are read while the current one runs.
 // The roofline of these rows is the matrix peak.
 #include "gsp_epilogue.h"
 
@@ -77,40 +79,71 @@ __device__ __forceinline__ int pair_exponent(float mx) {
     return mx > 0.f ? min(100, max(kPairExpFloor, ex - 13)) : kPairExpFloor;
 }
 
-__device__ __forceinline__ void split_pair(const f4& x, h4& hi, h4& lo) {
-    hi = __builtin_convertvector(x, h4);
-    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f4), h4);
+template <typename F, typename H>
+__device__ __forceinline__ void split_pair(const F& x, H& hi, H& lo) {
+    hi = __builtin_convertvector(x, H);
+    lo = __builtin_convertvector(x - __builtin_convertvector(hi, F), H);
 }
 
 __device__ __forceinline__ float max_abs4(const f4& x) {
     return fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
 }
 
-// Page staging: key row tid / 16 is moved by the 16 lanes of one DPP row;
-// lane part = tid % 16 moves the D / 64 four-element chunks at columns
-// 64 j + 4 part (each load instruction reads 256 contiguous bytes per row).
-template <int D>
-constexpr int kStageChunks = D / 64;
-static_assert(kBlockSize * 16 == kDecodeThreads, "one 16-lane row per key of the page");
+template <typename V>
+__device__ __forceinline__ float max_abs(const V& x) {
+    float m = fabsf(x[0]);
+#pragma unroll
+    for (int i = 1; i < (int)(sizeof(V) / sizeof(x[0])); ++i) m = fmaxf(m, fabsf(x[i]));
+    return m;
+}
 
-template <int D, typename KT>
-struct PfStage;
-
-template <int D>
-struct PfStage<D, float> {
-    f4 k[kStageChunks<D>];
-    f4 v[kStageChunks<D>];
+template <typename T, int W>
+struct VecW {
+    typedef T type __attribute__((ext_vector_type(W)));
 };
 
+template <typename V>
+__device__ __forceinline__ V buffer_load(__amdgpu_buffer_rsrc_t r, int off) {
+    if constexpr (sizeof(V) == 16) return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    else if constexpr (sizeof(V) == 8) return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+    else return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// Page staging.  K: key row tid / 16 is moved by the 16 lanes of one DPP row;
+// lane part = tid % 16 moves the D / 64 four-element chunks at columns
+// 64 j + 4 part (each load instruction reads 256 contiguous bytes per row).
+// V: lane vpart = tid % 32 moves columns kVW * vpart .. + kVW - 1 of the two
+// keys 2 kg and 2 kg + 1, kg = tid / 32, so that it can store each column's
+// key pair as one 32-bit word of the transposed V (below).
 template <int D>
-struct PfStage<D, _Float16> {
-    h4 k[kStageChunks<D>];
-    h4 v[kStageChunks<D>];
+constexpr int kStageChunks = D / 64;
+template <int D>
+constexpr int kVW = D / 32;
+static_assert(kBlockSize * 16 == kDecodeThreads, "one 16-lane row per key of the page");
+static_assert(kBlockSize / 2 * 32 == kDecodeThreads, "one 32-lane half-wave per key pair of the page");
+
+template <int D, typename KT>
+struct PfStage {
+    typedef KT kvec __attribute__((ext_vector_type(4)));
+    typedef typename VecW<KT, kVW<D>>::type vvec;
+    kvec k[kStageChunks<D>];
+    vvec v[2];  // keys 2 kg and 2 kg + 1
 };
 
 // LDS buffers (two), each holding a pair of pages: keys 0..15 of the first
-// page, then 16..31 of the second.  Rows are padded by 8 halves (16 bytes).
+// page, then 16..31 of the second.  K rows are padded by 8 halves (16 bytes).
+// V is stored transposed, one row of 32 keys per column, with the keys in
+// the order the P.V step consumes them: position 8 q + 4 h + r holds key
+// 4 q + r of page h, so lane group g reads its eight keys (4g .. 4g + 3 of
+// each page) as one 16-byte word.  Every fourth column row is followed by 8
+// halves of padding, which puts the 16 lanes of one read (columns 4n + i) on
+// distinct banks.
 constexpr int kPairKeys = 2 * kBlockSize;
+
+template <int D>
+constexpr int kVtLen = D * kPairKeys + (D / 4) * 8;
+
+__device__ __forceinline__ constexpr int vt_row(int col) { return col * kPairKeys + (col >> 2) * 8; }
 
 template <int D, typename KT>
 struct PfLds;
@@ -120,7 +153,7 @@ struct PfLds;
 template <int D>
 struct alignas(16) PfLdsBuf32 {
     _Float16 kh[kPairKeys * (D + 8)], kl[kPairKeys * (D + 8)];
-    _Float16 vh[kPairKeys * (D + 8)], vl[kPairKeys * (D + 8)];
+    _Float16 vh[kVtLen<D>], vl[kVtLen<D>];
     int ek[kPairKeys], ev[kPairKeys];  // per-key exponents of the K and V pairs
     int evw[2 * kDecodeWaves];          // largest V exponent of each wave's four keys, per page
 };
@@ -134,7 +167,7 @@ struct alignas(16) PfLds<D, float> {
 template <int D>
 struct alignas(16) PfLdsBuf16 {
     _Float16 k[kPairKeys * (D + 8)];
-    _Float16 v[kPairKeys * (D + 8)];
+    _Float16 v[kVtLen<D>];
 };
 
 template <int D>
@@ -143,37 +176,26 @@ struct alignas(16) PfLds<D, _Float16> {
     PfLdsBuf16<D> b[2];
 };
 
-// Element offset of lane tid's chunk j in a page (key row tid / 16).
+// Element offset of lane tid's K chunk j in a page (key row tid / 16).
 template <int D>
 __device__ __forceinline__ int stage_offset(int j) {
     return (threadIdx.x >> 4) * D + 64 * j + 4 * (threadIdx.x & 15);
 }
 
-template <int D>
-__device__ __forceinline__ void stage_load(PfStage<D, float>& sr, const float* kpage, const float* vpage, int ntok) {
-    const int bytes = ntok * D * 4;
+template <int D, typename KT>
+__device__ __forceinline__ void stage_load(PfStage<D, KT>& sr, const KT* kpage, const KT* vpage, int ntok) {
+    typedef typename PfStage<D, KT>::kvec kvec;
+    typedef typename PfStage<D, KT>::vvec vvec;
+    constexpr int kE = (int)sizeof(KT);
+    const int bytes = ntok * D * kE;
     const __amdgpu_buffer_rsrc_t rk = prefill_rsrc(kpage, bytes);
     const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(vpage, bytes);
 #pragma unroll
-    for (int i = 0; i < kStageChunks<D>; ++i) {
-        const int off = 4 * stage_offset<D>(i);
-        sr.k[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-        sr.v[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
-    }
-}
-
-template <int D>
-__device__ __forceinline__ void stage_load(PfStage<D, _Float16>& sr, const _Float16* kpage, const _Float16* vpage,
-                                           int ntok) {
-    const int bytes = ntok * D * 2;
-    const __amdgpu_buffer_rsrc_t rk = prefill_rsrc(kpage, bytes);
-    const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(vpage, bytes);
+    for (int i = 0; i < kStageChunks<D>; ++i) sr.k[i] = buffer_load<kvec>(rk, kE * stage_offset<D>(i));
+    const int kg = threadIdx.x >> 5;
+    const int vpart = threadIdx.x & 31;
 #pragma unroll
-    for (int i = 0; i < kStageChunks<D>; ++i) {
-        const int off = 2 * stage_offset<D>(i);
-        sr.k[i] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rk, off, 0, 0));
-        sr.v[i] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0));
-    }
+    for (int kk = 0; kk < 2; ++kk) sr.v[kk] = buffer_load<vvec>(rv, kE * ((2 * kg + kk) * D + kVW<D> * vpart));
 }
 
 // DPP lane moves within a row of 16 lanes (bound_ctrl off: every source lane is in the row).
@@ -201,20 +223,33 @@ __device__ __forceinline__ float cross_row_max(float x) {
     return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
+// Max over the 32 lanes of the caller's half-wave: its DPP row, then rows
+// swapped in pairs (lanes l and l ^ 16).
+__device__ __forceinline__ float half_wave_max(float x) {
+    x = row16_max(x);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
+
+// Max over lanes l and l ^ 32 (the two half-waves).
+__device__ __forceinline__ float half_swap_max(float x) {
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+
 template <int D>
 __device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D, float>& sh, int buf, int slot) {
     constexpr int kRow = PfLds<D, float>::kRow;
+    constexpr int W = kVW<D>;
+    typedef typename VecW<_Float16, W>::type hW;
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const int key = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
-    float mk = 0.f, mv = 0.f;
+    float mk = 0.f;
 #pragma unroll
-    for (int i = 0; i < kStageChunks<D>; ++i) {
-        mk = fmaxf(mk, max_abs4(sr.k[i]));
-        mv = fmaxf(mv, max_abs4(sr.v[i]));
-    }
+    for (int i = 0; i < kStageChunks<D>; ++i) mk = fmaxf(mk, max_abs4(sr.k[i]));
     const int ek = pair_exponent(row16_max(mk));
-    const int ev = pair_exponent(row16_max(mv));
-    const float dk = ldexpf(1.0f, -ek), dv = ldexpf(1.0f, -ev);
+    const float dk = ldexpf(1.0f, -ek);
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
         const int at = (slot * kBlockSize + key) * kRow + 64 * i + 4 * part;
@@ -222,30 +257,54 @@ __device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D
         split_pair(sr.k[i] * dk, hi, lo);
         *reinterpret_cast<h4*>(&sh.b[buf].kh[at]) = hi;
         *reinterpret_cast<h4*>(&sh.b[buf].kl[at]) = lo;
-        split_pair(sr.v[i] * dv, hi, lo);
-        *reinterpret_cast<h4*>(&sh.b[buf].vh[at]) = hi;
-        *reinterpret_cast<h4*>(&sh.b[buf].vl[at]) = lo;
     }
-    if (part == 0) {
-        sh.b[buf].ek[slot * kBlockSize + key] = ek;
-        sh.b[buf].ev[slot * kBlockSize + key] = ev;
+    if (part == 0) sh.b[buf].ek[slot * kBlockSize + key] = ek;
+
+    // V, transposed: the lane's columns each take its key pair as one word.
+    const int kg = threadIdx.x >> 5;
+    const int vpart = threadIdx.x & 31;
+    int ev[2];
+    hW hi[2], lo[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        ev[kk] = pair_exponent(half_wave_max(max_abs(sr.v[kk])));
+        split_pair(sr.v[kk] * ldexpf(1.0f, -ev[kk]), hi[kk], lo[kk]);
     }
-    // The page's largest V exponent: this wave's four keys, then one slot per wave.
-    const float evw = cross_row_max((float)ev);
+    const int pos = 8 * (kg >> 1) + 4 * slot + 2 * (kg & 1);  // keys 2 kg, 2 kg + 1 of page `slot`
+#pragma unroll
+    for (int c = 0; c < W; ++c) {
+        const int at = vt_row(W * vpart + c) + pos;
+        *reinterpret_cast<h2*>(&sh.b[buf].vh[at]) = h2{hi[0][c], hi[1][c]};
+        *reinterpret_cast<h2*>(&sh.b[buf].vl[at]) = h2{lo[0][c], lo[1][c]};
+    }
+    if (vpart == 0) {
+        sh.b[buf].ev[slot * kBlockSize + 2 * kg] = ev[0];
+        sh.b[buf].ev[slot * kBlockSize + 2 * kg + 1] = ev[1];
+    }
+    // The page's largest V exponent: this wave's four keys (two per half-wave),
+    // then one slot per wave.
+    const float evw = half_swap_max((float)max(ev[0], ev[1]));
     if ((threadIdx.x & 63) == 0) sh.b[buf].evw[slot * kDecodeWaves + (threadIdx.x >> 6)] = (int)evw;
 }
 
 template <int D>
 __device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLds<D, _Float16>& sh, int buf, int slot) {
     constexpr int kRow = PfLds<D, _Float16>::kRow;
+    constexpr int W = kVW<D>;
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const int key = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
         const int at = (slot * kBlockSize + key) * kRow + 64 * i + 4 * part;
         *reinterpret_cast<h4*>(&sh.b[buf].k[at]) = sr.k[i];
-        *reinterpret_cast<h4*>(&sh.b[buf].v[at]) = sr.v[i];
     }
+    const int kg = threadIdx.x >> 5;
+    const int vpart = threadIdx.x & 31;
+    const int pos = 8 * (kg >> 1) + 4 * slot + 2 * (kg & 1);
+#pragma unroll
+    for (int c = 0; c < W; ++c)
+        *reinterpret_cast<h2*>(&sh.b[buf].v[vt_row(W * vpart + c) + pos]) = h2{sr.v[0][c], sr.v[1][c]};
 }
 
 // Q operands of one tile for the K = 32 matrix cores, q[j] = Q[token n][32j + 8g
@@ -456,36 +515,43 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
         // iteration (the empty asm keeps them from being hoisted), so the
         // constant parts go into the instructions' immediate offsets.
         int kq = n * kRow + 8 * g;
-        int vq = 4 * g * kRow + 4 * n;
+        int vq = vt_row(4 * n) + 8 * g;
         asm volatile("" : "+v"(kq), "+v"(vq));
         f4 sc[2][kPrefillTiles];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int s = 0; s < kPrefillTiles; ++s) sc[h][s] = f4{0.f, 0.f, 0.f, 0.f};
+        // Step t = 2j + h takes page h's head dims 32j .. 32j + 31; its K words
+        // are read while step t - 1's products run.  Within a step the tiles'
+        // chains alternate, so no product waits on the one just issued.
+        auto read_k = [&](int t, h8& kh, h8& kl) {
+            const int at = kq + (t & 1) * kBlockSize * kRow + 32 * (t >> 1);
+            if constexpr (kSplitKV) {
+                kh = *reinterpret_cast<const h8*>(&sh.b[buf].kh[at]);
+                kl = *reinterpret_cast<const h8*>(&sh.b[buf].kl[at]);
+            } else {
+                kh = *reinterpret_cast<const h8*>(&sh.b[buf].k[at]);
+            }
+        };
+        h8 nkh, nkl = {};
+        read_k(0, nkh, nkl);
 #pragma unroll
-        for (int j = 0; j < D / 32; ++j) {
-            __builtin_amdgcn_sched_barrier(0);  // K reads one step at a time, as the V reads below
+        for (int t = 0; t < D / 16; ++t) {
+            const h8 kh = nkh, kl = nkl;
+            if (t + 1 < D / 16) read_k(t + 1, nkh, nkl);
+            __builtin_amdgcn_sched_barrier(0);  // one step's reads ahead, no more
+            const int j = t >> 1, h = t & 1;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int at = kq + h * kBlockSize * kRow + 32 * j;
-                if constexpr (kSplitKV) {
-                    const h8 kh = *reinterpret_cast<const h8*>(&sh.b[buf].kh[at]);
-                    const h8 kl = *reinterpret_cast<const h8*>(&sh.b[buf].kl[at]);
+            for (int s = 0; s < kPrefillTiles; ++s)
+                sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].hi[j], sc[h][s], 0, 0, 0);
 #pragma unroll
-                    for (int s = 0; s < kPrefillTiles; ++s) {
-                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].hi[j], sc[h][s], 0, 0, 0);
-                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].lo[j], sc[h][s], 0, 0, 0);
-                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, q[s].hi[j], sc[h][s], 0, 0, 0);
-                    }
-                } else {
-                    const h8 kx = *reinterpret_cast<const h8*>(&sh.b[buf].k[at]);
+            for (int s = 0; s < kPrefillTiles; ++s)
+                sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].lo[j], sc[h][s], 0, 0, 0);
+            if constexpr (kSplitKV) {
 #pragma unroll
-                    for (int s = 0; s < kPrefillTiles; ++s) {
-                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, q[s].hi[j], sc[h][s], 0, 0, 0);
-                        sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, q[s].lo[j], sc[h][s], 0, 0, 0);
-                    }
-                }
+                for (int s = 0; s < kPrefillTiles; ++s)
+                    sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, q[s].hi[j], sc[h][s], 0, 0, 0);
             }
         }
 
@@ -541,48 +607,36 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
             load_regs(2 * i + 3);
         }
 
-        // O += P' . V over the pair's 32 keys: output block 4c + i takes
+        // O += P' . V over the pair's 32 keys: output block b = 4c + i takes
         // B = V[keys][64c + 4n + i] for the same eight keys as the lane's P'
-        // (keys 4g .. 4g + 3 of each page).
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        // (keys 4g .. 4g + 3 of each page), one 16-byte word of the transposed
+        // V.  The words of block b + 1 are read while block b's products run.
+        auto read_v = [&](int b, h8& bh, h8& bl) {
+            const int at = vq + vt_row(64 * (b >> 2)) + kPairKeys * (b & 3);
+            if constexpr (kSplitKV) {
+                bh = *reinterpret_cast<const h8*>(&sh.b[buf].vh[at]);
+                bl = *reinterpret_cast<const h8*>(&sh.b[buf].vl[at]);
+            } else {
+                bh = *reinterpret_cast<const h8*>(&sh.b[buf].v[at]);
+            }
+        };
+        h8 nbh, nbl;
+        read_v(0, nbh, nbl);
 #pragma unroll
-        for (int c = 0; c < D / 64; ++c) {
+        for (int b = 0; b < D / 16; ++b) {
+            const h8 bh = nbh, bl = nbl;
+            if (b + 1 < D / 16) read_v(b + 1, nbh, nbl);
+            __builtin_amdgcn_sched_barrier(0);  // one block's reads ahead, no more
 #pragma unroll
-            for (int eh = 0; eh < 2; ++eh) {  // elements 2 eh and 2 eh + 1 of the lane's four columns
-                // One group of V reads at a time: hoisted together they would
-                // hold every group's operands at once.
-                __builtin_amdgcn_sched_barrier(0);
-                h2 vh[2][4], vl[2][4];
+            for (int s = 0; s < kPrefillTiles; ++s)
+                st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bh, st[s].o[b], 0, 0, 0);
 #pragma unroll
-                for (int h = 0; h < 2; ++h)
+            for (int s = 0; s < kPrefillTiles; ++s)
+                st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s], bh, st[s].o[b], 0, 0, 0);
+            if constexpr (kSplitKV) {
 #pragma unroll
-                    for (int kk = 0; kk < 4; ++kk) {
-                        const int at = vq + (h * kBlockSize + kk) * kRow + 64 * c + 2 * eh;
-                        if constexpr (kSplitKV) {
-                            vh[h][kk] = *reinterpret_cast<const h2*>(&sh.b[buf].vh[at]);
-                            vl[h][kk] = *reinterpret_cast<const h2*>(&sh.b[buf].vl[at]);
-                        } else {
-                            vh[h][kk] = *reinterpret_cast<const h2*>(&sh.b[buf].v[at]);
-                        }
-                    }
-#pragma unroll
-                for (int e2 = 0; e2 < 2; ++e2) {
-                    const int e = 2 * eh + e2;
-                    const h8 bh = {vh[0][0][e2], vh[0][1][e2], vh[0][2][e2], vh[0][3][e2],
-                                   vh[1][0][e2], vh[1][1][e2], vh[1][2][e2], vh[1][3][e2]};
-                    h8 bl;
-                    if constexpr (kSplitKV)
-                        bl = h8{vl[0][0][e2], vl[0][1][e2], vl[0][2][e2], vl[0][3][e2],
-                                vl[1][0][e2], vl[1][1][e2], vl[1][2][e2], vl[1][3][e2]};
-#pragma unroll
-                    for (int s = 0; s < kPrefillTiles; ++s) {
-                        f4 acc = st[s].o[4 * c + e];
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bh, acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s], bh, acc, 0, 0, 0);
-                        if constexpr (kSplitKV) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bl, acc, 0, 0, 0);
-                        st[s].o[4 * c + e] = acc;
-                    }
-                }
+                for (int s = 0; s < kPrefillTiles; ++s)
+                    st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bl, st[s].o[b], 0, 0, 0);
             }
         }
         if (more) stage_store<D>(sr, sh, buf ^ 1, 1);
