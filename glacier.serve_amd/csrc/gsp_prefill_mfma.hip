@@ -89,14 +89,6 @@ __device__ __forceinline__ float max_abs4(const f4& x) {
     return fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
 }
 
-template <typename V>
-__device__ __forceinline__ float max_abs(const V& x) {
-    float m = fabsf(x[0]);
-#pragma unroll
-    for (int i = 1; i < (int)(sizeof(V) / sizeof(x[0])); ++i) m = fmaxf(m, fabsf(x[i]));
-    return m;
-}
-
 template <typename T, int W>
 struct VecW {
     typedef T type __attribute__((ext_vector_type(W)));
@@ -132,18 +124,22 @@ struct PfStage {
 
 // LDS buffers (two), each holding a pair of pages: keys 0..15 of the first
 // page, then 16..31 of the second.  K rows are padded by 8 halves (16 bytes).
-// V is stored transposed, one row of 32 keys per column, with the keys in
-// the order the P.V step consumes them: position 8 q + 4 h + r holds key
-// 4 q + r of page h, so lane group g reads its eight keys (4g .. 4g + 3 of
-// each page) as one 16-byte word.  Every fourth column row is followed by 8
-// halves of padding, which puts the 16 lanes of one read (columns 4n + i) on
-// distinct banks.
+// V is stored transposed, one row per column, with the keys in the order the
+// P.V step consumes them: position 8 q + 4 h + r holds key 4 q + r of page h,
+// so lane group g reads its eight keys (4g .. 4g + 3 of each page) as one
+// 16-byte word.  A row of fp32 pages holds the 32 hi halves, then the 32 lo
+// halves.  Every fourth column row is followed by 8 halves of padding, which
+// puts the 16 lanes of one read (columns 4n + i) on distinct banks.
 constexpr int kPairKeys = 2 * kBlockSize;
 
-template <int D>
-constexpr int kVtLen = D * kPairKeys + (D / 4) * 8;
+template <bool kSplit>
+constexpr int kVtStride = kSplit ? 2 * kPairKeys : kPairKeys;
 
-__device__ __forceinline__ constexpr int vt_row(int col) { return col * kPairKeys + (col >> 2) * 8; }
+template <int D, bool kSplit>
+constexpr int kVtLen = D * kVtStride<kSplit> + (D / 4) * 8;
+
+template <bool kSplit>
+__device__ __forceinline__ constexpr int vt_row(int col) { return col * kVtStride<kSplit> + (col >> 2) * 8; }
 
 template <int D, typename KT>
 struct PfLds;
@@ -153,8 +149,9 @@ struct PfLds;
 template <int D>
 struct alignas(16) PfLdsBuf32 {
     _Float16 kh[kPairKeys * (D + 8)], kl[kPairKeys * (D + 8)];
-    _Float16 vh[kVtLen<D>], vl[kVtLen<D>];
-    int ek[kPairKeys], ev[kPairKeys];  // per-key exponents of the K and V pairs
+    _Float16 vt[kVtLen<D, true>];
+    float ks[kPairKeys];  // 2^e of each key's K pair
+    int ev[kPairKeys];    // exponent of each key's V pair
     int evw[2 * kDecodeWaves];          // largest V exponent of each wave's four keys, per page
 };
 
@@ -167,7 +164,7 @@ struct alignas(16) PfLds<D, float> {
 template <int D>
 struct alignas(16) PfLdsBuf16 {
     _Float16 k[kPairKeys * (D + 8)];
-    _Float16 v[kVtLen<D>];
+    _Float16 v[kVtLen<D, false>];
 };
 
 template <int D>
@@ -198,21 +195,6 @@ __device__ __forceinline__ void stage_load(PfStage<D, KT>& sr, const KT* kpage, 
     for (int kk = 0; kk < 2; ++kk) sr.v[kk] = buffer_load<vvec>(rv, kE * ((2 * kg + kk) * D + kVW<D> * vpart));
 }
 
-// DPP lane moves within a row of 16 lanes (bound_ctrl off: every source lane is in the row).
-template <int kCtrl>
-__device__ __forceinline__ float dpp_mov(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
-}
-
-// Max over the 16 lanes of the caller's DPP row (one key row of the page):
-// lane swaps within quads, then rotations by 4 and 8.
-__device__ __forceinline__ float row16_max(float x) {
-    x = fmaxf(x, dpp_mov<0xB1>(x));   // quad_perm [1, 0, 3, 2]
-    x = fmaxf(x, dpp_mov<0x4E>(x));   // quad_perm [2, 3, 0, 1]
-    x = fmaxf(x, dpp_mov<0x124>(x));  // row_ror:4
-    return fmaxf(x, dpp_mov<0x128>(x));  // row_ror:8
-}
-
 // Max of x over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four rows of a wave),
 // with the row swaps of gfx950: max of the swapped pair is the max across the
 // exchanged rows.
@@ -223,32 +205,70 @@ __device__ __forceinline__ float cross_row_max(float x) {
     return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
 }
 
-// Max over the 32 lanes of the caller's half-wave: its DPP row, then rows
-// swapped in pairs (lanes l and l ^ 16).
-__device__ __forceinline__ float half_wave_max(float x) {
-    x = row16_max(x);
-    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+// pair_exponent from the bit pattern of mx >= 0: for a normal mx, frexp's
+// exponent is the field minus 126; zero and subnormal maxima (field 0) land on
+// the floor as above.  Infinite and NaN maxima take the ceiling and stay
+// non-finite after scaling.
+__device__ __forceinline__ int pair_exponent_bits(uint32_t mb) {
+    return min(100, max(kPairExpFloor, (int)(mb >> 23) - 139));
 }
 
-// Max over lanes l and l ^ 32 (the two half-waves).
-__device__ __forceinline__ float half_swap_max(float x) {
-    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+// Largest |x[i]| as a bit pattern: the lane's elements go through
+// v_max3_f32 with its free |.| modifiers (written out, because fmaxf of
+// loaded values first quiets each input on its own instruction); lanes are
+// then combined with integer maxima, since non-negative floats order like
+// their bits.
+template <typename V>
+__device__ __forceinline__ uint32_t max_abs_bits(const V& x) {
+    constexpr int kN = (int)(sizeof(V) / sizeof(float));
+    static_assert(kN == 2 || kN == 4, "two or four elements");
+    float m;
+    if constexpr (kN == 4) {
+        asm("v_max3_f32 %0, |%1|, |%2|, |%3|" : "=v"(m) : "v"(x[0]), "v"(x[1]), "v"(x[2]));
+        asm("v_max_f32_e64 %0, %1, |%2|" : "=v"(m) : "v"(m), "v"(x[3]));
+    } else {
+        asm("v_max_f32_e64 %0, |%1|, |%2|" : "=v"(m) : "v"(x[0]), "v"(x[1]));
+    }
+    return __float_as_uint(m);
+}
+
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, kCtrl, 0xF, 0xF, true);
+}
+
+// Unsigned max over the 16 lanes of a DPP row (the moves fold into the maxima).
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t x) {
+    x = max(x, dpp_u32<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+    x = max(x, dpp_u32<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+    x = max(x, dpp_u32<0x124>(x));  // row_ror:4
+    return max(x, dpp_u32<0x128>(x));  // row_ror:8
+}
+
+// Unsigned max over lanes l and l ^ 16.
+__device__ __forceinline__ uint32_t swap16_max_u32(uint32_t x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return max(r[0], r[1]);
+}
+
+// Signed max over lanes l and l ^ 32.
+__device__ __forceinline__ int swap32_max_i32(int x) {
+    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
+    return max((int)r[0], (int)r[1]);
 }
 
 template <int D>
 __device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D, float>& sh, int buf, int slot) {
     constexpr int kRow = PfLds<D, float>::kRow;
     constexpr int W = kVW<D>;
-    typedef typename VecW<_Float16, W>::type hW;
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
     const int key = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
-    float mk = 0.f;
+    uint32_t mk = 0;
 #pragma unroll
-    for (int i = 0; i < kStageChunks<D>; ++i) mk = fmaxf(mk, max_abs4(sr.k[i]));
-    const int ek = pair_exponent(row16_max(mk));
+    for (int i = 0; i < kStageChunks<D>; ++i) mk = max(mk, max_abs_bits(sr.k[i]));
+    const int ek = pair_exponent_bits(row16_max_u32(mk));
     const float dk = ldexpf(1.0f, -ek);
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
@@ -258,24 +278,27 @@ __device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D
         *reinterpret_cast<h4*>(&sh.b[buf].kh[at]) = hi;
         *reinterpret_cast<h4*>(&sh.b[buf].kl[at]) = lo;
     }
-    if (part == 0) sh.b[buf].ek[slot * kBlockSize + key] = ek;
+    if (part == 0) sh.b[buf].ks[slot * kBlockSize + key] = ldexpf(1.0f, ek);
 
-    // V, transposed: the lane's columns each take its key pair as one word.
+    // V, transposed: each of the lane's columns takes its key pair as one
+    // word of hi halves and one of lo halves.
     const int kg = threadIdx.x >> 5;
     const int vpart = threadIdx.x & 31;
     int ev[2];
-    hW hi[2], lo[2];
+    float dv[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-        ev[kk] = pair_exponent(half_wave_max(max_abs(sr.v[kk])));
-        split_pair(sr.v[kk] * ldexpf(1.0f, -ev[kk]), hi[kk], lo[kk]);
+        ev[kk] = pair_exponent_bits(swap16_max_u32(row16_max_u32(max_abs_bits(sr.v[kk]))));
+        dv[kk] = ldexpf(1.0f, -ev[kk]);
     }
     const int pos = 8 * (kg >> 1) + 4 * slot + 2 * (kg & 1);  // keys 2 kg, 2 kg + 1 of page `slot`
 #pragma unroll
     for (int c = 0; c < W; ++c) {
-        const int at = vt_row(W * vpart + c) + pos;
-        *reinterpret_cast<h2*>(&sh.b[buf].vh[at]) = h2{hi[0][c], hi[1][c]};
-        *reinterpret_cast<h2*>(&sh.b[buf].vl[at]) = h2{lo[0][c], lo[1][c]};
+        const int at = vt_row<true>(W * vpart + c) + pos;
+        h2 hi, lo;
+        split_pair(f2{sr.v[0][c] * dv[0], sr.v[1][c] * dv[1]}, hi, lo);
+        *reinterpret_cast<h2*>(&sh.b[buf].vt[at]) = hi;
+        *reinterpret_cast<h2*>(&sh.b[buf].vt[at + kPairKeys]) = lo;
     }
     if (vpart == 0) {
         sh.b[buf].ev[slot * kBlockSize + 2 * kg] = ev[0];
@@ -283,8 +306,8 @@ __device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D
     }
     // The page's largest V exponent: this wave's four keys (two per half-wave),
     // then one slot per wave.
-    const float evw = half_swap_max((float)max(ev[0], ev[1]));
-    if ((threadIdx.x & 63) == 0) sh.b[buf].evw[slot * kDecodeWaves + (threadIdx.x >> 6)] = (int)evw;
+    const int evw = swap32_max_i32(max(ev[0], ev[1]));
+    if ((threadIdx.x & 63) == 0) sh.b[buf].evw[slot * kDecodeWaves + (threadIdx.x >> 6)] = evw;
 }
 
 template <int D>
@@ -304,7 +327,7 @@ __device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLd
     const int pos = 8 * (kg >> 1) + 4 * slot + 2 * (kg & 1);
 #pragma unroll
     for (int c = 0; c < W; ++c)
-        *reinterpret_cast<h2*>(&sh.b[buf].v[vt_row(W * vpart + c) + pos]) = h2{sr.v[0][c], sr.v[1][c]};
+        *reinterpret_cast<h2*>(&sh.b[buf].v[vt_row<false>(W * vpart + c) + pos]) = h2{sr.v[0][c], sr.v[1][c]};
 }
 
 // Q operands of one tile for the K = 32 matrix cores, q[j] = Q[token n][32j + 8g
@@ -342,7 +365,7 @@ __device__ __forceinline__ void load_tile_q(TileQ<D>& tq, const float* qrow, boo
     tq.sc = ldexpf(scale, e);
 }
 
-// Per-tile softmax state: O in units of 2^eo, the max m (log2 units) that
+// Per-tile softmax state: O (in the wave's units, see eo below), the max m (log2 units) that
 // token n's probabilities are taken against, partial sum l of token n over
 // this lane's keys.
 template <int D>
@@ -350,7 +373,6 @@ struct TileState {
     f4 o[D / 16];
     float m;
     float l;
-    int eo;
 };
 
 // A row's running max may grow this much (log2 units) before O and l are
@@ -456,7 +478,6 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
         for (int j = 0; j < D / 16; ++j) st[s].o[j] = f4{0.f, 0.f, 0.f, 0.f};
         st[s].m = -INFINITY;
         st[s].l = 0.f;
-        st[s].eo = -1000;  // below any page's V exponent: the first page sets it
     }
 
     const KT* kbase = static_cast<const KT*>(a.k_pool) + a.layer_offset + (int64_t)t.kvh * a.head_stride;
@@ -482,6 +503,9 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
     // Pages go in pairs (32 keys, one v_mfma_f32_16x16x32_f16 step of P.V).
     // The next pair is staged one page at a time: the first after this pair's
     // scores, the second at the end.
+    // O is kept in units of 2^(eo - 12), eo the largest V exponent so far; it is
+    // the same for every tile of the wave, which all see the same pages.
+    int eo = -1000;  // below any page's V exponent: the first page sets it
     const int pairs = (t.pages + 1) >> 1;
     for (int i = 0; i < pairs; ++i) {
         const int buf = i & 1;
@@ -497,14 +521,35 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
         if constexpr (kSplitKV) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                ks0[r] = ldexpf(1.0f, sh.b[buf].ek[4 * g + r]);
-                ks1[r] = ldexpf(1.0f, sh.b[buf].ek[kBlockSize + 4 * g + r]);
+                ks0[r] = sh.b[buf].ks[4 * g + r];
+                ks1[r] = sh.b[buf].ks[kBlockSize + 4 * g + r];
                 evk[r] = sh.b[buf].ev[4 * g + r];
                 evk[4 + r] = sh.b[buf].ev[kBlockSize + 4 * g + r];
             }
             evmax = sh.b[buf].evw[0];
 #pragma unroll
             for (int w = 1; w < 2 * kDecodeWaves; ++w) evmax = max(evmax, sh.b[buf].evw[w]);
+        }
+        // P' = P * pv[key]: 2^(e_v(key) - eo + 12) for fp32 pages (a pair with larger
+        // V exponents raises eo first, and O takes the factor eo_down), 2^12 for
+        // fp16 pages.
+        f4 pv0, pv1;
+        bool eo_up = false;
+        float eo_down = 1.f;
+        if constexpr (kSplitKV) {
+            if (evmax > eo) {
+                eo_up = true;
+                eo_down = ldexpf(1.0f, eo - evmax);  // 0 on the first pair
+                eo = evmax;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pv0[r] = ldexpf(1.0f, evk[r] - eo + kPScaleLog2);
+                pv1[r] = ldexpf(1.0f, evk[4 + r] - eo + kPScaleLog2);
+            }
+        } else {
+            pv0 = f4{1.f, 1.f, 1.f, 1.f} * (float)(1 << kPScaleLog2);
+            pv1 = pv0;
         }
 
         // S^T = K . Q^T for both pages (hi/lo products, one accumulation chain per
@@ -515,7 +560,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
         // iteration (the empty asm keeps them from being hoisted), so the
         // constant parts go into the instructions' immediate offsets.
         int kq = n * kRow + 8 * g;
-        int vq = vt_row(4 * n) + 8 * g;
+        int vq = vt_row<kSplitKV>(4 * n) + 8 * g;
         asm volatile("" : "+v"(kq), "+v"(vq));
         f4 sc[2][kPrefillTiles];
 #pragma unroll
@@ -572,23 +617,12 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
             bool rescale = false;
             pair_softmax<D>(ts, p0, p1, diag, key0, row_ctx, g, alpha_rows, rescale);
 
-            if constexpr (kSplitKV) {
-                // O in units of 2^eo: a pair with larger V exponents raises eo first.
-                if (evmax > ts.eo) {
-                    const float down = ldexpf(1.0f, ts.eo - evmax);  // 0 on the first pair
-                    alpha_rows *= down;
-                    rescale = true;
-                    ts.eo = evmax;
-                }
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    p0[r] = ldexpf(p0[r], evk[r] - ts.eo + kPScaleLog2);
-                    p1[r] = ldexpf(p1[r], evk[4 + r] - ts.eo + kPScaleLog2);
-                }
-            } else {
-                p0 *= (float)(1 << kPScaleLog2);
-                p1 *= (float)(1 << kPScaleLog2);
+            if (eo_up) {
+                alpha_rows *= eo_down;
+                rescale = true;
             }
+            p0 *= pv0;
+            p1 *= pv1;
             if (rescale) {
 #pragma unroll
                 for (int b = 0; b < D / 16; ++b) ts.o[b] *= alpha_rows;
@@ -612,10 +646,10 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
         // (keys 4g .. 4g + 3 of each page), one 16-byte word of the transposed
         // V.  The words of block b + 1 are read while block b's products run.
         auto read_v = [&](int b, h8& bh, h8& bl) {
-            const int at = vq + vt_row(64 * (b >> 2)) + kPairKeys * (b & 3);
+            const int at = vq + vt_row<kSplitKV>(64 * (b >> 2)) + kVtStride<kSplitKV> * (b & 3);
             if constexpr (kSplitKV) {
-                bh = *reinterpret_cast<const h8*>(&sh.b[buf].vh[at]);
-                bl = *reinterpret_cast<const h8*>(&sh.b[buf].vl[at]);
+                bh = *reinterpret_cast<const h8*>(&sh.b[buf].vt[at]);
+                bl = *reinterpret_cast<const h8*>(&sh.b[buf].vt[at + kPairKeys]);
             } else {
                 bh = *reinterpret_cast<const h8*>(&sh.b[buf].v[at]);
             }
@@ -651,7 +685,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
         float ls = st[s].l;
         ls += __shfl_xor(ls, 16);
         ls += __shfl_xor(ls, 32);
-        const float unit = ldexpf(1.0f, (kSplitKV ? st[s].eo : 0) - kPScaleLog2);
+        const float unit = ldexpf(1.0f, (kSplitKV ? eo : 0) - kPScaleLog2);
         f4 inv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) inv[r] = unit / __shfl(ls, 4 * g + r);
