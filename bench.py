@@ -185,6 +185,20 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     torch.cuda.synchronize()
     t_step_ms = (time.perf_counter() - t0) * 1e3 / n_step
 
+    # Distribution of single steps: each between its own events on the launch
+    # stream and waited for alone, so it includes one launch's start-up that the
+    # back-to-back mean hides.  Reported beside ms_per_step, never as value.
+    singles = []
+    for _ in range(max(20, min(200, steps))):
+        a0 = torch.cuda.Event(enable_timing=True)
+        a1 = torch.cuda.Event(enable_timing=True)
+        a0.record(stream)
+        attend()
+        a1.record(stream)
+        a1.synchronize()
+        singles.append(a0.elapsed_time(a1))
+    p10, p50, p90 = (float(x) for x in np.percentile(singles, [10, 50, 90]))
+
     kv_bytes = step.kv_bytes()
     gbs = kv_bytes / (ms_per_step * 1e-3) / 1e9
     kernel_gbs = kv_bytes / (kernel_ms * 1e-3) / 1e9
@@ -261,6 +275,8 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "seq_steps_per_s": round(step.num_rows / (ms_per_step * 1e-3), 1),
         "t_step_ms_incl_pack_upload": round(t_step_ms, 5),
+        "single_step_ms": {"p10": round(p10, 5), "median": round(p50, 5), "p90": round(p90, 5),
+                           "samples": len(singles), "note": "one step at a time, each waited for"},
         "seq_steps_per_s_incl_pack_upload": round(step.num_rows / (t_step_ms * 1e-3), 1),
         "kv_gbs_incl_pack_upload": round(kv_bytes / (t_step_ms * 1e-3) / 1e9, 1),
         "wall_ms_timed_region": round(wall_ms, 3),
