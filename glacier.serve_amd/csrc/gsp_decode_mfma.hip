@@ -459,7 +459,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
         if (pub >= 0 && tid == 0) counted = count_split(a, read_unit(a, pub));
         const bool merge_cnt = cnt >= 0 && sh.last;
         publish_unit<D, kMaxGroupMfma>(a, u, G, sh);
-        if (merge_cnt) merge_pair<D>(a, read_unit(a, cnt), G);
+        if (merge_cnt) merge_pair<D, kMaxGroupMfma, 0>(a, read_unit(a, cnt), G, sh);
         cnt = pub;
         pub = (u.split_info >> 16) > 1 ? ui : -1;
         __syncthreads();  // the epilogue LDS is reused by the next unit
@@ -477,8 +477,8 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
             sh.last_pub = pub >= 0 && prev_pub == (read_unit(a, pub).split_info >> 16) - 1;
         }
         __syncthreads();
-        if (sh.last) merge_pair<D>(a, read_unit(a, cnt), G);
-        if (sh.last_pub) merge_pair<D>(a, read_unit(a, pub), G);
+        if (sh.last) merge_pair<D, kMaxGroupMfma>(a, read_unit(a, cnt), G, sh);
+        if (sh.last_pub) merge_pair<D, kMaxGroupMfma>(a, read_unit(a, pub), G, sh);
     }
 }
 

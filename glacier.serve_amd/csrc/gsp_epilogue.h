@@ -96,11 +96,11 @@ __device__ __forceinline__ int count_split(const DecodeArgs& a, const DecodeUnit
 
 // The last split of u's pair to finish: out = sum_s 2^(m_s - M) O_s / sum_s
 // 2^(m_s - M) l_s over all partials of the pair, then the counter goes back
-// to zero.  Each thread loads the (m, l) and O of up to kMergeChunk splits at
-// once (one round trip for pairs cut into at most that many pieces) and folds
-// chunks together with a running max, as the online softmax does.
+// to zero.  General form, for pairs with many pieces: each thread loads the
+// (m, l) and O of up to kMergeChunk splits at once per element it owns and
+// folds chunks together with a running max, as the online softmax does.
 template <int D>
-__device__ __forceinline__ void merge_pair(const DecodeArgs& a, const DecodeUnit& u, int G) {
+__device__ __forceinline__ void merge_pair_chunked(const DecodeArgs& a, const DecodeUnit& u, int G) {
     const int tid = threadIdx.x;
     const int h0 = u.kvh * G;
     const int nsplit = u.split_info >> 16;
@@ -142,6 +142,115 @@ __device__ __forceinline__ void merge_pair(const DecodeArgs& a, const DecodeUnit
     if (tid == 0) __hip_atomic_store(pair_counter(a, u), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The same merge for pairs with nsplit * G <= one (m, l) per thread.  Each
+// coherent load pays a round trip to the memory side (about 1.3 us while HBM
+// is busy), so the loads are issued together: the pieces' (m, l), one pair per
+// thread, staged in LDS, and at the same time every out element this thread
+// owns (kIdx of them) for kChunk pieces.  Thread g then forms head g's max,
+// weights and sum once, and the weights go back through LDS.  A pair of up to
+// kChunk pieces merges in one round trip, against one per owned element and
+// chunk in the general form.  Up to kMergeChunk pieces, every sum runs in the
+// same order as there, with the same values.  `scr` is LDS the caller no
+// longer reads, with room for 2 * nsplit * G + G floats.
+template <int D, int kIdx, int kLoads>
+__device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const DecodeUnit& u, int G, float* scr) {
+    constexpr int kChunk = kLoads / kIdx;  // out loads in flight per thread: kIdx * kChunk
+    const int tid = threadIdx.x;
+    const int nsplit = u.split_info >> 16;
+    const int n_ml = nsplit * G;
+    const int h0 = u.kvh * G;
+    const int64_t piece = (int64_t)G * D;  // floats per piece in part_o
+    const float* po = a.part_o + (int64_t)u.slot * piece;
+    const float* pml = a.part_ml + (int64_t)u.slot * G * 2;
+    float* sm = scr;           // [s * G + g]: m, then the weight 2^(m - M)
+    float* sl = scr + n_ml;    // [s * G + g]: l
+    float* sinv = sl + n_ml;   // [g]: the sum over pieces (the divisor)
+
+    float mt = -INFINITY, lt = 0.f;
+    if (tid < n_ml) {
+        mt = coherent_load(pml + 2 * tid);
+        lt = coherent_load(pml + 2 * tid + 1);
+    }
+    // Piece bases are wave-uniform and the lane's offset is one unsigned
+    // index, so the loads take a scalar base and a 32-bit lane offset.
+    float os[kIdx][kChunk];
+    const unsigned lane_idx = (unsigned)tid;
+    auto load_chunk = [&](int s0) {
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            const float* pb = po + (int64_t)min(s0 + i, nsplit - 1) * piece;
+#pragma unroll
+            for (int k = 0; k < kIdx; ++k) {
+                const unsigned idx = lane_idx + (unsigned)(k * kDecodeThreads);
+                os[k][i] = (idx < (unsigned)(G * D) && s0 + i < nsplit) ? coherent_load(pb + idx) : 0.f;
+            }
+        }
+    };
+    load_chunk(0);
+    if (tid < n_ml) {
+        sm[tid] = mt;
+        sl[tid] = lt;
+    }
+    __syncthreads();
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, sm[s * G + tid]);
+        float L = 0.f;
+        for (int s = 0; s < nsplit; ++s) {
+            const float m = sm[s * G + tid];
+            const float f = m == -INFINITY ? 0.f : fast_exp2(m - M);
+            sm[s * G + tid] = f;
+            L = fmaf(sl[s * G + tid], f, L);
+        }
+        sinv[tid] = L;
+    }
+    __syncthreads();
+    float O[kIdx];
+#pragma unroll
+    for (int k = 0; k < kIdx; ++k) O[k] = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += kChunk) {
+        if (s0 > 0) load_chunk(s0);
+#pragma unroll
+        for (int k = 0; k < kIdx; ++k) {
+            const int g = min(G - 1, (tid + k * kDecodeThreads) / D);
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i)
+                if (s0 + i < nsplit) O[k] = fmaf(os[k][i], sm[(s0 + i) * G + g], O[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kIdx; ++k) {
+        const int idx = tid + k * kDecodeThreads;
+        if (idx < G * D) {
+            const int g = idx / D;
+            a.out[((int64_t)u.qi * a.n_heads + h0 + g) * D + (idx - g * D)] = O[k] / sinv[g];
+        }
+    }
+    if (tid == 0) __hip_atomic_store(pair_counter(a, u), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge entry: the wide form when the pair's (m, l) fit one per thread and
+// the LDS scratch, else the general one.  Called by every thread of the
+// workgroup (the condition is workgroup-uniform); the epilogue's LDS is
+// reused as scratch once all threads are past their reads of it.  kLoads is
+// the out loads a thread keeps in flight; 0 keeps the general form, for call
+// sites where the next unit's pages already hold most registers (the wide
+// form spills there).
+template <int D, int GMAX, int kLoads = 32>
+__device__ __forceinline__ void merge_pair(const DecodeArgs& a, const DecodeUnit& u, int G, EpilogueLds<D, GMAX>& sh) {
+    const int n_ml = (u.split_info >> 16) * G;
+    constexpr int kScratch = kDecodeWaves * GMAX * D;
+    if (kLoads > 0 && n_ml <= kDecodeThreads && 2 * n_ml + G <= kScratch && G * D <= 8 * kDecodeThreads) {
+        __syncthreads();
+        if (G * D <= 4 * kDecodeThreads)
+            merge_pair_wide<D, 4, (kLoads > 0 ? kLoads : 4)>(a, u, G, &sh.o[0][0][0]);
+        else
+            merge_pair_wide<D, 8, (kLoads > 0 ? kLoads : 8)>(a, u, G, &sh.o[0][0][0]);
+    } else {
+        merge_pair_chunked<D>(a, u, G);
+    }
+}
+
 // publish_unit, then for a split piece the counter protocol on the spot:
 // wait for the partial, count it, and merge the pair if it was the last one.
 template <int D, int GMAX>
@@ -154,7 +263,7 @@ __device__ __forceinline__ void finish_unit(const DecodeArgs& a, const DecodeUni
     __syncthreads();
     if (threadIdx.x == 0) sh.last = (count_split(a, u) == nsplit - 1);
     __syncthreads();
-    if (sh.last) merge_pair<D>(a, u, G);
+    if (sh.last) merge_pair<D, GMAX>(a, u, G, sh);
 }
 
 }  // namespace gsp
