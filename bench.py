@@ -288,6 +288,7 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     result.update(extra)
     result["host_prefix_cache"] = host_prefix_cache(gsp, step)
     result["rope_write"] = rope_write_timing(gsp, torch, ctx, stream, step)
+    result["matmul"] = matmul_timing(gsp, torch, ctx, stream, step)
 
     if cpu:
         result["cpu_baseline"], ref = cpu_baseline(step, q, k, v, cpu_budget_s)
@@ -297,6 +298,43 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     pool.destroy()
     ctx.close()
     return result
+
+
+def matmul_timing(gsp, torch, ctx, stream, step, calls: int = 50) -> dict:
+    """Device cost of the step's Q projection (QuantKernels.MatMulBatch, PagedTransformerRunner.cs:601):
+    hidden = n_heads * head_dim in and out, one batch row per query token of the step, random
+    weights as Q8_0 and as F32.  The products are fp32 on the fp32 matrix cores, so the roofline
+    is 157.3 TFLOP/s; weight streaming bounds it only for small batches."""
+    hidden = step.n_heads * step.head_dim
+    batch = int(step.total_q)
+    gen = torch.Generator(device="cuda").manual_seed(step.seed)
+    x = torch.randn((batch, hidden), device="cuda", generator=gen)
+    y = torch.empty((batch, hidden), device="cuda")
+    nb = hidden // 32
+    d = (torch.randn((hidden, nb, 1), device="cuda", generator=gen) * 0.01).half().view(torch.uint8)
+    q = torch.randint(-127, 128, (hidden, nb, 32), device="cuda", generator=gen, dtype=torch.int8).view(torch.uint8)
+    weights = {"q8_0": (gsp.WTYPE_Q8_0, torch.cat([d, q], dim=2).contiguous(), hidden * nb * 34),
+               "f32": (gsp.WTYPE_F32, torch.randn((hidden, hidden), device="cuda", generator=gen), hidden * hidden * 4)}
+    torch.cuda.synchronize()
+    flops = 2.0 * batch * hidden * hidden
+    out = {"in_dim": hidden, "out_dim": hidden, "batch": batch}
+    for name, (wt, w, wbytes) in weights.items():
+        args = (wt, w.data_ptr(), x.data_ptr(), y.data_ptr(), hidden, hidden, batch)
+        with torch.cuda.stream(stream):
+            for _ in range(5):
+                ctx.matmul_batch(*args)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(calls):
+                ctx.matmul_batch(*args)
+            e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / calls * 1e3
+        out[name] = {"us_per_call": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 2),
+                     "frac_fp32_matrix_peak": round(flops / (us * 1e-6) / 1e12 / 157.3, 4),
+                     "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1)}
+    return out
 
 
 def rope_write_timing(gsp, torch, ctx, stream, step, calls: int = 100) -> dict:

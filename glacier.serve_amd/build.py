@@ -22,6 +22,7 @@ SOURCES = [
     CSRC / "gsp_decode_mfma.hip",
     CSRC / "gsp_prefill_mfma.hip",
     CSRC / "gsp_pool_ops.hip",
+    CSRC / "gsp_matmul.hip",
     CSRC / "gsp_runtime.cpp",
     CSRC / "gsp_host_meta.cpp",
     CSRC / "gsp_status.cpp",

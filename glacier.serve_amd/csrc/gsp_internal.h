@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 namespace gsp {
@@ -139,6 +140,23 @@ struct RopeWriteArgs {
 };
 
 hipError_t launch_rope_write(int kv_f16, const RopeWriteArgs& a, hipStream_t stream);
+
+// Projection GEMM (gsp_matmul.hip): y[b][o] = sum_i W[o][i] x[b][i].
+constexpr int kWeightF32 = 0;   // GGUF type ids
+constexpr int kWeightQ8_0 = 8;
+struct MatmulArgs {
+    const void* w;       // out_dim rows of in_dim weights (F32, or Q8_0 blocks of 34 bytes)
+    const float* x;      // [batch][in_dim]
+    float* y;            // [batch][out_dim]
+    float* split_out;    // [splits][batch][out_dim] partials when splits > 1, else null
+    int32_t w_type;
+    int32_t in_dim;      // a multiple of 64
+    int32_t out_dim;
+    int32_t batch;
+    int32_t splits;            // K ranges over grid.z
+    int32_t chunks_per_split;  // 64-wide K chunks per range
+};
+hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream);
 
 struct CopyBlockArgs {
     void* k_pool;

@@ -1,0 +1,203 @@
+// Batched projection GEMM of the engine step, gfx950:
+//   y[b][o] = sum_i W[o][i] * x[b][i]
+// the product QuantKernels.MatMulBatch(type, W, x, y, inDim, outDim, batch)
+// computes around the attention step (PagedTransformerRunner.cs:601-603,659).
+// W holds out_dim rows of in_dim weights (the GGUF [in, out] layout) as F32 or
+// Q8_0 (blocks of 32 int8 with an fp16 scale d: w = d * q).
+//
+// The arithmetic is fp32: every weight is exact in fp32 (Q8_0's d * q has at
+// most 19 significant bits), and the products run on v_mfma_f32_16x16x4f32
+// with fp32 accumulation, so no operand is rounded below fp32.
+//
+// A workgroup (four waves) owns 64 weight rows (16 per wave, MFMA M) and 64
+// batch rows (four 16-column MFMA tiles, N) over a range of K, in 64-wide
+// chunks.  Each chunk of x is staged once in LDS and serves all four waves;
+// lane group g = lane / 16 supplies k = k0 + 16 g + s at step s of the chunk
+// in both operands, so each lane reads 16 contiguous weights of its row from
+// memory and 16 contiguous inputs of a batch row from LDS.  The next chunk's
+// weights and x load while the current chunk computes.  When the host splits
+// K over grid.z workgroups, each writes its sums to a partial buffer and a
+// second kernel adds the partials in order, so results do not depend on
+// timing.
+#include "gsp_internal.h"
+
+namespace gsp {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMmThreads = 256;
+constexpr int kMmRowsWg = 64;  // weight rows per workgroup, 16 per wave
+
+// The lane's 16 weights of row o at columns k0 + 16 g .. + 15.
+template <int WT>
+__device__ __forceinline__ void load_weights(float (&w)[16], const MatmulArgs& a, int o, int k0, int g);
+
+template <>
+__device__ __forceinline__ void load_weights<kWeightF32>(float (&w)[16], const MatmulArgs& a, int o, int k0, int g) {
+    const f4* p = reinterpret_cast<const f4*>(static_cast<const float*>(a.w) + (int64_t)o * a.in_dim + k0 + 16 * g);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f4 v = p[j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[4 * j + e] = v[e];
+    }
+}
+
+// Q8_0: a 64-wide chunk of a row is two 34-byte blocks, 68 bytes starting at a
+// multiple of 4 (in_dim is a multiple of 64).  Lane group g's 16 values sit at
+// bytes 2 + 16 g (g < 2, first block) or 36 + 16 (g - 2) (second block): the
+// lane reads the five dwords from (byte 0, 16, 36, 52) and shifts out the
+// first 2 (g < 2) or 0 bytes.  Its block's scale is the low half of dword 0
+// or the high half of dword 8.  Every dword read lies inside the chunk.
+template <>
+__device__ __forceinline__ void load_weights<kWeightQ8_0>(float (&w)[16], const MatmulArgs& a, int o, int k0, int g) {
+    const int64_t row_bytes = (int64_t)(a.in_dim / 32) * 34;
+    const uint32_t* cw = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)o * row_bytes +
+                                                           (int64_t)(k0 / 64) * 68);
+    const int first = g < 2 ? 4 * g : 9 + 4 * (g - 2);
+    const int shift = g < 2 ? 2 : 0;
+    uint32_t dw[5];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dw[i] = cw[first + i];
+    dw[4] = cw[g < 2 ? first + 4 : first + 3];  // only read as the high half of a 2-byte shift
+    const uint32_t sw = cw[g < 2 ? 0 : 8];
+    const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(g < 2 ? (sw & 0xFFFFu) : (sw >> 16)));
+    const float d = (float)dh;
+    const float bias = -128.0f * d;  // w = d * (u - 128) for the byte u = q ^ 0x80, exact in one fma
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t qd = __builtin_amdgcn_alignbyte(dw[i + 1], dw[i], shift) ^ 0x80808080u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[4 * i + e] = fmaf((float)((qd >> (8 * e)) & 0xFFu), d, bias);
+    }
+}
+
+template <int WT>
+__global__ __launch_bounds__(kMmThreads, 2) void matmul_batch_kernel(MatmulArgs a) {
+    // The chunk of x (64 batch rows x 64 k), two buffers; rows padded by one
+    // 16-byte word so that the 16 lanes of one read hit distinct banks.
+    __shared__ f4 xs[2][64][17];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int m = lane & 15;  // weight row of the wave's tile (A) and batch row within a tile (B)
+    const int g = lane >> 4;  // K group
+    const int o0 = blockIdx.x * kMmRowsWg + 16 * wave;
+    const int b0 = blockIdx.y * 64;
+    const int nt = min(4, (a.batch - b0 + 15) >> 4);  // batch tiles in use
+    const int o = min(o0 + m, a.out_dim - 1);          // rows past out_dim load row out_dim - 1, never stored
+    const int chunks = a.in_dim / 64;
+    const int c_begin = blockIdx.z * a.chunks_per_split;
+    const int c_end = min(chunks, c_begin + a.chunks_per_split);
+
+    // x staging: thread tid moves batch row tid / 4, columns 16 (tid % 4) .. + 15.
+    const int xr = tid >> 2;
+    const int xq = tid & 3;
+    const f4* xsrc = reinterpret_cast<const f4*>(a.x + (int64_t)min(b0 + xr, a.batch - 1) * a.in_dim + 16 * xq);
+    f4 xreg[4];
+    float wreg[16];
+    auto load_chunk = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xreg[j] = xsrc[16 * c + j];
+        load_weights<WT>(wreg, a, o, 64 * c, g);
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xs[buf][xr][4 * xq + j] = xreg[j];
+    };
+
+    f4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    if (c_begin < c_end) {
+        load_chunk(c_begin);
+        store_x(0);
+    }
+    __syncthreads();
+    for (int c = c_begin; c < c_end; ++c) {
+        const int buf = (c - c_begin) & 1;
+        float w[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) w[i] = wreg[i];
+        const bool more = c + 1 < c_end;
+        if (more) load_chunk(c + 1);  // the next chunk loads while this one computes
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if (t < nt) {
+                float xv[16];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f4 v = xs[buf][16 * t + m][4 * g + j];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) xv[4 * j + e] = v[e];
+                }
+#pragma unroll
+                for (int s2 = 0; s2 < 16; ++s2)
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[s2], xv[s2], acc[t], 0, 0, 0);
+            }
+        }
+        if (more) store_x(buf ^ 1);  // the other buffer's last readers passed the previous barrier
+        __syncthreads();
+    }
+
+    // Lane holds weight rows o0 + 4 g + r of batch row b0 + 16 t + m.
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int b = b0 + 16 * t + m;
+        if (t >= nt || b >= a.batch) continue;
+        float* dst = a.split_out ? a.split_out + ((int64_t)blockIdx.z * a.batch + b) * a.out_dim
+                                 : a.y + (int64_t)b * a.out_dim;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int oo = o0 + 4 * g + r;
+            if (oo < a.out_dim) dst[oo] = acc[t][r];
+        }
+    }
+}
+
+// y = the sum over z of the split partials, in z order; four elements per
+// thread and step when y and the partials are 16-byte aligned, else one.
+__global__ __launch_bounds__(kMmThreads) void matmul_reduce_kernel(MatmulArgs a) {
+    const int64_t n = (int64_t)a.batch * a.out_dim;
+    const int64_t stride = (int64_t)gridDim.x * kMmThreads;
+    const int64_t first = (int64_t)blockIdx.x * kMmThreads + threadIdx.x;
+    if (n % 4 == 0 && reinterpret_cast<uintptr_t>(a.y) % 16 == 0) {
+        const f4* src = reinterpret_cast<const f4*>(a.split_out);
+        f4* dst = reinterpret_cast<f4*>(a.y);
+        const int64_t n4 = n / 4;
+        for (int64_t i = first; i < n4; i += stride) {
+            f4 s = src[i];
+            for (int z = 1; z < a.splits; ++z) s += src[(int64_t)z * n4 + i];
+            dst[i] = s;
+        }
+        return;
+    }
+    for (int64_t i = first; i < n; i += stride) {
+        float s = a.split_out[i];
+        for (int z = 1; z < a.splits; ++z) s += a.split_out[(int64_t)z * n + i];
+        a.y[i] = s;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream) {
+    if (a.batch <= 0 || a.out_dim <= 0) return hipSuccess;
+    const dim3 grid((a.out_dim + kMmRowsWg - 1) / kMmRowsWg, (a.batch + 63) / 64, a.splits);
+    if (a.w_type == kWeightF32)
+        hipLaunchKernelGGL(matmul_batch_kernel<kWeightF32>, grid, dim3(kMmThreads), 0, stream, a);
+    else if (a.w_type == kWeightQ8_0)
+        hipLaunchKernelGGL(matmul_batch_kernel<kWeightQ8_0>, grid, dim3(kMmThreads), 0, stream, a);
+    else
+        return hipErrorInvalidValue;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.splits <= 1) return e;
+    const int64_t n = (int64_t)a.batch * a.out_dim;
+    const int blocks = (int)std::min<int64_t>((n / 4 + kMmThreads - 1) / kMmThreads + 1, 2048);
+    hipLaunchKernelGGL(matmul_reduce_kernel, dim3(blocks), dim3(kMmThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace gsp

@@ -141,6 +141,9 @@ struct gsp_ctx {
     size_t aux_words = 0;
     int32_t* d_aux = nullptr;
     size_t d_aux_words = 0;
+    // Split-K partials of gsp_matmul_batch.
+    float* d_mm = nullptr;
+    size_t d_mm_floats = 0;
     hipEvent_t aux_done = nullptr;
     bool aux_pending = false;
 
@@ -348,6 +351,7 @@ void gsp_shutdown(gsp_ctx* ctx) {
     if (ctx->aux) (void)hipHostFree(ctx->aux);
     if (ctx->d_step) (void)hipFree(ctx->d_step);
     if (ctx->d_aux) (void)hipFree(ctx->d_aux);
+    if (ctx->d_mm) (void)hipFree(ctx->d_mm);
     if (ctx->part) (void)hipFree(ctx->part);
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->staging_done) (void)hipEventDestroy(ctx->staging_done);
@@ -594,6 +598,55 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
     a.head_dim = d.head_dim;
     a.style = style;
     return check_hip(gsp::launch_rope_write(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "rope_write launch");
+}
+
+int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const float* x_dev, float* y_dev,
+                     int32_t in_dim, int32_t out_dim, int32_t batch) {
+    gsp::clear_error();
+    if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
+    if (in_dim < 0 || out_dim < 0 || batch < 0)
+        return gsp::fail(GSP_E_INVALID_ARG, "negative size (inDim %d, outDim %d, batch %d)", in_dim, out_dim, batch);
+    if (batch == 0 || out_dim == 0) return GSP_OK;
+    if (!w_dev || !x_dev || !y_dev) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument");
+    if (w_type != GSP_WTYPE_F32 && w_type != GSP_WTYPE_Q8_0)
+        return gsp::fail(GSP_E_UNSUPPORTED, "weight type %d: only F32 (%d) and Q8_0 (%d) are supported", w_type,
+                         GSP_WTYPE_F32, GSP_WTYPE_Q8_0);
+    if (in_dim == 0 || in_dim % 64 != 0)
+        return gsp::fail(GSP_E_UNSUPPORTED, "inDim must be a positive multiple of 64 (got %d)", in_dim);
+    const uintptr_t walign = w_type == GSP_WTYPE_F32 ? 16 : 4;
+    if (reinterpret_cast<uintptr_t>(w_dev) % walign != 0 || reinterpret_cast<uintptr_t>(x_dev) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(y_dev) % 4 != 0)
+        return gsp::fail(GSP_E_INVALID_ARG, "weights must be %d-byte aligned, x 16-byte aligned, y 4-byte aligned",
+                         (int)walign);
+    int rc = set_device(ctx);
+    if (rc) return rc;
+    // Split K over grid.z until the grid has about two workgroups (64 weight rows
+    // x 64 batch rows each) per CU, keeping at least two 64-wide chunks in every
+    // range so that loads overlap the products.
+    const int64_t chunks = in_dim / 64;
+    const int64_t base = (int64_t)((out_dim + 63) / 64) * ((batch + 63) / 64);
+    const int64_t want = std::max<int64_t>(1, (2 * (int64_t)std::max(1, ctx->num_cus) + base - 1) / base);
+    const int64_t splits_max = std::max<int64_t>(1, chunks / 2);
+    int64_t splits = std::min(want, splits_max);
+    const int64_t per = (chunks + splits - 1) / splits;
+    splits = (chunks + per - 1) / per;
+    gsp::MatmulArgs a;
+    a.w = w_dev;
+    a.x = x_dev;
+    a.y = y_dev;
+    a.split_out = nullptr;
+    a.w_type = w_type;
+    a.in_dim = in_dim;
+    a.out_dim = out_dim;
+    a.batch = batch;
+    a.splits = (int32_t)splits;
+    a.chunks_per_split = (int32_t)per;
+    if (splits > 1) {
+        rc = ensure_device(ctx, &ctx->d_mm, &ctx->d_mm_floats, (size_t)splits * batch * out_dim, false);
+        if (rc) return rc;
+        a.split_out = ctx->d_mm;
+    }
+    return check_hip(gsp::launch_matmul(a, ctx->stream), "matmul launch");
 }
 
 int gsp_pool_copy_block(gsp_ctx* ctx, gsp_pool* pool, int32_t src, int32_t dst, int32_t valid_tokens) {

@@ -50,6 +50,7 @@ PREFILL_TILES = 1
 PREFILL_PER_TOKEN = 2
 ROPE_PAIRS = 0
 ROPE_HALVES = 1
+WTYPE_F32, WTYPE_Q8_0 = 0, 8  # GGUF tensor type ids (gsp_matmul_batch)
 BLOCK_SIZE = 16
 
 
@@ -170,6 +171,7 @@ _SIGNATURES = {
     ),
     "gsp_pool_write_tokens": (ctypes.c_int, [vp, vp, i32, i32, i32p, i32p, vp, vp]),
     "gsp_rope_write_tokens": (ctypes.c_int, [vp, vp, i32, i32, i32p, i32p, i32p, i32, ctypes.c_float, i32, vp, vp, vp]),
+    "gsp_matmul_batch": (ctypes.c_int, [vp, i32, vp, vp, vp, i32, i32, i32]),
     "gsp_pool_copy_block": (ctypes.c_int, [vp, vp, i32, i32, i32]),
     "gsp_pool_upload": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
     "gsp_pool_download": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
@@ -284,6 +286,13 @@ class Context:
 
     def sync(self) -> None:
         _check(self._lib.gsp_sync(self._h))
+
+    def matmul_batch(self, w_type: int, w_ptr: int, x_ptr: int, y_ptr: int, in_dim: int, out_dim: int,
+                     batch: int) -> None:
+        """QuantKernels.MatMulBatch (PagedTransformerRunner.cs:601-603,659) on device pointers:
+        y[b][o] = sum_i W[o][i] x[b][i], W as F32 or Q8_0 rows (WTYPE_*)."""
+        _check(self._lib.gsp_matmul_batch(self._h, int(w_type), vp(w_ptr), vp(x_ptr), vp(y_ptr), int(in_dim),
+                                          int(out_dim), int(batch)))
 
     def set_split_pages(self, pages: int) -> None:
         """Largest split-KV unit in pages for the next pack (0: sized from the step and device)."""

@@ -40,7 +40,7 @@ extern "C" {
 #pragma GCC visibility push(default)
 #endif
 
-#define GSP_ABI_VERSION 5
+#define GSP_ABI_VERSION 6
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
 
 typedef enum gsp_status {
@@ -167,6 +167,23 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
                           const int32_t* positions, const int32_t* block_ids,
                           const int32_t* slots, int32_t n_heads, float freq_base, int32_t style,
                           float* q_dev, const float* k_dev, const float* v_dev);
+
+/* Weight types of gsp_matmul_batch: the GGUF tensor type ids. */
+#define GSP_WTYPE_F32 0
+#define GSP_WTYPE_Q8_0 8
+
+/* QuantKernels.MatMulBatch(type, weight, x, y, inDim, outDim, batchSize, xBlockSums)
+ * (PagedTransformerRunner.cs:601-603 for Q/K/V, :659 for the attention
+ * output): y[b][o] = sum_i W[o][i] * x[b][i] for b < batch, o < out_dim.  w_dev
+ * holds out_dim rows of in_dim weights (the GGUF [in, out] layout), as fp32
+ * (GSP_WTYPE_F32, 16-byte aligned) or Q8_0 (GSP_WTYPE_Q8_0: per 32 weights a
+ * little-endian fp16 scale d and 32 int8 q, w = d * q; 4-byte aligned).
+ * x_dev is [batch][in_dim] fp32 (16-byte aligned), y_dev [batch][out_dim] fp32,
+ * overwritten; all device pointers.  Products and sums are fp32.  in_dim must
+ * be a multiple of 64 (GSP_E_UNSUPPORTED otherwise, as for other weight
+ * types); the reference's block sums are not needed by these two types. */
+int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const float* x_dev, float* y_dev,
+                     int32_t in_dim, int32_t out_dim, int32_t batch);
 
 /* PagedBlockPool.CopyBlockData (PagedBlockPool.cs:304-327): copies the first
  * min(valid_tokens, block_size) slots of every layer and KV head of block

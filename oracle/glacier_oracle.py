@@ -1,7 +1,8 @@
 """ctypes wrapper of liboracle.so — TEST INFRASTRUCTURE ONLY.
 
 The oracle is the CPU restatement of the reference's paged-attention path
-(PagedAttentionKernel.cs:17-372, PagedBlockPool.cs, BlockTable.cs).  Only
+(PagedAttentionKernel.cs:17-372, PagedBlockPool.cs, BlockTable.cs), plus the
+Q8_0 weight encoding and the product of the projection GEMMs around it.  Only
 tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as
 the checker or the timed CPU baseline; the product never does.
 """
@@ -128,6 +129,51 @@ def rope(x: np.ndarray, pos: int, freq_base: float, style: int = ROPE_PAIRS) -> 
     dim = y.shape[-1]
     load().orc_rope(y.ctypes.data_as(f32p), y.size // dim, dim, int(pos), float(freq_base), int(style))
     return y
+
+
+# Projection GEMM weights (QuantKernels.MatMulBatch, PagedTransformerRunner.cs:601-603,659).
+WTYPE_F32, WTYPE_Q8_0 = 0, 8  # GGUF tensor type ids
+Q8_0_BLOCK, Q8_0_BYTES = 32, 34
+
+
+def q8_0_encode(values) -> np.ndarray:
+    """Q8_0 bytes of a float32 array whose length is a multiple of 32, as the reference's test
+    builder writes them (PhaseCServeRemediationTests.cs:1587-1622).  Per block of 32 values:
+    d = (Half)(maxAbs / 127f) (round to nearest even), invD = 1f / d in float32 (0 when d is 0),
+    q = MathF.Round(v * invD) (to nearest even) clamped to [-127, 127]; stored as d's two bytes
+    (little-endian) followed by the 32 int8."""
+    v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1, Q8_0_BLOCK)
+    d16 = (np.abs(v).max(axis=1) / np.float32(127.0)).astype(np.float16)
+    d = d16.astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(d > 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
+    q = np.clip(np.rint(v * inv[:, None]), -127, 127).astype(np.int8)
+    out = np.empty((v.shape[0], Q8_0_BYTES), np.uint8)
+    out[:, :2] = d16.view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = q.view(np.uint8)
+    return out.reshape(-1)
+
+
+def q8_0_decode(data, rows: int, cols: int) -> np.ndarray:
+    """Dequantised float64 [rows, cols] of Q8_0 rows (each row cols / 32 blocks): d * q."""
+    b = np.ascontiguousarray(data, dtype=np.uint8).reshape(rows, cols // Q8_0_BLOCK, Q8_0_BYTES)
+    d = np.ascontiguousarray(b[:, :, :2]).view(np.float16)[..., 0].astype(np.float64)
+    q = np.ascontiguousarray(b[:, :, 2:]).view(np.int8).astype(np.float64)
+    return (q * d[..., None]).reshape(rows, cols)
+
+
+def matmul_batch(w_type: int, w, x, in_dim: int, out_dim: int) -> np.ndarray:
+    """y[b][o] = sum_i W[o][i] * x[b][i] in float64: the product MatMulBatch computes (its own
+    arithmetic is closed code, so only this definition is restated).  W holds out_dim rows of in_dim
+    weights, the GGUF [in, out] layout; x is [batch, in_dim]."""
+    if w_type == WTYPE_F32:
+        wm = np.asarray(w, dtype=np.float32).reshape(out_dim, in_dim).astype(np.float64)
+    elif w_type == WTYPE_Q8_0:
+        wm = q8_0_decode(w, out_dim, in_dim)
+    else:
+        raise ValueError(f"weight type {w_type} is not restated")
+    xm = np.asarray(x, dtype=np.float32).reshape(-1, in_dim).astype(np.float64)
+    return xm @ wm.T
 
 
 class HostPool:

@@ -1,0 +1,92 @@
+"""gsp_matmul_batch (QuantKernels.MatMulBatch, PagedTransformerRunner.cs:601-603,659) against the oracle.
+
+y[b][o] = sum_i W[o][i] x[b][i] with F32 or Q8_0 weights.  The device forms every weight exactly
+in fp32 and sums fp32 products, so the bar is fp32 summation error: |y - y64| <= 1e-5 * sum_i
+|W[o][i] x[b][i]| + 1e-7, against the float64 oracle on the same encoded weights.  The shapes
+cover a single batch row, batches below, at and above one 64-row workgroup tile with ragged
+ends, output counts that are not multiples of 16, one K range and several (split K).
+"""
+import numpy as np
+import pytest
+
+import glacier_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    # (in_dim, out_dim, batch)
+    (64, 16, 1),
+    (128, 40, 5),
+    (896, 1152, 8),
+    (3584, 512, 64),
+    (256, 96, 100),
+    (4096, 48, 17),
+]
+
+
+def _weights(rng, w_type, out_dim, in_dim):
+    w = (rng.standard_normal((out_dim, in_dim)) * rng.choice([0.02, 1.0, 30.0], (out_dim, 1))).astype(np.float32)
+    if w_type == orc.WTYPE_F32:
+        return w, w.astype(np.float64)
+    data = orc.q8_0_encode(w)
+    return data, orc.q8_0_decode(data, out_dim, in_dim)
+
+
+def _run(torch, gsp, ctx, w_type, data, x, in_dim, out_dim, fill=np.nan):
+    wd = torch.from_numpy(np.ascontiguousarray(data)).cuda()
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    yd = torch.full((x.shape[0], out_dim), float(fill), device="cuda")
+    torch.cuda.synchronize()
+    ctx.matmul_batch(w_type, wd.data_ptr(), xd.data_ptr(), yd.data_ptr(), in_dim, out_dim, x.shape[0])
+    ctx.sync()
+    return yd.cpu().numpy()
+
+
+@pytest.mark.parametrize("w_type", [orc.WTYPE_F32, orc.WTYPE_Q8_0], ids=["f32", "q8_0"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"in{s[0]}_out{s[1]}_b{s[2]}")
+def test_matmul_matches_oracle(torch_mod, gsp, ctx, shape, w_type):
+    in_dim, out_dim, batch = shape
+    print(f"case matmul {shape} type={w_type}", flush=True)
+    rng = np.random.default_rng(in_dim + out_dim + batch + w_type)
+    data, wm = _weights(rng, w_type, out_dim, in_dim)
+    x = rng.standard_normal((batch, in_dim)).astype(np.float32)
+    got = _run(torch_mod, gsp, ctx, w_type, data, x, in_dim, out_dim)
+    ref = orc.matmul_batch(w_type, data, x, in_dim, out_dim)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wm).T
+    assert np.all(np.isfinite(got))
+    assert np.all(np.abs(got - ref) <= 1e-5 * mag + 1e-7)
+    # Deterministic: the split-K partials are added in a fixed order.
+    again = _run(torch_mod, gsp, ctx, w_type, data, x, in_dim, out_dim)
+    assert np.array_equal(got, again)
+
+
+def test_matmul_errors_and_empty(torch_mod, gsp, ctx):
+    torch = torch_mod
+    w = torch.zeros((16, 96), device="cuda")
+    x = torch.zeros((4, 128), device="cuda")
+    y = torch.full((4, 16), 7.0, device="cuda")
+    torch.cuda.synchronize()
+    with pytest.raises(gsp.Unsupported):  # Q4_0 and the other GGUF types are not supported
+        ctx.matmul_batch(2, w.data_ptr(), x.data_ptr(), y.data_ptr(), 64, 16, 4)
+    with pytest.raises(gsp.Unsupported):  # in_dim not a multiple of 64
+        ctx.matmul_batch(gsp.WTYPE_F32, w.data_ptr(), x.data_ptr(), y.data_ptr(), 96, 16, 4)
+    with pytest.raises(gsp.InvalidArgument):  # x not 16-byte aligned
+        ctx.matmul_batch(gsp.WTYPE_F32, w.data_ptr(), x.data_ptr() + 4, y.data_ptr(), 64, 16, 2)
+    with pytest.raises(gsp.InvalidArgument):
+        ctx.matmul_batch(gsp.WTYPE_F32, 0, x.data_ptr(), y.data_ptr(), 64, 16, 4)
+    ctx.matmul_batch(gsp.WTYPE_F32, w.data_ptr(), x.data_ptr(), y.data_ptr(), 64, 16, 0)  # batch 0: no work
+    ctx.sync()
+    assert torch.all(y == 7.0)
+
+
+def test_matmul_q_projection_then_attention_shapes(torch_mod, gsp, ctx):
+    """The Q projection of a Qwen2.5-7B layer (3584 -> 3584) for 64 decode rows, Q8_0 weights:
+    the product the reference runs before RoPE and attention (PagedTransformerRunner.cs:601)."""
+    rng = np.random.default_rng(11)
+    in_dim = out_dim = 3584
+    data, wm = _weights(rng, orc.WTYPE_Q8_0, out_dim, in_dim)
+    x = rng.standard_normal((64, in_dim)).astype(np.float32)
+    got = _run(torch_mod, gsp, ctx, orc.WTYPE_Q8_0, data, x, in_dim, out_dim)
+    ref = x.astype(np.float64) @ wm.T
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wm).T
+    assert np.all(np.abs(got - ref) <= 1e-5 * mag + 1e-7)
