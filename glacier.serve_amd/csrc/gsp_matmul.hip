@@ -29,19 +29,36 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kMmThreads = 256;
 constexpr int kMmRowsWg = 64;  // weight rows per workgroup, 16 per wave
 
-// The lane's 16 weights of row o at columns k0 + 16 g .. + 15.
+// The lane's 16 weights of row o at columns k0 + 16 g .. + 15, in two steps:
+// load_raw issues the loads into registers, expand turns them into floats.
+// A chunk's raw words are loaded one chunk ahead and expanded only when the
+// chunk is computed, so the loads have a whole chunk of products to arrive.
 template <int WT>
-__device__ __forceinline__ void load_weights(float (&w)[16], const MatmulArgs& a, int o, int k0, int g);
+struct WRaw;
 
 template <>
-__device__ __forceinline__ void load_weights<kWeightF32>(float (&w)[16], const MatmulArgs& a, int o, int k0, int g) {
+struct WRaw<kWeightF32> {
+    f4 v[4];
+};
+
+// Q8_0: five dwords holding the lane's 16 bytes, and the dword holding its scale.
+template <>
+struct WRaw<kWeightQ8_0> {
+    uint32_t dw[5];
+    uint32_t sw;
+};
+
+__device__ __forceinline__ void load_raw(WRaw<kWeightF32>& r, const MatmulArgs& a, int o, int k0, int g) {
     const f4* p = reinterpret_cast<const f4*>(static_cast<const float*>(a.w) + (int64_t)o * a.in_dim + k0 + 16 * g);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const f4 v = p[j];
+    for (int j = 0; j < 4; ++j) r.v[j] = p[j];
+}
+
+__device__ __forceinline__ void expand(float (&w)[16], const WRaw<kWeightF32>& r, int) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[4 * j + e] = v[e];
-    }
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[4 * j + e] = r.v[j][e];
 }
 
 // Q8_0: a 64-wide chunk of a row is two 34-byte blocks, 68 bytes starting at a
@@ -50,24 +67,25 @@ __device__ __forceinline__ void load_weights<kWeightF32>(float (&w)[16], const M
 // lane reads the five dwords from (byte 0, 16, 36, 52) and shifts out the
 // first 2 (g < 2) or 0 bytes.  Its block's scale is the low half of dword 0
 // or the high half of dword 8.  Every dword read lies inside the chunk.
-template <>
-__device__ __forceinline__ void load_weights<kWeightQ8_0>(float (&w)[16], const MatmulArgs& a, int o, int k0, int g) {
+__device__ __forceinline__ void load_raw(WRaw<kWeightQ8_0>& r, const MatmulArgs& a, int o, int k0, int g) {
     const int64_t row_bytes = (int64_t)(a.in_dim / 32) * 34;
     const uint32_t* cw = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)o * row_bytes +
                                                            (int64_t)(k0 / 64) * 68);
     const int first = g < 2 ? 4 * g : 9 + 4 * (g - 2);
-    const int shift = g < 2 ? 2 : 0;
-    uint32_t dw[5];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dw[i] = cw[first + i];
-    dw[4] = cw[g < 2 ? first + 4 : first + 3];  // only read as the high half of a 2-byte shift
-    const uint32_t sw = cw[g < 2 ? 0 : 8];
-    const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(g < 2 ? (sw & 0xFFFFu) : (sw >> 16)));
+    for (int i = 0; i < 4; ++i) r.dw[i] = cw[first + i];
+    r.dw[4] = cw[g < 2 ? first + 4 : first + 3];  // only read as the high half of a 2-byte shift
+    r.sw = cw[g < 2 ? 0 : 8];
+}
+
+__device__ __forceinline__ void expand(float (&w)[16], const WRaw<kWeightQ8_0>& r, int g) {
+    const int shift = g < 2 ? 2 : 0;
+    const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(g < 2 ? (r.sw & 0xFFFFu) : (r.sw >> 16)));
     const float d = (float)dh;
     const float bias = -128.0f * d;  // w = d * (u - 128) for the byte u = q ^ 0x80, exact in one fma
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t qd = __builtin_amdgcn_alignbyte(dw[i + 1], dw[i], shift) ^ 0x80808080u;
+        const uint32_t qd = __builtin_amdgcn_alignbyte(r.dw[i + 1], r.dw[i], shift) ^ 0x80808080u;
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[4 * i + e] = fmaf((float)((qd >> (8 * e)) & 0xFFu), d, bias);
     }
@@ -97,11 +115,11 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_batch_kernel(MatmulArgs 
     const int xq = tid & 3;
     const f4* xsrc = reinterpret_cast<const f4*>(a.x + (int64_t)min(b0 + xr, a.batch - 1) * a.in_dim + 16 * xq);
     f4 xreg[4];
-    float wreg[16];
+    WRaw<WT> wraw;
     auto load_chunk = [&](int c) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) xreg[j] = xsrc[16 * c + j];
-        load_weights<WT>(wreg, a, o, 64 * c, g);
+        load_raw(wraw, a, o, 64 * c, g);
     };
     auto store_x = [&](int buf) {
 #pragma unroll
@@ -119,8 +137,7 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_batch_kernel(MatmulArgs 
     for (int c = c_begin; c < c_end; ++c) {
         const int buf = (c - c_begin) & 1;
         float w[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) w[i] = wreg[i];
+        expand(w, wraw, g);
         const bool more = c + 1 < c_end;
         if (more) load_chunk(c + 1);  // the next chunk loads while this one computes
 #pragma unroll
