@@ -4,7 +4,7 @@ y[b][o] = sum_i W[o][i] x[b][i] with F32 or Q8_0 weights.  The device forms ever
 in fp32 and sums fp32 products, so the bar is fp32 summation error: |y - y64| <= 1e-5 * sum_i
 |W[o][i] x[b][i]| + 1e-7, against the float64 oracle on the same encoded weights.  The shapes
 cover a single batch row, batches below, at and above one 64-row workgroup tile with ragged
-ends, output counts that are not multiples of 16, one K range and several (split K).
+ends, output counts that are not multiples of 16 (or of 4), one K range and several (split K).
 """
 import numpy as np
 import pytest
@@ -21,6 +21,7 @@ SHAPES = [
     (3584, 512, 64),
     (256, 96, 100),
     (4096, 48, 17),
+    (512, 37, 3),  # out_dim odd: partial weight rows, and the reduce's one-element path
 ]
 
 
