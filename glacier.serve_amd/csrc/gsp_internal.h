@@ -155,6 +155,10 @@ struct MatmulArgs {
     int32_t batch;
     int32_t splits;            // K ranges over grid.z
     int32_t chunks_per_split;  // 64-wide K chunks per range
+    // Q8_0 path: x as scaled fp16 pairs, [batch][in_dim] each, and each row's exponent.
+    void* xh;
+    void* xl;
+    int32_t* xexp;
 };
 hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream);
 

@@ -174,6 +174,192 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_batch_kernel(MatmulArgs 
     }
 }
 
+// ---- Q8_0 weights on the fp16 matrix cores ----------------------------------
+//
+// One Q8_0 block (32 weights of a row) is one K step of v_mfma_f32_16x16x32_f16:
+// its int8 values are exact in fp16, and x enters as a pair x = 2^e (x_hi +
+// x_lo) of fp16 halves, scaled per batch row so that the row's largest |x|
+// lies in [2^12, 2^13) (the pair then carries ~22 significant bits and x_lo
+// stays a normal fp16 number).  A block's two products go into a fresh
+// accumulator, which the block's scale d then adds into the running sum;
+// 2^e multiplies the finished row.  The products are exact in fp32, so the
+// result differs from the fp32 kernel's only by summation order and the
+// ~2^-22 relative truncation of x.
+//
+// Tile layout (M = batch rows, N = weight rows): A lane l holds
+// x[batch 16 t + l % 16][k0 + 8 (l / 16) .. + 7], B lane l holds
+// q[row l % 16][the same k], and the result lane holds
+// y[batch 16 t + 4 (l / 16) + r][row l % 16]: the lane's own weight row, so
+// its block scale is its own.
+
+// x of one batch row as scaled fp16 pairs: one workgroup per row.
+__global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a) {
+    __shared__ float red[kMmThreads / 64];
+    const int b = blockIdx.x;
+    const float* xr = a.x + (int64_t)b * a.in_dim;
+    float mx = 0.f;
+    for (int i = threadIdx.x; i < a.in_dim; i += kMmThreads) mx = fmaxf(mx, fabsf(xr[i]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // e with mx * 2^-e in [2^12, 2^13), clamped so that 2^-e and 2^e stay normal.
+    int ex = 0;
+    if (mx > 0.f) (void)frexpf(mx, &ex);
+    const int e = mx > 0.f ? min(100, max(-100, ex - 13)) : 0;
+    const float down = ldexpf(1.0f, -e);
+    _Float16* xh = static_cast<_Float16*>(a.xh) + (int64_t)b * a.in_dim;
+    _Float16* xl = static_cast<_Float16*>(a.xl) + (int64_t)b * a.in_dim;
+    for (int i = threadIdx.x; i < a.in_dim; i += kMmThreads) {
+        const float v = xr[i] * down;
+        const _Float16 h = (_Float16)v;
+        xh[i] = h;
+        xl[i] = (_Float16)(v - (float)h);
+    }
+    if (threadIdx.x == 0) a.xexp[b] = e;
+}
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// Eight int8 (two dwords) as fp16: with u = q ^ 0x80, the half 0x6400 | u is
+// 1024 + u, so subtracting 1152 leaves q exactly.
+__device__ __forceinline__ h8 q8_to_h8(uint32_t d0, uint32_t d1) {
+    h8 r;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t u = (k ? d1 : d0) ^ 0x80808080u;
+        const uint32_t p0 = (u & 0xFFu) | ((u & 0xFF00u) << 8) | 0x64006400u;
+        const uint32_t p1 = ((u >> 16) & 0xFFu) | ((u >> 8) & 0xFF0000u) | 0x64006400u;
+        const h2 a0 = __builtin_bit_cast(h2, p0) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
+        const h2 a1 = __builtin_bit_cast(h2, p1) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
+        r[4 * k + 0] = a0[0];
+        r[4 * k + 1] = a0[1];
+        r[4 * k + 2] = a1[0];
+        r[4 * k + 3] = a1[1];
+    }
+    return r;
+}
+
+// The lane's raw words of one 64-wide chunk of its weight row (68 bytes at a
+// multiple of 4): block 0's eight values at bytes 2 + 8 g (dwords 2g .. 2g + 2,
+// shifted by 2), block 1's at 36 + 8 g (dwords 9 + 2g, 10 + 2g), and the two
+// scales (low half of dword 0, high half of dword 8).  All inside the chunk.
+struct Q8Raw {
+    uint32_t b0[3];
+    uint32_t b1[2];
+    uint32_t s0, s8;
+};
+
+__device__ __forceinline__ void load_q8_raw(Q8Raw& r, const MatmulArgs& a, int o, int c, int g) {
+    const int64_t row_bytes = (int64_t)(a.in_dim / 32) * 34;
+    const uint32_t* cw =
+        reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)o * row_bytes + (int64_t)c * 68);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) r.b0[i] = cw[2 * g + i];
+    r.b1[0] = cw[9 + 2 * g];
+    r.b1[1] = cw[10 + 2 * g];
+    r.s0 = cw[0];
+    r.s8 = cw[8];
+}
+
+__global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs a) {
+    // The chunk of x as fp16 pairs: [buffer][hi, lo][64 batch rows][64 halves + 8 padding].
+    __shared__ _Float16 xs[2][2][64][72];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 15;  // weight row within the wave's 16 (B column, result column)
+    const int g = lane >> 4;
+    const int o0 = blockIdx.x * kMmRowsWg + 16 * wave;
+    const int b0 = blockIdx.y * 64;
+    const int nt = min(4, (a.batch - b0 + 15) >> 4);
+    const int o = min(o0 + n, a.out_dim - 1);
+    const int chunks = a.in_dim / 64;
+    const int c_begin = blockIdx.z * a.chunks_per_split;
+    const int c_end = min(chunks, c_begin + a.chunks_per_split);
+
+    // x staging: thread tid moves batch row tid / 4, halves 16 (tid % 4) .. + 15 of hi and lo.
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const int xr = tid >> 2;
+    const int xq = tid & 3;
+    const int64_t xoff = (int64_t)min(b0 + xr, a.batch - 1) * a.in_dim + 16 * xq;
+    const u4* xh_src = reinterpret_cast<const u4*>(static_cast<const _Float16*>(a.xh) + xoff);
+    const u4* xl_src = reinterpret_cast<const u4*>(static_cast<const _Float16*>(a.xl) + xoff);
+    u4 xreg[4];
+    Q8Raw wraw;
+    auto load_chunk = [&](int c) {
+        xreg[0] = xh_src[8 * c];
+        xreg[1] = xh_src[8 * c + 1];
+        xreg[2] = xl_src[8 * c];
+        xreg[3] = xl_src[8 * c + 1];
+        load_q8_raw(wraw, a, o, c, g);
+    };
+    auto store_x = [&](int buf) {
+        *reinterpret_cast<u4*>(&xs[buf][0][xr][16 * xq]) = xreg[0];
+        *reinterpret_cast<u4*>(&xs[buf][0][xr][16 * xq + 8]) = xreg[1];
+        *reinterpret_cast<u4*>(&xs[buf][1][xr][16 * xq]) = xreg[2];
+        *reinterpret_cast<u4*>(&xs[buf][1][xr][16 * xq + 8]) = xreg[3];
+    };
+
+    f4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    if (c_begin < c_end) {
+        load_chunk(c_begin);
+        store_x(0);
+    }
+    __syncthreads();
+    for (int c = c_begin; c < c_end; ++c) {
+        const int buf = (c - c_begin) & 1;
+        // This chunk's two blocks of the lane's row: values and scales.
+        const h8 wq0 = q8_to_h8(__builtin_amdgcn_alignbyte(wraw.b0[1], wraw.b0[0], 2),
+                                __builtin_amdgcn_alignbyte(wraw.b0[2], wraw.b0[1], 2));
+        const h8 wq1 = q8_to_h8(wraw.b1[0], wraw.b1[1]);
+        const float d0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(wraw.s0 & 0xFFFFu));
+        const float d1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(wraw.s8 >> 16));
+        const bool more = c + 1 < c_end;
+        if (more) load_chunk(c + 1);  // the next chunk loads while this one computes
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if (t < nt) {
+                const int row = 16 * t + n;  // A row: batch row of this lane
+#pragma unroll
+                for (int blk = 0; blk < 2; ++blk) {
+                    const h8 ah = *reinterpret_cast<const h8*>(&xs[buf][0][row][32 * blk + 8 * g]);
+                    const h8 al = *reinterpret_cast<const h8*>(&xs[buf][1][row][32 * blk + 8 * g]);
+                    const h8 wq = blk ? wq1 : wq0;
+                    f4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, wq, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    part = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, wq, part, 0, 0, 0);
+                    const float d = blk ? d1 : d0;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(d, part[r], acc[t][r]);
+                }
+            }
+        }
+        if (more) store_x(buf ^ 1);  // the other buffer's last readers passed the previous barrier
+        __syncthreads();
+    }
+
+    // Lane holds batch rows b0 + 16 t + 4 g + r of weight row o0 + n.
+    const int oo = o0 + n;
+    if (oo >= a.out_dim) return;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int b = b0 + 16 * t + 4 * g + r;
+            if (t >= nt || b >= a.batch) continue;
+            const float v = ldexpf(acc[t][r], a.xexp[b]);
+            float* dst = a.split_out ? a.split_out + ((int64_t)blockIdx.z * a.batch + b) * a.out_dim
+                                     : a.y + (int64_t)b * a.out_dim;
+            dst[oo] = v;
+        }
+    }
+}
+
 // y = the sum over z of the split partials, in z order; four elements per
 // thread and step when y and the partials are 16-byte aligned, else one.
 __global__ __launch_bounds__(kMmThreads) void matmul_reduce_kernel(MatmulArgs a) {
@@ -205,7 +391,10 @@ hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream) {
     const dim3 grid((a.out_dim + kMmRowsWg - 1) / kMmRowsWg, (a.batch + 63) / 64, a.splits);
     if (a.w_type == kWeightF32)
         hipLaunchKernelGGL(matmul_batch_kernel<kWeightF32>, grid, dim3(kMmThreads), 0, stream, a);
-    else if (a.w_type == kWeightQ8_0)
+    else if (a.w_type == kWeightQ8_0 && a.xh) {
+        hipLaunchKernelGGL(matmul_split_x_kernel, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
+        hipLaunchKernelGGL(matmul_q8_f16_kernel, grid, dim3(kMmThreads), 0, stream, a);
+    } else if (a.w_type == kWeightQ8_0)
         hipLaunchKernelGGL(matmul_batch_kernel<kWeightQ8_0>, grid, dim3(kMmThreads), 0, stream, a);
     else
         return hipErrorInvalidValue;

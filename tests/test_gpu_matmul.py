@@ -1,8 +1,10 @@
 """gsp_matmul_batch (QuantKernels.MatMulBatch, PagedTransformerRunner.cs:601-603,659) against the oracle.
 
-y[b][o] = sum_i W[o][i] x[b][i] with F32 or Q8_0 weights.  The device forms every weight exactly
-in fp32 and sums fp32 products, so the bar is fp32 summation error: |y - y64| <= 1e-5 * sum_i
-|W[o][i] x[b][i]| + 1e-7, against the float64 oracle on the same encoded weights.  The shapes
+y[b][o] = sum_i W[o][i] x[b][i] with F32 or Q8_0 weights.  Every weight is exact in the device's
+arithmetic (fp32, or fp16 for Q8_0 values), x is kept to at least ~22 significant bits (fp32, or
+a scaled fp16 pair on the Q8_0 fp16 path) and products are summed in fp32, so the bar is fp32
+summation error: |y - y64| <= 1e-5 * sum_i |W[o][i] x[b][i]| + 1e-7, against the float64 oracle
+on the same encoded weights.  The shapes
 cover a single batch row, batches below, at and above one 64-row workgroup tile with ragged
 ends, output counts that are not multiples of 16 (or of 4), one K range and several (split K).
 """
@@ -22,6 +24,10 @@ SHAPES = [
     (256, 96, 100),
     (4096, 48, 17),
     (512, 37, 3),  # out_dim odd: partial weight rows, and the reduce's one-element path
+    # batch x out_dim >= 131072: Q8_0 takes the fp16 matrix-core path
+    (256, 2048, 70),
+    (512, 1300, 128),
+    (128, 2049, 65),
 ]
 
 
