@@ -608,8 +608,9 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
 
 // Q8_0 products with at least this many outputs (batch x out_dim) take the fp16
 // path: measured faster from Qwen2.5-7B's 3584 x 3584 projection at 64 rows
-// (27.8 vs 31.2 us) upwards, slower for 3584 x 512 at 64 rows (21.5 vs 16.2 us).
-constexpr int64_t kMatmulF16MinOutputs = 131072;
+// (229376 outputs: 27.8 vs 31.2 us) upwards, slower for 8192 x 8192 at 16 rows
+// (131072 outputs: 57.5 vs 51 us) and 3584 x 512 at 64 rows (21.5 vs 16.2 us).
+constexpr int64_t kMatmulF16MinOutputs = 196608;
 
 int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const float* x_dev, float* y_dev,
                      int32_t in_dim, int32_t out_dim, int32_t batch) {

@@ -24,10 +24,10 @@ SHAPES = [
     (256, 96, 100),
     (4096, 48, 17),
     (512, 37, 3),  # out_dim odd: partial weight rows, and the reduce's one-element path
-    # batch x out_dim >= 131072: Q8_0 takes the fp16 matrix-core path
-    (256, 2048, 70),
-    (512, 1300, 128),
-    (128, 2049, 65),
+    # batch x out_dim >= 196608: Q8_0 takes the fp16 matrix-core path
+    (256, 2048, 100),
+    (512, 1600, 128),
+    (128, 2049, 97),
 ]
 
 
