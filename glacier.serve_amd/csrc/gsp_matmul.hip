@@ -192,13 +192,20 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_batch_kernel(MatmulArgs 
 // y[batch 16 t + 4 (l / 16) + r][row l % 16]: the lane's own weight row, so
 // its block scale is its own.
 
-// x of one batch row as scaled fp16 pairs: one workgroup per row.
+// x of one batch row as scaled fp16 pairs: one workgroup per row, four
+// elements per access (in_dim is a multiple of 64, rows 16-byte aligned).
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a) {
     __shared__ float red[kMmThreads / 64];
     const int b = blockIdx.x;
-    const float* xr = a.x + (int64_t)b * a.in_dim;
+    const int n4 = a.in_dim / 4;
+    const f4* xr = reinterpret_cast<const f4*>(a.x + (int64_t)b * a.in_dim);
     float mx = 0.f;
-    for (int i = threadIdx.x; i < a.in_dim; i += kMmThreads) mx = fmaxf(mx, fabsf(xr[i]));
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += kMmThreads) {
+        const f4 v = xr[i];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
@@ -209,13 +216,14 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
     if (mx > 0.f) (void)frexpf(mx, &ex);
     const int e = mx > 0.f ? min(100, max(-100, ex - 13)) : 0;
     const float down = ldexpf(1.0f, -e);
-    _Float16* xh = static_cast<_Float16*>(a.xh) + (int64_t)b * a.in_dim;
-    _Float16* xl = static_cast<_Float16*>(a.xl) + (int64_t)b * a.in_dim;
-    for (int i = threadIdx.x; i < a.in_dim; i += kMmThreads) {
-        const float v = xr[i] * down;
-        const _Float16 h = (_Float16)v;
+    h4v* xh = reinterpret_cast<h4v*>(static_cast<_Float16*>(a.xh) + (int64_t)b * a.in_dim);
+    h4v* xl = reinterpret_cast<h4v*>(static_cast<_Float16*>(a.xl) + (int64_t)b * a.in_dim);
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += kMmThreads) {
+        const f4 v = xr[i] * down;
+        const h4v h = __builtin_convertvector(v, h4v);
         xh[i] = h;
-        xl[i] = (_Float16)(v - (float)h);
+        xl[i] = __builtin_convertvector(v - __builtin_convertvector(h, f4), h4v);
     }
     if (threadIdx.x == 0) a.xexp[b] = e;
 }
