@@ -5,10 +5,14 @@
 // W holds out_dim rows of in_dim weights (the GGUF [in, out] layout) as F32 or
 // Q8_0 (blocks of 32 int8 with an fp16 scale d: w = d * q).
 //
-// The arithmetic is fp32: every weight is exact in fp32 (Q8_0's d * q has at
-// most 19 significant bits), and the products run on v_mfma_f32_16x16x4f32
-// with fp32 accumulation, so no operand is rounded below fp32.
+// Two forms.  The fp32 form (matmul_batch_kernel, every F32 product and small
+// Q8_0 ones): every weight is exact in fp32 (Q8_0's d * q has at most 19
+// significant bits), and the products run on v_mfma_f32_16x16x4f32 with fp32
+// accumulation, so no operand is rounded below fp32.  The fp16 form
+// (matmul_q8_f16_kernel, large Q8_0 products, described further down) runs
+// one Q8_0 block per fp16 matrix step with x as a scaled fp16 pair.
 //
+// fp32 form:
 // A workgroup (four waves) owns 64 weight rows (16 per wave, MFMA M) and 64
 // batch rows (four 16-column MFMA tiles, N) over a range of K, in 64-wide
 // chunks.  Each chunk of x is staged once in LDS and serves all four waves;

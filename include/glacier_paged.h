@@ -179,7 +179,9 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
  * (GSP_WTYPE_F32, 16-byte aligned) or Q8_0 (GSP_WTYPE_Q8_0: per 32 weights a
  * little-endian fp16 scale d and 32 int8 q, w = d * q; 4-byte aligned).
  * x_dev is [batch][in_dim] fp32 (16-byte aligned), y_dev [batch][out_dim] fp32,
- * overwritten; all device pointers.  Products and sums are fp32.  in_dim must
+ * overwritten; all device pointers.  Every weight is used exactly, x keeps at
+ * least ~22 significant bits (large Q8_0 products take it as a scaled fp16
+ * pair on the fp16 matrix cores) and sums are fp32.  in_dim must
  * be a multiple of 64 (GSP_E_UNSUPPORTED otherwise, as for other weight
  * types); the reference's block sums are not needed by these two types. */
 int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const float* x_dev, float* y_dev,
