@@ -154,8 +154,9 @@ __device__ __forceinline__ void prepare_q(QRegs<D, _Float16>& qr, const QRaw<D>&
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     int ex = 0;
     if (mx > 0.f) (void)frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
-    // Scaled max in [2^12, 2^13); clamped so that 2^sh and 2^-sh stay normal floats.
-    const int sh = mx > 0.f ? min(100, max(-100, 13 - ex)) : 0;
+    // Scaled max in [2^12, 2^13); clamped so that 2^sh and 2^-sh stay normal
+    // floats.  The floor -115 keeps every finite head inside the fp16 range.
+    const int sh = mx > 0.f ? min(100, max(-115, 13 - ex)) : 0;
     const float up = ldexpf(1.0f, sh);
 #pragma unroll
     for (int j = 0; j < D / 16; ++j) {

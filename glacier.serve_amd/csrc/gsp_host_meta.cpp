@@ -255,6 +255,16 @@ int gsp_block_table_append_token(gsp_block_table* t, int32_t* block_id, int32_t*
         }
         t->ids.push_back(nb);
     } else {
+        // A partial last page that the table does not hold (a prefix attached
+        // with fewer ids than its token count needs none, but an empty one
+        // has no last page): the reference's _physicalBlockIds[^1] throws.
+        if (t->ids.empty()) {
+            *block_id = -1;
+            *offset = -1;
+            return gsp::fail(GSP_E_INVALID_ARG, "tokenCount %d is inside a page but the table holds no pages",
+                             t->token_count),
+                   -1;
+        }
         const int32_t last = t->ids.back();
         if (gsp_block_allocator_ref_count(a, last) > 1) {
             // Copy-on-write fork of a shared partial page (BlockTable.cs:60-73).
@@ -288,7 +298,7 @@ int gsp_block_table_append_tokens(gsp_block_table* t, int32_t n) {
     gsp::clear_error();
     if (!t) return gsp::fail(GSP_E_INVALID_ARG, "table is NULL"), 0;
     int32_t b, o, done = 0;
-    while (done < n && gsp_block_table_append_token(t, &b, &o)) ++done;
+    while (done < n && gsp_block_table_append_token(t, &b, &o) == 1) ++done;
     return done;
 }
 

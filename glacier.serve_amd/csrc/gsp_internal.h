@@ -177,4 +177,7 @@ struct CopyBlockArgs {
 
 hipError_t launch_copy_block(int kv_f16, const CopyBlockArgs& a, hipStream_t stream);
 
+// Sets n int32 words at p to `value` with a kernel (capturable, unlike hipMemsetAsync).
+hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t stream);
+
 }  // namespace gsp

@@ -23,6 +23,8 @@
 // K over grid.z workgroups, each writes its sums to a partial buffer and a
 // second kernel adds the partials in order, so results do not depend on
 // timing.
+#include <cfloat>
+
 #include "gsp_internal.h"
 
 namespace gsp {
@@ -215,10 +217,13 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    // e with mx * 2^-e in [2^12, 2^13), clamped so that 2^-e and 2^e stay normal.
+    // e with mx * 2^-e in [2^12, 2^13), clamped to [-126, 115] so that 2^-e
+    // and 2^e stay normal floats.  The ceiling covers every finite row (ex is
+    // at most 128), so no finite x overflows fp16; rows below 2^-113 keep
+    // their absolute fp16 rounding only.
     int ex = 0;
-    if (mx > 0.f) (void)frexpf(mx, &ex);
-    const int e = mx > 0.f ? min(100, max(-100, ex - 13)) : 0;
+    if (mx > 0.f && mx <= FLT_MAX) (void)frexpf(mx, &ex);
+    const int e = mx > 0.f ? (mx <= FLT_MAX ? min(115, max(-126, ex - 13)) : 115) : 0;
     const float down = ldexpf(1.0f, -e);
     h4v* xh = reinterpret_cast<h4v*>(static_cast<_Float16*>(a.xh) + (int64_t)b * a.in_dim);
     h4v* xl = reinterpret_cast<h4v*>(static_cast<_Float16*>(a.xl) + (int64_t)b * a.in_dim);
@@ -227,7 +232,12 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
         const f4 v = xr[i] * down;
         const h4v h = __builtin_convertvector(v, h4v);
         xh[i] = h;
-        xl[i] = __builtin_convertvector(v - __builtin_convertvector(h, f4), h4v);
+        // An infinite element rides on its hi half alone (Inf - Inf would make
+        // the lo half NaN), as it would through the fp32 form.
+        f4 l = v - __builtin_convertvector(h, f4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) l[c] = __builtin_isinf(v[c]) ? 0.f : l[c];
+        xl[i] = __builtin_convertvector(l, h4v);
     }
     if (threadIdx.x == 0) a.xexp[b] = e;
 }

@@ -97,7 +97,20 @@ __global__ __launch_bounds__(256) void copy_block_kernel(CopyBlockArgs a) {
     }
 }
 
+// Sets n int32 words to `value`.  Used instead of hipMemsetAsync where a
+// caller may capture the call into a graph.
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* p, int64_t n, int32_t value) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = value;
+}
+
 }  // namespace
+
+hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p, n, value);
+    return hipGetLastError();
+}
 
 hipError_t launch_write_tokens(int kv_f16, const WriteTokensArgs& a, hipStream_t stream) {
     if (a.n <= 0) return hipSuccess;

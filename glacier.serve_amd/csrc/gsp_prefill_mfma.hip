@@ -68,15 +68,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t prefill_rsrc(const void* base,
 }
 
 // Exponent e such that x * 2^-e has its largest |element| `mx` in [2^12, 2^13).
-// Clamped to [-100, 100] so that 2^-e and 2^e stay normal floats (inputs below
-// 2^-87 then keep their absolute fp16 rounding only).  An all-zero vector
+// Clamped to [-100, 115] so that 2^-e and 2^e stay normal floats (inputs below
+// 2^-87 then keep their absolute fp16 rounding only); the ceiling keeps every
+// finite vector inside the fp16 range.  An all-zero vector
 // (such as the slots past a page's valid tokens, which load as 0) gets the
 // floor -100, so it never raises the largest V exponent of a page.
 constexpr int kPairExpFloor = -100;
+constexpr int kPairExpCeil = 115;
 __device__ __forceinline__ int pair_exponent(float mx) {
     int ex = 0;
     if (mx > 0.f) (void)frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
-    return mx > 0.f ? min(100, max(kPairExpFloor, ex - 13)) : kPairExpFloor;
+    return mx > 0.f ? min(kPairExpCeil, max(kPairExpFloor, ex - 13)) : kPairExpFloor;
 }
 
 template <typename F, typename H>
@@ -210,7 +212,7 @@ __device__ __forceinline__ float cross_row_max(float x) {
 // the floor as above.  Infinite and NaN maxima take the ceiling and stay
 // non-finite after scaling.
 __device__ __forceinline__ int pair_exponent_bits(uint32_t mb) {
-    return min(100, max(kPairExpFloor, (int)(mb >> 23) - 139));
+    return min(kPairExpCeil, max(kPairExpFloor, (int)(mb >> 23) - 139));
 }
 
 // Largest |x[i]| as a bit pattern: the lane's elements go through

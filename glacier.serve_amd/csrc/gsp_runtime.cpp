@@ -219,6 +219,15 @@ int check_hip(hipError_t e, const char* what) {
 
 int set_device(const gsp_ctx* ctx) { return check_hip(hipSetDevice(ctx->device), "hipSetDevice"); }
 
+// Whether `stream` is capturing into a graph.  Nothing may then allocate,
+// free, synchronise or stage host memory on it.
+int is_capturing(hipStream_t stream, bool* out) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    const int rc = check_hip(hipStreamIsCapturing(stream, &st), "hipStreamIsCapturing");
+    *out = rc == GSP_OK && st != hipStreamCaptureStatusNone;
+    return rc;
+}
+
 // Grows a pinned host buffer (waiting for the upload that last used it).
 int ensure_pinned(int32_t** buf, size_t* cap, size_t words, hipEvent_t done, bool* pending) {
     if (*pending) {
@@ -240,11 +249,23 @@ int ensure_pinned(int32_t** buf, size_t* cap, size_t words, hipEvent_t done, boo
 }
 
 // Grows a device buffer.  The stream is synchronised first so no queued
-// kernel still reads the old allocation.
+// kernel still reads the old allocation.  A stream that is capturing into a
+// graph cannot do that: the call then fails with GSP_E_STATE, and the buffer
+// must be grown by an eager call first (gsp_step_pack sizes the attention
+// workspace for every group up to 16).  `zero` clears the new buffer with a
+// kernel on the stream.
 template <typename T>
 int ensure_device(gsp_ctx* ctx, T** buf, size_t* cap, size_t count, bool zero) {
     if (count <= *cap) return GSP_OK;
-    int rc = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    bool cap_on = false;
+    int rc = is_capturing(ctx->stream, &cap_on);
+    if (rc) return rc;
+    if (cap_on)
+        return gsp::fail(GSP_E_STATE,
+                         "device workspace must grow to %zu bytes, which cannot happen while the stream is "
+                         "capturing: run the same call once outside the capture first",
+                         count * sizeof(T));
+    rc = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     if (rc) return rc;
     size_t n = std::max(count, *cap * 2);
     if (*buf) (void)hipFree(*buf);
@@ -253,7 +274,11 @@ int ensure_device(gsp_ctx* ctx, T** buf, size_t* cap, size_t count, bool zero) {
     rc = check_hip(hipMalloc(reinterpret_cast<void**>(buf), n * sizeof(T)), "hipMalloc(workspace)");
     if (rc) return rc;
     if (zero) {
-        rc = check_hip(hipMemsetAsync(*buf, 0, n * sizeof(T), ctx->stream), "hipMemsetAsync");
+        rc = (n * sizeof(T)) % sizeof(int32_t) != 0
+                 ? gsp::fail(GSP_E_INVALID_ARG, "zeroed workspaces hold whole 32-bit words")
+                 : check_hip(gsp::launch_fill_i32(reinterpret_cast<int32_t*>(*buf),
+                                                  (int64_t)(n * sizeof(T) / sizeof(int32_t)), 0, ctx->stream),
+                             "fill launch");
         if (rc) return rc;
     }
     *cap = n;
@@ -815,6 +840,16 @@ static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max, bool pair) {
 int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc) {
     gsp::clear_error();
     if (!ctx || !pool || !desc) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool/desc is NULL");
+    {
+        // Refused before anything changes: the step already packed stays valid.
+        bool cap_on = false;
+        const int rc = is_capturing(ctx->stream, &cap_on);
+        if (rc) return rc;
+        if (cap_on)
+            return gsp::fail(GSP_E_STATE,
+                             "gsp_step_pack cannot run while the stream is capturing: it stages the step in "
+                             "host memory; pack eagerly, then capture gsp_attention_step");
+    }
     ctx->step_valid = false;
     const gsp_pool_desc& pd = pool->desc;
     const int32_t B = desc->num_rows;
@@ -830,8 +865,15 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     // plus the table and pool bounds) and size the packed arrays.
     int64_t total_q = 0, packed_pages = 0, kv_tokens = 0, pair_pages = 0, max_pages = 0;
     bool any_tiles = false;
-    if (B > 0 && desc->bt_offsets[0] < 0)
-        return gsp::fail(GSP_E_INVALID_ARG, "bt_offsets[0] must be >= 0");
+    if (desc->n_bt_ids < 0) return gsp::fail(GSP_E_INVALID_ARG, "n_bt_ids must be >= 0 (got %d)", desc->n_bt_ids);
+    // The CSR must stay inside the caller's id array: every row span is read
+    // through bt_offsets, so they are checked before any id is.
+    for (int32_t b = 0; b < B; ++b) {
+        const int32_t o0 = desc->bt_offsets[b], o1 = desc->bt_offsets[b + 1];
+        if (o0 < 0 || o1 < o0 || o1 > desc->n_bt_ids)
+            return gsp::fail(GSP_E_INVALID_ARG, "row %d: bt_offsets [%d, %d) outside [0, n_bt_ids = %d] or decreasing",
+                             b, o0, o1, desc->n_bt_ids);
+    }
     for (int32_t b = 0; b < B; ++b) {
         const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
         const int32_t pos = desc->positions[b];
@@ -844,7 +886,6 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         if (tc < 0) return gsp::fail(GSP_E_INVALID_ARG, "row %d: token count %d is negative", b, tc);
         if (tc > L) return gsp::fail(GSP_E_INVALID_ARG, "row %d: BlockTable token count %d exceeds maxSeqLen %d", b, tc, L);
         const int32_t span = desc->bt_offsets[b + 1] - desc->bt_offsets[b];
-        if (span < 0) return gsp::fail(GSP_E_INVALID_ARG, "row %d: bt_offsets decrease", b);
         const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
         const int64_t pages = (total_last + gsp::kBlockSize - 1) / gsp::kBlockSize;
         if (pages > span)
@@ -1032,6 +1073,13 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     if (rc) return rc;
     rc = ensure_pinned(&ctx->staging, &ctx->staging_words, words, ctx->staging_done, &ctx->staging_pending);
     if (!rc) rc = ensure_device(ctx, &ctx->d_step, &ctx->d_step_words, words, false);
+    // The split workspace for any group up to the decode tile, so that a
+    // captured gsp_attention_step of this step never has to grow it.
+    if (!rc && slots > 0)
+        rc = ensure_device(ctx, &ctx->part, &ctx->part_floats,
+                           (size_t)slots * gsp::kMaxGroupMfma * (size_t)(pd.v_head_dim + 2), false);
+    if (!rc && slots > 0)
+        rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, (size_t)total_q * H, true);
     if (rc) return rc;
 
     int32_t* st = ctx->staging;
@@ -1142,9 +1190,22 @@ int gsp_step_download(gsp_ctx* ctx, int32_t* row_offsets, int32_t* ids, int32_t*
 
 /* ------------------------------------------------------------ attention */
 
-int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t n_heads, const float* q_dev,
-                       float* out_dev, float attn_scale, const float* sink_logit) {
-    gsp::clear_error();
+}  // extern "C"
+
+namespace {
+
+// Split-KV workspace of one attention launch: the context's own (grown on
+// demand, outside graph capture) or a fixed device array (the allocation-free
+// entry point), whose counters are cleared before every launch.
+struct Workspace {
+    float* part = nullptr;
+    size_t part_floats = 0;
+    int32_t* counters = nullptr;
+    size_t counter_words = 0;
+};
+
+int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t n_heads, const float* q_dev,
+                     float* out_dev, float attn_scale, const float* sink_logit, const Workspace* fixed) {
     if (!ctx || !pool) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool is NULL");
     if (!ctx->step_valid) return gsp::fail(GSP_E_STATE, "gsp_step_pack must succeed before gsp_attention_step");
     const gsp_pool_desc& d = pool->desc;
@@ -1176,12 +1237,32 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     if (rc) return rc;
 
     const int32_t slots = ctx->num_slots;
+    float* part = ctx->part;
+    int32_t* counters = ctx->counters;
     if (slots > 0) {
-        const size_t per_slot = (size_t)group * (d.head_dim + 2);
-        rc = ensure_device(ctx, &ctx->part, &ctx->part_floats, (size_t)slots * per_slot, false);
-        // Counters start at zero and every launch leaves them at zero.
-        if (!rc) rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, (size_t)ctx->info.total_q * d.heads_kv, true);
-        if (rc) return rc;
+        const size_t part_need = (size_t)slots * group * (d.head_dim + 2);
+        const size_t counter_need = (size_t)ctx->info.total_q * d.heads_kv;
+        if (fixed) {
+            if (part_need > fixed->part_floats || counter_need > fixed->counter_words)
+                return gsp::fail(GSP_E_INVALID_ARG,
+                                 "the step needs %zu bytes of split-KV partials and %zu counters; the "
+                                 "allocation-free entry point holds %zu bytes and %zu counters",
+                                 part_need * sizeof(float), counter_need, fixed->part_floats * sizeof(float),
+                                 fixed->counter_words);
+            part = fixed->part;
+            counters = fixed->counters;
+            // The array keeps whatever the last call on this GPU left: clear the
+            // counters this launch uses (every launch leaves its own at zero).
+            rc = check_hip(gsp::launch_fill_i32(counters, (int64_t)counter_need, 0, ctx->stream), "fill launch");
+            if (rc) return rc;
+        } else {
+            rc = ensure_device(ctx, &ctx->part, &ctx->part_floats, part_need, false);
+            // Counters start at zero and every launch leaves them at zero.
+            if (!rc) rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, counter_need, true);
+            if (rc) return rc;
+            part = ctx->part;
+            counters = ctx->counters;
+        }
     }
 
     gsp::DecodeArgs a;
@@ -1195,9 +1276,9 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     a.bt_ids = ctx->d_step + ctx->off_ids;
     a.q = q_dev;
     a.out = out_dev;
-    a.part_o = ctx->part;
-    a.part_ml = ctx->part ? ctx->part + (size_t)slots * group * d.head_dim : nullptr;
-    a.counters = ctx->counters;
+    a.part_o = slots > 0 ? part : nullptr;
+    a.part_ml = slots > 0 ? part + (size_t)slots * group * d.head_dim : nullptr;
+    a.counters = slots > 0 ? counters : nullptr;
     a.n_heads = n_heads;
     a.n_kv = d.heads_kv;
     a.group = group;
@@ -1245,6 +1326,16 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
     return rc;
 }
 
+}  // namespace
+
+extern "C" {
+
+int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t n_heads, const float* q_dev,
+                       float* out_dev, float attn_scale, const float* sink_logit) {
+    gsp::clear_error();
+    return attention_launch(ctx, pool, layer, n_heads, q_dev, out_dev, attn_scale, sink_logit, nullptr);
+}
+
 int gsp_compute_attention(gsp_ctx* ctx, const gsp_pool* pool, int32_t stage_layer, int32_t model_layer, int32_t pos,
                           const float* q_dev, float* out_dev, const int32_t* block_ids, int32_t n_block_ids,
                           int32_t token_count, int32_t n_heads, int32_t n_heads_kv, int32_t head_dim,
@@ -1271,6 +1362,7 @@ int gsp_compute_attention(gsp_ctx* ctx, const gsp_pool* pool, int32_t stage_laye
     s.token_counts = &token_count;
     s.bt_offsets = offsets;
     s.bt_ids = n_block_ids ? block_ids : empty_ids;
+    s.n_bt_ids = n_block_ids;
     int rc = gsp_step_pack(ctx, pool, &s);
     if (rc) return rc;
     return gsp_attention_step(ctx, pool, stage_layer, n_heads, q_dev, out_dev, attn_scale, sink_logit);

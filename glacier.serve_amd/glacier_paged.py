@@ -115,6 +115,7 @@ class StepDesc(ctypes.Structure):
         ("token_counts", i32p),
         ("bt_offsets", i32p),
         ("bt_ids", i32p),
+        ("n_bt_ids", i32),
     ]
 
 
@@ -319,7 +320,10 @@ class Context:
         bt_ids: Sequence[int],
         max_seq_len: int,
         q_lens: Optional[Sequence[int]] = None,
+        n_bt_ids: Optional[int] = None,
     ) -> StepInfo:
+        """Packs one engine step (gsp_step_pack).  n_bt_ids defaults to len(bt_ids); the library
+        checks the CSR offsets against it."""
         pos = _i32(positions)
         tc = _i32(token_counts)
         off = _i32(bt_offsets)
@@ -333,6 +337,7 @@ class Context:
         d.token_counts = _ptr(tc)
         d.bt_offsets = _ptr(off)
         d.bt_ids = _ptr(ids)
+        d.n_bt_ids = len(bt_ids) if n_bt_ids is None else int(n_bt_ids)
         _check(self._lib.gsp_step_pack(self._h, pool.handle, ctypes.byref(d)))
         return self.step_info()
 
@@ -603,6 +608,8 @@ class BlockTable:
     def append_token(self):
         b, o = i32(), i32()
         ok = load().gsp_block_table_append_token(self._h, ctypes.byref(b), ctypes.byref(o))
+        if ok < 0:
+            _check(GSP_E_INVALID_ARG)
         return bool(ok), b.value, o.value
 
     def append_tokens(self, n: int) -> int:

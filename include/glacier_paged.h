@@ -40,7 +40,7 @@ extern "C" {
 #pragma GCC visibility push(default)
 #endif
 
-#define GSP_ABI_VERSION 6
+#define GSP_ABI_VERSION 7
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
 
 typedef enum gsp_status {
@@ -179,9 +179,12 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
  * (GSP_WTYPE_F32, 16-byte aligned) or Q8_0 (GSP_WTYPE_Q8_0: per 32 weights a
  * little-endian fp16 scale d and 32 int8 q, w = d * q; 4-byte aligned).
  * x_dev is [batch][in_dim] fp32 (16-byte aligned), y_dev [batch][out_dim] fp32,
- * overwritten; all device pointers.  Every weight is used exactly, x keeps at
- * least ~22 significant bits (large Q8_0 products take it as a scaled fp16
- * pair on the fp16 matrix cores) and sums are fp32.  in_dim must
+ * overwritten; all device pointers.  Every weight is used exactly and sums are
+ * fp32.  Small products keep x in fp32.  Large Q8_0 products take x as a
+ * scaled fp16 pair on the fp16 matrix cores: each element then carries an
+ * absolute error of at most ~2^-22 of its row's largest |x| (~22 significant
+ * bits for elements near the row max, fewer for much smaller ones; every
+ * finite x stays finite).  in_dim must
  * be a multiple of 64 (GSP_E_UNSUPPORTED otherwise, as for other weight
  * types); the reference's block sums are not needed by these two types. */
 int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const float* x_dev, float* y_dev,
@@ -213,6 +216,8 @@ typedef struct gsp_step_desc {
     const int32_t* token_counts; /* [B] BlockTable.TokenCount after slot allocation */
     const int32_t* bt_offsets;   /* [B+1] CSR offsets into bt_ids */
     const int32_t* bt_ids;       /* concatenated BlockTable.AsSpan() of each row */
+    int32_t n_bt_ids;            /* entries readable at bt_ids: the CSR must keep
+                                    0 <= bt_offsets[b] <= bt_offsets[b+1] <= n_bt_ids */
 } gsp_step_desc;
 
 /* Validates and packs one engine step for `pool` (its KV-head count and
@@ -226,7 +231,8 @@ typedef struct gsp_step_desc {
  * entries of a row are packed.  Errors (GSP_E_INVALID_ARG):
  *   max_seq_len <= 0; pos < 0 or pos + q_len - 1 >= max_seq_len
  *   (PagedAttentionKernel.cs:34-37); token_counts[b] > max_seq_len (:38-39);
- *   a row's table shorter than ceil(total/16); a block id outside the pool. */
+ *   bt_offsets outside [0, n_bt_ids] or decreasing; a row's table shorter
+ *   than ceil(total/16); a block id outside the pool. */
 int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc);
 
 /* Sizes of the packed step (for tests and the bench). */
@@ -377,7 +383,10 @@ void gsp_block_table_destroy(gsp_block_table* t);
 int gsp_block_table_attach_prefix(gsp_block_table* t, const int32_t* ids, int32_t n,
                                   int32_t token_count);
 /* AppendToken (BlockTable.cs:46-80): 1 on success, 0 on pool exhaustion with
- * the table unchanged and *block_id = *offset = -1. */
+ * the table unchanged and *block_id = *offset = -1.  -1 with GSP_E_INVALID_ARG
+ * set (table unchanged) where the reference throws: TokenCount is inside a
+ * page but the table holds no page (an empty prefix attached with a nonzero
+ * token count; `_physicalBlockIds[^1]`, BlockTable.cs:60). */
 int gsp_block_table_append_token(gsp_block_table* t, int32_t* block_id, int32_t* offset);
 /* AppendToken n times, as a prefill chunk reserves its slots
  * (PagedTransformerRunner.cs:383-401); stops at the first failure.  Returns

@@ -266,3 +266,22 @@ def test_llama8b_tables_product_equals_oracle():
     # Fragmented: pages of a row are not a contiguous run.
     runs = [np.all(np.diff(prod.table(b)) == 1) for b in range(prod.num_rows) if len(prod.table(b)) > 1]
     assert not all(runs)
+
+
+def test_append_token_on_an_empty_partial_table_raises():
+    """AttachPrefixBlocks accepts any token count (BlockTable.cs:31-39); the next
+    AppendToken inside a page then reads _physicalBlockIds[^1] and throws when the
+    table holds no page (:60).  The product raises InvalidArgument and leaves the
+    table and the pool unchanged, where it once read past an empty vector."""
+    a = gp.BlockAllocator(8, 16)
+    t = gp.BlockTable(a)
+    t.attach_prefix_blocks([], 5)
+    with pytest.raises(gp.InvalidArgument):
+        t.append_token()
+    assert t.token_count == 5 and t.block_count == 0 and a.free_blocks_count == 8
+    assert t.append_tokens(3) == 0
+    # At a page boundary an empty table simply allocates, as in the reference.
+    t2 = gp.BlockTable(a)
+    t2.attach_prefix_blocks([], 16)
+    ok, b, off = t2.append_token()
+    assert ok and b == 0 and off == 0 and t2.token_count == 17

@@ -66,3 +66,89 @@ def test_captured_step_replays_match_eager(torch_mod, gsp, ctx, kind):
     finally:
         ctx.set_stream(None)  # back to the context's own stream
         pool.destroy()
+
+
+def _graph_node_types(graph) -> list:
+    """Node types of a captured graph (hipGraphNodeType values), read through the HIP
+    runtime torch already loaded."""
+    import ctypes
+
+    path = next(ln.split()[-1] for ln in open("/proc/self/maps") if "libamdhip64" in ln)
+    hip = ctypes.CDLL(path)
+    hip.hipGraphGetNodes.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_size_t)]
+    hip.hipGraphNodeGetType.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]
+    handle = ctypes.c_void_p(int(graph.raw_cuda_graph()))
+    n = ctypes.c_size_t(0)
+    assert hip.hipGraphGetNodes(handle, None, ctypes.byref(n)) == 0
+    nodes = (ctypes.c_void_p * max(1, n.value))()
+    assert hip.hipGraphGetNodes(handle, nodes, ctypes.byref(n)) == 0
+    types = []
+    for i in range(n.value):
+        t = ctypes.c_int(-1)
+        assert hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(t)) == 0
+        types.append(t.value)
+    return types
+
+
+HIP_GRAPH_NODE_KERNEL, HIP_GRAPH_NODE_MEMCPY, HIP_GRAPH_NODE_MEMSET = 0, 1, 2
+
+
+def test_capture_of_a_step_larger_than_any_earlier(torch_mod, gsp):
+    """A fresh context packs a split step and captures it with no eager run first:
+    gsp_step_pack sized the workspace, so the capture holds kernels only (no
+    memset or copy node) and every replay equals the eager step.  Packing, and a
+    workspace that would have to grow, are refused during the capture."""
+    torch = torch_mod
+    step = workloads.small_step(seed=44, rows=20, n_heads=28, n_kv=4, head_dim=128, ctx_lo=200, ctx_hi=1500,
+                                total_blocks=4096)
+    print("graph case fresh-context capture", flush=True)
+    q, k, v = workloads.host_values(step)
+    fresh = gsp.Context(0)
+    pool, keep = to_device_pool(torch, gsp, fresh, step, k, v)
+    stream = torch.cuda.Stream()
+    fresh.set_stream(stream.cuda_stream)
+    try:
+        fresh.set_split_pages(4)
+        info = fresh.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids,
+                               step.max_seq_len)
+        fresh.set_split_pages(0)
+        assert info.split_pairs > 0
+        qd = torch.from_numpy(q).cuda()
+        w = torch.randn((64, 4096), device="cuda")
+        x = torch.randn((16, 4096), device="cuda")
+        y = torch.empty((16, 64), device="cuda")
+        out = torch.full((step.total_q, step.n_heads, step.head_dim), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph(keep_graph=True)
+        with torch.cuda.graph(graph, stream=stream):
+            fresh.attention_step(pool, 0, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
+            with pytest.raises(gsp.StateError, match="capturing"):
+                fresh.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids,
+                                step.max_seq_len)
+            # The first split-K product of this context would grow its partials.
+            with pytest.raises(gsp.StateError, match="capturing"):
+                fresh.matmul_batch(gsp.WTYPE_F32, w.data_ptr(), x.data_ptr(), y.data_ptr(), 4096, 64, 16)
+        types = _graph_node_types(graph)
+        assert HIP_GRAPH_NODE_KERNEL in types
+        assert HIP_GRAPH_NODE_MEMSET not in types and HIP_GRAPH_NODE_MEMCPY not in types, types
+        graph.instantiate()
+        # The refused pack left the packed step intact: the eager run after it uses it.
+        eager = torch.full_like(out, float("nan"))
+        with torch.cuda.stream(stream):
+            fresh.attention_step(pool, 0, step.n_heads, qd.data_ptr(), eager.data_ptr(), step.scale)
+        stream.synchronize()
+        assert max_err(eager.cpu().numpy(), oracle_step(step, q, k, v)) <= TOL[step.kv_dtype]
+        for rep in range(3):
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {rep} differs from the eager step"
+            with torch.cuda.stream(stream):
+                fresh.attention_step(pool, 0, step.n_heads, qd.data_ptr(), eager.data_ptr(), step.scale)
+            stream.synchronize()
+        del graph
+    finally:
+        fresh.set_stream(None)
+        pool.destroy()
+        fresh.close()

@@ -97,3 +97,29 @@ def test_matmul_q_projection_then_attention_shapes(torch_mod, gsp, ctx):
     ref = x.astype(np.float64) @ wm.T
     mag = np.abs(x.astype(np.float64)) @ np.abs(wm).T
     assert np.all(np.abs(got - ref) <= 1e-5 * mag + 1e-7)
+
+
+@pytest.mark.parametrize("w_type", [orc.WTYPE_F32, orc.WTYPE_Q8_0], ids=["f32", "q8_0"])
+def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type):
+    """Rows with one channel 1e4 times the rest, rows near 1e30 and rows near 1e-30, on a shape that
+    takes the Q8_0 fp16 path.  There x is a scaled fp16 pair whose error is bounded relative to its
+    row's largest |x| (at most ~2^-22 of it per element), so the bar adds that term; every finite row
+    stays finite.  The F32 form keeps x in fp32 and meets the plain fp32 summation bar."""
+    in_dim, out_dim, batch = 256, 2048, 100
+    rng = np.random.default_rng(77 + w_type)
+    data, wm = _weights(rng, w_type, out_dim, in_dim)
+    x = rng.standard_normal((batch, in_dim)).astype(np.float32)
+    x[0:30, rng.integers(0, in_dim, 30)] *= 1e4           # one outlier channel per row (some shared)
+    x[30:40] *= np.float32(1e30)                          # near the top of the fp32 range
+    x[40:50] *= np.float32(3e34)
+    x[50:60] *= np.float32(1e-30)                         # tiny rows
+    print(f"case matmul outliers type={w_type}", flush=True)
+    got = _run(torch_mod, gsp, ctx, w_type, data, x, in_dim, out_dim)
+    ref = orc.matmul_batch(w_type, data, x, in_dim, out_dim)
+    x64 = x.astype(np.float64)
+    mag = np.abs(x64) @ np.abs(wm).T
+    bar = 1e-5 * mag + 1e-7 * (np.abs(x64).max(axis=1, keepdims=True) > 1e-20)
+    if w_type == orc.WTYPE_Q8_0:
+        bar = bar + 2.0 ** -21 * np.abs(x64).max(axis=1, keepdims=True) * np.abs(wm).sum(axis=1)[None, :]
+    assert np.all(np.isfinite(got))
+    assert np.all(np.abs(got - ref) <= bar)

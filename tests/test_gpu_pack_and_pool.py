@@ -61,7 +61,11 @@ def test_pack_rejects_what_the_reference_throws_on(gsp, ctx):
     pack()
     for bad in (dict(positions=[16]), dict(positions=[-1]), dict(max_seq_len=0), dict(token_counts=[17]),
                 dict(token_counts=[-1]), dict(positions=[40], token_counts=[41], max_seq_len=64),
-                dict(bt_ids=[-3]), dict(bt_ids=[4]), dict(positions=[10], q_lens=[7])):
+                dict(bt_ids=[-3]), dict(bt_ids=[4]), dict(positions=[10], q_lens=[7]),
+                # CSR offsets outside the caller's id array, negative or decreasing: refused
+                # before any id is read (the array's length travels as n_bt_ids).
+                dict(bt_offsets=[0, 2]), dict(bt_offsets=[1, 2], bt_ids=[0, 0], n_bt_ids=1),
+                dict(bt_offsets=[-1, 1]), dict(bt_offsets=[1, 0]), dict(n_bt_ids=-1)):
         with pytest.raises(gsp.InvalidArgument):
             pack(**bad)
     # After a failed pack there is no step to run.
