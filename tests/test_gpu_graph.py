@@ -42,6 +42,7 @@ def test_captured_step_replays_match_eager(torch_mod, gsp, ctx, kind):
             assert info.split_pairs > 0
         qd = torch.from_numpy(q).cuda()
         eager = torch.full((step.total_q, step.n_heads, step.head_dim), float("nan"), device="cuda")
+        torch.cuda.synchronize()  # torch fills on its own stream
         with torch.cuda.stream(stream):
             ctx.attention_step(pool, 0, step.n_heads, qd.data_ptr(), eager.data_ptr(), step.scale)
         stream.synchronize()
@@ -134,6 +135,7 @@ def test_capture_of_a_step_larger_than_any_earlier(torch_mod, gsp):
         graph.instantiate()
         # The refused pack left the packed step intact: the eager run after it uses it.
         eager = torch.full_like(out, float("nan"))
+        torch.cuda.synchronize()
         with torch.cuda.stream(stream):
             fresh.attention_step(pool, 0, step.n_heads, qd.data_ptr(), eager.data_ptr(), step.scale)
         stream.synchronize()

@@ -119,6 +119,7 @@ def test_rope_write_then_attention(torch_mod, gsp, ctx, style):
                            vn.data_ptr())
     ctx.pack_step(pool, pos, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len)
     out = torch.full((rows, step.n_heads, step.head_dim), float("nan"), device="cuda")
+    torch.cuda.synchronize()  # torch fills on its own stream, the library on the context's
     ctx.attention_step(pool, 0, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
     ctx.sync()
     # Oracle: the same rotation and store on the host arenas, then the reference attention.
