@@ -23,6 +23,7 @@ SOURCES = [
     CSRC / "gsp_prefill_mfma.hip",
     CSRC / "gsp_pool_ops.hip",
     CSRC / "gsp_matmul.hip",
+    CSRC / "gsp_noalloc.hip",
     CSRC / "gsp_runtime.cpp",
     CSRC / "gsp_host_meta.cpp",
     CSRC / "gsp_status.cpp",

@@ -180,4 +180,10 @@ hipError_t launch_copy_block(int kv_f16, const CopyBlockArgs& a, hipStream_t str
 // Sets n int32 words at p to `value` with a kernel (capturable, unlike hipMemsetAsync).
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t stream);
 
+// Fixed device scratch of the allocation-free attention entry point
+// (gsp_noalloc.hip): one array per GPU, its address looked up once per device.
+hipError_t noalloc_setup(int device);
+// The device address of `device`'s scratch array, or null before noalloc_setup.
+void* noalloc_scratch(int device);
+
 }  // namespace gsp

@@ -363,6 +363,9 @@ int gsp_init(int device, gsp_ctx** out) {
     if (!rc) rc = check_hip(hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking), "hipStreamCreate");
     if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming), "hipEventCreate");
     if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming), "hipEventCreate");
+    // The allocation-free entry point's scratch: look up this device's copy
+    // of the array once, with the device current.
+    if (!rc) rc = check_hip(gsp::noalloc_setup(device), "hipGetSymbolAddress(scratch)");
     if (rc) {
         gsp_shutdown(ctx);
         return rc;
@@ -1326,6 +1329,10 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     return rc;
 }
 
+// Layout of the fixed scratch: counters first, then the partials.
+constexpr size_t kNoallocCounterWords = GSP_NOALLOC_COUNTERS;
+static_assert(kNoallocCounterWords * sizeof(int32_t) < GSP_NOALLOC_SCRATCH_BYTES, "counters fit the scratch");
+
 }  // namespace
 
 extern "C" {
@@ -1334,6 +1341,21 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
                        float* out_dev, float attn_scale, const float* sink_logit) {
     gsp::clear_error();
     return attention_launch(ctx, pool, layer, n_heads, q_dev, out_dev, attn_scale, sink_logit, nullptr);
+}
+
+int gsp_attention_step_noalloc(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t n_heads,
+                               const float* q_dev, float* out_dev, float attn_scale, const float* sink_logit) {
+    gsp::clear_error();
+    if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
+    char* base = static_cast<char*>(gsp::noalloc_scratch(ctx->device));
+    if (!base) return gsp::fail(GSP_E_STATE, "the scratch array of device %d was not set up", ctx->device);
+    Workspace ws;
+    ws.counters = reinterpret_cast<int32_t*>(base);
+    ws.counter_words = kNoallocCounterWords;
+    const size_t part_off = kNoallocCounterWords * sizeof(int32_t);
+    ws.part = reinterpret_cast<float*>(base + part_off);
+    ws.part_floats = (GSP_NOALLOC_SCRATCH_BYTES - part_off) / sizeof(float);
+    return attention_launch(ctx, pool, layer, n_heads, q_dev, out_dev, attn_scale, sink_logit, &ws);
 }
 
 int gsp_compute_attention(gsp_ctx* ctx, const gsp_pool* pool, int32_t stage_layer, int32_t model_layer, int32_t pos,

@@ -52,6 +52,8 @@ ROPE_PAIRS = 0
 ROPE_HALVES = 1
 WTYPE_F32, WTYPE_Q8_0 = 0, 8  # GGUF tensor type ids (gsp_matmul_batch)
 BLOCK_SIZE = 16
+NOALLOC_SCRATCH_BYTES = 16 << 20  # GSP_NOALLOC_SCRATCH_BYTES: fixed scratch of attention_step_noalloc per GPU
+NOALLOC_COUNTERS = 65536          # GSP_NOALLOC_COUNTERS: its leading int32 counters
 
 
 class GspError(RuntimeError):
@@ -184,6 +186,7 @@ _SIGNATURES = {
     "gsp_set_prefill_path": (ctypes.c_int, [vp, i32]),
     "gsp_set_decode_bins": (ctypes.c_int, [vp, i32]),
     "gsp_attention_step": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, ctypes.c_float, fp]),
+    "gsp_attention_step_noalloc": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, ctypes.c_float, fp]),
     "gsp_compute_attention": (
         ctypes.c_int,
         [vp, vp, i32, i32, i32, vp, vp, i32p, i32, i32, i32, i32, i32, i32, ctypes.c_float, fp, i32, fp],
@@ -363,6 +366,20 @@ class Context:
             sink = ctypes.pointer(ctypes.c_float(sink_logit))
         _check(
             self._lib.gsp_attention_step(
+                self._h, pool.handle, int(layer), int(n_heads), vp(q_ptr), vp(out_ptr), float(attn_scale), sink
+            )
+        )
+
+    def attention_step_noalloc(
+        self, pool: "Pool", layer: int, n_heads: int, q_ptr: int, out_ptr: int, attn_scale: float, sink_logit=None
+    ) -> None:
+        """attention_step with the split-KV workspace in the library's fixed per-GPU scratch array:
+        allocates nothing (for graph capture and tight loops); calls that overlap on one GPU race."""
+        sink = None
+        if sink_logit is not None:
+            sink = ctypes.pointer(ctypes.c_float(sink_logit))
+        _check(
+            self._lib.gsp_attention_step_noalloc(
                 self._h, pool.handle, int(layer), int(n_heads), vp(q_ptr), vp(out_ptr), float(attn_scale), sink
             )
         )

@@ -315,6 +315,28 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
                        const float* q_dev, float* out_dev, float attn_scale,
                        const float* sink_logit);
 
+/* Allocation-free variant of gsp_attention_step.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results as gsp_attention_step, but the split-KV
+ * workspace (partial outputs and per-(query, KV head) counters) lives in a
+ * fixed device array of GSP_NOALLOC_SCRATCH_BYTES per GPU instead of context
+ * memory: the call never allocates or frees, whatever the step's size.  The
+ * array's first GSP_NOALLOC_COUNTERS int32 words are counters (a step may use
+ * total_q * heads_kv of them) and the rest holds partials (a step uses
+ * partial_slots * (n_heads / heads_kv) * (v_head_dim + 2) floats); a step that
+ * needs more fails with GSP_E_INVALID_ARG before anything is enqueued.  Each
+ * call clears the counters it uses with a kernel on the context's stream.
+ * Every call on one GPU shares that GPU's array, which keeps the last call's
+ * contents: calls that overlap on one GPU (two contexts' streams, or threads)
+ * race and must be ordered by the caller.  The packed step must come from an
+ * earlier gsp_step_pack (which may allocate, and cannot be captured). */
+#define GSP_NOALLOC_SCRATCH_BYTES (16u << 20)
+#define GSP_NOALLOC_COUNTERS 65536u
+int gsp_attention_step_noalloc(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t n_heads,
+                               const float* q_dev, float* out_dev, float attn_scale,
+                               const float* sink_logit);
+
 /* Single-sequence drop-in for ComputeAttention with the reference's argument
  * list (PagedAttentionKernel.cs:17-32): the BlockTable is passed as its id span
  * plus TokenCount; head geometry must match the pool.  head_scores is not
