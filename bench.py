@@ -1,27 +1,38 @@
 #!/usr/bin/env python3
 """Benchmark of the ragged continuous-batch paged-attention step on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload qwen7b_decode] [--all]
+    python bench.py [--steps K] [--warmup W] [--workload qwen7b_decode] [--all] [--layers L]
+    python bench.py --summarize-trace KERNEL_TRACE.csv --kernel NAME --last K
+    python bench.py --summarize-pmc COUNTER_COLLECTION.csv --kernel NAME --last K
 
 A step is one gsp_attention_step over one packed engine step (one layer, all
 rows), with Q, the KV pool and the packed tables already resident in HBM.
-Prints ONE JSON line (per workload with --all):
+The pool holds L layers (default 4) and step i attends layer i mod L, as the
+layers of an engine tick do, so no step re-reads pages that an earlier step
+left in the 256 MB Infinity Cache.  Prints ONE JSON line (per workload with
+--all):
   value        KV GB/s = algorithmic KV bytes / ms_per_step (every valid K/V
                element counted once), unit GB/s
   roofline     the dominant kernel: decode = algorithmic KV bytes / its mean
                launch time (K launches back to back between HIP events on the
                launch stream) vs 8 TB/s; for steps with prefill rows each kernel is
-               also timed alone on its rows (roofline_decode, roofline_prefill;
-               prefill = 4*d*nH FLOPs per causal (query, key) pair vs the
-               157.3 TFLOP/s fp32 matrix peak; the kernel reaches it through
-               fp16 matrix cores with hi + lo operand pairs, so its share of
-               the fp16 peak is reported too)
+               also timed alone on its rows (roofline_decode, roofline_prefill).
+               The prefill kernel computes fp32 attention (4*d*nH FLOPs per
+               causal (query, key) pair) on the fp16 matrix cores as hi + lo
+               operand pairs, 3 fp16 products per fp32 product (2 for fp16
+               pages): its roofline is those fp16 products against the
+               2.5 PFLOP/s dense fp16 matrix peak.
   cpu_baseline the CPU oracle (C++ restatement of the reference kernel) timed
                on this host on the same inputs
+--profile-only runs only the packed step's warmup and timed launches (and, for
+steps with prefill rows, each kernel alone on its rows), so that a rocprofv3
+trace of it holds exactly those launches; --summarize-trace / --summarize-pmc
+then average the last K launches of a kernel in that trace or counter file.
 """
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -44,12 +55,21 @@ FP16_MFMA_PEAK_TFS = 2500.0  # MI355X dense fp16 matrix peak
 PREFILL_TILE_MIN_Q = 16     # rows the library runs as prefill tiles by default
 
 
-def cpu_threads() -> int:
+# Host threads a job may use per GPU on the measurement hosts: their CPU share
+# is 16 cores per GPU, whatever sched_getaffinity shows.
+HOST_CPU_SHARE = 16
+
+
+def visible_cores() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except Exception:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return os.cpu_count() or 1
+
+
+def cpu_threads() -> int:
+    """Every core this process may run on, up to the host's per-GPU CPU share."""
+    return max(1, min(HOST_CPU_SHARE, visible_cores()))
 
 
 def cpu_model() -> str:
@@ -62,23 +82,23 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def time_substep(gsp, torch, ctx, stream, pool, sub, q, q_index, steps: int) -> float:
+def time_substep(gsp, torch, ctx, stream, pool, sub, q, q_index, steps: int, layers: int) -> float:
     """Mean ms of one gsp_attention_step over `sub` (a subset of the step's rows,
     same pool; one kernel launch per step): `steps` steps back to back between
-    two HIP events on the launch stream."""
+    two HIP events on the launch stream, step i on layer i mod `layers`."""
     idx = torch.from_numpy(q_index).to(q.device)
     qs = q.index_select(0, idx).contiguous()
     out = torch.empty((sub.total_q, sub.n_heads, sub.head_dim), device=q.device, dtype=torch.float32)
     ctx.pack_step(pool, sub.positions, sub.token_counts, sub.bt_offsets, sub.bt_ids, sub.max_seq_len,
                   q_lens=sub.q_lens)
-    for _ in range(3):
-        ctx.attention_step(pool, 0, sub.n_heads, qs.data_ptr(), out.data_ptr(), sub.scale)
+    for i in range(3):
+        ctx.attention_step(pool, i % layers, sub.n_heads, qs.data_ptr(), out.data_ptr(), sub.scale)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
-    for _ in range(steps):
-        ctx.attention_step(pool, 0, sub.n_heads, qs.data_ptr(), out.data_ptr(), sub.scale)
+    for i in range(steps):
+        ctx.attention_step(pool, i % layers, sub.n_heads, qs.data_ptr(), out.data_ptr(), sub.scale)
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
@@ -97,7 +117,7 @@ def profiled_traffic(workload: str, kernel: str):
     return None
 
 
-def describe(step) -> dict:
+def describe(step, layers: int) -> dict:
     import numpy as np
 
     ctx = step.row_ctx()
@@ -111,6 +131,8 @@ def describe(step) -> dict:
         "kv_dtype": step.kv_dtype,
         "block_size": 16,
         "pool_blocks": step.total_blocks,
+        "pool_layers": layers,
+        "layer_per_step": "step i attends layer i mod pool_layers",
         "ctx_min": int(ctx.min()),
         "ctx_mean": round(float(ctx.mean()), 1),
         "ctx_max": int(ctx.max()),
@@ -124,7 +146,8 @@ def describe(step) -> dict:
     return d
 
 
-def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: float) -> dict:
+def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: float, layers: int = 4,
+                 decode_path: str = "auto", profile_only: bool = False) -> dict:
     import numpy as np
     import torch
 
@@ -132,15 +155,16 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     import workloads
 
     step = getattr(workloads, name)()
-    q, k, v = workloads.device_values(torch, step)
+    q, k, v = workloads.device_values(torch, step, layers=layers)
     torch.cuda.synchronize()
     ctx = gsp.Context(0)
+    ctx.set_decode_path({"auto": gsp.DECODE_AUTO, "dpp": gsp.DECODE_DPP, "mfma": gsp.DECODE_MFMA}[decode_path])
     # A dedicated torch stream: the library launches on it and the events below
     # are recorded on it (torch's default stream is the null handle).
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     ctx.set_stream(stream.cuda_stream)
-    pool = gsp.Pool.wrap(ctx, k.data_ptr(), v.data_ptr(), step.total_blocks, 1, step.n_kv, step.head_dim,
+    pool = gsp.Pool.wrap(ctx, k.data_ptr(), v.data_ptr(), step.total_blocks, layers, step.n_kv, step.head_dim,
                          gsp.KV_F16 if step.kv_dtype == "f16" else gsp.KV_F32)
     out = torch.empty((step.total_q, step.n_heads, step.head_dim), device="cuda", dtype=torch.float32)
 
@@ -148,69 +172,41 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         return ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
                              q_lens=step.q_lens)
 
-    def attend():
-        ctx.attention_step(pool, 0, step.n_heads, q.data_ptr(), out.data_ptr(), step.scale)
+    def attend(layer):
+        ctx.attention_step(pool, layer, step.n_heads, q.data_ptr(), out.data_ptr(), step.scale)
 
     info = pack()
-    for _ in range(warmup):
-        attend()
+    for i in range(warmup):
+        attend(i % layers)
     torch.cuda.synchronize()
 
-    # Timed region: K steps back to back, events on the launch stream.
+    # Timed region: K steps back to back, step i on layer i mod L, events on the
+    # launch stream.
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record(stream)
-    for _ in range(steps):
-        attend()
+    for i in range(steps):
+        attend(i % layers)
     e1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     ms_per_step = e0.elapsed_time(e1) / steps
 
     # A decode-only step is one launch of the decode kernel, so its mean launch
-    # duration over the timed region is ms_per_step.  (Events around every
-    # launch would add their own gaps; rocprofv3's kernel trace agrees with
-    # ms_per_step to about 1%.)
+    # duration over the timed region is ms_per_step.
     kernel_ms = ms_per_step
-
-    # Engine-step time: pinned pack + one H2D copy + kernel, host-synchronous per step.
-    n_step = max(10, steps // 4)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(n_step):
-        pack()
-        attend()
-    torch.cuda.synchronize()
-    t_step_ms = (time.perf_counter() - t0) * 1e3 / n_step
-
-    # Distribution of single steps: each between its own events on the launch
-    # stream and waited for alone, so it includes one launch's start-up that the
-    # back-to-back mean hides.  Reported beside ms_per_step, never as value.
-    singles = []
-    for _ in range(max(20, min(200, steps))):
-        a0 = torch.cuda.Event(enable_timing=True)
-        a1 = torch.cuda.Event(enable_timing=True)
-        a0.record(stream)
-        attend()
-        a1.record(stream)
-        a1.synchronize()
-        singles.append(a0.elapsed_time(a1))
-    p10, p50, p90 = (float(x) for x in np.percentile(singles, [10, 50, 90]))
-
     kv_bytes = step.kv_bytes()
     gbs = kv_bytes / (ms_per_step * 1e-3) / 1e9
-    kernel_gbs = kv_bytes / (kernel_ms * 1e-3) / 1e9
-    got = out.cpu().numpy()
 
     decode_roof = {
         "bound": "hbm",
-        "kernel": KERNEL_NAME,
-        "achieved": round(kernel_gbs, 1),
+        "kernel": KERNEL_NAME if decode_path != "dpp" else "paged_decode_kernel",
+        "achieved": round(kv_bytes / (kernel_ms * 1e-3) / 1e9, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
-        "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+        "frac": round(kv_bytes / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "traffic": profiled_traffic(name, KERNEL_NAME),
         "algorithmic_bytes_per_launch": kv_bytes,
         "mean_launch_ms": round(kernel_ms, 5),
@@ -223,31 +219,28 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         # (one launch of one kernel per step), and report the longer one.
         rows_d = np.nonzero(step.lens < PREFILL_TILE_MIN_Q)[0]
         sub_p, qi_p = step.subset(tiled)
-        pre_ms = time_substep(gsp, torch, ctx, stream, pool, sub_p, q, qi_p, steps)
+        pre_ms = time_substep(gsp, torch, ctx, stream, pool, sub_p, q, qi_p, steps, layers)
         flops = sub_p.prefill_flops()
         tfs = flops / (pre_ms * 1e-3) / 1e12
         products = 3 if step.kv_dtype == "f32" else 2
         prefill_roof = {
             "bound": "mfma",
             "kernel": PREFILL_KERNEL_NAME,
-            "achieved": round(tfs, 2),
-            "peak": FP32_MFMA_PEAK_TFS,
+            # fp16 matrix-core products per second: fp32 attention runs as
+            # `products` fp16 products (hi + lo operand pairs) per fp32 product.
+            "achieved": round(tfs * products, 2),
+            "peak": FP16_MFMA_PEAK_TFS,
             "unit": "TFLOP/s",
-            "frac": round(tfs / FP32_MFMA_PEAK_TFS, 4),
+            "frac": round(tfs * products / FP16_MFMA_PEAK_TFS, 4),
             "traffic": profiled_traffic(name, PREFILL_KERNEL_NAME),
             "algorithmic_flops_per_launch": int(flops),
+            "fp16_products_per_fp32_product": products,
+            "fp32_attention_tflops": round(tfs, 2),
             "mean_launch_ms": round(pre_ms, 5),
-            # The algorithm is fp32 and `frac` is against the fp32 matrix peak.  The
-            # kernel runs it on the fp16 matrix cores with operands split into hi + lo
-            # fp16 pairs: `products` fp16 products per fp32 one, so it can pass the
-            # fp32 peak; this is the same work against the fp16 matrix peak.
-            "matrix_unit": "fp16 (operands as hi + lo fp16 pairs)",
-            "products_per_fp32_product": products,
-            "frac_of_fp16_matrix_peak": round(tfs * products / FP16_MFMA_PEAK_TFS, 4),
         }
         if len(rows_d):
             sub_d, qi_d = step.subset(rows_d)
-            dec_ms = time_substep(gsp, torch, ctx, stream, pool, sub_d, q, qi_d, steps)
+            dec_ms = time_substep(gsp, torch, ctx, stream, pool, sub_d, q, qi_d, steps, layers)
             dgbs = sub_d.kv_bytes() / (dec_ms * 1e-3) / 1e9
             decode_roof.update({"achieved": round(dgbs, 1), "frac": round(dgbs / HBM_PEAK_GBS, 4),
                                 "algorithmic_bytes_per_launch": sub_d.kv_bytes(), "mean_launch_ms": round(dec_ms, 5),
@@ -256,7 +249,9 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
             dec_ms = 0.0
         extra["roofline_decode"] = decode_roof
         extra["roofline_prefill"] = prefill_roof
+        extra["mixed_vs_parts"] = round(ms_per_step / (pre_ms + dec_ms), 4)
         roofline = prefill_roof if pre_ms >= dec_ms else decode_roof
+        pack()  # the full step again, for what follows
 
     result = {
         "metric": METRIC,
@@ -271,30 +266,92 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         "vs_baseline": None,
         "dtype": step.kv_dtype,
         "data": "synthetic: Q, K, V ~ N(0,1) drawn on the GPU from the recorded seed",
-        "config": describe(step),
+        "config": describe(step, layers),
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
-        "seq_steps_per_s": round(step.num_rows / (ms_per_step * 1e-3), 1),
-        "t_step_ms_incl_pack_upload": round(t_step_ms, 5),
+    }
+    if profile_only:
+        result["roofline"] = roofline
+        result.update(extra)
+        pool.destroy()
+        ctx.close()
+        return result
+
+    # Engine-step time t_step: the host pack (validation, scheduling, one
+    # pinned staging buffer and one host-to-device copy) plus the attention of
+    # one layer, issued back to back as an engine loop issues them.  The copy
+    # of step i+1 runs on the library's copy stream while step i's kernel runs.
+    # t_step is the median period of the loop once it is in steady state (host
+    # hiccups of a millisecond show up in the mean, reported beside it).
+    n_step = max(40, steps)
+    for i in range(5):
+        pack()
+        attend(i % layers)
+    pack_ns, periods = [], []
+    torch.cuda.synchronize()
+    t0 = t_prev = time.perf_counter()
+    for i in range(n_step):
+        info_i = pack()
+        attend(i % layers)
+        t_now = time.perf_counter()
+        periods.append(t_now - t_prev)
+        t_prev = t_now
+        pack_ns.append(info_i.pack_host_ns)
+    torch.cuda.synchronize()
+    t_step_mean_ms = (time.perf_counter() - t0) * 1e3 / n_step
+    t_step_ms = float(np.median(periods[n_step // 4:])) * 1e3
+
+    # Distribution of single steps: each between its own events on the launch
+    # stream and waited for alone, so it includes one launch's start-up that the
+    # back-to-back mean hides.  Reported beside ms_per_step, never as value.
+    singles = []
+    for i in range(max(20, min(200, steps))):
+        a0 = torch.cuda.Event(enable_timing=True)
+        a1 = torch.cuda.Event(enable_timing=True)
+        a0.record(stream)
+        attend(i % layers)
+        a1.record(stream)
+        a1.synchronize()
+        singles.append(a0.elapsed_time(a1))
+    p10, p50, p90 = (float(x) for x in np.percentile(singles, [10, 50, 90]))
+
+    # The output checked against the oracle: layer 0.
+    attend(0)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    result.update({
+        "seq_steps_per_s": round(step.num_rows / (t_step_ms * 1e-3), 1),
+        "t_step_ms": round(t_step_ms, 5),
+        "t_step_breakdown": {
+            "definition": "seq_steps_per_s = B / t_step; t_step = one engine step: host pack (one H2D copy) + "
+                          "one layer's attention, issued back to back through the Python binding; median period",
+            "t_step_ms_mean": round(t_step_mean_ms, 5),
+            "t_step_ms_p90": round(float(np.percentile(periods[n_step // 4:], 90)) * 1e3, 5),
+            "t_step_ms_max": round(max(periods) * 1e3, 3),
+            "pack_host_us_median": round(float(np.median(pack_ns)) / 1e3, 2),
+            "kernel_ms": round(kernel_ms, 5),
+            "steps": n_step,
+        },
+        "seq_steps_per_s_kernel_only": round(step.num_rows / (ms_per_step * 1e-3), 1),
+        "kv_gbs_incl_pack_upload": round(kv_bytes / (t_step_ms * 1e-3) / 1e9, 1),
         "single_step_ms": {"p10": round(p10, 5), "median": round(p50, 5), "p90": round(p90, 5),
                            "samples": len(singles), "note": "one step at a time, each waited for"},
-        "seq_steps_per_s_incl_pack_upload": round(step.num_rows / (t_step_ms * 1e-3), 1),
-        "kv_gbs_incl_pack_upload": round(kv_bytes / (t_step_ms * 1e-3) / 1e9, 1),
         "wall_ms_timed_region": round(wall_ms, 3),
         "step_info": {"decode_units": info.decode_units, "split_pairs": info.split_pairs,
                       "partial_slots": info.partial_slots, "pages_per_split": info.pages_per_split,
-                      "packed_pages": info.packed_pages, "staging_bytes": int(info.staging_bytes)},
+                      "packed_pages": info.packed_pages, "staging_bytes": int(info.staging_bytes),
+                      "decode_bins": info.decode_bins, "prefill_tiles": info.prefill_tiles},
         "roofline": roofline,
-    }
+    })
     result.update(extra)
-    result["host_prefix_cache"] = host_prefix_cache(gsp, step)
-    result["rope_write"] = rope_write_timing(gsp, torch, ctx, stream, step)
-    result["matmul"] = matmul_timing(gsp, torch, ctx, stream, step)
-
     if cpu:
         result["cpu_baseline"], ref = cpu_baseline(step, q, k, v, cpu_budget_s)
         err = float(np.nanmax(np.abs(got.astype(np.float64) - ref.astype(np.float64))))
         tol = 2e-3 if step.kv_dtype == "f16" else 1e-4
         result["parity"] = {"max_abs_err_vs_oracle": err, "tol": tol, "ok": bool(err <= tol)}
+    result["host_prefix_cache"] = host_prefix_cache(gsp, step)
+    # Last, since it writes new K/V into the pool at each row's newest position.
+    result["kv_write"] = kv_write_timing(gsp, torch, ctx, stream, step, pool, layers)
+    result["matmul"] = matmul_timing(gsp, torch, ctx, stream, step)
     pool.destroy()
     ctx.close()
     return result
@@ -337,43 +394,53 @@ def matmul_timing(gsp, torch, ctx, stream, step, calls: int = 50) -> dict:
     return out
 
 
-def rope_write_timing(gsp, torch, ctx, stream, step, calls: int = 100) -> dict:
-    """Device cost of the step's K/V write with RoPE (QuantKernels.RoPE then
-    PagedBlockPool.Store, PagedTransformerRunner.cs:620-634, fused): one new token
-    per decode row and the chunk's tokens for prefill rows, into a scratch pool of
-    the step's geometry.  Each call restages positions, blocks and slots from the
-    host, as an engine tick does."""
+def kv_write_timing(gsp, torch, ctx, stream, step, pool, layers: int, calls: int = 100) -> dict:
+    """Per-layer device cost of the step's own K/V write with RoPE (QuantKernels.RoPE then
+    PagedBlockPool.Store, PagedTransformerRunner.cs:620-634, fused): each query token's new K/V
+    into the slot of its position, layer i mod L per call.  gsp_rope_write_step reads positions,
+    blocks and slots from the packed step (one upload per tick, none per layer);
+    gsp_rope_write_tokens, timed beside it, restages host arrays on every call."""
     import numpy as np
 
     n = step.total_q
-    pos = np.concatenate([int(p) + np.arange(int(l)) for p, l in zip(step.positions, step.lens)]).astype(np.int32)
-    blocks = (np.arange(n) // 16).astype(np.int32)
-    slots = (np.arange(n) % 16).astype(np.int32)
-    pool = gsp.Pool.create(ctx, total_blocks=int(blocks[-1]) + 1, layers=1, heads_kv=step.n_kv, head_dim=step.head_dim,
-                           kv_dtype=gsp.KV_F16 if step.kv_dtype == "f16" else gsp.KV_F32)
     gen = torch.Generator(device="cuda").manual_seed(step.seed)
     q = torch.randn((n, step.n_heads, step.head_dim), device="cuda", generator=gen)
     k = torch.randn((n, step.n_kv, step.head_dim), device="cuda", generator=gen)
     v = torch.randn((n, step.n_kv, step.head_dim), device="cuda", generator=gen)
-    args = (0, pos, blocks, slots, step.n_heads, 1000000.0, gsp.ROPE_HALVES, q.data_ptr(), k.data_ptr(), v.data_ptr())
-    with torch.cuda.stream(stream):
-        for _ in range(5):
-            pool.rope_write_tokens(*args)
+    base, style = 1000000.0, gsp.ROPE_HALVES
+    pos, blocks, slots = [], [], []
+    for b in range(step.num_rows):
+        for i in range(int(step.lens[b])):
+            p = int(step.positions[b]) + i
+            pos.append(p)
+            blocks.append(int(step.table(b)[p // 16]))
+            slots.append(p % 16)
+    pos, blocks, slots = (np.array(x, np.int32) for x in (pos, blocks, slots))
+    torch.cuda.synchronize()
+
+    def timed(fn) -> float:
+        for i in range(5):
+            fn(i)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for _ in range(calls):
-            pool.rope_write_tokens(*args)
+        for i in range(calls):
+            fn(i)
         e1.record(stream)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) / calls * 1e3
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / calls * 1e3
+
+    us_step = timed(lambda i: pool.rope_write_step(i % layers, step.n_heads, base, style, q.data_ptr(), k.data_ptr(),
+                                                   v.data_ptr()))
+    us_host = timed(lambda i: pool.rope_write_tokens(i % layers, pos, blocks, slots, step.n_heads, base, style,
+                                                     q.data_ptr(), k.data_ptr(), v.data_ptr()))
     elem = 2 if step.kv_dtype == "f16" else 4
     moved = n * (2 * step.n_heads * step.head_dim * 4 + 2 * step.n_kv * step.head_dim * 4
                  + 2 * step.n_kv * step.head_dim * elem)
-    pool.destroy()
-    return {"tokens": n, "us_per_call": round(us, 2), "bytes_per_call": moved,
-            "gbs": round(moved / (us * 1e-6) / 1e9, 1),
-            "note": "Q rotated in place, K rotated and stored, V stored; includes the per-call host staging"}
+    return {"tokens": n, "us_per_layer_call": round(us_step, 2), "bytes_per_call": moved,
+            "gbs": round(moved / (us_step * 1e-6) / 1e9, 1), "us_per_call_host_arrays": round(us_host, 2),
+            "note": "gsp_rope_write_step: Q rotated in place, K rotated and stored, V stored, slots from the "
+                    "packed step; the host-array form restages ids per call"}
 
 
 def host_prefix_cache(gsp, step) -> dict:
@@ -416,8 +483,9 @@ def cpu_baseline(step, q, k, v, budget_s: float):
     # The oracle reads only the pages the step uses: gather and upcast them.
     used, inv = np.unique(step.bt_ids, return_inverse=True)
     idx = torch.from_numpy(used.astype(np.int64)).cuda()
-    kh = k.index_select(0, idx).float().cpu().numpy()
-    vh = v.index_select(0, idx).float().cpu().numpy()
+    # Layer 0 only: the layer the GPU output is checked on.
+    kh = k.index_select(0, idx)[:, :1].float().cpu().numpy()
+    vh = v.index_select(0, idx)[:, :1].float().cpu().numpy()
     qh = q.cpu().numpy()
     ids = inv.astype(np.int32)
     pool = orc.HostPool(kh, vh)
@@ -442,12 +510,53 @@ def cpu_baseline(step, q, k, v, budget_s: float):
         "cores": nt,
         "kind": "port",
         "sample": f"whole {step.name} step ({step.num_rows} rows), median of {len(times)} steps "
-                  f"(budget {budget_s:.0f} s), {nt} threads on '{cpu_model()}', ISA level {orc.host_isa()} "
-                  f"(2=AVX-512, 1=AVX2); C++ restatement of the reference C# kernel",
+                  f"(budget {budget_s:.0f} s), {nt} threads on '{cpu_model()}' ({visible_cores()} cores visible "
+                  f"to the process, {HOST_CPU_SHARE} per GPU allotted to a job on this host), ISA level "
+                  f"{orc.host_isa()} (2=AVX-512, 1=AVX2); C++ restatement of the reference C# kernel",
         "ms_per_step": round(med * 1e3, 3),
         "seq_steps_per_s": round(step.num_rows / med, 1),
     }
     return rec, out.copy()
+
+
+def summarize_trace(path: str, kernel: str, last: int) -> dict:
+    """Launch durations of `kernel` in a rocprofv3 kernel-trace CSV: all launches, and the
+    last `last` of them in dispatch order (the timed region of a --profile-only run)."""
+    import csv
+
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if kernel in r["Kernel_Name"]:
+                rows.append((int(r["Dispatch_Id"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    rows.sort()
+    durs = [d for _, d in rows]
+    sel = durs[-last:] if last > 0 else durs
+    if not sel:
+        raise SystemExit(f"no launch of {kernel} in {path}")
+    return {"kernel": kernel, "calls": len(durs), "avg_ns_all": round(statistics.mean(durs), 1),
+            "max_ns_all": max(durs), "last": len(sel), "avg_ns_last": round(statistics.mean(sel), 1),
+            "median_ns_last": statistics.median(sel), "min_ns_last": min(sel), "max_ns_last": max(sel)}
+
+
+def summarize_pmc(path: str, kernel: str, last: int) -> dict:
+    """Per-dispatch counter values of `kernel` in a rocprofv3 counter-collection CSV,
+    averaged over its last `last` dispatches."""
+    import csv
+
+    per = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if kernel in r["Kernel_Name"]:
+                d = per.setdefault(int(r["Dispatch_Id"]), {})
+                d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    ids = sorted(per)
+    sel = ids[-last:] if last > 0 else ids
+    if not sel:
+        raise SystemExit(f"no dispatch of {kernel} in {path}")
+    names = sorted({c for i in sel for c in per[i]})
+    return {"kernel": kernel, "dispatches": len(ids), "last": len(sel),
+            "mean": {c: round(statistics.mean(per[i].get(c, 0.0) for i in sel), 3) for c in names}}
 
 
 def main() -> int:
@@ -462,14 +571,39 @@ def main() -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run a device copy of this many MiB (a known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
+    ap.add_argument("--layers", type=int, default=4,
+                    help="pool layers; step i attends layer i mod LAYERS (1 re-reads one layer every step)")
+    ap.add_argument("--decode-path", default="auto", choices=["auto", "mfma", "dpp"],
+                    help="decode kernel (auto = the matrix-core kernel)")
+    ap.add_argument("--profile-only", action="store_true",
+                    help="only the warmup and timed launches (plus each kernel alone for mixed steps)")
+    ap.add_argument("--summarize-trace", metavar="CSV", help="summarize a rocprofv3 kernel-trace CSV and exit")
+    ap.add_argument("--summarize-pmc", metavar="CSV", help="summarize a rocprofv3 counter-collection CSV and exit")
+    ap.add_argument("--kernel", default=KERNEL_NAME, help="kernel name (substring) for the summaries")
+    ap.add_argument("--last", type=int, default=0, help="average the last N launches only (0: all)")
     args = ap.parse_args()
+    if args.summarize_trace or args.summarize_pmc:
+        if args.summarize_trace:
+            print(json.dumps(summarize_trace(args.summarize_trace, args.kernel, args.last)))
+        if args.summarize_pmc:
+            print(json.dumps(summarize_pmc(args.summarize_pmc, args.kernel, args.last)))
+        return 0
+    if args.layers < 1:
+        print("--layers must be >= 1", file=sys.stderr)
+        return 2
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this path is not sharded across GPUs "
               "in this build", file=sys.stderr)
         return 2
     names = WORKLOADS if args.all else [args.workload]
+    # Python's cyclic collector stops the host for tens of milliseconds now and
+    # then (torch keeps a large object graph); the timed loops run without it.
+    gc.collect()
+    gc.disable()
     for name in names:
-        res = run_workload(name, args.steps, args.warmup, cpu=not args.no_cpu, cpu_budget_s=args.cpu_budget)
+        res = run_workload(name, args.steps, args.warmup, cpu=not (args.no_cpu or args.profile_only),
+                           cpu_budget_s=args.cpu_budget, layers=args.layers, decode_path=args.decode_path,
+                           profile_only=args.profile_only)
         print(json.dumps(res), flush=True)
     if args.copy_calibration > 0:
         import torch

@@ -146,12 +146,17 @@ __device__ __forceinline__ void merge_pair_chunked(const DecodeArgs& a, const De
 // coherent load pays a round trip to the memory side (about 1.3 us while HBM
 // is busy), so the loads are issued together: the pieces' (m, l), one pair per
 // thread, staged in LDS, and at the same time every out element this thread
-// owns (kIdx of them) for kChunk pieces.  Thread g then forms head g's max,
+// owns (kIdx of them) for kChunk pieces.  Thread g then forms head g's
 // weights and sum once, and the weights go back through LDS.  A pair of up to
 // kChunk pieces merges in one round trip, against one per owned element and
-// chunk in the general form.  Up to kMergeChunk pieces, every sum runs in the
-// same order as there, with the same values.  `scr` is LDS the caller no
-// longer reads, with room for 2 * nsplit * G + G floats.
+// chunk in the general form.
+// Which form merges a pair depends on timing (the general one inside a
+// workgroup's unit loop, this one after its last unit), so this form repeats
+// the general form's arithmetic exactly: per group of kMergeChunk pieces the
+// running max, the rescale of the sums by 2^(M - M_chunk), and the weights
+// 2^(m_s - M_chunk), with every product and sum in the same order.  Results
+// are then bit for bit the same whichever form runs.  `scr` is LDS the caller
+// no longer reads, with room for 2 * nsplit * G + (nchunks + 1) * G floats.
 template <int D, int kIdx, int kLoads>
 __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const DecodeUnit& u, int G, float* scr) {
     constexpr int kChunk = kLoads / kIdx;  // out loads in flight per thread: kIdx * kChunk
@@ -162,9 +167,11 @@ __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const Decod
     const int64_t piece = (int64_t)G * D;  // floats per piece in part_o
     const float* po = a.part_o + (int64_t)u.slot * piece;
     const float* pml = a.part_ml + (int64_t)u.slot * G * 2;
-    float* sm = scr;           // [s * G + g]: m, then the weight 2^(m - M)
+    const int nchunks = (nsplit + kMergeChunk - 1) / kMergeChunk;
+    float* sm = scr;           // [s * G + g]: m, then the weight 2^(m - M_chunk)
     float* sl = scr + n_ml;    // [s * G + g]: l
     float* sinv = sl + n_ml;   // [g]: the sum over pieces (the divisor)
+    float* sr = sinv + G;      // [c * G + g]: the rescale 2^(M - M_chunk) at chunk c
 
     float mt = -INFINITY, lt = 0.f;
     if (tid < n_ml) {
@@ -193,14 +200,22 @@ __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const Decod
     }
     __syncthreads();
     if (tid < G) {
-        float M = -INFINITY;
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, sm[s * G + tid]);
-        float L = 0.f;
-        for (int s = 0; s < nsplit; ++s) {
-            const float m = sm[s * G + tid];
-            const float f = m == -INFINITY ? 0.f : fast_exp2(m - M);
-            sm[s * G + tid] = f;
-            L = fmaf(sl[s * G + tid], f, L);
+        // merge_pair_chunked's recurrence for head `tid`.
+        float M = -INFINITY, L = 0.f;
+        for (int c = 0; c < nchunks; ++c) {
+            const int s1 = min(nsplit, (c + 1) * kMergeChunk);
+            float Mc = M;
+            for (int s = c * kMergeChunk; s < s1; ++s) Mc = fmaxf(Mc, sm[s * G + tid]);
+            const float r = fast_exp2(M - Mc);  // 0 on the first chunk (M = -inf)
+            sr[c * G + tid] = r;
+            L *= r;
+            for (int s = c * kMergeChunk; s < s1; ++s) {
+                const float m = sm[s * G + tid];
+                const float f = m == -INFINITY ? 0.f : fast_exp2(m - Mc);
+                sm[s * G + tid] = f;
+                L = fmaf(sl[s * G + tid], f, L);
+            }
+            M = Mc;
         }
         sinv[tid] = L;
     }
@@ -214,8 +229,13 @@ __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const Decod
         for (int k = 0; k < kIdx; ++k) {
             const int g = min(G - 1, (tid + k * kDecodeThreads) / D);
 #pragma unroll
-            for (int i = 0; i < kChunk; ++i)
-                if (s0 + i < nsplit) O[k] = fmaf(os[k][i], sm[(s0 + i) * G + g], O[k]);
+            for (int i = 0; i < kChunk; ++i) {
+                const int s = s0 + i;
+                if (s < nsplit) {
+                    if (s % kMergeChunk == 0) O[k] *= sr[(s / kMergeChunk) * G + g];
+                    O[k] = fmaf(os[k][i], sm[s * G + g], O[k]);
+                }
+            }
         }
     }
 #pragma unroll
@@ -238,9 +258,11 @@ __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const Decod
 // form spills there).
 template <int D, int GMAX, int kLoads = 32>
 __device__ __forceinline__ void merge_pair(const DecodeArgs& a, const DecodeUnit& u, int G, EpilogueLds<D, GMAX>& sh) {
-    const int n_ml = (u.split_info >> 16) * G;
+    const int nsplit = u.split_info >> 16;
+    const int n_ml = nsplit * G;
+    const int n_scr = 2 * n_ml + ((nsplit + kMergeChunk - 1) / kMergeChunk + 1) * G;
     constexpr int kScratch = kDecodeWaves * GMAX * D;
-    if (kLoads > 0 && n_ml <= kDecodeThreads && 2 * n_ml + G <= kScratch && G * D <= 8 * kDecodeThreads) {
+    if (kLoads > 0 && n_ml <= kDecodeThreads && n_scr <= kScratch && G * D <= 8 * kDecodeThreads) {
         __syncthreads();
         if (G * D <= 4 * kDecodeThreads)
             merge_pair_wide<D, 4, (kLoads > 0 ? kLoads : 4)>(a, u, G, &sh.o[0][0][0]);

@@ -9,11 +9,13 @@ namespace {
 
 // PagedBlockPool.Store (PagedBlockPool.cs:151-161) for n tokens at once:
 // token i, KV head h -> K/V[block_ids[i]][layer][h][slots[i]][:].  One
-// workgroup per (token, head); fp32 -> fp16 rounds to nearest even.
+// workgroup per (token, head); fp32 -> fp16 rounds to nearest even.  A token
+// with block id -1 has no slot and is skipped.
 template <typename KT>
 __global__ __launch_bounds__(128) void write_tokens_kernel(WriteTokensArgs a) {
     const int i = blockIdx.x;
     const int h = blockIdx.y;
+    if (a.block_ids[i] < 0) return;
     const int64_t dst = (int64_t)a.block_ids[i] * a.block_stride + a.layer_offset +
                         (int64_t)h * a.head_stride + (int64_t)a.slots[i] * a.head_dim;
     const int64_t src = ((int64_t)i * a.n_kv + h) * a.head_dim;
@@ -31,7 +33,8 @@ __global__ __launch_bounds__(128) void write_tokens_kernel(WriteTokensArgs a) {
 // RoFormer): the angle is formed and reduced to [-pi, pi] in fp64, so it
 // stays exact at long positions, and its cosine and sine are taken once per
 // token in fp32.  Q heads are rotated in place, K heads are rotated into the
-// pool slot and V is stored as is; fp16 pools round to nearest even.
+// pool slot and V is stored as is; fp16 pools round to nearest even.  A token
+// with block id -1 has no slot: its Q is rotated, its K and V are not stored.
 template <typename KT>
 __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
     __shared__ float cs[kRopeMaxHalf][2];
@@ -48,9 +51,10 @@ __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
         cs[j][1] = s;
     }
     __syncthreads();
+    const bool stored = a.block_ids[i] >= 0;
     const int64_t dst = (int64_t)a.block_ids[i] * a.block_stride + a.layer_offset + (int64_t)a.slots[i] * d;
     const bool pairs = a.style == GSP_ROPE_PAIRS;
-    const int heads = a.n_heads + a.n_kv;
+    const int heads = a.n_heads + (stored ? a.n_kv : 0);
     for (int idx = threadIdx.x; idx < heads * half; idx += blockDim.x) {
         const int h = idx / half;
         const int j = idx - h * half;
@@ -72,7 +76,7 @@ __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
             kd[e1] = static_cast<KT>(x0 * s + x1 * c);
         }
     }
-    for (int idx = threadIdx.x; idx < a.n_kv * d; idx += blockDim.x) {
+    for (int idx = threadIdx.x; stored && idx < a.n_kv * d; idx += blockDim.x) {
         const int hk = idx / d;
         const int e = idx - hk * d;
         static_cast<KT*>(a.v_pool)[dst + (int64_t)hk * a.head_stride + e] =

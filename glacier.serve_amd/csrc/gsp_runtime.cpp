@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -127,14 +128,31 @@ struct gsp_ctx {
     hipEvent_t fork_ev = nullptr;
     hipEvent_t join_ev = nullptr;
 
-    // Step staging: pinned host buffer, its device mirror, and an event that
-    // marks when the last upload out of the staging buffer has completed.
-    int32_t* staging = nullptr;
-    size_t staging_words = 0;
-    int32_t* d_step = nullptr;
-    size_t d_step_words = 0;
-    hipEvent_t staging_done = nullptr;
-    bool staging_pending = false;
+    // Step staging, double-buffered: successive packs alternate between two
+    // slots, each a pinned host buffer and its device mirror.  A slot's upload
+    // runs on copy_stream once the last kernel that read the slot's previous
+    // step has finished (kernel_done), so it overlaps the kernels of the step
+    // before; the kernels of a step wait for its upload (upload_done).
+    static constexpr int kSlots = 2;
+    hipStream_t copy_stream = nullptr;
+    int32_t* staging[kSlots] = {};
+    size_t staging_words[kSlots] = {};
+    int32_t* d_step_slot[kSlots] = {};
+    size_t d_step_words[kSlots] = {};
+    hipEvent_t upload_done[kSlots] = {};
+    hipEvent_t kernel_done[kSlots] = {};
+    bool upload_pending[kSlots] = {};
+    // The host has seen the slot's upload complete (gsp_sync): only then may
+    // a graph capture read the slot, since a capture takes no event nodes.
+    bool upload_synced[kSlots] = {};
+    // A capture read the slot: its next upload first waits for the context's
+    // stream on the host, where the graph's replays normally run.
+    bool slot_captured[kSlots] = {};
+    // No kernel of the packed step has been enqueued yet: the first one
+    // marks the end of the previous step's kernels and waits for the upload.
+    bool step_fresh = false;
+    int slot = 0;               // slot of the packed step
+    int32_t* d_step = nullptr;  // d_step_slot[slot]
 
     // Auxiliary staging for pool writes.
     int32_t* aux = nullptr;
@@ -155,7 +173,7 @@ struct gsp_ctx {
     bool step_valid = false;
     gsp_step_info info{};
     int32_t max_id = -1;
-    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_units = 0, off_tiles = 0, off_bins = 0;
+    size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_wr = 0, off_units = 0, off_tiles = 0, off_bins = 0;
     int32_t num_units = 0;      // decode units of the packed step
     int32_t num_bins = 0;       // decode workgroups (bins of units) of the packed step
     int32_t num_tiles = 0;      // prefill tiles of the packed step
@@ -228,10 +246,52 @@ int is_capturing(hipStream_t stream, bool* out) {
     return rc;
 }
 
+// Kernels of the packed step read its device slot: they wait for the slot's
+// upload, and the slot's next upload waits for them (step_done).  A graph
+// capture records no event node: it needs the upload complete on the host
+// already (gsp_sync after gsp_step_pack), and marks the slot so that its next
+// upload first drains the context's stream, where the replays run.
+// Only the first kernel call of a step does so: it records kernel_done of the
+// other slot (everything enqueued before it, i.e. the previous step's
+// kernels) and waits for its own upload; later calls of the step follow it on
+// the same stream.  A pack that finds no call since the previous pack records
+// that marker itself (pack_mark_previous).
+int step_begin(gsp_ctx* ctx, bool* capturing) {
+    int rc = is_capturing(ctx->stream, capturing);
+    if (rc) return rc;
+    if (*capturing) {
+        if (!ctx->upload_synced[ctx->slot])
+            return gsp::fail(GSP_E_STATE,
+                             "the packed step's upload is not known to be complete: call gsp_sync after "
+                             "gsp_step_pack and before capturing");
+        ctx->slot_captured[ctx->slot] = true;
+        return GSP_OK;
+    }
+    if (!ctx->step_fresh) return GSP_OK;
+    rc = check_hip(hipEventRecord(ctx->kernel_done[ctx->slot ^ 1], ctx->stream), "hipEventRecord(step kernels)");
+    if (!rc && !ctx->upload_synced[ctx->slot])
+        rc = check_hip(hipStreamWaitEvent(ctx->stream, ctx->upload_done[ctx->slot], 0), "hipStreamWaitEvent(upload)");
+    if (!rc) ctx->step_fresh = false;
+    return rc;
+}
+
+int step_done(gsp_ctx*, bool) { return GSP_OK; }
+
+// Waits on the host for `ev`, spinning on the query first: a sleeping wait can
+// add milliseconds to a step that is only microseconds behind.
+int host_wait(hipEvent_t ev, const char* what) {
+    for (int i = 0; i < 200000; ++i) {
+        const hipError_t e = hipEventQuery(ev);
+        if (e == hipSuccess) return GSP_OK;
+        if (e != hipErrorNotReady) return check_hip(e, what);
+    }
+    return check_hip(hipEventSynchronize(ev), what);
+}
+
 // Grows a pinned host buffer (waiting for the upload that last used it).
 int ensure_pinned(int32_t** buf, size_t* cap, size_t words, hipEvent_t done, bool* pending) {
     if (*pending) {
-        int rc = check_hip(hipEventSynchronize(done), "hipEventSynchronize(staging)");
+        int rc = host_wait(done, "hipEventSynchronize(staging)");
         if (rc) return rc;
         *pending = false;
     }
@@ -358,7 +418,14 @@ int gsp_init(int device, gsp_ctx** out) {
     ctx->arch = info.arch;
     rc = set_device(ctx);
     if (!rc) rc = check_hip(hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking), "hipStreamCreate");
-    if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->staging_done, hipEventDisableTiming), "hipEventCreate");
+    if (!rc) rc = check_hip(hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking), "hipStreamCreate");
+    for (int j = 0; j < gsp_ctx::kSlots && !rc; ++j) {
+        rc = check_hip(hipEventCreateWithFlags(&ctx->upload_done[j], hipEventDisableTiming), "hipEventCreate");
+        if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->kernel_done[j], hipEventDisableTiming), "hipEventCreate");
+        // Recorded once on the idle stream, so the first waits on them pass.
+        if (!rc) rc = check_hip(hipEventRecord(ctx->upload_done[j], ctx->own_stream), "hipEventRecord");
+        if (!rc) rc = check_hip(hipEventRecord(ctx->kernel_done[j], ctx->own_stream), "hipEventRecord");
+    }
     if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->aux_done, hipEventDisableTiming), "hipEventCreate");
     if (!rc) rc = check_hip(hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking), "hipStreamCreate");
     if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming), "hipEventCreate");
@@ -379,16 +446,21 @@ void gsp_shutdown(gsp_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->staging) (void)hipHostFree(ctx->staging);
+    if (ctx->copy_stream) (void)hipStreamSynchronize(ctx->copy_stream);
+    for (int j = 0; j < gsp_ctx::kSlots; ++j) {
+        if (ctx->staging[j]) (void)hipHostFree(ctx->staging[j]);
+        if (ctx->d_step_slot[j]) (void)hipFree(ctx->d_step_slot[j]);
+        if (ctx->upload_done[j]) (void)hipEventDestroy(ctx->upload_done[j]);
+        if (ctx->kernel_done[j]) (void)hipEventDestroy(ctx->kernel_done[j]);
+    }
+    if (ctx->copy_stream) (void)hipStreamDestroy(ctx->copy_stream);
     if (ctx->aux) (void)hipHostFree(ctx->aux);
-    if (ctx->d_step) (void)hipFree(ctx->d_step);
     if (ctx->d_aux) (void)hipFree(ctx->d_aux);
     if (ctx->d_mm) (void)hipFree(ctx->d_mm);
     if (ctx->d_mmx) (void)hipFree(ctx->d_mmx);
     if (ctx->d_mmexp) (void)hipFree(ctx->d_mmexp);
     if (ctx->part) (void)hipFree(ctx->part);
     if (ctx->counters) (void)hipFree(ctx->counters);
-    if (ctx->staging_done) (void)hipEventDestroy(ctx->staging_done);
     if (ctx->aux_done) (void)hipEventDestroy(ctx->aux_done);
     if (ctx->side_stream) (void)hipStreamSynchronize(ctx->side_stream);
     if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
@@ -419,8 +491,11 @@ int gsp_sync(gsp_ctx* ctx) {
     gsp::clear_error();
     if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
     int rc = set_device(ctx);
+    if (!rc) rc = check_hip(hipStreamSynchronize(ctx->copy_stream), "hipStreamSynchronize(copy)");
+    if (!rc) rc = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     if (rc) return rc;
-    return check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    for (int j = 0; j < gsp_ctx::kSlots; ++j) ctx->upload_synced[j] = true;
+    return GSP_OK;
 }
 
 int gsp_set_split_pages(gsp_ctx* ctx, int32_t pages) {
@@ -528,6 +603,74 @@ int gsp_pool_arenas(const gsp_pool* pool, void** k_dev, void** v_dev, size_t* k_
     return GSP_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Store of n tokens whose block ids and slots are already on the device.
+int store_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const int32_t* d_blocks,
+                 const int32_t* d_slots, const float* k_dev, const float* v_dev) {
+    const gsp_pool_desc& d = pool->desc;
+    gsp::WriteTokensArgs a;
+    a.k_pool = pool->k;
+    a.v_pool = pool->v;
+    a.block_stride = pool->block_stride_k;
+    a.layer_offset = (int64_t)layer * pool->layer_stride_k;
+    a.head_stride = pool->head_stride_k;
+    a.block_ids = d_blocks;
+    a.slots = d_slots;
+    a.k = k_dev;
+    a.v = v_dev;
+    a.n = n;
+    a.n_kv = d.heads_kv;
+    a.head_dim = d.head_dim;
+    return check_hip(gsp::launch_write_tokens(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "write_tokens launch");
+}
+
+int check_rope_args(const gsp_pool* pool, int32_t n_heads, float freq_base, int32_t style, const float* q_dev) {
+    if (n_heads < 0) return gsp::fail(GSP_E_INVALID_ARG, "nHeads must be >= 0 (got %d)", n_heads);
+    if (n_heads > 0 && !q_dev) return gsp::fail(GSP_E_INVALID_ARG, "q is NULL with nHeads %d", n_heads);
+    if (style != GSP_ROPE_PAIRS && style != GSP_ROPE_HALVES)
+        return gsp::fail(GSP_E_INVALID_ARG, "unknown RoPE pairing %d", style);
+    if (!(freq_base > 0.0f) || !std::isfinite(freq_base))
+        return gsp::fail(GSP_E_INVALID_ARG, "RoPE frequency base must be positive and finite");
+    const gsp_pool_desc& d = pool->desc;
+    if (d.v_head_dim != d.head_dim) return gsp::fail(GSP_E_UNSUPPORTED, "vHeadDim != headDim is not supported on the device pool");
+    if (d.head_dim % 2 != 0 || d.head_dim > 2 * gsp::kRopeMaxHalf)
+        return gsp::fail(GSP_E_UNSUPPORTED, "RoPE needs an even headDim <= %d (got %d)", 2 * gsp::kRopeMaxHalf, d.head_dim);
+    return GSP_OK;
+}
+
+// RoPE then Store of n tokens whose positions, block ids and slots are already on the device.
+int rope_store_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const int32_t* d_pos,
+                      const int32_t* d_blocks, const int32_t* d_slots, int32_t n_heads, float freq_base,
+                      int32_t style, float* q_dev, const float* k_dev, const float* v_dev) {
+    const gsp_pool_desc& d = pool->desc;
+    gsp::RopeWriteArgs a;
+    a.k_pool = pool->k;
+    a.v_pool = pool->v;
+    a.block_stride = pool->block_stride_k;
+    a.layer_offset = (int64_t)layer * pool->layer_stride_k;
+    a.head_stride = pool->head_stride_k;
+    a.positions = d_pos;
+    a.block_ids = d_blocks;
+    a.slots = d_slots;
+    a.q = q_dev;
+    a.k = k_dev;
+    a.v = v_dev;
+    a.log2_base = std::log2((double)freq_base);
+    a.n = n;
+    a.n_heads = n_heads;
+    a.n_kv = d.heads_kv;
+    a.head_dim = d.head_dim;
+    a.style = style;
+    return check_hip(gsp::launch_rope_write(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "rope_write launch");
+}
+
+}  // namespace
+
+extern "C" {
+
 int gsp_pool_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const int32_t* block_ids,
                           const int32_t* slots, const float* k_dev, const float* v_dev) {
     gsp::clear_error();
@@ -557,20 +700,7 @@ int gsp_pool_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
     if (!rc) rc = check_hip(hipEventRecord(ctx->aux_done, ctx->stream), "hipEventRecord");
     if (rc) return rc;
     ctx->aux_pending = true;
-    gsp::WriteTokensArgs a;
-    a.k_pool = pool->k;
-    a.v_pool = pool->v;
-    a.block_stride = pool->block_stride_k;
-    a.layer_offset = (int64_t)layer * pool->layer_stride_k;
-    a.head_stride = pool->head_stride_k;
-    a.block_ids = ctx->d_aux;
-    a.slots = ctx->d_aux + n;
-    a.k = k_dev;
-    a.v = v_dev;
-    a.n = n;
-    a.n_kv = d.heads_kv;
-    a.head_dim = d.head_dim;
-    return check_hip(gsp::launch_write_tokens(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "write_tokens launch");
+    return store_tokens(ctx, pool, layer, n, ctx->d_aux, ctx->d_aux + n, k_dev, v_dev);
 }
 
 int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const int32_t* positions,
@@ -581,16 +711,9 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
     if (n < 0) return gsp::fail(GSP_E_INVALID_ARG, "n must be >= 0 (got %d)", n);
     if (n == 0) return GSP_OK;
     if (!positions || !block_ids || !slots || !k_dev || !v_dev) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument");
-    if (n_heads < 0) return gsp::fail(GSP_E_INVALID_ARG, "nHeads must be >= 0 (got %d)", n_heads);
-    if (n_heads > 0 && !q_dev) return gsp::fail(GSP_E_INVALID_ARG, "q is NULL with nHeads %d", n_heads);
-    if (style != GSP_ROPE_PAIRS && style != GSP_ROPE_HALVES)
-        return gsp::fail(GSP_E_INVALID_ARG, "unknown RoPE pairing %d", style);
-    if (!(freq_base > 0.0f) || !std::isfinite(freq_base))
-        return gsp::fail(GSP_E_INVALID_ARG, "RoPE frequency base must be positive and finite");
+    int rc = check_rope_args(pool, n_heads, freq_base, style, q_dev);
+    if (rc) return rc;
     const gsp_pool_desc& d = pool->desc;
-    if (d.v_head_dim != d.head_dim) return gsp::fail(GSP_E_UNSUPPORTED, "vHeadDim != headDim is not supported on the device pool");
-    if (d.head_dim % 2 != 0 || d.head_dim > 2 * gsp::kRopeMaxHalf)
-        return gsp::fail(GSP_E_UNSUPPORTED, "RoPE needs an even headDim <= %d (got %d)", 2 * gsp::kRopeMaxHalf, d.head_dim);
     if (layer < 0 || layer >= d.layers) return gsp::fail(GSP_E_INVALID_ARG, "layer %d out of range [0, %d)", layer, d.layers);
     for (int32_t i = 0; i < n; ++i) {
         if (positions[i] < 0) return gsp::fail(GSP_E_INVALID_ARG, "token %d: position %d is negative", i, positions[i]);
@@ -599,7 +722,7 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
         if (slots[i] < 0 || slots[i] >= d.block_size)
             return gsp::fail(GSP_E_INVALID_ARG, "slot %d out of range [0, %d)", slots[i], d.block_size);
     }
-    int rc = set_device(ctx);
+    rc = set_device(ctx);
     if (rc) return rc;
     const size_t words = 3 * (size_t)n;
     rc = ensure_pinned(&ctx->aux, &ctx->aux_words, words, ctx->aux_done, &ctx->aux_pending);
@@ -613,25 +736,67 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
     if (!rc) rc = check_hip(hipEventRecord(ctx->aux_done, ctx->stream), "hipEventRecord");
     if (rc) return rc;
     ctx->aux_pending = true;
-    gsp::RopeWriteArgs a;
-    a.k_pool = pool->k;
-    a.v_pool = pool->v;
-    a.block_stride = pool->block_stride_k;
-    a.layer_offset = (int64_t)layer * pool->layer_stride_k;
-    a.head_stride = pool->head_stride_k;
-    a.positions = ctx->d_aux;
-    a.block_ids = ctx->d_aux + n;
-    a.slots = ctx->d_aux + 2 * (size_t)n;
-    a.q = q_dev;
-    a.k = k_dev;
-    a.v = v_dev;
-    a.log2_base = std::log2((double)freq_base);
-    a.n = n;
-    a.n_heads = n_heads;
-    a.n_kv = d.heads_kv;
-    a.head_dim = d.head_dim;
-    a.style = style;
-    return check_hip(gsp::launch_rope_write(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "rope_write launch");
+    return rope_store_tokens(ctx, pool, layer, n, ctx->d_aux, ctx->d_aux + n, ctx->d_aux + 2 * (size_t)n, n_heads,
+                             freq_base, style, q_dev, k_dev, v_dev);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The packed step's own K/V write: query token i's K and V go to the slot of
+// its position (positions[b] + i of its row), read from the device copy of
+// the step, so every layer of a tick reuses one upload.
+int check_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, const float* k_dev, const float* v_dev) {
+    if (!ctx || !pool) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool is NULL");
+    if (!ctx->step_valid) return gsp::fail(GSP_E_STATE, "gsp_step_pack must succeed before a step write");
+    const gsp_pool_desc& d = pool->desc;
+    if (d.heads_kv != ctx->step_heads_kv || d.total_blocks < ctx->step_blocks)
+        return gsp::fail(GSP_E_INVALID_ARG, "the step was packed for a pool with %d KV heads and %d blocks",
+                         ctx->step_heads_kv, ctx->step_blocks);
+    if (ctx->max_id >= d.total_blocks)
+        return gsp::fail(GSP_E_INVALID_ARG, "block id %d out of range [0, %d)", ctx->max_id, d.total_blocks);
+    if (layer < 0 || layer >= d.layers) return gsp::fail(GSP_E_INVALID_ARG, "layer %d out of range [0, %d)", layer, d.layers);
+    if (ctx->info.total_q > 0 && (!k_dev || !v_dev)) return gsp::fail(GSP_E_INVALID_ARG, "k/v must not be NULL");
+    return set_device(ctx);
+}
+
+}  // namespace
+
+extern "C" {
+
+int gsp_pool_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, const float* k_dev, const float* v_dev) {
+    gsp::clear_error();
+    int rc = check_write_step(ctx, pool, layer, k_dev, v_dev);
+    if (rc) return rc;
+    const int32_t n = ctx->info.total_q;
+    if (n == 0) return GSP_OK;
+    bool cap = false;
+    rc = step_begin(ctx, &cap);
+    if (rc) return rc;
+    const int32_t* wr = ctx->d_step + ctx->off_wr;
+    rc = store_tokens(ctx, pool, layer, n, wr + n, wr + 2 * (size_t)n, k_dev, v_dev);
+    const int rd = step_done(ctx, cap);
+    return rc ? rc : rd;
+}
+
+int gsp_rope_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_heads, float freq_base, int32_t style,
+                        float* q_dev, const float* k_dev, const float* v_dev) {
+    gsp::clear_error();
+    int rc = check_write_step(ctx, pool, layer, k_dev, v_dev);
+    if (rc) return rc;
+    rc = check_rope_args(pool, n_heads, freq_base, style, q_dev);
+    if (rc) return rc;
+    const int32_t n = ctx->info.total_q;
+    if (n == 0) return GSP_OK;
+    bool cap = false;
+    rc = step_begin(ctx, &cap);
+    if (rc) return rc;
+    const int32_t* wr = ctx->d_step + ctx->off_wr;
+    rc = rope_store_tokens(ctx, pool, layer, n, wr, wr + n, wr + 2 * (size_t)n, n_heads, freq_base, style, q_dev,
+                           k_dev, v_dev);
+    const int rd = step_done(ctx, cap);
+    return rc ? rc : rd;
 }
 
 // Q8_0 products with at least this many outputs (batch x out_dim) take the fp16
@@ -843,6 +1008,7 @@ static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max, bool pair) {
 int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc) {
     gsp::clear_error();
     if (!ctx || !pool || !desc) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool/desc is NULL");
+    const auto t_pack0 = std::chrono::steady_clock::now();
     {
         // Refused before anything changes: the step already packed stays valid.
         bool cap_on = false;
@@ -1063,6 +1229,10 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     off += (size_t)packed_pages;
     const size_t off_ctx = off;
     off += (size_t)total_q;
+    // Where each query token's own K/V goes (gsp_*_write_step): its position,
+    // and the block and slot of that position, or block -1 without a slot.
+    const size_t off_wr = off;
+    off += 3 * (size_t)total_q;
     off = align_up(off, 8);
     const size_t off_units = off;
     off += n_units * (sizeof(DecodeUnit) / sizeof(int32_t));
@@ -1074,8 +1244,18 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
 
     int rc = set_device(ctx);
     if (rc) return rc;
-    rc = ensure_pinned(&ctx->staging, &ctx->staging_words, words, ctx->staging_done, &ctx->staging_pending);
-    if (!rc) rc = ensure_device(ctx, &ctx->d_step, &ctx->d_step_words, words, false);
+    // The other slot than the step packed last: its kernels may still run.
+    const int slot = ctx->slot ^ 1;
+    if (ctx->slot_captured[slot]) {  // replays of a graph that read this slot
+        rc = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        if (rc) return rc;
+        ctx->slot_captured[slot] = false;
+    }
+    rc = ensure_pinned(&ctx->staging[slot], &ctx->staging_words[slot], words, ctx->upload_done[slot],
+                       &ctx->upload_pending[slot]);
+    if (!rc && words > ctx->d_step_words[slot])  // no upload may still write the old buffer
+        rc = check_hip(hipStreamSynchronize(ctx->copy_stream), "hipStreamSynchronize(copy)");
+    if (!rc) rc = ensure_device(ctx, &ctx->d_step_slot[slot], &ctx->d_step_words[slot], words, false);
     // The split workspace for any group up to the decode tile, so that a
     // captured gsp_attention_step of this step never has to grow it.
     if (!rc && slots > 0)
@@ -1085,18 +1265,22 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, (size_t)total_q * H, true);
     if (rc) return rc;
 
-    int32_t* st = ctx->staging;
+    int32_t* st = ctx->staging[slot];
     std::memset(st, 0, kHdrWords * sizeof(int32_t));
     int32_t max_id = -1;
     {
         int32_t* rows = st + off_rows;
         int32_t* ids = st + off_ids;
-        int64_t w = 0;
+        int32_t* wr_pos = st + off_wr;
+        int32_t* wr_blk = wr_pos + total_q;
+        int32_t* wr_slot = wr_blk + total_q;
+        int64_t w = 0, qi = 0;
         rows[0] = 0;
         for (int32_t b = 0; b < B; ++b) {
             const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
-            const int64_t total_last =
-                ql > 0 ? std::min<int64_t>(desc->token_counts[b], (int64_t)desc->positions[b] + ql) : 0;
+            const int32_t pos = desc->positions[b];
+            const int32_t tc = desc->token_counts[b];
+            const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
             const int64_t pages = (total_last + gsp::kBlockSize - 1) / gsp::kBlockSize;
             const int32_t* src = desc->bt_ids + desc->bt_offsets[b];
             for (int64_t i = 0; i < pages; ++i) {
@@ -1104,6 +1288,16 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                 max_id = std::max(max_id, src[i]);
             }
             rows[b + 1] = (int32_t)w;
+            // A query token at p < TokenCount has its slot in the packed pages
+            // (p < total_last); the reference stores its K/V there before
+            // attending (PagedTransformerRunner.cs:620-634, :437-452).
+            for (int32_t i = 0; i < ql; ++i, ++qi) {
+                const int64_t p = (int64_t)pos + i;
+                wr_pos[qi] = (int32_t)p;
+                const bool has = p < tc;
+                wr_blk[qi] = has ? src[p / gsp::kBlockSize] : -1;
+                wr_slot[qi] = has ? (int32_t)(p % gsp::kBlockSize) : 0;
+            }
         }
     }
     if (total_q) std::memcpy(st + off_ctx, ctx->q_ctx.data(), (size_t)total_q * sizeof(int32_t));
@@ -1122,15 +1316,29 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     st[kHdrTiles] = (int32_t)n_tiles;
     st[kHdrBins] = n_bins;
 
-    rc = check_hip(hipMemcpyAsync(ctx->d_step, st, words * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream),
-                   "hipMemcpyAsync(step)");
-    if (!rc) rc = check_hip(hipEventRecord(ctx->staging_done, ctx->stream), "hipEventRecord");
+    // One copy for the whole step, on the copy stream, once the kernels that
+    // read this slot's previous step are done.  They are marked by the first
+    // kernel call of the step after them; without such a call (two packs in a
+    // row), everything enqueued so far is marked here.
+    if (ctx->step_fresh)
+        rc = check_hip(hipEventRecord(ctx->kernel_done[slot], ctx->stream), "hipEventRecord(step kernels)");
+    if (!rc) rc = check_hip(hipStreamWaitEvent(ctx->copy_stream, ctx->kernel_done[slot], 0), "hipStreamWaitEvent(copy)");
+    if (!rc)
+        rc = check_hip(hipMemcpyAsync(ctx->d_step_slot[slot], st, words * sizeof(int32_t), hipMemcpyHostToDevice,
+                                      ctx->copy_stream),
+                       "hipMemcpyAsync(step)");
+    if (!rc) rc = check_hip(hipEventRecord(ctx->upload_done[slot], ctx->copy_stream), "hipEventRecord");
     if (rc) return rc;
-    ctx->staging_pending = true;
+    ctx->upload_pending[slot] = true;
+    ctx->upload_synced[slot] = false;
+    ctx->step_fresh = true;
+    ctx->slot = slot;
+    ctx->d_step = ctx->d_step_slot[slot];
 
     ctx->off_rows = off_rows;
     ctx->off_ids = off_ids;
     ctx->off_ctx = off_ctx;
+    ctx->off_wr = off_wr;
     ctx->off_units = off_units;
     ctx->off_tiles = off_tiles;
     ctx->off_bins = off_bins;
@@ -1156,6 +1364,8 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->info.prefill_pairs = tiled_pairs;
     ctx->info.decode_bins = n_bins;
     ctx->info.reserved = 0;
+    ctx->info.pack_host_ns =
+        std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t_pack0).count();
     ctx->step_valid = true;
     return GSP_OK;
 }
@@ -1174,7 +1384,9 @@ int gsp_step_download(gsp_ctx* ctx, int32_t* row_offsets, int32_t* ids, int32_t*
     if (!ctx->step_valid) return gsp::fail(GSP_E_STATE, "no packed step");
     int rc = set_device(ctx);
     if (!rc) rc = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (!rc) rc = check_hip(hipEventSynchronize(ctx->upload_done[ctx->slot]), "hipEventSynchronize(upload)");
     if (rc) return rc;
+    ctx->upload_synced[ctx->slot] = true;
     const gsp_step_info& in = ctx->info;
     if (row_offsets)
         rc = check_hip(hipMemcpy(row_offsets, ctx->d_step + ctx->off_rows, ((size_t)in.num_rows + 1) * sizeof(int32_t),
@@ -1254,10 +1466,6 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
                                  fixed->counter_words);
             part = fixed->part;
             counters = fixed->counters;
-            // The array keeps whatever the last call on this GPU left: clear the
-            // counters this launch uses (every launch leaves its own at zero).
-            rc = check_hip(gsp::launch_fill_i32(counters, (int64_t)counter_need, 0, ctx->stream), "fill launch");
-            if (rc) return rc;
         } else {
             rc = ensure_device(ctx, &ctx->part, &ctx->part_floats, part_need, false);
             // Counters start at zero and every launch leaves them at zero.
@@ -1266,6 +1474,17 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
             part = ctx->part;
             counters = ctx->counters;
         }
+    }
+
+    bool capturing = false;
+    rc = step_begin(ctx, &capturing);
+    if (rc) return rc;
+    if (fixed && slots > 0) {
+        // The array keeps whatever the last call on this GPU left: clear the
+        // counters this launch uses (every launch leaves its own at zero).
+        rc = check_hip(gsp::launch_fill_i32(counters, (int64_t)ctx->info.total_q * d.heads_kv, 0, ctx->stream),
+                       "fill launch");
+        if (rc) return rc;
     }
 
     gsp::DecodeArgs a;
@@ -1326,7 +1545,8 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
         const int jw = jc ? jc : check_hip(hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0), "hipStreamWaitEvent(join)");
         if (!rc) rc = jw;
     }
-    return rc;
+    const int rd = step_done(ctx, capturing);
+    return rc ? rc : rd;
 }
 
 // Layout of the fixed scratch: counters first, then the partials.

@@ -138,6 +138,7 @@ class StepInfo(ctypes.Structure):
         ("prefill_pairs", ctypes.c_int64),
         ("decode_bins", i32),
         ("reserved", i32),
+        ("pack_host_ns", ctypes.c_int64),
     ]
 
 
@@ -175,6 +176,8 @@ _SIGNATURES = {
     "gsp_pool_write_tokens": (ctypes.c_int, [vp, vp, i32, i32, i32p, i32p, vp, vp]),
     "gsp_rope_write_tokens": (ctypes.c_int, [vp, vp, i32, i32, i32p, i32p, i32p, i32, ctypes.c_float, i32, vp, vp, vp]),
     "gsp_matmul_batch": (ctypes.c_int, [vp, i32, vp, vp, vp, i32, i32, i32]),
+    "gsp_pool_write_step": (ctypes.c_int, [vp, vp, i32, vp, vp]),
+    "gsp_rope_write_step": (ctypes.c_int, [vp, vp, i32, i32, ctypes.c_float, i32, vp, vp, vp]),
     "gsp_pool_copy_block": (ctypes.c_int, [vp, vp, i32, i32, i32]),
     "gsp_pool_upload": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
     "gsp_pool_download": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
@@ -324,7 +327,8 @@ class Context:
         max_seq_len: int,
         q_lens: Optional[Sequence[int]] = None,
         n_bt_ids: Optional[int] = None,
-    ) -> StepInfo:
+        want_info: bool = True,
+    ) -> Optional[StepInfo]:
         """Packs one engine step (gsp_step_pack).  n_bt_ids defaults to len(bt_ids); the library
         checks the CSR offsets against it."""
         pos = _i32(positions)
@@ -342,7 +346,7 @@ class Context:
         d.bt_ids = _ptr(ids)
         d.n_bt_ids = len(bt_ids) if n_bt_ids is None else int(n_bt_ids)
         _check(self._lib.gsp_step_pack(self._h, pool.handle, ctypes.byref(d)))
-        return self.step_info()
+        return self.step_info() if want_info else None
 
     def step_info(self) -> StepInfo:
         info = StepInfo()
@@ -496,6 +500,17 @@ class Pool:
         _check(load().gsp_rope_write_tokens(self._ctx.handle, self._h, int(layer), len(b), _ptr(p), _ptr(b), _ptr(s),
                                             int(n_heads), float(freq_base), int(style), vp(q_ptr), vp(k_ptr),
                                             vp(v_ptr)))
+
+    def write_step(self, layer: int, k_ptr: int, v_ptr: int) -> None:
+        """Store of the packed step's own tokens (gsp_pool_write_step): query token i's K/V into the
+        slot of its position, from the step's device copy (no host arrays, no upload)."""
+        _check(load().gsp_pool_write_step(self._ctx.handle, self._h, int(layer), vp(k_ptr), vp(v_ptr)))
+
+    def rope_write_step(self, layer: int, n_heads: int, freq_base: float, style: int, q_ptr: int, k_ptr: int,
+                        v_ptr: int) -> None:
+        """RoPE then Store of the packed step's own tokens at their positions (gsp_rope_write_step)."""
+        _check(load().gsp_rope_write_step(self._ctx.handle, self._h, int(layer), int(n_heads), float(freq_base),
+                                          int(style), vp(q_ptr), vp(k_ptr), vp(v_ptr)))
 
     def copy_block_data(self, src: int, dst: int, valid_tokens: int) -> None:
         """PagedBlockPool.CopyBlockData (PagedBlockPool.cs:304-327) on the device."""

@@ -40,7 +40,7 @@ extern "C" {
 #pragma GCC visibility push(default)
 #endif
 
-#define GSP_ABI_VERSION 7
+#define GSP_ABI_VERSION 8
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
 
 typedef enum gsp_status {
@@ -103,7 +103,9 @@ void gsp_shutdown(gsp_ctx* ctx);
 int gsp_set_stream(gsp_ctx* ctx, void* hip_stream);
 void* gsp_get_stream(gsp_ctx* ctx);
 
-/* Blocks until all work enqueued on the context's stream has finished. */
+/* Blocks until all work enqueued on the context's stream, and the upload of
+ * the packed step, have finished.  After it the packed step may be read by a
+ * graph capture (see gsp_attention_step). */
 int gsp_sync(gsp_ctx* ctx);
 
 /* ------------------------------------------------------------------------ */
@@ -167,6 +169,24 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
                           const int32_t* positions, const int32_t* block_ids,
                           const int32_t* slots, int32_t n_heads, float freq_base, int32_t style,
                           float* q_dev, const float* k_dev, const float* v_dev);
+
+/* The K/V writes of a packed step, from the step's own device copy: no host
+ * arrays, no upload and no host wait, so every layer of an engine tick reuses
+ * the one upload of gsp_step_pack and the call can be captured.  Query token
+ * i of row b (position positions[b] + i) stores k_dev[i] and v_dev[i]
+ * ([total_q][heads_kv][head_dim] fp32, device) into the slot of that position
+ * in the row's table, as the reference stores each new token before attending
+ * (PagedTransformerRunner.cs:620-634 for decode, :437-452 for a prefill
+ * chunk).  A token at a position >= the row's token_counts[b] has no slot and
+ * is not stored.  gsp_rope_write_step first applies gsp_rope_write_tokens's
+ * rotation at that position: q_dev ([total_q][n_heads][head_dim]) in place
+ * (n_heads 0: left alone) and K on its way into the pool.  The pool must have
+ * the geometry the step was packed for. */
+int gsp_pool_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, const float* k_dev,
+                        const float* v_dev);
+int gsp_rope_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_heads,
+                        float freq_base, int32_t style, float* q_dev, const float* k_dev,
+                        const float* v_dev);
 
 /* Weight types of gsp_matmul_batch: the GGUF tensor type ids. */
 #define GSP_WTYPE_F32 0
@@ -252,6 +272,8 @@ typedef struct gsp_step_info {
     int64_t prefill_pairs;       /* sum over tiled query tokens of total (causal key count) */
     int32_t decode_bins;         /* decode workgroups: each runs one bin of units back to back */
     int32_t reserved;
+    int64_t pack_host_ns;        /* host time of the gsp_step_pack call that made the step:
+                                    validation, scheduling, staging and the copy's enqueue */
 } gsp_step_info;
 
 int gsp_step_get_info(const gsp_ctx* ctx, gsp_step_info* out);
@@ -310,7 +332,18 @@ int gsp_set_prefill_path(gsp_ctx* ctx, int32_t path);
  * block_size 16.  Work is enqueued on the context's stream.  A step with both
  * decode units and prefill tiles runs the tiles on a second stream of the
  * context, forked from and joined back into that stream, so the call is still
- * ordered as a whole on the context's stream (and can be captured). */
+ * ordered as a whole on the context's stream.
+ *
+ * Step uploads: gsp_step_pack alternates between two device slots and copies
+ * the step on a copy stream of the context, so the upload of step i+1
+ * overlaps the kernels of step i; the kernels of a step wait for its upload,
+ * and a slot is rewritten only after the kernels that read it are done.
+ * Graph capture: the call can be captured on the context's stream once the
+ * packed step's upload is known complete (gsp_sync after gsp_step_pack;
+ * otherwise GSP_E_STATE).  The graph holds the step's kernels only and reads
+ * the packed step's slot: it is valid until the next gsp_step_pack.  The pack
+ * after that reuses the slot and first waits on the host for the context's
+ * stream; replays launched on other streams must have finished by then. */
 int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t n_heads,
                        const float* q_dev, float* out_dev, float attn_scale,
                        const float* sink_logit);

@@ -219,3 +219,28 @@ def test_repeated_steps_reuse_counters(torch_mod, gsp, ctx):
         got = gpu_step(torch_mod, gsp, ctx, step, q, pool, split_pages=[1, 2, 5, 0, 3, 1][i])
         assert max_err(got, ref) <= 1e-4
     pool.destroy()
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "f16"])
+def test_split_merges_are_bit_reproducible(torch_mod, gsp, ctx, kv_dtype):
+    """A split pair is merged by whichever workgroup counts its last piece, inside
+    its unit loop (general form) or after its last unit (wide form), so the form
+    depends on timing.  Both run the same arithmetic, so pairs of many pieces
+    (1- and 2-page splits: up to 60 pieces) give the same bits on every run."""
+    from gpu_helpers import TOL, gpu_step, max_err, oracle_step, to_device_pool
+
+    torch = torch_mod
+    step = workloads.small_step(seed=81, rows=20, n_heads=28, n_kv=4, head_dim=128, kv_dtype=kv_dtype, ctx_lo=300,
+                                ctx_hi=960, total_blocks=2048)
+    q, k, v = workloads.host_values(step)
+    pool, keep = to_device_pool(torch, gsp, ctx, step, k, v)
+    try:
+        ref = oracle_step(step, q, k, v)
+        for split in (1, 2):
+            print(f"case reproducible merges {kv_dtype} split={split}", flush=True)
+            outs = [gpu_step(torch, gsp, ctx, step, q, pool, split_pages=split) for _ in range(6)]
+            assert max_err(outs[0], ref) <= TOL[kv_dtype]
+            for r, o in enumerate(outs[1:], 1):
+                assert np.array_equal(o, outs[0]), f"split {split}: run {r} differs from run 0"
+    finally:
+        pool.destroy()

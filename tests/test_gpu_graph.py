@@ -50,6 +50,7 @@ def test_captured_step_replays_match_eager(torch_mod, gsp, ctx, kind):
         assert max_err(eager.cpu().numpy(), ref) <= TOL[step.kv_dtype]
 
         out = torch.full_like(eager, float("nan"))
+        ctx.sync()  # the step's upload is known complete: a capture may read it
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             ctx.attention_step(pool, 0, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
@@ -97,8 +98,9 @@ HIP_GRAPH_NODE_KERNEL, HIP_GRAPH_NODE_MEMCPY, HIP_GRAPH_NODE_MEMSET = 0, 1, 2
 def test_capture_of_a_step_larger_than_any_earlier(torch_mod, gsp):
     """A fresh context packs a split step and captures it with no eager run first:
     gsp_step_pack sized the workspace, so the capture holds kernels only (no
-    memset or copy node) and every replay equals the eager step.  Packing, and a
-    workspace that would have to grow, are refused during the capture."""
+    memset, copy or event node) and every replay equals the eager step.  A
+    capture before gsp_sync (the step's upload not yet known complete), packing,
+    and a workspace that would have to grow are refused during the capture."""
     torch = torch_mod
     step = workloads.small_step(seed=44, rows=20, n_heads=28, n_kv=4, head_dim=128, ctx_lo=200, ctx_hi=1500,
                                 total_blocks=4096)
@@ -120,6 +122,13 @@ def test_capture_of_a_step_larger_than_any_earlier(torch_mod, gsp):
         y = torch.empty((16, 64), device="cuda")
         out = torch.full((step.total_q, step.n_heads, step.head_dim), float("nan"), device="cuda")
         torch.cuda.synchronize()
+        early = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(early, stream=stream):
+            out.add_(0.0)  # something for the capture to hold
+            with pytest.raises(gsp.StateError, match="gsp_sync"):
+                fresh.attention_step(pool, 0, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
+        del early
+        fresh.sync()
         graph = torch.cuda.CUDAGraph(keep_graph=True)
         with torch.cuda.graph(graph, stream=stream):
             fresh.attention_step(pool, 0, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
@@ -131,7 +140,7 @@ def test_capture_of_a_step_larger_than_any_earlier(torch_mod, gsp):
                 fresh.matmul_batch(gsp.WTYPE_F32, w.data_ptr(), x.data_ptr(), y.data_ptr(), 4096, 64, 16)
         types = _graph_node_types(graph)
         assert HIP_GRAPH_NODE_KERNEL in types
-        assert HIP_GRAPH_NODE_MEMSET not in types and HIP_GRAPH_NODE_MEMCPY not in types, types
+        assert set(types) == {HIP_GRAPH_NODE_KERNEL}, types
         graph.instantiate()
         # The refused pack left the packed step intact: the eager run after it uses it.
         eager = torch.full_like(out, float("nan"))

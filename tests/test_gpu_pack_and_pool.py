@@ -191,3 +191,41 @@ def test_cow_fork_copies_page_on_device(torch_mod, gsp, ctx):
     assert alloc.free_blocks_count == 16
     alloc.attach_pool(None, None)
     pool.destroy()
+
+
+def test_back_to_back_packs_without_host_sync(torch_mod, gsp, ctx):
+    """Packs alternate between two device slots whose uploads run on the library's
+    copy stream: a pack may overwrite a slot only after the kernels of the step
+    packed two calls earlier have read it.  Nine packs of three different steps,
+    each followed by its attention and its KV write, with no host sync between
+    them: every output must match the oracle."""
+    from gpu_helpers import TOL, max_err, oracle_step, to_device_pool
+
+    torch = torch_mod
+    base = workloads.small_step(seed=61, rows=24, n_heads=28, n_kv=4, head_dim=128, ctx_lo=40, ctx_hi=600,
+                                total_blocks=1024)
+    steps = [base.subset(np.arange(0, 24))[0], base.subset(np.arange(3, 10))[0], base.subset(np.arange(10, 24, 2))[0]]
+    q, k, v = workloads.host_values(base, layers=2)
+    pool, keep = to_device_pool(torch, gsp, ctx, base, k, v)
+    qs = [torch.from_numpy(np.ascontiguousarray(q[: s.total_q])).cuda() for s in steps]
+    outs = [torch.full((s.total_q, s.n_heads, s.head_dim), float("nan"), device="cuda") for s in steps for _ in
+            range(3)]
+    kn = torch.zeros((24, 4, 128), device="cuda")
+    torch.cuda.synchronize()
+    try:
+        for i in range(9):
+            s = steps[i % 3]
+            ctx.set_split_pages(2 + i % 3)  # different schedules, different step sizes
+            ctx.pack_step(pool, s.positions, s.token_counts, s.bt_offsets, s.bt_ids, s.max_seq_len, want_info=False)
+            ctx.attention_step(pool, 0, s.n_heads, qs[i % 3].data_ptr(), outs[(i % 3) * 3 + i // 3].data_ptr(),
+                               s.scale)
+            pool.write_step(1, kn.data_ptr(), kn.data_ptr())  # layer 1: attention reads layer 0
+        ctx.set_split_pages(0)
+        ctx.sync()
+        for j, s in enumerate(steps):
+            ref = oracle_step(s, q[: s.total_q], k, v)
+            for r in range(3):
+                assert max_err(outs[j * 3 + r].cpu().numpy(), ref) <= TOL["f32"], f"step {j} repeat {r}"
+    finally:
+        ctx.set_split_pages(0)
+        pool.destroy()

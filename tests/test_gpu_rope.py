@@ -133,3 +133,84 @@ def test_rope_write_then_attention(torch_mod, gsp, ctx, style):
     ref = oracle_step(step2, qr, k2, v2)
     assert max_err(out.cpu().numpy(), ref) <= 1e-4
     pool.destroy()
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_step_writes_match_the_explicit_writes(torch_mod, gsp, ctx, dt):
+    """gsp_rope_write_step / gsp_pool_write_step store each query token's K/V at the
+    slot of its own position, read from the packed step: bit for bit what
+    gsp_rope_write_tokens / gsp_pool_write_tokens store given the same positions,
+    blocks and slots as host arrays, and checked against the oracle's rotation.  The
+    step mixes decode rows, a prefill chunk, a row whose position lies past its
+    TokenCount (no slot: nothing stored, Q still rotated) and an empty row."""
+    torch = torch_mod
+    nh, nkv, d, base = 28, 4, 128, 1000000.0
+    q_lens = np.array([1, 19, 1, 0, 1], np.int32)
+    step = workloads.small_step(seed=95, rows=5, n_heads=nh, n_kv=nkv, head_dim=d, kv_dtype=dt, ctx_lo=5,
+                                ctx_hi=200, total_blocks=256, q_lens=q_lens)
+    step.positions[2] = step.token_counts[2] + 3  # clamped row: attends TokenCount tokens, has no slot
+    print(f"case step writes {dt}", flush=True)
+    rng = np.random.default_rng(96)
+    nq = step.total_q
+    q = rng.standard_normal((nq, nh, d)).astype(np.float32)
+    k = rng.standard_normal((nq, nkv, d)).astype(np.float32)
+    v = rng.standard_normal((nq, nkv, d)).astype(np.float32)
+    # Expected destinations, from the tables on the host.
+    pos, blocks, slots, stored = [], [], [], []
+    for b in range(step.num_rows):
+        for i in range(int(step.lens[b])):
+            p = int(step.positions[b]) + i
+            pos.append(p)
+            has = p < int(step.token_counts[b])
+            stored.append(has)
+            blocks.append(int(step.table(b)[p // 16]) if has else -1)
+            slots.append(p % 16)
+    pos, blocks, slots, stored = (np.array(x) for x in (pos, blocks, slots, stored))
+    assert stored.sum() == nq - 1  # exactly the clamped row's token has no slot
+    kind = gsp.KV_F16 if dt == "f16" else gsp.KV_F32
+    npdt = np.float16 if dt == "f16" else np.float32
+    pools = [gsp.Pool.create(ctx, total_blocks=step.total_blocks, layers=2, heads_kv=nkv, head_dim=d, kv_dtype=kind)
+             for _ in range(4)]
+    qs = [torch.from_numpy(q).cuda() for _ in range(2)]
+    kd = torch.from_numpy(k).cuda()
+    vd = torch.from_numpy(v).cuda()
+    torch.cuda.synchronize()
+    ctx.pack_step(pools[0], step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
+                  q_lens=step.q_lens)
+    pools[0].rope_write_step(1, nh, base, 1, qs[0].data_ptr(), kd.data_ptr(), vd.data_ptr())
+    pools[1].write_step(1, kd.data_ptr(), vd.data_ptr())
+    sel = np.nonzero(stored)[0]
+    qsel = torch.from_numpy(np.ascontiguousarray(q[sel])).cuda()
+    ksel = torch.from_numpy(np.ascontiguousarray(k[sel])).cuda()
+    vsel = torch.from_numpy(np.ascontiguousarray(v[sel])).cuda()
+    torch.cuda.synchronize()
+    pools[2].rope_write_tokens(1, pos[sel], blocks[sel], slots[sel], nh, base, 1, qsel.data_ptr(), ksel.data_ptr(),
+                               vsel.data_ptr())
+    pools[3].write_tokens(1, blocks[sel], slots[sel], ksel.data_ptr(), vsel.data_ptr())
+    ctx.sync()
+    _, _, kb, vb = pools[0].arenas()
+    arenas = [(p.download(0, kb).view(npdt), p.download(1, vb).view(npdt)) for p in pools]
+    assert np.array_equal(arenas[0][0], arenas[2][0]) and np.array_equal(arenas[0][1], arenas[2][1])
+    assert np.array_equal(arenas[1][0], arenas[3][0]) and np.array_equal(arenas[1][1], arenas[3][1])
+    got_q = qs[0].cpu().numpy()
+    assert np.array_equal(got_q[sel], qsel.cpu().numpy())
+    K = arenas[0][0].reshape(step.total_blocks, 2, nkv, 16, d)
+    V = arenas[0][1].reshape(step.total_blocks, 2, nkv, 16, d)
+    tol = 2e-3 if dt == "f16" else 2e-6
+    for i in range(nq):
+        assert max_err(got_q[i], orc.rope(q[i], int(pos[i]), base, 1)) <= 2e-6, f"q of token {i}"
+        if stored[i]:
+            got_k = K[blocks[i], 1, :, slots[i]].astype(np.float32)
+            assert max_err(got_k, orc.rope(k[i], int(pos[i]), base, 1)) <= tol, f"k of token {i}"
+            assert np.array_equal(V[blocks[i], 1, :, slots[i]], v[i].astype(npdt))
+    mask = np.ones(K.shape, bool)
+    mask[blocks[sel], 1, :, slots[sel]] = False
+    assert not K[mask].any() and not V[mask].any()
+    with pytest.raises(gsp.InvalidArgument):  # a layer outside the pool
+        pools[1].write_step(2, kd.data_ptr(), vd.data_ptr())
+    small = gsp.Pool.create(ctx, total_blocks=8, layers=1, heads_kv=nkv, head_dim=d, kv_dtype=kind)
+    with pytest.raises(gsp.InvalidArgument):  # not the pool geometry the step was packed for
+        small.write_step(0, kd.data_ptr(), vd.data_ptr())
+    small.destroy()
+    for p in pools:
+        p.destroy()

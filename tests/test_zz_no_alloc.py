@@ -106,6 +106,7 @@ def test_noalloc_captured_replays_match_eager(torch_mod, gsp, ctx):
             ctx.attention_step(pool, 0, step.n_heads, qd.data_ptr(), eager.data_ptr(), step.scale)
         stream.synchronize()
         out = torch.full_like(eager, float("nan"))
+        ctx.sync()  # the step's upload is known complete: a capture may read it
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             ctx.attention_step_noalloc(pool, 0, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
