@@ -196,7 +196,15 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, const DecodeUni
         }
     }
     __syncthreads();
-    finish_unit<D, G>(a, u, G, sh);
+    Tile t;  // the whole group (this kernel serves groups up to 8), full-width rows
+    t.G = G;
+    t.hoff = 0;
+    t.gs = G;
+    t.dv = D;
+    t.part_o = a.part_o;
+    t.part_ml = a.part_ml;
+    t.counters = a.counters;
+    finish_unit<D, G>(a, u, t, sh);
 }
 
 // One workgroup per bin; the bin's units run back to back.

@@ -26,6 +26,22 @@
 // kDecodeWaves-th page of its unit with the next page's loads in flight
 // while the current one is computed; the four waves merge through LDS and
 // split units merge in the epilogue (gsp_epilogue.h).
+//
+// Shapes.  The fixed-shape instantiations (kExact) take head_dim ==
+// v_head_dim == DP in {64, 128} and 16-token pages, all compile-time.  The
+// general ones take any even head_dim and v_head_dim up to DP (64, 128 or
+// 256) and pages of 1..16 tokens at run time, the domain of the reference GPU
+// runner (CudaPagedTransformerRunner.cs:402-412) and of the CPU kernel's
+// generic path (PagedAttentionKernel.cs:326-370):
+//  - a page of bs < 16 tokens fills the tile's first bs rows; the rest read
+//    as zero (past the descriptor's range) and are masked like a short page;
+//  - dims past head_dim (v_head_dim) are loaded from an offset past the
+//    descriptor's range, so they read as zero without a fetch; Q's are zero,
+//    so padded dims add nothing to S, and padded O columns are never stored;
+//  - kVec4 loads 4 dims per piece (head_dim, v_head_dim multiples of 4);
+//    kVec2 loads 2 (any even widths), so a piece never straddles a row.
+// A GQA group above 16 heads runs as tiles of 16 over grid.y, each tile
+// rereading the pages (the reference CPU kernel rereads them per head).
 #include "gsp_epilogue.h"
 
 namespace gsp {
@@ -33,6 +49,27 @@ namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+enum DecodeMode { kExact = 0, kVec4 = 1, kVec2 = 2 };
+
+constexpr int kTileTokens = 16;  // token rows of a page tile (MFMA M for S^T)
+// An element offset past any page's descriptor range: the load reads zero
+// and fetches nothing.
+constexpr int kOutOfRange = 1 << 28;
+
+// Widths and page size of a launch: compile-time for kExact, run time otherwise.
+template <int DP, int MODE>
+struct Geo {
+    int d, dv, bs;
+    __device__ explicit Geo(const DecodeArgs& a) : d(a.head_dim), dv(a.v_head_dim), bs(a.block_size) {}
+};
+template <int DP>
+struct Geo<DP, kExact> {
+    static constexpr int d = DP, dv = DP, bs = kBlockSize;
+    __device__ explicit Geo(const DecodeArgs&) {}
+};
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const void* base, int bytes) {
     // Raw buffer (stride 0) of `bytes` bytes; offsets at or past the end read 0.
@@ -74,9 +111,54 @@ struct Raw4<_Float16> {
     }
 };
 
-template <int D, typename KT>
+// Two consecutive elements at element offset `off`.
+template <typename KT>
+struct Raw2;
+template <>
+struct Raw2<float> {
+    typedef f2 T;
+    __device__ static f2 load(__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(r, off * 4, 0, 0));
+    }
+};
+template <>
+struct Raw2<_Float16> {
+    typedef h2 T;
+    __device__ static h2 load(__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(h2, __builtin_amdgcn_raw_buffer_load_b32(r, off * 2, 0, 0));
+    }
+};
+
+// Four elements of a row at dims dim .. dim+3 (element offset `row + dim`),
+// zero past `width`, as one piece (kVec4) or two (kVec2).
+template <typename KT, int MODE>
+__device__ __forceinline__ typename Raw4<KT>::T load4(__amdgpu_buffer_rsrc_t r, int row, int dim, int width) {
+    if constexpr (MODE == kVec2) {
+        const auto lo = Raw2<KT>::load(r, dim < width ? row + dim : kOutOfRange);
+        const auto hi = Raw2<KT>::load(r, dim + 2 < width ? row + dim + 2 : kOutOfRange);
+        return typename Raw4<KT>::T{lo[0], lo[1], hi[0], hi[1]};
+    } else {
+        return Raw4<KT>::load(r, dim < width ? row + dim : kOutOfRange);
+    }
+}
+
+template <int D, typename KT, int MODE>
 __device__ __forceinline__ void load_page(PageRegs<D, KT>& pr, const KT* kpage, const KT* vpage, int ntok, int n,
-                                          int g) {
+                                          int g, const Geo<D, MODE>& geo) {
+    if constexpr (MODE != kExact) {
+        // Rows are head_dim (v_head_dim) elements apart; a row past ntok, or
+        // dims past the width, read as zero.
+        const __amdgpu_buffer_rsrc_t rk = page_rsrc(kpage, ntok * geo.d * (int)sizeof(KT));
+        const __amdgpu_buffer_rsrc_t rv = page_rsrc(vpage, ntok * geo.dv * (int)sizeof(KT));
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) pr.k[j] = load4<KT, MODE>(rk, n * geo.d, 16 * j + 4 * g, geo.d);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int c = 0; c < D / 64; ++c)
+                pr.v[kk][c] = load4<KT, MODE>(rv, (4 * g + kk) * geo.dv, 64 * c + 4 * n, geo.dv);
+        return;
+    }
     const int bytes = ntok * D * (int)sizeof(KT);
     const __amdgpu_buffer_rsrc_t rk = page_rsrc(kpage, bytes);
     const __amdgpu_buffer_rsrc_t rv = page_rsrc(vpage, bytes);
@@ -129,11 +211,24 @@ struct QRegs<D, _Float16> {
     float sc;
 };
 
-template <int D>
-__device__ __forceinline__ void load_q(QRaw<D>& qr, const DecodeArgs& a, int qi, int kvh, int G, int n, int g) {
-    const float* qrow = a.q + ((int64_t)qi * a.n_heads + kvh * G + (n < G ? n : 0)) * D;
+// Q row of head `h` (the tile's head n, or its first head for padding
+// lanes); dims past head_dim are zero.
+template <int D, int MODE>
+__device__ __forceinline__ void load_q(QRaw<D>& qr, const DecodeArgs& a, int qi, int h, int g, const Geo<D, MODE>& geo) {
+    const float* qrow = a.q + ((int64_t)qi * a.n_heads + h) * geo.d;
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) qr.q[j] = *reinterpret_cast<const f4*>(qrow + 16 * j + 4 * g);
+    for (int j = 0; j < D / 16; ++j) {
+        const int dim = 16 * j + 4 * g;
+        if constexpr (MODE == kExact) {
+            qr.q[j] = *reinterpret_cast<const f4*>(qrow + dim);
+        } else if constexpr (MODE == kVec4) {
+            qr.q[j] = dim < geo.d ? *reinterpret_cast<const f4*>(qrow + dim) : f4{0.f, 0.f, 0.f, 0.f};
+        } else {
+            const f2 lo = dim < geo.d ? *reinterpret_cast<const f2*>(qrow + dim) : f2{0.f, 0.f};
+            const f2 hi = dim + 2 < geo.d ? *reinterpret_cast<const f2*>(qrow + dim + 2) : f2{0.f, 0.f};
+            qr.q[j] = f4{lo[0], lo[1], hi[0], hi[1]};
+        }
+    }
 }
 
 template <int D>
@@ -244,7 +339,7 @@ template <int D, typename KT>
 __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D, KT>& pr, const QRegs<D, KT>& qr,
                                              int ntok, int g) {
     f4 s = page_scores<D>(pr, qr);
-    if (ntok < kBlockSize) {
+    if (ntok < kTileTokens) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (4 * g + r >= ntok) s[r] = -INFINITY;
@@ -314,21 +409,23 @@ __device__ __forceinline__ int second_block(const DecodeArgs& a, int ui, int wav
     return ld_meta(reinterpret_cast<const int32_t*>(a.units + ui) + 12 + wave);
 }
 
-template <int D, typename KT>
+template <int D, typename KT, int MODE>
 __device__ __forceinline__ void load_first_page(PageRegs<D, KT>& pr, const DecodeArgs& a, const DecodeUnit& u, int blk,
-                                                int wave, int n, int g) {
+                                                int wave, int n, int g, const Geo<D, MODE>& geo) {
     const int p = u.page_begin + wave;
     if (p < u.page_end) {
-        const int64_t off = a.layer_offset + (int64_t)u.kvh * a.head_stride + (int64_t)blk * a.block_stride;
-        load_page<D, KT>(pr, static_cast<const KT*>(a.k_pool) + off, static_cast<const KT*>(a.v_pool) + off,
-                         min(kBlockSize, u.ctx - p * kBlockSize), n, g);
+        const int64_t koff = a.layer_offset + (int64_t)u.kvh * a.head_stride + (int64_t)blk * a.block_stride;
+        const int64_t voff = a.v_layer_offset + (int64_t)u.kvh * a.v_head_stride + (int64_t)blk * a.v_block_stride;
+        load_page<D, KT, MODE>(pr, static_cast<const KT*>(a.k_pool) + koff, static_cast<const KT*>(a.v_pool) + voff,
+                               min(geo.bs, u.ctx - p * geo.bs), n, g, geo);
     }
 }
 
-// One workgroup per bin: unit blockIdx.x, then units [bin_rest[b], bin_rest[b + 1]),
-// back to back.  Before a unit's epilogue (wave merge, output or partial) the
-// next unit's Q and first pages are already requested, so the CU's load
-// stream keeps going across unit boundaries.
+// One workgroup per (bin, tile of heads): unit blockIdx.x, then units
+// [bin_rest[b], bin_rest[b + 1]), back to back, for the tile blockIdx.y of
+// each unit's GQA group.  Before a unit's epilogue (wave merge, output or
+// partial) the next unit's Q and first pages are already requested, so the
+// CU's load stream keeps going across unit boundaries.
 //
 // A split piece's partial is published without waiting for it.  The split
 // counter protocol then runs at points where waiting is free: at the end of
@@ -339,11 +436,11 @@ __device__ __forceinline__ void load_first_page(PageRegs<D, KT>& pr, const Decod
 // page loop, again with nothing else in flight, and the last split of a pair
 // merges it in that unit's epilogue.  A workgroup's last one or two pieces settle after its
 // final unit.
-template <int D, typename KT>
-__global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(DecodeArgs a) {
+template <int D, typename KT, int MODE>
+__global__ __launch_bounds__(kDecodeThreads, D >= 256 ? 1 : 2) void paged_decode_mfma_kernel(DecodeArgs a) {
     __shared__ EpilogueLds<D, kMaxGroupMfma> sh;
 
-    const int G = a.group;
+    const Geo<D, MODE> geo(a);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -351,13 +448,30 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
     const int g = lane >> 4;
     const int first = blockIdx.x;
 
+    // This workgroup's tile of the group: heads [hoff, hoff + G).
+    Tile t;
+    t.hoff = kDecodeTileHeads * (int)blockIdx.y;
+    t.G = min(kDecodeTileHeads, a.group - t.hoff);
+    t.gs = a.slot_heads;
+    t.dv = geo.dv;
+    {
+        const int64_t tile = blockIdx.y;
+        t.part_o = a.part_o ? a.part_o + tile * a.num_slots * a.slot_heads * geo.dv : nullptr;
+        t.part_ml = a.part_ml ? a.part_ml + tile * a.num_slots * a.slot_heads * 2 : nullptr;
+        t.counters = a.counters ? a.counters + tile * a.total_q * a.n_kv : nullptr;
+    }
+    const int G = t.G;
+    // Heads n >= G of the 16-wide tile read the tile's first head: their S, P
+    // and O columns stay finite and are never stored.
+    const int hq = t.hoff + (n < G ? n : 0);
+
     QRaw<D> qraw;
     PageRegs<D, KT> ra, rb;
     {
         const DecodeUnit u0 = read_unit(a, first);
         const int blk0 = first_block(a, first, wave);
-        load_q<D>(qraw, a, u0.qi, u0.kvh, G, n, g);
-        load_first_page<D, KT>(ra, a, u0, blk0, wave, n, g);
+        load_q<D, MODE>(qraw, a, u0.qi, u0.kvh * a.group + hq, g, geo);
+        load_first_page<D, KT, MODE>(ra, a, u0, blk0, wave, n, g, geo);
     }
     const int rb0 = ld_meta(a.bin_rest + first);
     const int re = ld_meta(a.bin_rest + first + 1);
@@ -390,7 +504,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
         st.l = 0.f;
 
         const KT* kbase = static_cast<const KT*>(a.k_pool) + a.layer_offset + (int64_t)u.kvh * a.head_stride;
-        const KT* vbase = static_cast<const KT*>(a.v_pool) + a.layer_offset + (int64_t)u.kvh * a.head_stride;
+        const KT* vbase = static_cast<const KT*>(a.v_pool) + a.v_layer_offset + (int64_t)u.kvh * a.v_head_stride;
         const int32_t* bt = a.bt_ids + u.bt_base;
 
         // Two page buffers in flight: load page p + kDecodeWaves while computing page p.
@@ -399,19 +513,19 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
             const int pn = p + kDecodeWaves;
             if (pn < u.page_end && !rb_ready) {
                 const int64_t blk = ld_meta(bt + pn);
-                load_page<D, KT>(rb, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
-                                 min(kBlockSize, u.ctx - pn * kBlockSize), n, g);
+                load_page<D, KT, MODE>(rb, kbase + blk * a.block_stride, vbase + blk * a.v_block_stride,
+                                       min(geo.bs, u.ctx - pn * geo.bs), n, g, geo);
             }
             rb_ready = false;
-            compute_page<D, KT>(st, ra, q, min(kBlockSize, u.ctx - p * kBlockSize), g);
+            compute_page<D, KT>(st, ra, q, min(geo.bs, u.ctx - p * geo.bs), g);
             if (pn >= u.page_end) break;
             const int pnn = pn + kDecodeWaves;
             if (pnn < u.page_end) {
                 const int64_t blk = ld_meta(bt + pnn);
-                load_page<D, KT>(ra, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
-                                 min(kBlockSize, u.ctx - pnn * kBlockSize), n, g);
+                load_page<D, KT, MODE>(ra, kbase + blk * a.block_stride, vbase + blk * a.v_block_stride,
+                                       min(geo.bs, u.ctx - pnn * geo.bs), n, g, geo);
             }
-            compute_page<D, KT>(st, rb, q, min(kBlockSize, u.ctx - pn * kBlockSize), g);
+            compute_page<D, KT>(st, rb, q, min(geo.bs, u.ctx - pn * geo.bs), g);
             p = pnn;
         }
 
@@ -426,12 +540,15 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
         // per wave in flight.
         rb_ready = false;
         if (has_next) {
-            load_q<D>(qraw, a, un.qi, un.kvh, G, n, g);
-            load_first_page<D, KT>(ra, a, un, blkn, wave, n, g);
+            load_q<D, MODE>(qraw, a, un.qi, un.kvh * a.group + hq, g, geo);
+            load_first_page<D, KT, MODE>(ra, a, un, blkn, wave, n, g, geo);
             if (has_n2) {
-                const int64_t off = a.layer_offset + (int64_t)un.kvh * a.head_stride + (int64_t)blkn2 * a.block_stride;
-                load_page<D, KT>(rb, static_cast<const KT*>(a.k_pool) + off, static_cast<const KT*>(a.v_pool) + off,
-                                 min(kBlockSize, un.ctx - pn2 * kBlockSize), n, g);
+                const int64_t koff = a.layer_offset + (int64_t)un.kvh * a.head_stride + (int64_t)blkn2 * a.block_stride;
+                const int64_t voff =
+                    a.v_layer_offset + (int64_t)un.kvh * a.v_head_stride + (int64_t)blkn2 * a.v_block_stride;
+                load_page<D, KT, MODE>(rb, static_cast<const KT*>(a.k_pool) + koff,
+                                       static_cast<const KT*>(a.v_pool) + voff, min(geo.bs, un.ctx - pn2 * geo.bs), n,
+                                       g, geo);
                 rb_ready = true;
             }
         }
@@ -457,10 +574,10 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
         __syncthreads();
         // Every wave has waited for its part of `pub`'s partial: count it.
         // The answer is read at the end of the next page loop.
-        if (pub >= 0 && tid == 0) counted = count_split(a, read_unit(a, pub));
+        if (pub >= 0 && tid == 0) counted = count_split(a, read_unit(a, pub), t);
         const bool merge_cnt = cnt >= 0 && sh.last;
-        publish_unit<D, kMaxGroupMfma>(a, u, G, sh);
-        if (merge_cnt) merge_pair<D, kMaxGroupMfma, 0>(a, read_unit(a, cnt), G, sh);
+        publish_unit<D, kMaxGroupMfma>(a, u, t, sh);
+        if (merge_cnt) merge_pair<D, kMaxGroupMfma, 0>(a, read_unit(a, cnt), t, sh);
         cnt = pub;
         pub = (u.split_info >> 16) > 1 ? ui : -1;
         __syncthreads();  // the epilogue LDS is reused by the next unit
@@ -472,36 +589,54 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_decode_mfma_kernel(De
         wait_vm_complete();
         __syncthreads();
         int prev_pub = 0;
-        if (pub >= 0 && tid == 0) prev_pub = count_split(a, read_unit(a, pub));
+        if (pub >= 0 && tid == 0) prev_pub = count_split(a, read_unit(a, pub), t);
         if (tid == 0) {
             sh.last = cnt >= 0 && prev == (read_unit(a, cnt).split_info >> 16) - 1;
             sh.last_pub = pub >= 0 && prev_pub == (read_unit(a, pub).split_info >> 16) - 1;
         }
         __syncthreads();
-        if (sh.last) merge_pair<D, kMaxGroupMfma>(a, read_unit(a, cnt), G, sh);
-        if (sh.last_pub) merge_pair<D, kMaxGroupMfma>(a, read_unit(a, pub), G, sh);
+        if (sh.last) merge_pair<D, kMaxGroupMfma>(a, read_unit(a, cnt), t, sh);
+        if (sh.last_pub) merge_pair<D, kMaxGroupMfma>(a, read_unit(a, pub), t, sh);
     }
+}
+
+template <int D, typename KT, int MODE>
+void launch_one(dim3 grid, const DecodeArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<D, KT, MODE>), grid, dim3(kDecodeThreads), 0, stream, a);
+}
+
+template <typename KT>
+hipError_t launch_typed(dim3 grid, const DecodeArgs& a, hipStream_t stream) {
+    const int d = a.head_dim, dv = a.v_head_dim;
+    if (d == dv && a.block_size == kBlockSize && (d == 64 || d == 128)) {
+        if (d == 128)
+            launch_one<128, KT, kExact>(grid, a, stream);
+        else
+            launch_one<64, KT, kExact>(grid, a, stream);
+    } else if (d % 2 || dv % 2 || d < 2 || dv < 2 || d > 256 || dv > 256 || a.block_size < 1 ||
+               a.block_size > kTileTokens) {
+        return hipErrorInvalidValue;
+    } else if (d % 4 == 0 && dv % 4 == 0) {
+        const int w = max(d, dv);
+        if (w <= 64)
+            launch_one<64, KT, kVec4>(grid, a, stream);
+        else if (w <= 128)
+            launch_one<128, KT, kVec4>(grid, a, stream);
+        else
+            launch_one<256, KT, kVec4>(grid, a, stream);
+    } else {
+        launch_one<256, KT, kVec2>(grid, a, stream);
+    }
+    return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_decode_mfma(int head_dim, int kv_f16, int num_bins, const DecodeArgs& a, hipStream_t stream) {
+hipError_t launch_decode_mfma(int kv_f16, int num_bins, const DecodeArgs& a, hipStream_t stream) {
     if (num_bins <= 0) return hipSuccess;
-    dim3 grid(num_bins);
-    if (head_dim == 128) {
-        if (kv_f16)
-            hipLaunchKernelGGL((paged_decode_mfma_kernel<128, _Float16>), grid, dim3(kDecodeThreads), 0, stream, a);
-        else
-            hipLaunchKernelGGL((paged_decode_mfma_kernel<128, float>), grid, dim3(kDecodeThreads), 0, stream, a);
-    } else if (head_dim == 64) {
-        if (kv_f16)
-            hipLaunchKernelGGL((paged_decode_mfma_kernel<64, _Float16>), grid, dim3(kDecodeThreads), 0, stream, a);
-        else
-            hipLaunchKernelGGL((paged_decode_mfma_kernel<64, float>), grid, dim3(kDecodeThreads), 0, stream, a);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
+    if (a.group < 1) return hipErrorInvalidValue;
+    const dim3 grid(num_bins, (a.group + kDecodeTileHeads - 1) / kDecodeTileHeads);
+    return kv_f16 ? launch_typed<_Float16>(grid, a, stream) : launch_typed<float>(grid, a, stream);
 }
 
 }  // namespace gsp

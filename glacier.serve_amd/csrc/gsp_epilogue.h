@@ -30,7 +30,22 @@ __device__ __forceinline__ float coherent_load(const float* p) {
 // this wave, stores included, has completed.
 __device__ __forceinline__ void wait_vm_complete() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// LDS of the epilogue: the four waves' states.
+// The query heads one decode workgroup serves for a unit's KV head.  A GQA
+// group of up to 16 heads is one tile; a larger group is cut into tiles of 16
+// (the last one smaller), one per grid.y, each with its own partials and
+// counters.  dv is the output width (v_head_dim); the partials of a tile are
+// [slot][gs][dv] and [slot][gs][2], its counters [total_q][n_kv].
+struct Tile {
+    int G;              // heads in this tile
+    int hoff;           // first head of the tile within its KV head's group
+    int gs;             // heads per partial slot
+    int dv;             // output width
+    float* part_o;
+    float* part_ml;
+    int32_t* counters;
+};
+
+// LDS of the epilogue: the four waves' states (rows of D >= dv floats).
 template <int D, int GMAX>
 struct EpilogueLds {
     float o[kDecodeWaves][GMAX][D];
@@ -43,23 +58,28 @@ struct EpilogueLds {
 // Splits merged per round trip by the last split of a pair.
 constexpr int kMergeChunk = 8;
 
+__device__ __forceinline__ float* out_row(const DecodeArgs& a, const DecodeUnit& u, const Tile& t, int g) {
+    return a.out + ((int64_t)u.qi * a.n_heads + (int64_t)u.kvh * a.group + t.hoff + g) * t.dv;
+}
+
 // Merges the four waves' states (LDS) of unit u and writes the result: the
 // normalised output of an unsplit unit, or the (max, sum, unnormalised out)
 // partial of a split piece, stored coherently.  Nothing here waits for the
 // stores; the caller orders them before the pair's counter is bumped.
 template <int D, int GMAX>
-__device__ __forceinline__ void publish_unit(const DecodeArgs& a, const DecodeUnit& u, int G,
+__device__ __forceinline__ void publish_unit(const DecodeArgs& a, const DecodeUnit& u, const Tile& t,
                                              EpilogueLds<D, GMAX>& sh) {
     const int tid = threadIdx.x;
-    const int h0 = u.kvh * G;
+    const int G = t.G;
+    const int dv = t.dv;
     const int split = u.split_info & 0xFFFF;
     const int nsplit = u.split_info >> 16;
     const int64_t pair = (int64_t)u.slot;  // first partial slot of the pair (-1: unsplit)
 
     // A wave without pages has m = -inf and weighs 0.
-    for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
-        const int g = idx / D;
-        const int e = idx - g * D;
+    for (int idx = tid; idx < G * dv; idx += kDecodeThreads) {
+        const int g = idx / dv;
+        const int e = idx - g * dv;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, sh.m[w][g]);
@@ -72,26 +92,26 @@ __device__ __forceinline__ void publish_unit(const DecodeArgs& a, const DecodeUn
             O = fmaf(sh.o[w][g][e], f, O);
         }
         if (nsplit == 1) {
-            a.out[((int64_t)u.qi * a.n_heads + h0 + g) * D + e] = O / L;
+            out_row(a, u, t, g)[e] = O / L;
         } else {
-            const int64_t ps = (pair + split) * G + g;
-            coherent_store(a.part_o + ps * D + e, O);
+            const int64_t ps = (pair + split) * t.gs + g;
+            coherent_store(t.part_o + ps * dv + e, O);
             if (e == 0) {
-                coherent_store(a.part_ml + ps * 2 + 0, M);
-                coherent_store(a.part_ml + ps * 2 + 1, L);
+                coherent_store(t.part_ml + ps * 2 + 0, M);
+                coherent_store(t.part_ml + ps * 2 + 1, L);
             }
         }
     }
 }
 
-__device__ __forceinline__ int* pair_counter(const DecodeArgs& a, const DecodeUnit& u) {
-    return a.counters + (int64_t)u.qi * a.n_kv + u.kvh;
+__device__ __forceinline__ int* pair_counter(const DecodeArgs& a, const DecodeUnit& u, const Tile& t) {
+    return t.counters + (int64_t)u.qi * a.n_kv + u.kvh;
 }
 
 // Counts one finished split of u's pair; returns the count before it.  The
 // split's partial must be complete (stored and waited for by every wave).
-__device__ __forceinline__ int count_split(const DecodeArgs& a, const DecodeUnit& u) {
-    return __hip_atomic_fetch_add(pair_counter(a, u), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ int count_split(const DecodeArgs& a, const DecodeUnit& u, const Tile& t) {
+    return __hip_atomic_fetch_add(pair_counter(a, u, t), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The last split of u's pair to finish: out = sum_s 2^(m_s - M) O_s / sum_s
@@ -99,18 +119,18 @@ __device__ __forceinline__ int count_split(const DecodeArgs& a, const DecodeUnit
 // to zero.  General form, for pairs with many pieces: each thread loads the
 // (m, l) and O of up to kMergeChunk splits at once per element it owns and
 // folds chunks together with a running max, as the online softmax does.
-template <int D>
-__device__ __forceinline__ void merge_pair_chunked(const DecodeArgs& a, const DecodeUnit& u, int G) {
+__device__ __forceinline__ void merge_pair_chunked(const DecodeArgs& a, const DecodeUnit& u, const Tile& t) {
     const int tid = threadIdx.x;
-    const int h0 = u.kvh * G;
+    const int G = t.G;
+    const int dv = t.dv;
     const int nsplit = u.split_info >> 16;
     const int64_t pair = (int64_t)u.slot;
-    const int64_t stride = (int64_t)G * D;
-    for (int idx = tid; idx < G * D; idx += kDecodeThreads) {
-        const int g = idx / D;
-        const int e = idx - g * D;
-        const float* po = a.part_o + (pair * G + g) * D + e;
-        const float* pml = a.part_ml + (pair * G + g) * 2;
+    const int64_t stride = (int64_t)t.gs * dv;
+    for (int idx = tid; idx < G * dv; idx += kDecodeThreads) {
+        const int g = idx / dv;
+        const int e = idx - g * dv;
+        const float* po = t.part_o + (pair * t.gs + g) * dv + e;
+        const float* pml = t.part_ml + (pair * t.gs + g) * 2;
         float M = -INFINITY, L = 0.f, O = 0.f;
         for (int s0 = 0; s0 < nsplit; s0 += kMergeChunk) {
             float ms[kMergeChunk], ls[kMergeChunk], os[kMergeChunk];
@@ -118,8 +138,8 @@ __device__ __forceinline__ void merge_pair_chunked(const DecodeArgs& a, const De
             for (int i = 0; i < kMergeChunk; ++i) {
                 const bool in = s0 + i < nsplit;
                 const int s = in ? s0 + i : s0;
-                ms[i] = coherent_load(pml + (int64_t)s * G * 2 + 0);
-                ls[i] = coherent_load(pml + (int64_t)s * G * 2 + 1);
+                ms[i] = coherent_load(pml + (int64_t)s * t.gs * 2 + 0);
+                ls[i] = coherent_load(pml + (int64_t)s * t.gs * 2 + 1);
                 os[i] = coherent_load(po + s * stride);
                 if (!in) ms[i] = -INFINITY;
             }
@@ -137,9 +157,9 @@ __device__ __forceinline__ void merge_pair_chunked(const DecodeArgs& a, const De
             }
             M = Mc;
         }
-        a.out[((int64_t)u.qi * a.n_heads + h0 + g) * D + e] = O / L;
+        out_row(a, u, t, g)[e] = O / L;
     }
-    if (tid == 0) __hip_atomic_store(pair_counter(a, u), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(pair_counter(a, u, t), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The same merge for pairs with nsplit * G <= one (m, l) per thread.  Each
@@ -157,16 +177,17 @@ __device__ __forceinline__ void merge_pair_chunked(const DecodeArgs& a, const De
 // 2^(m_s - M_chunk), with every product and sum in the same order.  Results
 // are then bit for bit the same whichever form runs.  `scr` is LDS the caller
 // no longer reads, with room for 2 * nsplit * G + (nchunks + 1) * G floats.
-template <int D, int kIdx, int kLoads>
-__device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const DecodeUnit& u, int G, float* scr) {
+template <int kIdx, int kLoads>
+__device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const DecodeUnit& u, const Tile& t, float* scr) {
     constexpr int kChunk = kLoads / kIdx;  // out loads in flight per thread: kIdx * kChunk
     const int tid = threadIdx.x;
+    const int G = t.G;
+    const int dv = t.dv;
     const int nsplit = u.split_info >> 16;
     const int n_ml = nsplit * G;
-    const int h0 = u.kvh * G;
-    const int64_t piece = (int64_t)G * D;  // floats per piece in part_o
-    const float* po = a.part_o + (int64_t)u.slot * piece;
-    const float* pml = a.part_ml + (int64_t)u.slot * G * 2;
+    const int64_t piece = (int64_t)t.gs * dv;  // floats per piece in part_o
+    const float* po = t.part_o + (int64_t)u.slot * piece;
+    const float* pml = t.part_ml + (int64_t)u.slot * t.gs * 2;
     const int nchunks = (nsplit + kMergeChunk - 1) / kMergeChunk;
     float* sm = scr;           // [s * G + g]: m, then the weight 2^(m - M_chunk)
     float* sl = scr + n_ml;    // [s * G + g]: l
@@ -175,8 +196,10 @@ __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const Decod
 
     float mt = -INFINITY, lt = 0.f;
     if (tid < n_ml) {
-        mt = coherent_load(pml + 2 * tid);
-        lt = coherent_load(pml + 2 * tid + 1);
+        const int s = tid / G;
+        const int g = tid - s * G;
+        mt = coherent_load(pml + ((int64_t)s * t.gs + g) * 2);
+        lt = coherent_load(pml + ((int64_t)s * t.gs + g) * 2 + 1);
     }
     // Piece bases are wave-uniform and the lane's offset is one unsigned
     // index, so the loads take a scalar base and a 32-bit lane offset.
@@ -189,7 +212,7 @@ __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const Decod
 #pragma unroll
             for (int k = 0; k < kIdx; ++k) {
                 const unsigned idx = lane_idx + (unsigned)(k * kDecodeThreads);
-                os[k][i] = (idx < (unsigned)(G * D) && s0 + i < nsplit) ? coherent_load(pb + idx) : 0.f;
+                os[k][i] = (idx < (unsigned)(G * dv) && s0 + i < nsplit) ? coherent_load(pb + idx) : 0.f;
             }
         }
     };
@@ -227,7 +250,7 @@ __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const Decod
         if (s0 > 0) load_chunk(s0);
 #pragma unroll
         for (int k = 0; k < kIdx; ++k) {
-            const int g = min(G - 1, (tid + k * kDecodeThreads) / D);
+            const int g = min(G - 1, (tid + k * kDecodeThreads) / dv);
 #pragma unroll
             for (int i = 0; i < kChunk; ++i) {
                 const int s = s0 + i;
@@ -241,12 +264,12 @@ __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const Decod
 #pragma unroll
     for (int k = 0; k < kIdx; ++k) {
         const int idx = tid + k * kDecodeThreads;
-        if (idx < G * D) {
-            const int g = idx / D;
-            a.out[((int64_t)u.qi * a.n_heads + h0 + g) * D + (idx - g * D)] = O[k] / sinv[g];
+        if (idx < G * dv) {
+            const int g = idx / dv;
+            out_row(a, u, t, g)[idx - g * dv] = O[k] / sinv[g];
         }
     }
-    if (tid == 0) __hip_atomic_store(pair_counter(a, u), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(pair_counter(a, u, t), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Merge entry: the wide form when the pair's (m, l) fit one per thread and
@@ -257,35 +280,37 @@ __device__ __forceinline__ void merge_pair_wide(const DecodeArgs& a, const Decod
 // sites where the next unit's pages already hold most registers (the wide
 // form spills there).
 template <int D, int GMAX, int kLoads = 32>
-__device__ __forceinline__ void merge_pair(const DecodeArgs& a, const DecodeUnit& u, int G, EpilogueLds<D, GMAX>& sh) {
+__device__ __forceinline__ void merge_pair(const DecodeArgs& a, const DecodeUnit& u, const Tile& t,
+                                           EpilogueLds<D, GMAX>& sh) {
     const int nsplit = u.split_info >> 16;
-    const int n_ml = nsplit * G;
-    const int n_scr = 2 * n_ml + ((nsplit + kMergeChunk - 1) / kMergeChunk + 1) * G;
+    const int n_ml = nsplit * t.G;
+    const int n_scr = 2 * n_ml + ((nsplit + kMergeChunk - 1) / kMergeChunk + 1) * t.G;
     constexpr int kScratch = kDecodeWaves * GMAX * D;
-    if (kLoads > 0 && n_ml <= kDecodeThreads && n_scr <= kScratch && G * D <= 8 * kDecodeThreads) {
+    const int n_out = t.G * t.dv;
+    if (kLoads > 0 && n_ml <= kDecodeThreads && n_scr <= kScratch && n_out <= 8 * kDecodeThreads) {
         __syncthreads();
-        if (G * D <= 4 * kDecodeThreads)
-            merge_pair_wide<D, 4, (kLoads > 0 ? kLoads : 4)>(a, u, G, &sh.o[0][0][0]);
+        if (n_out <= 4 * kDecodeThreads)
+            merge_pair_wide<4, (kLoads > 0 ? kLoads : 4)>(a, u, t, &sh.o[0][0][0]);
         else
-            merge_pair_wide<D, 8, (kLoads > 0 ? kLoads : 8)>(a, u, G, &sh.o[0][0][0]);
+            merge_pair_wide<8, (kLoads > 0 ? kLoads : 8)>(a, u, t, &sh.o[0][0][0]);
     } else {
-        merge_pair_chunked<D>(a, u, G);
+        merge_pair_chunked(a, u, t);
     }
 }
 
 // publish_unit, then for a split piece the counter protocol on the spot:
 // wait for the partial, count it, and merge the pair if it was the last one.
 template <int D, int GMAX>
-__device__ __forceinline__ void finish_unit(const DecodeArgs& a, const DecodeUnit& u, int G,
+__device__ __forceinline__ void finish_unit(const DecodeArgs& a, const DecodeUnit& u, const Tile& t,
                                             EpilogueLds<D, GMAX>& sh) {
-    publish_unit<D, GMAX>(a, u, G, sh);
+    publish_unit<D, GMAX>(a, u, t, sh);
     const int nsplit = u.split_info >> 16;
     if (nsplit == 1) return;
     wait_vm_complete();
     __syncthreads();
-    if (threadIdx.x == 0) sh.last = (count_split(a, u) == nsplit - 1);
+    if (threadIdx.x == 0) sh.last = (count_split(a, u, t) == nsplit - 1);
     __syncthreads();
-    if (sh.last) merge_pair<D, GMAX>(a, u, G, sh);
+    if (sh.last) merge_pair<D, GMAX>(a, u, t, sh);
 }
 
 }  // namespace gsp

@@ -37,9 +37,12 @@ static_assert(sizeof(DecodeUnit) == 64, "DecodeUnit is packed as 16 int32");
 struct DecodeArgs {
     const void* k_pool;
     const void* v_pool;
-    int64_t block_stride;  // elements per block over all layers and heads
-    int64_t layer_offset;  // layer * heads_kv * 16 * head_dim
-    int64_t head_stride;   // 16 * head_dim
+    int64_t block_stride;  // K elements per block over all layers and heads
+    int64_t layer_offset;  // layer * heads_kv * block_size * head_dim
+    int64_t head_stride;   // block_size * head_dim
+    int64_t v_block_stride;  // the same for V (v_head_dim per slot)
+    int64_t v_layer_offset;
+    int64_t v_head_stride;
     // Workgroup b runs unit b first, then units [bin_rest[b], bin_rest[b + 1]):
     // the first unit of every bin sits at the bin's own index, so a workgroup
     // can fetch it without waiting for the offsets.
@@ -48,14 +51,28 @@ struct DecodeArgs {
     const int32_t* bt_ids;
     const float* q;        // [total_q][n_heads][head_dim]
     float* out;            // [total_q][n_heads][head_dim]
-    float* part_o;         // [slot][group][head_dim] unnormalised partial outputs
-    float* part_ml;        // [slot][group][2] running max (log2 units) and sum
-    int32_t* counters;     // [total_q][n_kv] splits finished; zero between launches
+    // Split-KV workspace, per tile of heads (grid.y; one tile for groups up
+    // to 16): partials [tile][slot][slot_heads][v_head_dim] and
+    // [tile][slot][slot_heads][2] (running max in log2 units, sum), counters
+    // [tile][total_q][n_kv] of splits finished, zero between launches.
+    float* part_o;
+    float* part_ml;
+    int32_t* counters;
     int32_t n_heads;
     int32_t n_kv;
     int32_t group;         // query heads per KV head
     float scale_log2;      // attn_scale * log2(e)
+    int32_t head_dim;      // K/Q width
+    int32_t v_head_dim;    // V/out width
+    int32_t block_size;    // tokens per page, 1..16
+    int32_t total_q;
+    int32_t num_slots;     // partial slots per tile
+    int32_t slot_heads;    // heads per partial slot: min(group, 16)
 };
+
+// Query heads per decode tile (the matrix-core kernel's 16-wide N): larger
+// GQA groups run as several tiles over grid.y.
+constexpr int kDecodeTileHeads = 16;
 
 // One prefill tile, one workgroup per (tile, group of up to 8 query heads):
 // up to 16 consecutive query tokens of one row against one KV head.  Query
@@ -97,8 +114,11 @@ hipError_t launch_prefill_mfma(int head_dim, int kv_f16, int num_tiles, const Pr
 // Launches the DPP decode kernel instantiated for (head_dim, kv dtype, group <= 8),
 // one workgroup per bin.
 hipError_t launch_decode(int head_dim, int kv_f16, int num_bins, const DecodeArgs& a, hipStream_t stream);
-// Launches the MFMA decode kernel for (head_dim, kv dtype); group <= 16.
-hipError_t launch_decode_mfma(int head_dim, int kv_f16, int num_bins, const DecodeArgs& a, hipStream_t stream);
+// Launches the MFMA decode kernel, one workgroup per (bin, tile of 16 heads).
+// head_dim == v_head_dim in {64, 128} with 16-token pages take the fixed-shape
+// instantiations; any other even head_dim / v_head_dim <= 256 and block size
+// <= 16 take the general ones.
+hipError_t launch_decode_mfma(int kv_f16, int num_bins, const DecodeArgs& a, hipStream_t stream);
 
 struct WriteTokensArgs {
     void* k_pool;
@@ -106,13 +126,17 @@ struct WriteTokensArgs {
     int64_t block_stride;
     int64_t layer_offset;
     int64_t head_stride;
-    const int32_t* block_ids;  // [n]
+    int64_t v_block_stride;
+    int64_t v_layer_offset;
+    int64_t v_head_stride;
+    const int32_t* block_ids;  // [n]; -1: no slot, nothing stored
     const int32_t* slots;      // [n]
-    const float* k;            // [n][n_kv][d]
-    const float* v;            // [n][n_kv][d]
+    const float* k;            // [n][n_kv][head_dim]
+    const float* v;            // [n][n_kv][v_head_dim]
     int32_t n;
     int32_t n_kv;
     int32_t head_dim;
+    int32_t v_head_dim;
 };
 
 hipError_t launch_write_tokens(int kv_f16, const WriteTokensArgs& a, hipStream_t stream);
@@ -125,17 +149,21 @@ struct RopeWriteArgs {
     int64_t block_stride;
     int64_t layer_offset;
     int64_t head_stride;
+    int64_t v_block_stride;
+    int64_t v_layer_offset;
+    int64_t v_head_stride;
     const int32_t* positions;  // [n]
     const int32_t* block_ids;  // [n]
     const int32_t* slots;      // [n]
     float* q;                  // [n][n_heads][d], rotated in place (n_heads 0: none)
     const float* k;            // [n][n_kv][d], rotated into the pool
-    const float* v;            // [n][n_kv][d], stored as is
+    const float* v;            // [n][n_kv][v_head_dim], stored as is
     double log2_base;          // log2(freq_base)
     int32_t n;
     int32_t n_heads;
     int32_t n_kv;
     int32_t head_dim;
+    int32_t v_head_dim;
     int32_t style;             // GSP_ROPE_PAIRS or GSP_ROPE_HALVES
 };
 
@@ -167,12 +195,15 @@ struct CopyBlockArgs {
     void* v_pool;
     int64_t block_stride;
     int64_t head_stride;
+    int64_t v_block_stride;
+    int64_t v_head_stride;
     int32_t src;
     int32_t dst;
-    int32_t valid_tokens;  // already clamped to [1, 16]
+    int32_t valid_tokens;  // already clamped to [1, block_size]
     int32_t layers;
     int32_t n_kv;
     int32_t head_dim;
+    int32_t v_head_dim;
 };
 
 hipError_t launch_copy_block(int kv_f16, const CopyBlockArgs& a, hipStream_t stream);

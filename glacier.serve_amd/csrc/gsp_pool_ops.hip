@@ -16,15 +16,15 @@ __global__ __launch_bounds__(128) void write_tokens_kernel(WriteTokensArgs a) {
     const int i = blockIdx.x;
     const int h = blockIdx.y;
     if (a.block_ids[i] < 0) return;
-    const int64_t dst = (int64_t)a.block_ids[i] * a.block_stride + a.layer_offset +
-                        (int64_t)h * a.head_stride + (int64_t)a.slots[i] * a.head_dim;
-    const int64_t src = ((int64_t)i * a.n_kv + h) * a.head_dim;
-    KT* kd = static_cast<KT*>(a.k_pool) + dst;
-    KT* vd = static_cast<KT*>(a.v_pool) + dst;
-    for (int e = threadIdx.x; e < a.head_dim; e += blockDim.x) {
-        kd[e] = static_cast<KT>(a.k[src + e]);
-        vd[e] = static_cast<KT>(a.v[src + e]);
-    }
+    const int64_t blk = a.block_ids[i];
+    const int64_t slot = a.slots[i];
+    KT* kd = static_cast<KT*>(a.k_pool) + blk * a.block_stride + a.layer_offset + h * a.head_stride + slot * a.head_dim;
+    KT* vd = static_cast<KT*>(a.v_pool) + blk * a.v_block_stride + a.v_layer_offset + h * a.v_head_stride +
+             slot * a.v_head_dim;
+    const float* ks = a.k + ((int64_t)i * a.n_kv + h) * a.head_dim;
+    const float* vs = a.v + ((int64_t)i * a.n_kv + h) * a.v_head_dim;
+    for (int e = threadIdx.x; e < a.head_dim; e += blockDim.x) kd[e] = static_cast<KT>(ks[e]);
+    for (int e = threadIdx.x; e < a.v_head_dim; e += blockDim.x) vd[e] = static_cast<KT>(vs[e]);
 }
 
 // QuantKernels.RoPE then PagedBlockPool.Store for n tokens
@@ -53,6 +53,8 @@ __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
     __syncthreads();
     const bool stored = a.block_ids[i] >= 0;
     const int64_t dst = (int64_t)a.block_ids[i] * a.block_stride + a.layer_offset + (int64_t)a.slots[i] * d;
+    const int dv = a.v_head_dim;
+    const int64_t vdst = (int64_t)a.block_ids[i] * a.v_block_stride + a.v_layer_offset + (int64_t)a.slots[i] * dv;
     const bool pairs = a.style == GSP_ROPE_PAIRS;
     const int heads = a.n_heads + (stored ? a.n_kv : 0);
     for (int idx = threadIdx.x; idx < heads * half; idx += blockDim.x) {
@@ -76,11 +78,11 @@ __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
             kd[e1] = static_cast<KT>(x0 * s + x1 * c);
         }
     }
-    for (int idx = threadIdx.x; stored && idx < a.n_kv * d; idx += blockDim.x) {
-        const int hk = idx / d;
-        const int e = idx - hk * d;
-        static_cast<KT*>(a.v_pool)[dst + (int64_t)hk * a.head_stride + e] =
-            static_cast<KT>(a.v[((int64_t)i * a.n_kv + hk) * d + e]);
+    for (int idx = threadIdx.x; stored && idx < a.n_kv * dv; idx += blockDim.x) {
+        const int hk = idx / dv;
+        const int e = idx - hk * dv;
+        static_cast<KT*>(a.v_pool)[vdst + (int64_t)hk * a.v_head_stride + e] =
+            static_cast<KT>(a.v[((int64_t)i * a.n_kv + hk) * dv + e]);
     }
 }
 
@@ -89,16 +91,14 @@ __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
 template <typename KT>
 __global__ __launch_bounds__(256) void copy_block_kernel(CopyBlockArgs a) {
     const int lh = blockIdx.x;  // layer * n_kv + head: pages are consecutive
-    const int64_t n = (int64_t)a.valid_tokens * a.head_dim;
-    const int64_t off = (int64_t)lh * a.head_stride;
-    const KT* ks = static_cast<const KT*>(a.k_pool) + (int64_t)a.src * a.block_stride + off;
-    const KT* vs = static_cast<const KT*>(a.v_pool) + (int64_t)a.src * a.block_stride + off;
-    KT* kd = static_cast<KT*>(a.k_pool) + (int64_t)a.dst * a.block_stride + off;
-    KT* vd = static_cast<KT*>(a.v_pool) + (int64_t)a.dst * a.block_stride + off;
-    for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
-        kd[e] = ks[e];
-        vd[e] = vs[e];
-    }
+    const int64_t nk = (int64_t)a.valid_tokens * a.head_dim;
+    const int64_t nv = (int64_t)a.valid_tokens * a.v_head_dim;
+    const KT* ks = static_cast<const KT*>(a.k_pool) + (int64_t)a.src * a.block_stride + (int64_t)lh * a.head_stride;
+    const KT* vs = static_cast<const KT*>(a.v_pool) + (int64_t)a.src * a.v_block_stride + (int64_t)lh * a.v_head_stride;
+    KT* kd = static_cast<KT*>(a.k_pool) + (int64_t)a.dst * a.block_stride + (int64_t)lh * a.head_stride;
+    KT* vd = static_cast<KT*>(a.v_pool) + (int64_t)a.dst * a.v_block_stride + (int64_t)lh * a.v_head_stride;
+    for (int64_t e = threadIdx.x; e < nk; e += blockDim.x) kd[e] = ks[e];
+    for (int64_t e = threadIdx.x; e < nv; e += blockDim.x) vd[e] = vs[e];
 }
 
 // Sets n int32 words to `value`.  Used instead of hipMemsetAsync where a

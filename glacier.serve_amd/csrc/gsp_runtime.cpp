@@ -107,8 +107,8 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // the decode kernel's split-KV parallelism over long prefixes.
 constexpr int32_t kPrefillAutoMinQ = 16;
 
-bool row_is_tiled(int32_t path, int32_t q_len) {
-    if (path == GSP_PREFILL_PER_TOKEN || q_len < 2) return false;
+bool row_is_tiled(int32_t path, int32_t q_len, bool tileable) {
+    if (!tileable || path == GSP_PREFILL_PER_TOKEN || q_len < 2) return false;
     return path == GSP_PREFILL_TILES || q_len >= kPrefillAutoMinQ;
 }
 
@@ -180,6 +180,8 @@ struct gsp_ctx {
     int32_t num_slots = 0;      // partial slots of the packed step
     int32_t step_heads_kv = 0;  // pool geometry the step was packed for
     int32_t step_blocks = 0;
+    int32_t step_block_size = 0;
+    bool step_tileable = false;
 
     // Split-KV workspace: partials and per-(query, KV head) split counters.
     float* part = nullptr;
@@ -354,8 +356,9 @@ int validate_pool_desc(const gsp_pool_desc* d) {
     if (d->block_size < 1) return gsp::fail(GSP_E_INVALID_ARG, "blockSize must be >= 1 (got %d)", d->block_size);
     if (d->kv_dtype != GSP_KV_F32 && d->kv_dtype != GSP_KV_F16)
         return gsp::fail(GSP_E_INVALID_ARG, "unknown kv_dtype %d", d->kv_dtype);
-    if (d->block_size != GSP_BLOCK_SIZE)
-        return gsp::fail(GSP_E_UNSUPPORTED, "device pool supports blockSize 16 only (got %d)", d->block_size);
+    if (d->block_size > GSP_MAX_BLOCK_SIZE)
+        return gsp::fail(GSP_E_UNSUPPORTED, "device pool supports blockSize up to %d (got %d)", GSP_MAX_BLOCK_SIZE,
+                         d->block_size);
     return GSP_OK;
 }
 
@@ -617,6 +620,9 @@ int store_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const i
     a.block_stride = pool->block_stride_k;
     a.layer_offset = (int64_t)layer * pool->layer_stride_k;
     a.head_stride = pool->head_stride_k;
+    a.v_block_stride = pool->block_stride_v;
+    a.v_layer_offset = (int64_t)layer * pool->layer_stride_v;
+    a.v_head_stride = pool->head_stride_v;
     a.block_ids = d_blocks;
     a.slots = d_slots;
     a.k = k_dev;
@@ -624,6 +630,7 @@ int store_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const i
     a.n = n;
     a.n_kv = d.heads_kv;
     a.head_dim = d.head_dim;
+    a.v_head_dim = d.v_head_dim;
     return check_hip(gsp::launch_write_tokens(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "write_tokens launch");
 }
 
@@ -635,7 +642,6 @@ int check_rope_args(const gsp_pool* pool, int32_t n_heads, float freq_base, int3
     if (!(freq_base > 0.0f) || !std::isfinite(freq_base))
         return gsp::fail(GSP_E_INVALID_ARG, "RoPE frequency base must be positive and finite");
     const gsp_pool_desc& d = pool->desc;
-    if (d.v_head_dim != d.head_dim) return gsp::fail(GSP_E_UNSUPPORTED, "vHeadDim != headDim is not supported on the device pool");
     if (d.head_dim % 2 != 0 || d.head_dim > 2 * gsp::kRopeMaxHalf)
         return gsp::fail(GSP_E_UNSUPPORTED, "RoPE needs an even headDim <= %d (got %d)", 2 * gsp::kRopeMaxHalf, d.head_dim);
     return GSP_OK;
@@ -652,6 +658,9 @@ int rope_store_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, co
     a.block_stride = pool->block_stride_k;
     a.layer_offset = (int64_t)layer * pool->layer_stride_k;
     a.head_stride = pool->head_stride_k;
+    a.v_block_stride = pool->block_stride_v;
+    a.v_layer_offset = (int64_t)layer * pool->layer_stride_v;
+    a.v_head_stride = pool->head_stride_v;
     a.positions = d_pos;
     a.block_ids = d_blocks;
     a.slots = d_slots;
@@ -663,6 +672,7 @@ int rope_store_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, co
     a.n_heads = n_heads;
     a.n_kv = d.heads_kv;
     a.head_dim = d.head_dim;
+    a.v_head_dim = d.v_head_dim;
     a.style = style;
     return check_hip(gsp::launch_rope_write(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "rope_write launch");
 }
@@ -679,7 +689,6 @@ int gsp_pool_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
     if (n == 0) return GSP_OK;
     if (!block_ids || !slots || !k_dev || !v_dev) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument");
     const gsp_pool_desc& d = pool->desc;
-    if (d.v_head_dim != d.head_dim) return gsp::fail(GSP_E_UNSUPPORTED, "vHeadDim != headDim is not supported on the device pool");
     if (layer < 0 || layer >= d.layers) return gsp::fail(GSP_E_INVALID_ARG, "layer %d out of range [0, %d)", layer, d.layers);
     for (int32_t i = 0; i < n; ++i) {
         if (block_ids[i] < 0 || block_ids[i] >= d.total_blocks)
@@ -751,9 +760,10 @@ int check_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, const float* k
     if (!ctx || !pool) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool is NULL");
     if (!ctx->step_valid) return gsp::fail(GSP_E_STATE, "gsp_step_pack must succeed before a step write");
     const gsp_pool_desc& d = pool->desc;
-    if (d.heads_kv != ctx->step_heads_kv || d.total_blocks < ctx->step_blocks)
-        return gsp::fail(GSP_E_INVALID_ARG, "the step was packed for a pool with %d KV heads and %d blocks",
-                         ctx->step_heads_kv, ctx->step_blocks);
+    if (d.heads_kv != ctx->step_heads_kv || d.total_blocks < ctx->step_blocks || d.block_size != ctx->step_block_size)
+        return gsp::fail(GSP_E_INVALID_ARG,
+                         "the step was packed for a pool with %d KV heads, %d blocks and %d-token pages",
+                         ctx->step_heads_kv, ctx->step_blocks, ctx->step_block_size);
     if (ctx->max_id >= d.total_blocks)
         return gsp::fail(GSP_E_INVALID_ARG, "block id %d out of range [0, %d)", ctx->max_id, d.total_blocks);
     if (layer < 0 || layer >= d.layers) return gsp::fail(GSP_E_INVALID_ARG, "layer %d out of range [0, %d)", layer, d.layers);
@@ -875,7 +885,6 @@ int gsp_pool_copy_block(gsp_ctx* ctx, gsp_pool* pool, int32_t src, int32_t dst, 
     if (src < 0 || src >= d.total_blocks || dst < 0 || dst >= d.total_blocks)
         return gsp::fail(GSP_E_INVALID_ARG, "block ids (%d, %d) out of range [0, %d)", src, dst, d.total_blocks);
     if (valid_tokens <= 0) return GSP_OK;
-    if (d.v_head_dim != d.head_dim) return gsp::fail(GSP_E_UNSUPPORTED, "vHeadDim != headDim is not supported on the device pool");
     int rc = set_device(ctx);
     if (rc) return rc;
     gsp::CopyBlockArgs a;
@@ -883,12 +892,15 @@ int gsp_pool_copy_block(gsp_ctx* ctx, gsp_pool* pool, int32_t src, int32_t dst, 
     a.v_pool = pool->v;
     a.block_stride = pool->block_stride_k;
     a.head_stride = pool->head_stride_k;
+    a.v_block_stride = pool->block_stride_v;
+    a.v_head_stride = pool->head_stride_v;
     a.src = src;
     a.dst = dst;
     a.valid_tokens = std::min(valid_tokens, d.block_size);
     a.layers = d.layers;
     a.n_kv = d.heads_kv;
     a.head_dim = d.head_dim;
+    a.v_head_dim = d.v_head_dim;
     return check_hip(gsp::launch_copy_block(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "copy_block launch");
 }
 
@@ -1029,6 +1041,10 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         return gsp::fail(GSP_E_INVALID_ARG, "positions/token_counts/bt_offsets/bt_ids must not be NULL");
     const int32_t L = desc->max_seq_len;
     const int32_t H = pd.heads_kv;
+    const int32_t bs = pd.block_size;
+    // Prefill tiles serve 16-token pages of equal K and V widths 64 or 128;
+    // rows of other pools run as per-query decode units.
+    const bool tileable = bs == 16 && pd.head_dim == pd.v_head_dim && (pd.head_dim == 64 || pd.head_dim == 128);
 
     // Pass 1: validate rows (the reference's throws, PagedAttentionKernel.cs:34-39,
     // plus the table and pool bounds) and size the packed arrays.
@@ -1056,7 +1072,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         if (tc > L) return gsp::fail(GSP_E_INVALID_ARG, "row %d: BlockTable token count %d exceeds maxSeqLen %d", b, tc, L);
         const int32_t span = desc->bt_offsets[b + 1] - desc->bt_offsets[b];
         const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
-        const int64_t pages = (total_last + gsp::kBlockSize - 1) / gsp::kBlockSize;
+        const int64_t pages = (total_last + bs - 1) / bs;
         if (pages > span)
             return gsp::fail(GSP_E_INVALID_ARG, "row %d: %lld tokens need %lld blocks but the table holds %d", b,
                              (long long)total_last, (long long)pages, span);
@@ -1068,14 +1084,14 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         total_q += ql;
         packed_pages += pages;
         kv_tokens += total_last;
-        if (row_is_tiled(ctx->prefill_path, ql)) {  // tiles, not split-KV units
+        if (row_is_tiled(ctx->prefill_path, ql, tileable)) {  // tiles, not split-KV units
             any_tiles = any_tiles || tc > 0;
             continue;
         }
         max_pages = std::max(max_pages, pages);
         for (int32_t i = 0; i < ql; ++i) {
             const int64_t tot = std::min<int64_t>(tc, (int64_t)pos + i + 1);
-            pair_pages += (tot + gsp::kBlockSize - 1) / gsp::kBlockSize;
+            pair_pages += (tot + bs - 1) / bs;
         }
     }
     if (total_q > INT32_MAX / 4 || packed_pages > INT32_MAX / 4 || pair_pages * H > INT32_MAX / 2)
@@ -1113,10 +1129,10 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
             ctx->query_pages.clear();
             for (int32_t b = 0; b < B; ++b) {
                 const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
-                if (row_is_tiled(ctx->prefill_path, ql)) continue;
+                if (row_is_tiled(ctx->prefill_path, ql, tileable)) continue;
                 for (int32_t i = 0; i < ql; ++i) {
                     const int64_t tot = std::min<int64_t>(desc->token_counts[b], (int64_t)desc->positions[b] + i + 1);
-                    if (tot > 0) ctx->query_pages.push_back((int32_t)((tot + gsp::kBlockSize - 1) / gsp::kBlockSize));
+                    if (tot > 0) ctx->query_pages.push_back((int32_t)((tot + bs - 1) / bs));
                 }
             }
             int64_t best_cost = INT64_MAX;
@@ -1148,7 +1164,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
             const int32_t pos = desc->positions[b];
             const int32_t tc = desc->token_counts[b];
             const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
-            if (row_is_tiled(ctx->prefill_path, ql)) {
+            if (row_is_tiled(ctx->prefill_path, ql, tileable)) {
                 // Causal tiles of 16 query tokens; a row with TokenCount 0 has
                 // total 0 for every token and gets none (out left untouched).
                 for (int32_t i = 0; i < ql; ++i)
@@ -1162,7 +1178,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                         t.ntok = std::min(gsp::kPrefillTileTokens, ql - t0);
                         t.token_count = tc;
                         const int64_t last = std::min<int64_t>(tc, (int64_t)t.pos0 + t.ntok);
-                        t.pages = (int32_t)((last + gsp::kBlockSize - 1) / gsp::kBlockSize);
+                        t.pages = (int32_t)((last + bs - 1) / bs);
                         t.reserved = 0;
                         for (int32_t kvh = 0; kvh < H; ++kvh) {
                             t.kvh = kvh;
@@ -1173,14 +1189,14 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                     tiled_queries += ql;
                 }
                 qi += ql;
-                bt_base += (total_last + gsp::kBlockSize - 1) / gsp::kBlockSize;
+                bt_base += (total_last + bs - 1) / bs;
                 continue;
             }
             for (int32_t i = 0; i < ql; ++i, ++qi) {
                 const int32_t tot = (int32_t)std::min<int64_t>(tc, (int64_t)pos + i + 1);
                 ctx->q_ctx[qi] = tot;
                 if (tot <= 0) continue;
-                const int32_t pages = (tot + gsp::kBlockSize - 1) / gsp::kBlockSize;
+                const int32_t pages = (tot + bs - 1) / bs;
                 const int32_t nsplit = (int32_t)std::min<int64_t>((pages + target - 1) / target, gsp::kMaxSplits);
                 const int32_t base = pages / nsplit, extra = pages % nsplit;
                 for (int32_t kvh = 0; kvh < H; ++kvh) {
@@ -1209,7 +1225,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                     }
                 }
             }
-            bt_base += (total_last + gsp::kBlockSize - 1) / gsp::kBlockSize;
+            bt_base += (total_last + bs - 1) / bs;
         }
     }
     std::stable_sort(ctx->units.begin(), ctx->units.end(), [](const DecodeUnit& x, const DecodeUnit& y) {
@@ -1281,7 +1297,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
             const int32_t pos = desc->positions[b];
             const int32_t tc = desc->token_counts[b];
             const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
-            const int64_t pages = (total_last + gsp::kBlockSize - 1) / gsp::kBlockSize;
+            const int64_t pages = (total_last + bs - 1) / bs;
             const int32_t* src = desc->bt_ids + desc->bt_offsets[b];
             for (int64_t i = 0; i < pages; ++i) {
                 ids[w++] = src[i];
@@ -1295,8 +1311,8 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                 const int64_t p = (int64_t)pos + i;
                 wr_pos[qi] = (int32_t)p;
                 const bool has = p < tc;
-                wr_blk[qi] = has ? src[p / gsp::kBlockSize] : -1;
-                wr_slot[qi] = has ? (int32_t)(p % gsp::kBlockSize) : 0;
+                wr_blk[qi] = has ? src[p / bs] : -1;
+                wr_slot[qi] = has ? (int32_t)(p % bs) : 0;
             }
         }
     }
@@ -1349,6 +1365,8 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->num_tiles = (int32_t)n_tiles;
     ctx->step_heads_kv = H;
     ctx->step_blocks = pd.total_blocks;
+    ctx->step_block_size = bs;
+    ctx->step_tileable = tileable;
     ctx->info.num_rows = B;
     ctx->info.total_q = (int32_t)total_q;
     ctx->info.packed_pages = (int32_t)packed_pages;
@@ -1425,25 +1443,30 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     if (!ctx->step_valid) return gsp::fail(GSP_E_STATE, "gsp_step_pack must succeed before gsp_attention_step");
     const gsp_pool_desc& d = pool->desc;
     if (sink_logit) return gsp::fail(GSP_E_UNSUPPORTED, "attention sinks are not supported on the GPU path");
-    if (d.v_head_dim != d.head_dim)
-        return gsp::fail(GSP_E_UNSUPPORTED, "vHeadDim (%d) != headDim (%d) is not supported", d.v_head_dim, d.head_dim);
-    if (d.head_dim != 64 && d.head_dim != 128)
-        return gsp::fail(GSP_E_UNSUPPORTED, "headDim %d is not supported (64 or 128)", d.head_dim);
+    // The reference GPU runner's domain (CudaPagedTransformerRunner.cs:408-412).
+    if (d.head_dim % 2 || d.v_head_dim % 2 || d.head_dim > 256 || d.v_head_dim > 256)
+        return gsp::fail(GSP_E_UNSUPPORTED, "headDim (%d) and vHeadDim (%d) must be even and at most 256", d.head_dim,
+                         d.v_head_dim);
     if (layer < 0 || layer >= d.layers) return gsp::fail(GSP_E_INVALID_ARG, "layer %d out of range [0, %d)", layer, d.layers);
     if (n_heads < 1 || n_heads % d.heads_kv != 0)
         return gsp::fail(GSP_E_INVALID_ARG, "nHeads (%d) must be a positive multiple of nHeadsKv (%d)", n_heads, d.heads_kv);
-    if (d.heads_kv != ctx->step_heads_kv || d.total_blocks < ctx->step_blocks)
-        return gsp::fail(GSP_E_INVALID_ARG, "the step was packed for a pool with %d KV heads and %d blocks",
-                         ctx->step_heads_kv, ctx->step_blocks);
+    if (d.heads_kv != ctx->step_heads_kv || d.total_blocks < ctx->step_blocks || d.block_size != ctx->step_block_size ||
+        (ctx->num_tiles > 0 && !ctx->step_tileable))
+        return gsp::fail(GSP_E_INVALID_ARG,
+                         "the step was packed for a pool with %d KV heads, %d blocks and %d-token pages",
+                         ctx->step_heads_kv, ctx->step_blocks, ctx->step_block_size);
     const int group = n_heads / d.heads_kv;
-    // The matrix-core kernel serves groups up to its 16-wide tile; the DPP
-    // kernel is kept for explicit selection (groups up to 8).
-    const bool use_mfma = ctx->decode_path == GSP_DECODE_MFMA ||
-                          (ctx->decode_path == GSP_DECODE_AUTO && group <= gsp::kMaxGroupMfma);
-    const int max_group = ctx->decode_path == GSP_DECODE_DPP ? gsp::kMaxGroup : gsp::kMaxGroupMfma;
-    // Prefill tiles take any group (eight heads per workgroup); decode units do not.
-    if (ctx->num_units > 0 && group > max_group)
-        return gsp::fail(GSP_E_UNSUPPORTED, "GQA group %d exceeds %d query heads per KV head", group, max_group);
+    // The matrix-core kernel serves any group, 16 query heads per tile; the
+    // DPP kernel is kept for explicit selection (fixed shapes, groups up to 8).
+    const bool use_mfma = ctx->decode_path != GSP_DECODE_DPP;
+    if (!use_mfma && ctx->num_units > 0 &&
+        (group > gsp::kMaxGroup || d.head_dim != d.v_head_dim || (d.head_dim != 64 && d.head_dim != 128) ||
+         d.block_size != gsp::kBlockSize))
+        return gsp::fail(GSP_E_UNSUPPORTED,
+                         "the DPP decode kernel serves headDim 64 or 128, 16-token pages and groups up to %d",
+                         gsp::kMaxGroup);
+    const int tiles = use_mfma ? (group + gsp::kDecodeTileHeads - 1) / gsp::kDecodeTileHeads : 1;
+    const int slot_heads = use_mfma ? std::min(group, gsp::kDecodeTileHeads) : group;
     if (ctx->max_id >= d.total_blocks)
         return gsp::fail(GSP_E_INVALID_ARG, "block id %d out of range [0, %d)", ctx->max_id, d.total_blocks);
     if (ctx->num_units == 0 && ctx->num_tiles == 0) return GSP_OK;
@@ -1454,9 +1477,9 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     const int32_t slots = ctx->num_slots;
     float* part = ctx->part;
     int32_t* counters = ctx->counters;
+    const size_t counter_need = (size_t)ctx->info.total_q * d.heads_kv * tiles;
     if (slots > 0) {
-        const size_t part_need = (size_t)slots * group * (d.head_dim + 2);
-        const size_t counter_need = (size_t)ctx->info.total_q * d.heads_kv;
+        const size_t part_need = (size_t)slots * tiles * slot_heads * (d.v_head_dim + 2);
         if (fixed) {
             if (part_need > fixed->part_floats || counter_need > fixed->counter_words)
                 return gsp::fail(GSP_E_INVALID_ARG,
@@ -1482,8 +1505,7 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     if (fixed && slots > 0) {
         // The array keeps whatever the last call on this GPU left: clear the
         // counters this launch uses (every launch leaves its own at zero).
-        rc = check_hip(gsp::launch_fill_i32(counters, (int64_t)ctx->info.total_q * d.heads_kv, 0, ctx->stream),
-                       "fill launch");
+        rc = check_hip(gsp::launch_fill_i32(counters, (int64_t)counter_need, 0, ctx->stream), "fill launch");
         if (rc) return rc;
     }
 
@@ -1493,18 +1515,27 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     a.block_stride = pool->block_stride_k;
     a.layer_offset = (int64_t)layer * pool->layer_stride_k;
     a.head_stride = pool->head_stride_k;
+    a.v_block_stride = pool->block_stride_v;
+    a.v_layer_offset = (int64_t)layer * pool->layer_stride_v;
+    a.v_head_stride = pool->head_stride_v;
     a.units = reinterpret_cast<const DecodeUnit*>(ctx->d_step + ctx->off_units);
     a.bin_rest = ctx->d_step + ctx->off_bins;
     a.bt_ids = ctx->d_step + ctx->off_ids;
     a.q = q_dev;
     a.out = out_dev;
     a.part_o = slots > 0 ? part : nullptr;
-    a.part_ml = slots > 0 ? part + (size_t)slots * group * d.head_dim : nullptr;
+    a.part_ml = slots > 0 ? part + (size_t)slots * tiles * slot_heads * d.v_head_dim : nullptr;
     a.counters = slots > 0 ? counters : nullptr;
     a.n_heads = n_heads;
     a.n_kv = d.heads_kv;
     a.group = group;
     a.scale_log2 = attn_scale * 1.4426950408889634f;
+    a.head_dim = d.head_dim;
+    a.v_head_dim = d.v_head_dim;
+    a.block_size = d.block_size;
+    a.total_q = ctx->info.total_q;
+    a.num_slots = slots;
+    a.slot_heads = slot_heads;
     const int f16 = d.kv_dtype == GSP_KV_F16;
     // Decode units stream from HBM and prefill tiles keep the matrix cores
     // busy: with both in the step, the tiles go to the side stream, forked
@@ -1517,8 +1548,7 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
         if (rc) return rc;
     }
     if (ctx->num_units > 0) {
-        rc = use_mfma ? check_hip(gsp::launch_decode_mfma(d.head_dim, f16, ctx->num_bins, a, ctx->stream),
-                                  "decode (mfma) launch")
+        rc = use_mfma ? check_hip(gsp::launch_decode_mfma(f16, ctx->num_bins, a, ctx->stream), "decode (mfma) launch")
                       : check_hip(gsp::launch_decode(d.head_dim, f16, ctx->num_bins, a, ctx->stream),
                                   "decode (dpp) launch");
         if (rc) return rc;

@@ -44,6 +44,12 @@ class Step:
     q_lens: Optional[np.ndarray] = None
     seed: int = 0
     notes: dict = field(default_factory=dict)
+    block_size: int = BLOCK_SIZE
+    v_head_dim: Optional[int] = None  # None: head_dim
+
+    @property
+    def dv(self) -> int:
+        return self.v_head_dim if self.v_head_dim else self.head_dim
 
     @property
     def num_rows(self) -> int:
@@ -76,7 +82,7 @@ class Step:
 
     def kv_bytes(self) -> int:
         """Algorithmic KV bytes of one step: every valid K and V element once."""
-        return self.kv_tokens() * self.n_kv * 2 * self.head_dim * self.elem_bytes
+        return self.kv_tokens() * self.n_kv * (self.head_dim + self.dv) * self.elem_bytes
 
     def decode_mask(self) -> np.ndarray:
         return self.lens == 1
@@ -109,7 +115,8 @@ class Step:
         sub = Step(self.name, self.n_heads, self.n_kv, self.head_dim, self.kv_dtype, self.total_blocks,
                    self.max_seq_len, positions=self.positions[rows].astype(np.int32),
                    token_counts=self.token_counts[rows].astype(np.int32), bt_offsets=offsets, bt_ids=ids,
-                   q_lens=q_lens, seed=self.seed, notes=dict(self.notes))
+                   q_lens=q_lens, seed=self.seed, notes=dict(self.notes), block_size=self.block_size,
+                   v_head_dim=self.v_head_dim)
         return sub, q_index
 
 
@@ -124,16 +131,18 @@ def _slices(rng: np.random.Generator, total_blocks: int, pages: np.ndarray) -> T
     return offsets, np.ascontiguousarray(perm[:need])
 
 
-def _pages(tokens) -> np.ndarray:
-    return ((np.asarray(tokens, np.int64) + BLOCK_SIZE - 1) // BLOCK_SIZE).astype(np.int32)
+def _pages(tokens, block_size: int = BLOCK_SIZE) -> np.ndarray:
+    return ((np.asarray(tokens, np.int64) + block_size - 1) // block_size).astype(np.int32)
 
 
 def decode_step(name: str, rng: np.random.Generator, ctx: np.ndarray, n_heads: int, n_kv: int, head_dim: int,
-                kv_dtype: str, total_blocks: int, max_seq_len: int, seed: int) -> Step:
+                kv_dtype: str, total_blocks: int, max_seq_len: int, seed: int, block_size: int = BLOCK_SIZE,
+                v_head_dim: Optional[int] = None) -> Step:
     ctx = np.asarray(ctx, np.int32)
-    offsets, ids = _slices(rng, total_blocks, _pages(ctx))
+    offsets, ids = _slices(rng, total_blocks, _pages(ctx, block_size))
     return Step(name, n_heads, n_kv, head_dim, kv_dtype, total_blocks, max_seq_len, positions=ctx - 1,
-                token_counts=ctx.copy(), bt_offsets=offsets, bt_ids=ids, seed=seed)
+                token_counts=ctx.copy(), bt_offsets=offsets, bt_ids=ids, seed=seed, block_size=block_size,
+                v_head_dim=v_head_dim)
 
 
 def qwen05b_decode(seed: int = SEED_BASE + 1) -> Step:
@@ -242,20 +251,22 @@ CONFIGS = {
 
 def small_step(seed: int, rows: int, n_heads: int, n_kv: int, head_dim: int, kv_dtype: str = "f32",
                ctx_lo: int = 1, ctx_hi: int = 64, total_blocks: int = 256, max_seq_len: int = 4096,
-               q_lens: Optional[np.ndarray] = None) -> Step:
+               q_lens: Optional[np.ndarray] = None, block_size: int = BLOCK_SIZE,
+               v_head_dim: Optional[int] = None) -> Step:
     """A small seeded ragged step for parity tests; rows with q_len > 1 are causal prefill rows."""
     rng = np.random.default_rng(seed)
     if q_lens is None:
         ctx = rng.integers(ctx_lo, ctx_hi + 1, size=rows).astype(np.int32)
         st = decode_step(f"small{seed}", rng, ctx, n_heads, n_kv, head_dim, kv_dtype, total_blocks, max_seq_len,
-                         seed)
+                         seed, block_size=block_size, v_head_dim=v_head_dim)
         return st
     q_lens = np.asarray(q_lens, np.int32)
     prior = rng.integers(ctx_lo - 1 if ctx_lo > 0 else 0, ctx_hi + 1, size=rows).astype(np.int32)
     tokens = prior + q_lens
-    offsets, ids = _slices(rng, total_blocks, _pages(tokens))
+    offsets, ids = _slices(rng, total_blocks, _pages(tokens, block_size))
     return Step(f"small{seed}", n_heads, n_kv, head_dim, kv_dtype, total_blocks, max_seq_len, positions=prior,
-                token_counts=tokens, bt_offsets=offsets, bt_ids=ids, q_lens=q_lens, seed=seed)
+                token_counts=tokens, bt_offsets=offsets, bt_ids=ids, q_lens=q_lens, seed=seed,
+                block_size=block_size, v_head_dim=v_head_dim)
 
 
 def device_values(torch, step: Step, layers: int = 1):
@@ -267,10 +278,10 @@ def device_values(torch, step: Step, layers: int = 1):
     g = torch.Generator(device="cuda")
     g.manual_seed(int(step.seed) & 0x7FFFFFFFFFFFFFFF)
     q = torch.randn((step.total_q, step.n_heads, step.head_dim), generator=g, device="cuda", dtype=torch.float32)
-    shape = (step.total_blocks, layers, step.n_kv, BLOCK_SIZE, step.head_dim)
     dt = torch.float16 if step.kv_dtype == "f16" else torch.float32
     arenas = []
-    for _ in range(2):
+    for dim in (step.head_dim, step.dv):
+        shape = (step.total_blocks, layers, step.n_kv, step.block_size, dim)
         a = torch.empty(shape, device="cuda", dtype=dt)
         flat = a.view(step.total_blocks, -1)
         for b0 in range(0, step.total_blocks, 4096):  # bounded fp32 temporaries
@@ -288,9 +299,8 @@ def host_values(step: Step, rng: Optional[np.random.Generator] = None, layers: i
     """
     rng = rng or np.random.default_rng(step.seed ^ 0x5EED)
     q = rng.standard_normal((step.total_q, step.n_heads, step.head_dim), dtype=np.float32)
-    shape = (step.total_blocks, layers, step.n_kv, BLOCK_SIZE, step.head_dim)
-    k = rng.standard_normal(shape, dtype=np.float32)
-    v = rng.standard_normal(shape, dtype=np.float32)
+    k = rng.standard_normal((step.total_blocks, layers, step.n_kv, step.block_size, step.head_dim), dtype=np.float32)
+    v = rng.standard_normal((step.total_blocks, layers, step.n_kv, step.block_size, step.dv), dtype=np.float32)
     if step.kv_dtype == "f16":
         k = k.astype(np.float16).astype(np.float32)
         v = v.astype(np.float16).astype(np.float32)

@@ -42,6 +42,7 @@ extern "C" {
 
 #define GSP_ABI_VERSION 8
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
+#define GSP_MAX_BLOCK_SIZE 16 /* largest page size of a device pool */
 
 typedef enum gsp_status {
     GSP_OK = 0,
@@ -121,7 +122,7 @@ typedef struct gsp_pool_desc {
     int32_t heads_kv;
     int32_t head_dim;
     int32_t v_head_dim;  /* <= 0 means head_dim (PagedBlockPool.cs:73) */
-    int32_t block_size;  /* must be 16 */
+    int32_t block_size;  /* tokens per page, 1 .. GSP_MAX_BLOCK_SIZE */
     int32_t kv_dtype;    /* gsp_kv_dtype */
 } gsp_pool_desc;
 
@@ -327,9 +328,16 @@ int gsp_set_prefill_path(gsp_ctx* ctx, int32_t path);
  * dot(q, k) * attn_scale (:64-65), softmax over the row's `total` tokens (:70),
  * out = sum p_t v_t (:73-370).  sink_logit must be NULL: attention sinks are
  * unsupported on the GPU path, as in CudaPagedTransformerRunner.cs:431.
- * Supported: head_dim == v_head_dim in {64, 128}; n_heads % heads_kv == 0 and
- * n_heads / heads_kv <= 16 (any group for a step of prefill tiles only);
- * block_size 16.  Work is enqueued on the context's stream.  A step with both
+ * Supported, the domain of the reference GPU runner
+ * (CudaPagedTransformerRunner.cs:402-412) and then some: head_dim and
+ * v_head_dim even and at most 256 (v_head_dim may differ from head_dim, as
+ * in the CPU kernel's generic path, PagedAttentionKernel.cs:326-370); any
+ * GQA group (n_heads % heads_kv == 0); pages of 1..16 tokens.  The pool must
+ * have the KV heads, block count and page size the step was packed for.
+ * Rows with q_len >= 16 run as prefill tiles when head_dim == v_head_dim is 64
+ * or 128 with 16-token pages, else as per-query decode units.  GSP_DECODE_DPP
+ * serves head_dim 64 or 128, 16-token pages and groups up to 8 only.  Work is
+ * enqueued on the context's stream.  A step with both
  * decode units and prefill tiles runs the tiles on a second stream of the
  * context, forked from and joined back into that stream, so the call is still
  * ordered as a whole on the context's stream.

@@ -16,7 +16,8 @@ def to_device_pool(torch, gsp, ctx, step, k, v):
     kd = torch.from_numpy(np.ascontiguousarray(k)).to(device="cuda", dtype=dt)
     vd = torch.from_numpy(np.ascontiguousarray(v)).to(device="cuda", dtype=dt)
     pool = gsp.Pool.wrap(ctx, kd.data_ptr(), vd.data_ptr(), step.total_blocks, k.shape[1], step.n_kv,
-                         step.head_dim, gsp.KV_F16 if step.kv_dtype == "f16" else gsp.KV_F32)
+                         step.head_dim, gsp.KV_F16 if step.kv_dtype == "f16" else gsp.KV_F32, v_head_dim=step.dv,
+                         block_size=step.block_size)
     return pool, (kd, vd)
 
 
@@ -31,7 +32,7 @@ def gpu_step(torch, gsp, ctx, step, q, pool, layer=0, split_pages=0, fill=np.nan
         ctx.set_split_pages(0)
         ctx.set_decode_bins(0)
     qd = torch.from_numpy(np.ascontiguousarray(q, dtype=np.float32)).cuda()
-    out = torch.full((step.total_q, step.n_heads, step.head_dim), float(fill), dtype=torch.float32, device="cuda")
+    out = torch.full((step.total_q, step.n_heads, step.dv), float(fill), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     ctx.attention_step(pool, layer, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
     ctx.sync()
@@ -39,8 +40,8 @@ def gpu_step(torch, gsp, ctx, step, q, pool, layer=0, split_pages=0, fill=np.nan
 
 
 def oracle_step(step, q, k, v, layer=0, threads=8, fill=np.nan):
-    pool = orc.HostPool(k, v)
-    out = np.full((step.total_q, step.n_heads, step.head_dim), fill, np.float32)
+    pool = orc.HostPool(k, v, block_size=step.block_size)
+    out = np.full((step.total_q, step.n_heads, step.dv), fill, np.float32)
     orc.attention_step(pool, layer, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, q, step.n_heads,
                        step.scale, step.max_seq_len, q_lens=step.q_lens, out=out, n_threads=threads)
     return out
@@ -55,5 +56,6 @@ def compact(step: workloads.Step):
     used, inv = np.unique(step.bt_ids, return_inverse=True)
     s = workloads.Step(step.name, step.n_heads, step.n_kv, step.head_dim, step.kv_dtype, len(used),
                        step.max_seq_len, step.positions, step.token_counts, step.bt_offsets,
-                       inv.astype(np.int32), step.q_lens, step.seed, dict(step.notes))
+                       inv.astype(np.int32), step.q_lens, step.seed, dict(step.notes), step.block_size,
+                       step.v_head_dim)
     return s, used

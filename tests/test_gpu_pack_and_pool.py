@@ -89,8 +89,7 @@ def test_attention_rejects_ids_outside_the_pool(torch_mod, gsp, ctx):
     with pytest.raises(gsp.InvalidArgument):  # packed for another pool geometry
         ctx.attention_step(pool2, 0, 2, q.data_ptr(), q.data_ptr(), 0.125)
     pool2.destroy()
-    with pytest.raises(gsp.Unsupported):  # GQA group above 16 is rejected before any launch
-        ctx.attention_step(pool, 0, 17, q.data_ptr(), q.data_ptr(), 0.125)
+    # (Groups above 16 run as tiles of 16 heads: tests/test_gpu_shapes.py.)
     ctx.set_decode_path(gsp.DECODE_DPP)
     try:
         with pytest.raises(gsp.Unsupported):  # the DPP kernel stops at 8
