@@ -5,81 +5,10 @@
 // (BlockTable.cs:13-117).  Pages themselves live in a device pool; an attached
 // pool receives the copy-on-write page copies.
 #include <algorithm>
-#include <atomic>
-#include <memory>
-#include <mutex>
-#include <unordered_map>
-#include <vector>
 
-#include "../../include/glacier_paged.h"
+#include "gsp_host_meta.h"
 #include "gsp_status.h"
 #include "gsp_xxh3.h"
-
-struct gsp_block_allocator {
-    int32_t total = 0;
-    int32_t block_size = 0;
-    std::mutex stack_mu;
-    std::vector<int32_t> free_stack;  // back() is the top of the LIFO stack
-    std::unique_ptr<std::atomic<int32_t>[]> allocated;
-    std::unique_ptr<std::atomic<int32_t>[]> refs;
-    std::unique_ptr<std::atomic<uint64_t>[]> hashes;  // prefix hash bound to each block (0: none)
-    std::mutex map_mu;
-    std::unordered_map<uint64_t, int32_t> prefix_map;  // prefix hash -> block
-    gsp_ctx* ctx = nullptr;
-    gsp_pool* pool = nullptr;
-
-    bool try_allocate(int32_t* id) {
-        int32_t b;
-        {
-            std::lock_guard<std::mutex> lk(stack_mu);
-            if (free_stack.empty()) {
-                *id = -1;
-                return false;
-            }
-            b = free_stack.back();
-            free_stack.pop_back();
-        }
-        allocated[b].store(1);
-        refs[b].store(1);
-        hashes[b].store(0);
-        *id = b;
-        return true;
-    }
-
-    int32_t release(int32_t id) {
-        if (id < 0 || id >= total) return 0;
-        const int32_t remaining = refs[id].fetch_sub(1) - 1;
-        if (remaining < 0) {
-            refs[id].store(0);
-            return 0;
-        }
-        if (remaining == 0) {
-            // A freed block leaves the prefix cache, unless its hash has since
-            // been bound to another block (:263-271).
-            const uint64_t h = hashes[id].load();
-            if (h != 0) {
-                {
-                    std::lock_guard<std::mutex> lk(map_mu);
-                    const auto it = prefix_map.find(h);
-                    if (it != prefix_map.end() && it->second == id) prefix_map.erase(it);
-                }
-                hashes[id].store(0);
-            }
-            int32_t expected = 1;
-            if (allocated[id].compare_exchange_strong(expected, 0)) {
-                std::lock_guard<std::mutex> lk(stack_mu);
-                free_stack.push_back(id);
-            }
-        }
-        return remaining;
-    }
-};
-
-struct gsp_block_table {
-    gsp_block_allocator* alloc = nullptr;
-    std::vector<int32_t> ids;
-    int32_t token_count = 0;
-};
 
 extern "C" {
 
@@ -108,19 +37,6 @@ int gsp_block_allocator_create(int32_t total_blocks, int32_t block_size, gsp_blo
 }
 
 void gsp_block_allocator_destroy(gsp_block_allocator* a) { delete a; }
-
-int gsp_block_allocator_attach_pool(gsp_block_allocator* a, gsp_ctx* ctx, gsp_pool* pool) {
-    gsp::clear_error();
-    if (!a) return gsp::fail(GSP_E_INVALID_ARG, "allocator is NULL");
-    if ((ctx == nullptr) != (pool == nullptr)) return gsp::fail(GSP_E_INVALID_ARG, "ctx and pool must both be set or both NULL");
-    if (pool) {
-        size_t kb = 0;
-        if (gsp_pool_arenas(pool, nullptr, nullptr, &kb, nullptr) != GSP_OK) return GSP_E_INVALID_ARG;
-    }
-    a->ctx = ctx;
-    a->pool = pool;
-    return GSP_OK;
-}
 
 int gsp_block_allocator_try_allocate(gsp_block_allocator* a, int32_t* block_id) {
     gsp::clear_error();
@@ -275,8 +191,8 @@ int gsp_block_table_append_token(gsp_block_table* t, int32_t* block_id, int32_t*
                 *offset = -1;
                 return 0;
             }
-            if (a->pool) {
-                int rc = gsp_pool_copy_block(a->ctx, a->pool, last, forked, in_block);
+            if (a->copy_page) {
+                int rc = a->copy_page(a->ctx, a->pool, last, forked, in_block);
                 if (rc) {
                     a->release(forked);
                     *block_id = -1;

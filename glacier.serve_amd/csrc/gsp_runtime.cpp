@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/glacier_paged.h"
+#include "gsp_host_meta.h"
 #include "gsp_internal.h"
 #include "gsp_status.h"
 
@@ -876,6 +877,19 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
         a.split_out = ctx->d_mm;
     }
     return check_hip(gsp::launch_matmul(a, ctx->stream), "matmul launch");
+}
+
+int gsp_block_allocator_attach_pool(gsp_block_allocator* a, gsp_ctx* ctx, gsp_pool* pool) {
+    gsp::clear_error();
+    if (!a) return gsp::fail(GSP_E_INVALID_ARG, "allocator is NULL");
+    if ((ctx == nullptr) != (pool == nullptr)) return gsp::fail(GSP_E_INVALID_ARG, "ctx and pool must both be set or both NULL");
+    if (pool && pool->desc.total_blocks < a->total)
+        return gsp::fail(GSP_E_INVALID_ARG, "the pool holds %d blocks, the allocator %d", pool->desc.total_blocks,
+                         a->total);
+    a->ctx = ctx;
+    a->pool = pool;
+    a->copy_page = pool ? gsp_pool_copy_block : nullptr;
+    return GSP_OK;
 }
 
 int gsp_pool_copy_block(gsp_ctx* ctx, gsp_pool* pool, int32_t src, int32_t dst, int32_t valid_tokens) {

@@ -213,7 +213,9 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
 
 /* PagedBlockPool.CopyBlockData (PagedBlockPool.cs:304-327): copies the first
  * min(valid_tokens, block_size) slots of every layer and KV head of block
- * `src` to block `dst`, on the device.  valid_tokens <= 0 is a no-op. */
+ * `src` to block `dst`, on the device.  valid_tokens <= 0 is a no-op.  It only
+ * enqueues a kernel, so copy-on-write forks of an attached pool may run on
+ * several threads at once, as the reference's concurrent forks do. */
 int gsp_pool_copy_block(gsp_ctx* ctx, gsp_pool* pool, int32_t src, int32_t dst,
                         int32_t valid_tokens);
 
@@ -405,7 +407,10 @@ void gsp_block_allocator_destroy(gsp_block_allocator* a);
 
 /* Attaches a device pool so that copy-on-write forks copy page contents on the
  * device (PagedBlockPool.TryForkBlock, :332-342).  NULL detaches; without a
- * pool a fork only allocates, as the reference's metadata-only pool does. */
+ * pool a fork only allocates, as the reference's metadata-only pool does.  The
+ * pool must hold at least the allocator's blocks.  The allocator itself is
+ * safe to use from several threads at once (a mutex-guarded free stack,
+ * atomic refcounts and a guarded prefix map), as the reference's pool is. */
 int gsp_block_allocator_attach_pool(gsp_block_allocator* a, gsp_ctx* ctx, gsp_pool* pool);
 
 /* TryAllocateBlock (:178-189): 1 and *block_id on success, 0 and -1 if empty. */

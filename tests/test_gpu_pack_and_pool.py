@@ -228,3 +228,60 @@ def test_back_to_back_packs_without_host_sync(torch_mod, gsp, ctx):
     finally:
         ctx.set_split_pages(0)
         pool.destroy()
+
+
+def test_concurrent_cow_forks_copy_pages_on_device(torch_mod, gsp, ctx):
+    """PrefixHashKvCacheAdversarialTests.cs:43-107 with the pages on the device: 16
+    sequences share one block holding tokens 0..7 and append token 8 at once from 16
+    threads.  Each fork copies the shared page on the device; afterwards every
+    sequence's page holds the prefix tokens and its own token 8."""
+    import threading
+
+    torch = torch_mod
+    nkv, d = 1, 16
+    pool = gsp.Pool.create(ctx, total_blocks=64, layers=1, heads_kv=nkv, head_dim=d)
+    alloc = gsp.BlockAllocator(64)
+    alloc.attach_pool(ctx, pool)
+    ok, shared = alloc.try_allocate_block()
+    assert ok
+    prefix = torch.arange(8 * d, dtype=torch.float32, device="cuda").reshape(8, nkv, d) + 100.0
+    torch.cuda.synchronize()
+    pool.write_tokens(0, [shared] * 8, list(range(8)), prefix.data_ptr(), prefix.data_ptr())
+    ctx.sync()
+    for _ in range(15):
+        alloc.retain_block(shared)
+    tables = [gsp.BlockTable(alloc) for _ in range(16)]
+    for t in tables:
+        t.attach_prefix_blocks([shared], 8)
+    got = [None] * 16
+    barrier = threading.Barrier(16)
+
+    def one(i):
+        barrier.wait()
+        got[i] = tables[i].append_token()
+
+    threads = [threading.Thread(target=one, args=(i,)) for i in range(16)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    ctx.sync()
+    ids = [g[1] for g in got]
+    assert all(g[0] and g[2] == 8 for g in got) and len(set(ids)) == 16
+    marks = torch.stack([torch.full((nkv, d), 1000.0 + i, device="cuda") for i in range(16)])
+    torch.cuda.synchronize()
+    pool.write_tokens(0, ids, [8] * 16, marks.data_ptr(), marks.data_ptr())
+    ctx.sync()
+    _, _, kb, vb = pool.arenas()
+    K = pool.download(0, kb).view(np.float32).reshape(64, 1, nkv, 16, d)
+    V = pool.download(1, vb).view(np.float32).reshape(64, 1, nkv, 16, d)
+    want = prefix.cpu().numpy()
+    for i, b in enumerate(ids):
+        assert np.array_equal(K[b, 0, :, :8].transpose(1, 0, 2), want), f"sequence {i}: prefix of block {b}"
+        assert np.array_equal(V[b, 0, :, :8].transpose(1, 0, 2), want)
+        assert np.all(K[b, 0, :, 8] == 1000.0 + i) and np.all(V[b, 0, :, 8] == 1000.0 + i)
+    for t in tables:
+        t.release_all()
+    assert alloc.free_blocks_count == 64
+    alloc.attach_pool(None, None)
+    pool.destroy()
