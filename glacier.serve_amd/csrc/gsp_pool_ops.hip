@@ -10,21 +10,43 @@ namespace {
 // PagedBlockPool.Store (PagedBlockPool.cs:151-161) for n tokens at once:
 // token i, KV head h -> K/V[block_ids[i]][layer][h][slots[i]][:].  One
 // workgroup per (token, head); fp32 -> fp16 rounds to nearest even.  A token
-// with block id -1 has no slot and is skipped.
+// with block id -1 has no slot and is skipped.  The first 256 elements of a
+// head are loaded (two per thread) together with the block id and slot, so
+// the usual head costs one memory round trip; wider heads loop on.
 template <typename KT>
 __global__ __launch_bounds__(128) void write_tokens_kernel(WriteTokensArgs a) {
     const int i = blockIdx.x;
     const int h = blockIdx.y;
-    if (a.block_ids[i] < 0) return;
+    const float* ks = a.k + ((int64_t)i * a.n_kv + h) * a.head_dim;
+    const float* vs = a.v + ((int64_t)i * a.n_kv + h) * a.v_head_dim;
+    const int e0 = threadIdx.x, e1 = threadIdx.x + 128;
+    const float k0 = e0 < a.head_dim ? ks[e0] : 0.f, k1 = e1 < a.head_dim ? ks[e1] : 0.f;
+    const float v0 = e0 < a.v_head_dim ? vs[e0] : 0.f, v1 = e1 < a.v_head_dim ? vs[e1] : 0.f;
     const int64_t blk = a.block_ids[i];
     const int64_t slot = a.slots[i];
+    if (blk < 0) return;
     KT* kd = static_cast<KT*>(a.k_pool) + blk * a.block_stride + a.layer_offset + h * a.head_stride + slot * a.head_dim;
     KT* vd = static_cast<KT*>(a.v_pool) + blk * a.v_block_stride + a.v_layer_offset + h * a.v_head_stride +
              slot * a.v_head_dim;
-    const float* ks = a.k + ((int64_t)i * a.n_kv + h) * a.head_dim;
-    const float* vs = a.v + ((int64_t)i * a.n_kv + h) * a.v_head_dim;
-    for (int e = threadIdx.x; e < a.head_dim; e += blockDim.x) kd[e] = static_cast<KT>(ks[e]);
-    for (int e = threadIdx.x; e < a.v_head_dim; e += blockDim.x) vd[e] = static_cast<KT>(vs[e]);
+    if (e0 < a.head_dim) kd[e0] = static_cast<KT>(k0);
+    if (e1 < a.head_dim) kd[e1] = static_cast<KT>(k1);
+    if (e0 < a.v_head_dim) vd[e0] = static_cast<KT>(v0);
+    if (e1 < a.v_head_dim) vd[e1] = static_cast<KT>(v1);
+    for (int e = e0 + 256; e < a.head_dim; e += 128) kd[e] = static_cast<KT>(ks[e]);
+    for (int e = e0 + 256; e < a.v_head_dim; e += 128) vd[e] = static_cast<KT>(vs[e]);
+}
+
+// The angle of pair j at position `pos` reduced to [-pi, pi] in fp64, then its
+// cosine and sine in fp32 (shared by both RoPE kernels).
+__device__ inline void rope_angle(double pos, int j, int d, double log2_base, float* c, float* s) {
+    const double ang = pos * exp2(-(2.0 * j / d) * log2_base);
+    const double r = ang - 6.283185307179586 * rint(ang * 0.15915494309189535);
+    sincosf((float)r, s, c);
+}
+
+__device__ inline void rope_turn(float x0, float x1, float c, float s, float* y0, float* y1) {
+    *y0 = x0 * c - x1 * s;
+    *y1 = x0 * s + x1 * c;
 }
 
 // QuantKernels.RoPE then PagedBlockPool.Store for n tokens
@@ -42,14 +64,7 @@ __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
     const int d = a.head_dim;
     const int half = d >> 1;
     const double pos = (double)a.positions[i];
-    for (int j = threadIdx.x; j < half; j += blockDim.x) {
-        const double ang = pos * exp2(-(2.0 * j / d) * a.log2_base);
-        const double r = ang - 6.283185307179586 * rint(ang * 0.15915494309189535);
-        float s, c;
-        sincosf((float)r, &s, &c);
-        cs[j][0] = c;
-        cs[j][1] = s;
-    }
+    for (int j = threadIdx.x; j < half; j += blockDim.x) rope_angle(pos, j, d, a.log2_base, &cs[j][0], &cs[j][1]);
     __syncthreads();
     const bool stored = a.block_ids[i] >= 0;
     const int64_t dst = (int64_t)a.block_ids[i] * a.block_stride + a.layer_offset + (int64_t)a.slots[i] * d;
@@ -83,6 +98,108 @@ __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
         const int e = idx - hk * dv;
         static_cast<KT*>(a.v_pool)[vdst + (int64_t)hk * a.v_head_stride + e] =
             static_cast<KT>(a.v[((int64_t)i * a.n_kv + hk) * dv + e]);
+    }
+}
+
+template <typename KT>
+__device__ inline void store4(KT* p, const float4& x) {
+    if constexpr (sizeof(KT) == 4) {
+        *reinterpret_cast<float4*>(p) = x;
+    } else {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        h4 h = {(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w};
+        *reinterpret_cast<h4*>(p) = h;
+    }
+}
+
+// The same RoPE and Store with 16-byte accesses, for head_dim % 8 == 0,
+// v_head_dim % 4 == 0 and 16-byte aligned buffers.  A token's work is a list
+// of items: per Q head and per K head, head_dim / 8 items of four rotation
+// pairs (two float4 of the head), then per V head v_head_dim / 4 items of one
+// float4.  Workgroup (token, y) takes items [256 y, 256 y + 256), one per
+// thread.  The item list does not depend on the token's block id (a token
+// with none skips its K and V stores at the end), so each thread issues its
+// loads together with the token's position, block and slot, before the angle
+// table is built: a workgroup costs about one memory round trip.
+template <typename KT>
+__global__ __launch_bounds__(256) void rope_write_vec_kernel(RopeWriteArgs a) {
+    __shared__ float cs[kRopeMaxHalf][2];
+    const int i = blockIdx.x;
+    const int d = a.head_dim;
+    const int half = d >> 1;
+    const int dv = a.v_head_dim;
+    const int per_head = d >> 3;
+    const int nq = a.n_heads * per_head;
+    const int nk = a.n_kv * per_head;
+    const int nv = a.n_kv * (dv >> 2);
+    const int t = blockIdx.y * 256 + threadIdx.x;
+    const bool pairs = a.style == GSP_ROPE_PAIRS;
+
+    // Item geometry: the head's two float4 (or the V float4) and the first pair.
+    int kind = 3;  // 0 Q, 1 K, 2 V, 3 none
+    int h = 0, m = 0;
+    if (t < nq) {
+        kind = 0;
+        h = t / per_head;
+        m = t - h * per_head;
+    } else if (t < nq + nk) {
+        kind = 1;
+        h = (t - nq) / per_head;
+        m = (t - nq) - h * per_head;
+    } else if (t < nq + nk + nv) {
+        kind = 2;
+        h = (t - nq - nk) / (dv >> 2);
+        m = (t - nq - nk) - h * (dv >> 2);
+    }
+    // halves: elements 4m.. and half+4m.., pairs 4m..4m+3; pairs: elements 8m.. and 8m+4.., pairs 4m..4m+3.
+    const int e0 = pairs ? 8 * m : 4 * m;
+    const int e1 = pairs ? 8 * m + 4 : 4 * m + half;
+    const float* src = kind == 0 ? a.q + ((int64_t)i * a.n_heads + h) * d
+                     : kind == 1 ? a.k + ((int64_t)i * a.n_kv + h) * d
+                                 : a.v + ((int64_t)i * a.n_kv + h) * dv;
+    float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+    if (kind == 0 || kind == 1) {
+        x0 = *reinterpret_cast<const float4*>(src + e0);
+        x1 = *reinterpret_cast<const float4*>(src + e1);
+    } else if (kind == 2) {
+        x0 = *reinterpret_cast<const float4*>(src + 4 * m);
+    }
+
+    const double pos = (double)a.positions[i];
+    const int64_t blk = a.block_ids[i];
+    const int64_t slot = a.slots[i];
+    for (int j = threadIdx.x; j < half; j += 256) rope_angle(pos, j, d, a.log2_base, &cs[j][0], &cs[j][1]);
+    __syncthreads();
+
+    if (kind == 3 || (kind != 0 && blk < 0)) return;
+    if (kind == 2) {
+        KT* vd = static_cast<KT*>(a.v_pool) + blk * a.v_block_stride + a.v_layer_offset +
+                 (int64_t)h * a.v_head_stride + slot * dv;
+        store4(vd + 4 * m, x0);
+        return;
+    }
+    const int j0 = 4 * m;
+    float4 y0, y1;
+    if (pairs) {
+        rope_turn(x0.x, x0.y, cs[j0][0], cs[j0][1], &y0.x, &y0.y);
+        rope_turn(x0.z, x0.w, cs[j0 + 1][0], cs[j0 + 1][1], &y0.z, &y0.w);
+        rope_turn(x1.x, x1.y, cs[j0 + 2][0], cs[j0 + 2][1], &y1.x, &y1.y);
+        rope_turn(x1.z, x1.w, cs[j0 + 3][0], cs[j0 + 3][1], &y1.z, &y1.w);
+    } else {
+        rope_turn(x0.x, x1.x, cs[j0][0], cs[j0][1], &y0.x, &y1.x);
+        rope_turn(x0.y, x1.y, cs[j0 + 1][0], cs[j0 + 1][1], &y0.y, &y1.y);
+        rope_turn(x0.z, x1.z, cs[j0 + 2][0], cs[j0 + 2][1], &y0.z, &y1.z);
+        rope_turn(x0.w, x1.w, cs[j0 + 3][0], cs[j0 + 3][1], &y0.w, &y1.w);
+    }
+    if (kind == 0) {
+        float* q = a.q + ((int64_t)i * a.n_heads + h) * d;
+        *reinterpret_cast<float4*>(q + e0) = y0;
+        *reinterpret_cast<float4*>(q + e1) = y1;
+    } else {
+        KT* kd = static_cast<KT*>(a.k_pool) + blk * a.block_stride + a.layer_offset + (int64_t)h * a.head_stride +
+                 slot * d;
+        store4(kd + e0, y0);
+        store4(kd + e1, y1);
     }
 }
 
@@ -129,10 +246,21 @@ hipError_t launch_write_tokens(int kv_f16, const WriteTokensArgs& a, hipStream_t
 hipError_t launch_rope_write(int kv_f16, const RopeWriteArgs& a, hipStream_t stream) {
     if (a.n <= 0) return hipSuccess;
     if (a.head_dim > 2 * kRopeMaxHalf || (a.head_dim & 1)) return hipErrorInvalidValue;
-    if (kv_f16)
+    const auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    const bool vec = a.head_dim % 8 == 0 && a.v_head_dim % 4 == 0 && al16(a.q) && al16(a.k) && al16(a.v) &&
+                     al16(a.k_pool) && al16(a.v_pool);
+    if (vec) {
+        const int items = (a.n_heads + a.n_kv) * (a.head_dim / 8) + a.n_kv * (a.v_head_dim / 4);
+        const dim3 grid(a.n, (items + 255) / 256);
+        if (kv_f16)
+            hipLaunchKernelGGL(rope_write_vec_kernel<_Float16>, grid, dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL(rope_write_vec_kernel<float>, grid, dim3(256), 0, stream, a);
+    } else if (kv_f16) {
         hipLaunchKernelGGL(rope_write_kernel<_Float16>, dim3(a.n), dim3(256), 0, stream, a);
-    else
+    } else {
         hipLaunchKernelGGL(rope_write_kernel<float>, dim3(a.n), dim3(256), 0, stream, a);
+    }
     return hipGetLastError();
 }
 

@@ -21,6 +21,8 @@ CASES = [
     (14, 2, 64, "f32", 10000.0),
     (32, 8, 128, "f16", 500000.0),
     (8, 8, 64, "f16", 10000.0),
+    (12, 4, 80, "f16", 10000.0),  # 16-byte kernel, half of 40 pairs
+    (6, 2, 36, "f32", 10000.0),   # head_dim % 8 != 0: the per-element kernel
 ]
 
 
