@@ -360,8 +360,10 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
 def matmul_timing(gsp, torch, ctx, stream, step, calls: int = 50) -> dict:
     """Device cost of the step's Q projection (QuantKernels.MatMulBatch, PagedTransformerRunner.cs:601):
     hidden = n_heads * head_dim in and out, one batch row per query token of the step, random
-    weights as Q8_0 and as F32.  The products are fp32 on the fp32 matrix cores, so the roofline
-    is 157.3 TFLOP/s; weight streaming bounds it only for small batches."""
+    weights as Q8_0 and as F32.  Each call takes the next of enough weight copies to span 512 MB,
+    twice the Infinity Cache, as a model's layers do (`us_per_call`); `us_per_call_warm` repeats one
+    copy.  Q8_0 runs on the fp16 matrix cores (x as scaled fp16 pairs), F32 on the fp32 ones; the
+    bytes bound is the weights at 8 TB/s."""
     hidden = step.n_heads * step.head_dim
     batch = int(step.total_q)
     gen = torch.Generator(device="cuda").manual_seed(step.seed)
@@ -370,27 +372,36 @@ def matmul_timing(gsp, torch, ctx, stream, step, calls: int = 50) -> dict:
     nb = hidden // 32
     d = (torch.randn((hidden, nb, 1), device="cuda", generator=gen) * 0.01).half().view(torch.uint8)
     q = torch.randint(-127, 128, (hidden, nb, 32), device="cuda", generator=gen, dtype=torch.int8).view(torch.uint8)
-    weights = {"q8_0": (gsp.WTYPE_Q8_0, torch.cat([d, q], dim=2).contiguous(), hidden * nb * 34),
+    q8 = torch.cat([d, q], dim=2).contiguous()
+    weights = {"q8_0": (gsp.WTYPE_Q8_0, q8, hidden * nb * 34),
                "f32": (gsp.WTYPE_F32, torch.randn((hidden, hidden), device="cuda", generator=gen), hidden * hidden * 4)}
     torch.cuda.synchronize()
     flops = 2.0 * batch * hidden * hidden
     out = {"in_dim": hidden, "out_dim": hidden, "batch": batch}
     for name, (wt, w, wbytes) in weights.items():
-        args = (wt, w.data_ptr(), x.data_ptr(), y.data_ptr(), hidden, hidden, batch)
-        with torch.cuda.stream(stream):
-            for _ in range(5):
-                ctx.matmul_batch(*args)
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(calls):
-                ctx.matmul_batch(*args)
-            e1.record(stream)
+        copies = [w] + [w.clone() for _ in range(max(1, -(-(512 << 20) // wbytes)) - 1)]
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) / calls * 1e3
-        out[name] = {"us_per_call": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 2),
-                     "frac_fp32_matrix_peak": round(flops / (us * 1e-6) / 1e12 / 157.3, 4),
-                     "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1)}
+
+        def timed(pick) -> float:
+            with torch.cuda.stream(stream):
+                for i in range(5):
+                    ctx.matmul_batch(wt, pick(i).data_ptr(), x.data_ptr(), y.data_ptr(), hidden, hidden, batch)
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for i in range(calls):
+                    ctx.matmul_batch(wt, pick(i).data_ptr(), x.data_ptr(), y.data_ptr(), hidden, hidden, batch)
+                e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / calls * 1e3
+
+        us = timed(lambda i: copies[i % len(copies)])
+        us_warm = timed(lambda i: w)
+        out[name] = {"us_per_call": round(us, 2), "us_per_call_warm": round(us_warm, 2), "weight_copies": len(copies),
+                     "tflops": round(flops / (us * 1e-6) / 1e12, 2),
+                     "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1),
+                     "frac_hbm_peak_weights": round(wbytes / (us * 1e-6) / 8e12, 4)}
+        del copies
     return out
 
 

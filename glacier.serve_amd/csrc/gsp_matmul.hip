@@ -25,6 +25,7 @@
 // timing.
 #include <cfloat>
 
+#include "gsp_epilogue.h"
 #include "gsp_internal.h"
 
 namespace gsp {
@@ -201,16 +202,37 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_batch_kernel(MatmulArgs 
 // x of one batch row as scaled fp16 pairs: one workgroup per row, four
 // elements per access (in_dim is a multiple of 64, rows 16-byte aligned).
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+// kTiled: both halves go to a.xh in the order the small-batch kernel's A
+// operands are read, tile by tile: for M tile t (batch rows 16 t ..) and chunk
+// c, 4096 bytes as [block][hi, lo][lane g * 16 + m][8 halves], the halves
+// x[16 t + m][64 c + 32 block + 8 g ..].  A wave then loads one operand of one
+// block as 1 KB in one instruction.
+template <bool kTiled>
 __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a) {
     __shared__ float red[kMmThreads / 64];
     const int b = blockIdx.x;
     const int n4 = a.in_dim / 4;
     const f4* xr = reinterpret_cast<const f4*>(a.x + (int64_t)b * a.in_dim);
+    // Rows of up to 16384 values stay in registers between the two passes
+    // (every load issued at once, indexes clamped); longer rows are read twice.
+    constexpr int kHeld = 16;
+    const bool held = n4 <= kHeld * kMmThreads;
+    f4 hv[kHeld];
     float mx = 0.f;
+    if (held) {
+#pragma unroll
+        for (int j = 0; j < kHeld; ++j)
+            if (kMmThreads * j < n4) hv[j] = xr[min((int)threadIdx.x + kMmThreads * j, n4 - 1)];
+#pragma unroll
+        for (int j = 0; j < kHeld; ++j)
+            if (kMmThreads * j < n4)
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(hv[j][0]), fabsf(hv[j][1])), fmaxf(fabsf(hv[j][2]), fabsf(hv[j][3]))));
+    } else {
 #pragma unroll 4
-    for (int i = threadIdx.x; i < n4; i += kMmThreads) {
-        const f4 v = xr[i];
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        for (int i = threadIdx.x; i < n4; i += kMmThreads) {
+            const f4 v = xr[i];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
@@ -227,17 +249,37 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
     const float down = ldexpf(1.0f, -e);
     h4v* xh = reinterpret_cast<h4v*>(static_cast<_Float16*>(a.xh) + (int64_t)b * a.in_dim);
     h4v* xl = reinterpret_cast<h4v*>(static_cast<_Float16*>(a.xl) + (int64_t)b * a.in_dim);
-#pragma unroll 4
-    for (int i = threadIdx.x; i < n4; i += kMmThreads) {
-        const f4 v = xr[i] * down;
+    _Float16* xt = static_cast<_Float16*>(a.xh);
+    const int64_t tile0 = (int64_t)(b >> 4) * (a.in_dim / 64);
+    auto put = [&](int i, f4 raw) {
+        const f4 v = raw * down;
         const h4v h = __builtin_convertvector(v, h4v);
-        xh[i] = h;
         // An infinite element rides on its hi half alone (Inf - Inf would make
         // the lo half NaN), as it would through the fp32 form.
         f4 l = v - __builtin_convertvector(h, f4);
 #pragma unroll
         for (int c = 0; c < 4; ++c) l[c] = __builtin_isinf(v[c]) ? 0.f : l[c];
-        xl[i] = __builtin_convertvector(l, h4v);
+        const h4v lh = __builtin_convertvector(l, h4v);
+        if (kTiled) {
+            const int k = 4 * i;
+            const int64_t base = ((tile0 + (k >> 6)) * 2 + ((k >> 5) & 1)) * 2 * 512 +
+                                 (((k >> 3) & 3) * 16 + (b & 15)) * 8 + (k & 7);
+            *reinterpret_cast<h4v*>(xt + base) = h;
+            *reinterpret_cast<h4v*>(xt + base + 512) = lh;
+        } else {
+            xh[i] = h;
+            xl[i] = lh;
+        }
+    };
+    if (held) {
+#pragma unroll
+        for (int j = 0; j < kHeld; ++j) {
+            const int i = threadIdx.x + kMmThreads * j;
+            if (i < n4) put(i, hv[j]);
+        }
+    } else {
+#pragma unroll 4
+        for (int i = threadIdx.x; i < n4; i += kMmThreads) put(i, xr[i]);
     }
     if (threadIdx.x == 0) a.xexp[b] = e;
 }
@@ -246,14 +288,15 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 // Eight int8 (two dwords) as fp16: with u = q ^ 0x80, the half 0x6400 | u is
-// 1024 + u, so subtracting 1152 leaves q exactly.
+// 1024 + u, so subtracting 1152 leaves q exactly.  v_perm_b32 pairs each byte
+// of u with a 0x64 byte from the constant operand.
 __device__ __forceinline__ h8 q8_to_h8(uint32_t d0, uint32_t d1) {
     h8 r;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const uint32_t u = (k ? d1 : d0) ^ 0x80808080u;
-        const uint32_t p0 = (u & 0xFFu) | ((u & 0xFF00u) << 8) | 0x64006400u;
-        const uint32_t p1 = ((u >> 16) & 0xFFu) | ((u >> 8) & 0xFF0000u) | 0x64006400u;
+        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0, 64, u1, 64
+        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2, 64, u3, 64
         const h2 a0 = __builtin_bit_cast(h2, p0) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
         const h2 a1 = __builtin_bit_cast(h2, p1) - h2{(_Float16)1152.0f, (_Float16)1152.0f};
         r[4 * k + 0] = a0[0];
@@ -382,6 +425,190 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
     }
 }
 
+// ---- Q8_0 weights, batches of up to 64 rows ---------------------------------
+//
+// matmul_q8_f16_small_kernel<NT, CH> is the fp16 form for batches of at most
+// 64 rows (NT M tiles of 16), laid out so that nothing waits in line:
+//   - x comes from the pre-pass in tile order (matmul_split_x_kernel<true>):
+//     a wave loads the A operands of its M tile straight into registers, one
+//     KB per instruction, every chunk of its range at once, with no LDS and no
+//     barrier between chunks;
+//   - the workgroup's 64 weight rows over its range of at most CH chunks are
+//     expanded to fp16 once, into LDS, with their block scales as floats;
+//   - wave w takes M tile w NT / 4 and NT of the four N tiles (16 weight rows
+//     each), so every staged operand serves several matrix steps;
+//   - two workgroups fit on a CU;
+//   - with K split over grid.z, each workgroup stores its tile coherently,
+//     waits for the stores and counts itself on the output tile's counter; the
+//     last one adds the ranges' tiles in z order (its own from registers),
+//     every load issued before the first add, and resets the counter.  No
+//     reduce launch, and results do not depend on timing.
+constexpr int kSmMaxPartials = 32;  // K ranges x tiles per lane the merge holds at most
+constexpr int kSmRowHalves = 8 * 64 + 8;  // an LDS weight row: 8 chunks of 64 halves, +16 bytes
+
+template <int NT, int CH>
+__global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(MatmulArgs a) {
+    static_assert(CH <= 8, "an LDS weight row holds 8 chunks");
+    __shared__ _Float16 wh[kMmRowsWg * kSmRowHalves];  // [weight row][chunk][64 halves]
+    __shared__ float wd[kMmRowsWg][2 * CH + 1];        // block scales [weight row][2 chunk + block]
+    __shared__ int last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int chunks = a.in_dim / 64;
+    const int c_begin = blockIdx.z * a.chunks_per_split;
+    const int nc = min(chunks, c_begin + a.chunks_per_split) - c_begin;  // 1..CH (host)
+    constexpr int kWavesPerM = 4 / NT;
+    const int mt = wave / kWavesPerM;           // the wave's M tile
+    const int nt0 = (wave % kWavesPerM) * NT;   // its first N tile
+
+    // A operands of the wave's M tile, all chunks at once: [chunk][block][hi, lo].
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    const h8* xt = reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.xh)) +
+                   ((int64_t)mt * chunks + c_begin) * 256 + lane;
+    h8 ax[CH][2][2];
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+        if (i < nc)
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+                for (int part = 0; part < 2; ++part) ax[i][blk][part] = xt[i * 256 + (blk * 2 + part) * 64];
+
+    // Weights to fp16: unit u = 64 r + 8 i + 4 block + gg (row r, chunk i, lane
+    // group gg) is eight values; thread tid takes units tid + 256 k, that is
+    // one fixed (chunk, block, lane group) of rows tid / 64 + 4 k.  A wave's
+    // units are one row's chunks, so its loads cover whole 68-byte windows.
+    // Every unit's four dwords load first (raw buffer loads whose lane offset
+    // is fixed per thread plus a row step): block 0's values sit at dwords
+    // 2 gg .. 2 gg + 2 shifted by 2 bytes, block 1's at 9 + 2 gg, 10 + 2 gg,
+    // and the scale is the low half of dword 0 or the high half of dword 8.
+    // Units of chunks past the range load the range's last chunk and store
+    // nothing; rows past out_dim read as zero (past the buffer's end).
+    {
+        constexpr int kU = (kMmRowsWg * 64) / kMmThreads;
+        const int row_bytes = chunks * 68;
+        const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes),
+            (short)0, rows_here * row_bytes, 0x00020000);
+        const int r0 = tid >> 6;
+        const int i = (tid >> 3) & 7;
+        const int blk = (tid >> 2) & 1;
+        const int gg = tid & 3;
+        const int s0 = blk ? 9 + 2 * gg : 2 * gg;
+        const int voff = r0 * row_bytes + (c_begin + min(i, nc - 1)) * 68;
+        uint32_t wdw[kU][4];
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            // The row step stays in the lane offset: the range check covers the
+            // lane offset, not the scalar one.
+            const int vk = voff + 4 * k * row_bytes;
+            wdw[k][0] = __builtin_amdgcn_raw_buffer_load_b32(wr, vk + 4 * s0, 0, 0);
+            wdw[k][1] = __builtin_amdgcn_raw_buffer_load_b32(wr, vk + 4 * s0 + 4, 0, 0);
+            wdw[k][2] = __builtin_amdgcn_raw_buffer_load_b32(wr, vk + 4 * min(s0 + 2, 16), 0, 0);
+            wdw[k][3] = __builtin_amdgcn_raw_buffer_load_b32(wr, vk + 32 * blk, 0, 0);
+        }
+        const int sh = blk ? 0 : 2;
+        _Float16* wdst = &wh[r0 * kSmRowHalves + i * 64 + blk * 32 + gg * 8];
+        float* ddst = &wd[r0][2 * i + blk];
+        if (i < nc) {
+#pragma unroll
+            for (int k = 0; k < kU; ++k) {
+                const h8 q = q8_to_h8(__builtin_amdgcn_alignbyte(wdw[k][1], wdw[k][0], sh),
+                                      __builtin_amdgcn_alignbyte(wdw[k][2], wdw[k][1], sh));
+                const uint32_t sw = blk ? wdw[k][3] >> 16 : wdw[k][3];
+                *reinterpret_cast<h8*>(wdst + 4 * k * kSmRowHalves) = q;
+                ddst[4 * k * (2 * CH + 1)] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xFFFFu));  // four lane groups store the same value
+            }
+        }
+    }
+    __syncthreads();
+
+    f4 acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        if (i < nc) {
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    const int r = 16 * (nt0 + j) + n;  // B column: the lane's weight row
+                    const h8 wq = *reinterpret_cast<const h8*>(&wh[r * kSmRowHalves + i * 64 + blk * 32 + g * 8]);
+                    const float d = wd[r][2 * i + blk];
+                    f4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i][blk][0], wq, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    part = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i][blk][1], wq, part, 0, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[j][q] = fmaf(d, part[q], acc[j][q]);
+                }
+            }
+        }
+    }
+
+    // Lane holds batch rows 16 mt + 4 g + q of weight rows 64 x + 16 (nt0 + j) + n,
+    // scaled by 2^-xexp of the batch row.
+    float v[NT][4];
+    int bq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bq[q] = 16 * mt + 4 * g + q;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = a.xexp[min(bq[q], a.batch - 1)];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) v[j][q] = ldexpf(acc[j][q], e);
+    }
+    const int obase = blockIdx.x * kMmRowsWg + 16 * nt0 + n;
+    if (a.splits == 1) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (obase + 16 * j < a.out_dim && bq[q] < a.batch) a.y[(int64_t)bq[q] * a.out_dim + obase + 16 * j] = v[j][q];
+        return;
+    }
+    const int z = blockIdx.z;
+    const int64_t plane = (int64_t)a.batch * a.out_dim;
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (obase + 16 * j < a.out_dim && bq[q] < a.batch)
+                coherent_store(a.split_out + z * plane + (int64_t)bq[q] * a.out_dim + obase + 16 * j, v[j][q]);
+    wait_vm_complete();
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(a.counters + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               a.splits - 1;
+    __syncthreads();
+    if (!last) return;
+    constexpr int kZ = kSmMaxPartials / NT;
+    float p[NT][4][kZ];
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float* pb = a.split_out + (int64_t)min(bq[q], a.batch - 1) * a.out_dim + min(obase + 16 * j, a.out_dim - 1);
+#pragma unroll
+            for (int zz = 0; zz < kZ; ++zz) p[j][q][zz] = coherent_load(pb + min(zz, a.splits - 1) * plane);
+        }
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float s = z == 0 ? v[j][q] : p[j][q][0];
+#pragma unroll
+            for (int zz = 1; zz < kZ; ++zz)
+                if (zz < a.splits) s += zz == z ? v[j][q] : p[j][q][zz];
+            if (obase + 16 * j < a.out_dim && bq[q] < a.batch) a.y[(int64_t)bq[q] * a.out_dim + obase + 16 * j] = s;
+        }
+    if (tid == 0) __hip_atomic_store(a.counters + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // y = the sum over z of the split partials, in z order; four elements per
 // thread and step when y and the partials are 16-byte aligned, else one.
 __global__ __launch_bounds__(kMmThreads) void matmul_reduce_kernel(MatmulArgs a) {
@@ -408,13 +635,38 @@ __global__ __launch_bounds__(kMmThreads) void matmul_reduce_kernel(MatmulArgs a)
 
 }  // namespace
 
+int matmul_small_chunks(int) { return 8; }
+
+int64_t matmul_small_x_halves(int batch, int in_dim) {
+    return (int64_t)(batch <= 16 ? 1 : batch <= 32 ? 2 : 4) * 16 * in_dim * 2;  // NT whole M tiles, hi and lo
+}
+
+int matmul_small_max_splits(int batch) { return kSmMaxPartials / (batch <= 16 ? 1 : batch <= 32 ? 2 : 4); }
+
+hipError_t launch_matmul_q8_small(const MatmulArgs& a, hipStream_t stream) {
+    if (a.batch <= 0 || a.out_dim <= 0) return hipSuccess;
+    if (a.batch > 64 || a.w_type != kWeightQ8_0 || !a.xh || !a.xl || !a.xexp ||
+        a.chunks_per_split > matmul_small_chunks(a.batch) || a.splits > matmul_small_max_splits(a.batch) ||
+        (a.splits > 1 && (!a.split_out || !a.counters)))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(matmul_split_x_kernel<true>, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
+    const dim3 grid((a.out_dim + kMmRowsWg - 1) / kMmRowsWg, 1, a.splits);
+    if (a.batch <= 16)
+        hipLaunchKernelGGL((matmul_q8_f16_small_kernel<1, 8>), grid, dim3(kMmThreads), 0, stream, a);
+    else if (a.batch <= 32)
+        hipLaunchKernelGGL((matmul_q8_f16_small_kernel<2, 8>), grid, dim3(kMmThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((matmul_q8_f16_small_kernel<4, 8>), grid, dim3(kMmThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream) {
     if (a.batch <= 0 || a.out_dim <= 0) return hipSuccess;
     const dim3 grid((a.out_dim + kMmRowsWg - 1) / kMmRowsWg, (a.batch + 63) / 64, a.splits);
     if (a.w_type == kWeightF32)
         hipLaunchKernelGGL(matmul_batch_kernel<kWeightF32>, grid, dim3(kMmThreads), 0, stream, a);
     else if (a.w_type == kWeightQ8_0 && a.xh) {
-        hipLaunchKernelGGL(matmul_split_x_kernel, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
+        hipLaunchKernelGGL(matmul_split_x_kernel<false>, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
         hipLaunchKernelGGL(matmul_q8_f16_kernel, grid, dim3(kMmThreads), 0, stream, a);
     } else if (a.w_type == kWeightQ8_0)
         hipLaunchKernelGGL(matmul_batch_kernel<kWeightQ8_0>, grid, dim3(kMmThreads), 0, stream, a);

@@ -28,6 +28,13 @@ SHAPES = [
     (256, 2048, 100),
     (512, 1600, 128),
     (128, 2049, 97),
+    # batch <= 64 and batch x out_dim >= 65536: Q8_0 takes the small-batch fp16 kernel
+    # (one, two and four M tiles, ragged batch tiles and weight-row tiles, 1 to 16 K ranges)
+    (3584, 1040, 64),
+    (1024, 4100, 17),
+    (8192, 4160, 16),
+    (192, 8192, 9),
+    (640, 2050, 33),
 ]
 
 
@@ -99,14 +106,17 @@ def test_matmul_q_projection_then_attention_shapes(torch_mod, gsp, ctx):
     assert np.all(np.abs(got - ref) <= 1e-5 * mag + 1e-7)
 
 
+@pytest.mark.parametrize("batch", [100, 60], ids=["b100", "b60"])
 @pytest.mark.parametrize("w_type", [orc.WTYPE_F32, orc.WTYPE_Q8_0], ids=["f32", "q8_0"])
-def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type):
-    """Rows with one channel 1e4 times the rest, rows near 1e30 and rows near 1e-30, on a shape that
-    takes the Q8_0 fp16 path.  There x is a scaled fp16 pair whose error is bounded relative to its
-    row's largest |x| (at most ~2^-22 of it per element), so the bar adds that term; every finite row
-    stays finite.  The F32 form keeps x in fp32 and meets the plain fp32 summation bar."""
-    in_dim, out_dim, batch = 256, 2048, 100
-    rng = np.random.default_rng(77 + w_type)
+def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, batch):
+    """Rows with one channel 1e4 times the rest, rows near 1e30 and rows near 1e-30.  Q8_0 takes an
+    fp16 path at both batches (the two-kernel form at 100 rows, the one-launch form at 60, whose
+    per-row exponents grow as larger values arrive).  There x is a scaled fp16 pair whose error is
+    bounded relative to its row's largest |x| (at most ~2^-22 of it per element), so the bar adds
+    that term; every finite row stays finite.  The F32 form keeps x in fp32 and meets the plain fp32
+    summation bar."""
+    in_dim, out_dim = 4096, 2048
+    rng = np.random.default_rng(77 + w_type + batch)
     data, wm = _weights(rng, w_type, out_dim, in_dim)
     x = rng.standard_normal((batch, in_dim)).astype(np.float32)
     x[0:30, rng.integers(0, in_dim, 30)] *= 1e4           # one outlier channel per row (some shared)
