@@ -111,6 +111,13 @@ struct PrefillArgs {
 // Launches the MFMA prefill kernel for (head_dim, kv dtype).
 hipError_t launch_prefill_mfma(int head_dim, int kv_f16, int num_tiles, const PrefillArgs& a, hipStream_t stream);
 
+// Launches a step with both decode bins and prefill tiles as one kernel (the
+// matrix-core decode of the fixed shapes, head_dim == v_head_dim in {64, 128},
+// 16-token pages, and the prefill tiles).  DecodeArgs and PrefillArgs are
+// those of the two separate launches.
+hipError_t launch_mixed_mfma(int head_dim, int kv_f16, int num_bins, int num_tiles, const DecodeArgs& da,
+                             const PrefillArgs& pa, hipStream_t stream);
+
 // Launches the DPP decode kernel instantiated for (head_dim, kv dtype, group <= 8),
 // one workgroup per bin.
 hipError_t launch_decode(int head_dim, int kv_f16, int num_bins, const DecodeArgs& a, hipStream_t stream);

@@ -51,7 +51,7 @@
 // V goes in transposed, so each PV B operand is one 16-byte LDS read, and the
 // K and V operands of the next matrix step are read while the current one runs.
 // The roofline of these rows is the matrix peak.
-#include "gsp_epilogue.h"
+#include "gsp_decode_body.h"
 
 namespace gsp {
 namespace {
@@ -449,14 +449,13 @@ __device__ __forceinline__ void pair_softmax(TileState<D>& st, f4& s0, f4& s1, b
 // hot loop has no branches; a tile past the group (zero Q) is simply not
 // stored.  It costs no time: the page barrier waits for the busiest wave.
 template <int D, typename KT, int TILES>
-__global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(PrefillArgs a) {
+__device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D, KT>& sh, int bx, int by) {
     constexpr int kPrefillTiles = TILES;
     constexpr int kRow = PfLds<D, KT>::kRow;
     constexpr bool kSplitKV = sizeof(KT) == 4;  // fp32 pages enter as hi + lo pairs
-    __shared__ PfLds<D, KT> sh;
 
-    const PrefillTile t = a.tiles[blockIdx.x];
-    const int hc = blockIdx.y * kDecodeWaves * TILES;  // first head of this workgroup within the group
+    const PrefillTile t = a.tiles[bx];
+    const int hc = by * kDecodeWaves * TILES;  // first head of this workgroup within the group
     const int G = min(kDecodeWaves * TILES, a.group - hc);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -708,6 +707,52 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
     }
 }
 
+template <int D, typename KT, int TILES>
+__global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(PrefillArgs a) {
+    __shared__ PfLds<D, KT> sh;
+    prefill_tile_body<D, KT, TILES>(a, sh, blockIdx.x, blockIdx.y);
+}
+
+// A step with both decode units and prefill tiles in one launch: workgroups
+// x < num_bins run decode bin x (decode_bins_body, grid.y = its tiles of 16
+// heads), the others prefill tile x - num_bins (grid.y = its groups of 4 TILES
+// heads); a workgroup past its kind's grid.y returns at once.  The decode
+// workgroups come first, so each is dispatched onto a CU whose other slot
+// takes a tile: HBM-bound and matrix-bound waves share the CUs in one kernel,
+// with no second stream (streams share the device's few hardware queues, and
+// two kernels on one queue run one after the other).
+template <int D, typename KT, int TILES>
+__global__ __launch_bounds__(kDecodeThreads, 2) void paged_mixed_mfma_kernel(DecodeArgs da, PrefillArgs pa, int num_bins,
+                                                                          int decode_y, int tile_y) {
+    __shared__ union {
+        EpilogueLds<D, kMaxGroupMfma> d;
+        PfLds<D, KT> p;
+    } sh;
+    const int bx = blockIdx.x;
+    const int by = blockIdx.y;
+    if (bx < num_bins) {
+        if (by < decode_y) decode_bins_body<D, KT, kExact>(da, sh.d, bx, by);
+    } else if (by < tile_y) {
+        prefill_tile_body<D, KT, TILES>(pa, sh.p, bx - num_bins, by);
+    }
+}
+
+template <int D, typename KT>
+hipError_t launch_mixed(int num_bins, int num_tiles, const DecodeArgs& da, const PrefillArgs& pa, hipStream_t stream) {
+    const int tiles = pa.group > kDecodeWaves ? 2 : 1;
+    const int per_wg = kDecodeWaves * tiles;
+    const int decode_y = (da.group + kDecodeTileHeads - 1) / kDecodeTileHeads;
+    const int tile_y = (pa.group + per_wg - 1) / per_wg;
+    const dim3 grid(num_bins + num_tiles, max(decode_y, tile_y));
+    if (tiles == 2)
+        hipLaunchKernelGGL((paged_mixed_mfma_kernel<D, KT, 2>), grid, dim3(kDecodeThreads), 0, stream, da, pa, num_bins,
+                           decode_y, tile_y);
+    else
+        hipLaunchKernelGGL((paged_mixed_mfma_kernel<D, KT, 1>), grid, dim3(kDecodeThreads), 0, stream, da, pa, num_bins,
+                           decode_y, tile_y);
+    return hipGetLastError();
+}
+
 template <int D, typename KT>
 hipError_t launch_tiles(int num_tiles, const PrefillArgs& a, hipStream_t stream) {
     const int tiles = a.group > kDecodeWaves ? 2 : 1;
@@ -722,6 +767,17 @@ hipError_t launch_tiles(int num_tiles, const PrefillArgs& a, hipStream_t stream)
 }
 
 }  // namespace
+
+hipError_t launch_mixed_mfma(int head_dim, int kv_f16, int num_bins, int num_tiles, const DecodeArgs& da,
+                             const PrefillArgs& pa, hipStream_t stream) {
+    if (num_bins <= 0 || num_tiles <= 0 || da.group < 1 || pa.group != da.group) return hipErrorInvalidValue;
+    if (da.head_dim != head_dim || da.v_head_dim != head_dim || da.block_size != kBlockSize) return hipErrorInvalidValue;
+    if (head_dim == 128) return kv_f16 ? launch_mixed<128, _Float16>(num_bins, num_tiles, da, pa, stream)
+                                       : launch_mixed<128, float>(num_bins, num_tiles, da, pa, stream);
+    if (head_dim == 64) return kv_f16 ? launch_mixed<64, _Float16>(num_bins, num_tiles, da, pa, stream)
+                                      : launch_mixed<64, float>(num_bins, num_tiles, da, pa, stream);
+    return hipErrorInvalidValue;
+}
 
 hipError_t launch_prefill_mfma(int head_dim, int kv_f16, int num_tiles, const PrefillArgs& a, hipStream_t stream) {
     if (num_tiles <= 0) return hipSuccess;

@@ -123,11 +123,16 @@ struct gsp_ctx {
     std::string arch;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
-    // A step with both decode units and prefill tiles runs the tiles on
-    // side_stream, forked from and joined back into `stream` with the events.
-    hipStream_t side_stream = nullptr;
+    // A step with both decode units and prefill tiles runs the decode kernel
+    // on side_stream[0] and the tiles on side_stream[1], forked from `stream`
+    // and joined back into it with the events.  Streams share the device's
+    // few hardware queues (4 by default) in creation order, so a stream the
+    // caller made may share a queue with either; the two side streams are
+    // created one after the other and so take different queues, and the two
+    // kernels run side by side whatever `stream` is.
+    hipStream_t side_stream[2] = {nullptr, nullptr};
     hipEvent_t fork_ev = nullptr;
-    hipEvent_t join_ev = nullptr;
+    hipEvent_t join_ev[2] = {nullptr, nullptr};
 
     // Step staging, double-buffered: successive packs alternate between two
     // slots, each a pinned host buffer and its device mirror.  A slot's upload
@@ -433,9 +438,11 @@ int gsp_init(int device, gsp_ctx** out) {
         if (!rc) rc = check_hip(hipEventRecord(ctx->kernel_done[j], ctx->own_stream), "hipEventRecord");
     }
     if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->aux_done, hipEventDisableTiming), "hipEventCreate");
-    if (!rc) rc = check_hip(hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking), "hipStreamCreate");
+    for (int j = 0; j < 2 && !rc; ++j)
+        rc = check_hip(hipStreamCreateWithFlags(&ctx->side_stream[j], hipStreamNonBlocking), "hipStreamCreate");
     if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming), "hipEventCreate");
-    if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming), "hipEventCreate");
+    for (int j = 0; j < 2 && !rc; ++j)
+        rc = check_hip(hipEventCreateWithFlags(&ctx->join_ev[j], hipEventDisableTiming), "hipEventCreate");
     // The allocation-free entry point's scratch: look up this device's copy
     // of the array once, with the device current.
     if (!rc) rc = check_hip(gsp::noalloc_setup(device), "hipGetSymbolAddress(scratch)");
@@ -469,10 +476,13 @@ void gsp_shutdown(gsp_ctx* ctx) {
     if (ctx->part) (void)hipFree(ctx->part);
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->aux_done) (void)hipEventDestroy(ctx->aux_done);
-    if (ctx->side_stream) (void)hipStreamSynchronize(ctx->side_stream);
+    for (int j = 0; j < 2; ++j)
+        if (ctx->side_stream[j]) (void)hipStreamSynchronize(ctx->side_stream[j]);
     if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
-    if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
-    if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
+    for (int j = 0; j < 2; ++j) {
+        if (ctx->join_ev[j]) (void)hipEventDestroy(ctx->join_ev[j]);
+        if (ctx->side_stream[j]) (void)hipStreamDestroy(ctx->side_stream[j]);
+    }
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     (void)hipGetLastError();
     delete ctx;
@@ -1595,43 +1605,61 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     a.num_slots = slots;
     a.slot_heads = slot_heads;
     const int f16 = d.kv_dtype == GSP_KV_F16;
+    gsp::PrefillArgs p;
+    p.k_pool = a.k_pool;
+    p.v_pool = a.v_pool;
+    p.block_stride = a.block_stride;
+    p.layer_offset = a.layer_offset;
+    p.head_stride = a.head_stride;
+    p.tiles = reinterpret_cast<const PrefillTile*>(ctx->d_step + ctx->off_tiles);
+    p.bt_ids = a.bt_ids;
+    p.q = q_dev;
+    p.out = out_dev;
+    p.n_heads = n_heads;
+    p.n_kv = d.heads_kv;
+    p.group = group;
+    p.scale_log2 = a.scale_log2;
     // Decode units stream from HBM and prefill tiles keep the matrix cores
-    // busy: with both in the step, the tiles go to the side stream, forked
-    // here and joined back below, so the two kernels share the GPU.
+    // busy.  With both in the step and the matrix-core decode (tiles exist
+    // only for its fixed shapes), one kernel runs both kinds of workgroup side
+    // by side.  With the DPP decode, each kernel goes to its own side stream,
+    // forked here and joined back below.
+    if (use_mfma && ctx->num_units > 0 && ctx->num_tiles > 0) {
+        rc = check_hip(gsp::launch_mixed_mfma(d.head_dim, f16, ctx->num_bins, ctx->num_tiles, a, p, ctx->stream),
+                       "mixed step launch");
+        const int rd = step_done(ctx, capturing);
+        return rc ? rc : rd;
+    }
     const bool fork = ctx->num_units > 0 && ctx->num_tiles > 0;
-    hipStream_t tile_stream = fork ? ctx->side_stream : ctx->stream;
+    hipStream_t decode_stream = fork ? ctx->side_stream[0] : ctx->stream;
+    hipStream_t tile_stream = fork ? ctx->side_stream[1] : ctx->stream;
     if (fork) {
         rc = check_hip(hipEventRecord(ctx->fork_ev, ctx->stream), "hipEventRecord(fork)");
-        if (!rc) rc = check_hip(hipStreamWaitEvent(ctx->side_stream, ctx->fork_ev, 0), "hipStreamWaitEvent(fork)");
+        for (int j = 0; j < 2 && !rc; ++j)
+            rc = check_hip(hipStreamWaitEvent(ctx->side_stream[j], ctx->fork_ev, 0), "hipStreamWaitEvent(fork)");
         if (rc) return rc;
     }
     if (ctx->num_units > 0) {
-        rc = use_mfma ? check_hip(gsp::launch_decode_mfma(f16, ctx->num_bins, a, ctx->stream), "decode (mfma) launch")
-                      : check_hip(gsp::launch_decode(d.head_dim, f16, ctx->num_bins, a, ctx->stream),
+        rc = use_mfma ? check_hip(gsp::launch_decode_mfma(f16, ctx->num_bins, a, decode_stream), "decode (mfma) launch")
+                      : check_hip(gsp::launch_decode(d.head_dim, f16, ctx->num_bins, a, decode_stream),
                                   "decode (dpp) launch");
+        if (rc && fork) {
+            // Join what was forked, so the side streams hold nothing of this step.
+            for (int j = 0; j < 2; ++j)
+                if (hipEventRecord(ctx->join_ev[j], ctx->side_stream[j]) == hipSuccess)
+                    (void)hipStreamWaitEvent(ctx->stream, ctx->join_ev[j], 0);
+        }
         if (rc) return rc;
     }
-    if (ctx->num_tiles > 0) {
-        gsp::PrefillArgs p;
-        p.k_pool = a.k_pool;
-        p.v_pool = a.v_pool;
-        p.block_stride = a.block_stride;
-        p.layer_offset = a.layer_offset;
-        p.head_stride = a.head_stride;
-        p.tiles = reinterpret_cast<const PrefillTile*>(ctx->d_step + ctx->off_tiles);
-        p.bt_ids = a.bt_ids;
-        p.q = q_dev;
-        p.out = out_dev;
-        p.n_heads = n_heads;
-        p.n_kv = d.heads_kv;
-        p.group = group;
-        p.scale_log2 = a.scale_log2;
+    if (ctx->num_tiles > 0)
         rc = check_hip(gsp::launch_prefill_mfma(d.head_dim, f16, ctx->num_tiles, p, tile_stream), "prefill launch");
-    }
     if (fork) {
-        const int jc = check_hip(hipEventRecord(ctx->join_ev, ctx->side_stream), "hipEventRecord(join)");
-        const int jw = jc ? jc : check_hip(hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0), "hipStreamWaitEvent(join)");
-        if (!rc) rc = jw;
+        for (int j = 0; j < 2; ++j) {
+            const int jc = check_hip(hipEventRecord(ctx->join_ev[j], ctx->side_stream[j]), "hipEventRecord(join)");
+            const int jw =
+                jc ? jc : check_hip(hipStreamWaitEvent(ctx->stream, ctx->join_ev[j], 0), "hipStreamWaitEvent(join)");
+            if (!rc) rc = jw;
+        }
     }
     const int rd = step_done(ctx, capturing);
     return rc ? rc : rd;
