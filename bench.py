@@ -539,15 +539,21 @@ def summarize_trace(path: str, kernel: str, last: int) -> dict:
     with open(path, newline="") as f:
         for r in csv.DictReader(f):
             if kernel in r["Kernel_Name"]:
-                rows.append((int(r["Dispatch_Id"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+                rows.append((int(r["Dispatch_Id"]), int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     rows.sort()
-    durs = [d for _, d in rows]
-    sel = durs[-last:] if last > 0 else durs
+    durs = [e - s for _, s, e in rows]
+    sel = rows[-last:] if last > 0 else rows
     if not sel:
         raise SystemExit(f"no launch of {kernel} in {path}")
-    return {"kernel": kernel, "calls": len(durs), "avg_ns_all": round(statistics.mean(durs), 1),
-            "max_ns_all": max(durs), "last": len(sel), "avg_ns_last": round(statistics.mean(sel), 1),
-            "median_ns_last": statistics.median(sel), "min_ns_last": min(sel), "max_ns_last": max(sel)}
+    sel_d = [e - s for _, s, e in sel]
+    out = {"kernel": kernel, "calls": len(durs), "avg_ns_all": round(statistics.mean(durs), 1),
+           "max_ns_all": max(durs), "last": len(sel), "avg_ns_last": round(statistics.mean(sel_d), 1),
+           "median_ns_last": statistics.median(sel_d), "min_ns_last": min(sel_d), "max_ns_last": max(sel_d)}
+    if len(sel) > 1:
+        # Start-to-start period of the selected launches (back to back in the
+        # timed region): the kernel plus the gap before the next launch.
+        out["avg_period_ns_last"] = round((sel[-1][1] - sel[0][1]) / (len(sel) - 1), 1)
+    return out
 
 
 def summarize_pmc(path: str, kernel: str, last: int) -> dict:
