@@ -278,8 +278,9 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
 
     # Engine-step time t_step: the host pack (validation, scheduling, one
     # pinned staging buffer and one host-to-device copy) plus the attention of
-    # one layer, issued back to back as an engine loop issues them.  The copy
-    # of step i+1 runs on the library's copy stream while step i's kernel runs.
+    # one layer, issued back to back as an engine loop issues them.  Step i+1
+    # is packed on the host while step i's kernel runs; its copy follows that
+    # kernel on the stream.
     # t_step is the median period of the loop once it is in steady state (host
     # hiccups of a millisecond show up in the mean, reported beside it).
     n_step = max(40, steps)

@@ -135,18 +135,19 @@ struct gsp_ctx {
     hipEvent_t join_ev[2] = {nullptr, nullptr};
 
     // Step staging, double-buffered: successive packs alternate between two
-    // slots, each a pinned host buffer and its device mirror.  A slot's upload
-    // runs on copy_stream once the last kernel that read the slot's previous
-    // step has finished (kernel_done), so it overlaps the kernels of the step
-    // before; the kernels of a step wait for its upload (upload_done).
+    // slots, each a pinned host buffer and its device mirror.  A step's upload
+    // is one copy on the context's stream, so stream order puts it after the
+    // kernels that read the slot's previous step and before the kernels of
+    // this one; no event crosses streams.  upload_done (recorded after the
+    // copy) tells the host when the pinned buffer may be written again: the
+    // pack two steps later usually finds it done, since the GPU is at most a
+    // step behind.
     static constexpr int kSlots = 2;
-    hipStream_t copy_stream = nullptr;
     int32_t* staging[kSlots] = {};
     size_t staging_words[kSlots] = {};
     int32_t* d_step_slot[kSlots] = {};
     size_t d_step_words[kSlots] = {};
     hipEvent_t upload_done[kSlots] = {};
-    hipEvent_t kernel_done[kSlots] = {};
     bool upload_pending[kSlots] = {};
     // The host has seen the slot's upload complete (gsp_sync): only then may
     // a graph capture read the slot, since a capture takes no event nodes.
@@ -154,9 +155,6 @@ struct gsp_ctx {
     // A capture read the slot: its next upload first waits for the context's
     // stream on the host, where the graph's replays normally run.
     bool slot_captured[kSlots] = {};
-    // No kernel of the packed step has been enqueued yet: the first one
-    // marks the end of the previous step's kernels and waits for the upload.
-    bool step_fresh = false;
     int slot = 0;               // slot of the packed step
     int32_t* d_step = nullptr;  // d_step_slot[slot]
 
@@ -210,8 +208,11 @@ struct gsp_ctx {
     int64_t cached_bins = 0;
 
     // Host scratch reused across steps.
-    std::vector<DecodeUnit> units;
-    std::vector<DecodeUnit> units_binned;
+    std::vector<DecodeUnit> units;    // in the order they were built
+    std::vector<int32_t> unit_order;  // unit indices, longest first (stable)
+    std::vector<int32_t> unit_place;  // unit indices in their packed order (assign_bins)
+    std::vector<int32_t> len_count;   // counting sort of unit_order
+    std::vector<int32_t> stage_host;  // the step image, built in cached memory, then copied to the pinned slot
     std::vector<int32_t> bin_units;   // [num_bins + 1] offsets of each bin's units after its first
     std::vector<int32_t> unit_bin;
     std::vector<std::pair<int64_t, int32_t>> bin_heap;
@@ -256,16 +257,12 @@ int is_capturing(hipStream_t stream, bool* out) {
     return rc;
 }
 
-// Kernels of the packed step read its device slot: they wait for the slot's
-// upload, and the slot's next upload waits for them (step_done).  A graph
-// capture records no event node: it needs the upload complete on the host
-// already (gsp_sync after gsp_step_pack), and marks the slot so that its next
-// upload first drains the context's stream, where the replays run.
-// Only the first kernel call of a step does so: it records kernel_done of the
-// other slot (everything enqueued before it, i.e. the previous step's
-// kernels) and waits for its own upload; later calls of the step follow it on
-// the same stream.  A pack that finds no call since the previous pack records
-// that marker itself (pack_mark_previous).
+// Kernels of the packed step read its device slot, which its upload wrote
+// earlier on the same stream.  A graph capture needs the upload complete on
+// the host already (gsp_sync after gsp_step_pack): the captured kernels run
+// at replay time, long after the copy that preceded the capture.  It marks
+// the slot so that the slot's next upload first drains the context's stream,
+// where the replays run.
 int step_begin(gsp_ctx* ctx, bool* capturing) {
     int rc = is_capturing(ctx->stream, capturing);
     if (rc) return rc;
@@ -275,14 +272,8 @@ int step_begin(gsp_ctx* ctx, bool* capturing) {
                              "the packed step's upload is not known to be complete: call gsp_sync after "
                              "gsp_step_pack and before capturing");
         ctx->slot_captured[ctx->slot] = true;
-        return GSP_OK;
     }
-    if (!ctx->step_fresh) return GSP_OK;
-    rc = check_hip(hipEventRecord(ctx->kernel_done[ctx->slot ^ 1], ctx->stream), "hipEventRecord(step kernels)");
-    if (!rc && !ctx->upload_synced[ctx->slot])
-        rc = check_hip(hipStreamWaitEvent(ctx->stream, ctx->upload_done[ctx->slot], 0), "hipStreamWaitEvent(upload)");
-    if (!rc) ctx->step_fresh = false;
-    return rc;
+    return GSP_OK;
 }
 
 int step_done(gsp_ctx*, bool) { return GSP_OK; }
@@ -429,13 +420,10 @@ int gsp_init(int device, gsp_ctx** out) {
     ctx->arch = info.arch;
     rc = set_device(ctx);
     if (!rc) rc = check_hip(hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking), "hipStreamCreate");
-    if (!rc) rc = check_hip(hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking), "hipStreamCreate");
     for (int j = 0; j < gsp_ctx::kSlots && !rc; ++j) {
         rc = check_hip(hipEventCreateWithFlags(&ctx->upload_done[j], hipEventDisableTiming), "hipEventCreate");
-        if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->kernel_done[j], hipEventDisableTiming), "hipEventCreate");
         // Recorded once on the idle stream, so the first waits on them pass.
         if (!rc) rc = check_hip(hipEventRecord(ctx->upload_done[j], ctx->own_stream), "hipEventRecord");
-        if (!rc) rc = check_hip(hipEventRecord(ctx->kernel_done[j], ctx->own_stream), "hipEventRecord");
     }
     if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->aux_done, hipEventDisableTiming), "hipEventCreate");
     for (int j = 0; j < 2 && !rc; ++j)
@@ -459,14 +447,11 @@ void gsp_shutdown(gsp_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->copy_stream) (void)hipStreamSynchronize(ctx->copy_stream);
     for (int j = 0; j < gsp_ctx::kSlots; ++j) {
         if (ctx->staging[j]) (void)hipHostFree(ctx->staging[j]);
         if (ctx->d_step_slot[j]) (void)hipFree(ctx->d_step_slot[j]);
         if (ctx->upload_done[j]) (void)hipEventDestroy(ctx->upload_done[j]);
-        if (ctx->kernel_done[j]) (void)hipEventDestroy(ctx->kernel_done[j]);
     }
-    if (ctx->copy_stream) (void)hipStreamDestroy(ctx->copy_stream);
     if (ctx->aux) (void)hipHostFree(ctx->aux);
     if (ctx->d_aux) (void)hipFree(ctx->d_aux);
     if (ctx->d_mm) (void)hipFree(ctx->d_mm);
@@ -508,7 +493,6 @@ int gsp_sync(gsp_ctx* ctx) {
     gsp::clear_error();
     if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
     int rc = set_device(ctx);
-    if (!rc) rc = check_hip(hipStreamSynchronize(ctx->copy_stream), "hipStreamSynchronize(copy)");
     if (!rc) rc = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     if (rc) return rc;
     for (int j = 0; j < gsp_ctx::kSlots; ++j) ctx->upload_synced[j] = true;
@@ -1013,11 +997,13 @@ int gsp_pool_download(gsp_ctx* ctx, gsp_pool* pool, int32_t which, size_t offset
 //    about half of a balanced CU bin.  Pairing needs two units per CU bin.
 //  - Within a bin, split pieces run first and whole pairs last, each group
 //    keeping the longest-first order, so merges finish before the tail.
-// Layout: units[b] is bin b's first unit; the other units follow, bin by
+// Works on unit indices: unit_order (longest first) in, unit_place out.
+// Layout: unit_place[b] is bin b's first unit; the other units follow, bin by
 // bin, with bin b's at [bin_units[b], bin_units[b + 1]).  No bin is empty.
 // Returns the bin count.
 static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max, bool pair) {
-    const size_t n = ctx->units.size();
+    const std::vector<int32_t>& ord = ctx->unit_order;
+    const size_t n = ord.size();
     const int32_t nb = (int32_t)std::min<int64_t>(bins_max, (int64_t)n);
     ctx->bin_units.assign((size_t)nb + 1, 0);
     if (nb == 0) return 0;
@@ -1032,7 +1018,7 @@ static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max, bool pair) {
     auto& count = ctx->bin_cursor;
     count.assign((size_t)nl, 0);
     for (size_t i = 0; i < n; ++i) {
-        const DecodeUnit& u = ctx->units[i];
+        const DecodeUnit& u = ctx->units[(size_t)ord[i]];
         std::pop_heap(heap.begin(), heap.end(), later);
         const int32_t b = heap.back().second;
         ctx->unit_bin[i] = b;
@@ -1047,7 +1033,7 @@ static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max, bool pair) {
         load.assign((size_t)nb, 0);
         for (int pass = 0; pass < 2; ++pass)
             for (size_t i = 0; i < n; ++i) {
-                const DecodeUnit& u = ctx->units[i];
+                const DecodeUnit& u = ctx->units[(size_t)ord[i]];
                 const bool split = (u.split_info >> 16) > 1;
                 if (split != (pass == 0)) continue;
                 const int32_t c = ctx->unit_bin[i];
@@ -1065,23 +1051,22 @@ static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max, bool pair) {
     for (int32_t b = 0; b < nb; ++b) ctx->bin_units[(size_t)b + 1] += ctx->bin_units[(size_t)b] - 1;
     auto& cursor = ctx->bin_cursor;
     cursor.assign((size_t)nb, -1);  // -1: the bin's first unit is still to place
-    ctx->units_binned.resize(n);
+    ctx->unit_place.resize(n);
     for (int pass = 0; pass < 2; ++pass) {
         const bool want_split = pass == 0;
         for (size_t i = 0; i < n; ++i) {
-            const DecodeUnit& u = ctx->units[i];
+            const DecodeUnit& u = ctx->units[(size_t)ord[i]];
             if (((u.split_info >> 16) > 1) != want_split) continue;
             const int32_t b = ctx->unit_bin[i];
             int32_t& cur = cursor[(size_t)b];
             if (cur < 0) {
-                ctx->units_binned[(size_t)b] = u;
+                ctx->unit_place[(size_t)b] = ord[i];
                 cur = ctx->bin_units[(size_t)b];
             } else {
-                ctx->units_binned[(size_t)cur++] = u;
+                ctx->unit_place[(size_t)cur++] = ord[i];
             }
         }
     }
-    std::swap(ctx->units, ctx->units_binned);
     return nb;
 }
 
@@ -1296,9 +1281,21 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
             bt_base += (total_last + bs - 1) / bs;
         }
     }
-    std::stable_sort(ctx->units.begin(), ctx->units.end(), [](const DecodeUnit& x, const DecodeUnit& y) {
-        return (x.page_end - x.page_begin) > (y.page_end - y.page_begin);
-    });
+    // Longest first, ties in build order: a counting sort of unit indices by
+    // page count (the records themselves move once, into the step image).
+    {
+        int32_t max_len = 0;
+        for (const DecodeUnit& u : ctx->units) max_len = std::max(max_len, u.page_end - u.page_begin);
+        auto& cnt = ctx->len_count;
+        cnt.assign((size_t)max_len + 2, 0);
+        for (const DecodeUnit& u : ctx->units) cnt[(size_t)(max_len - (u.page_end - u.page_begin)) + 1] += 1;
+        for (size_t l = 1; l < cnt.size(); ++l) cnt[l] += cnt[l - 1];
+        ctx->unit_order.resize(ctx->units.size());
+        for (size_t i = 0; i < ctx->units.size(); ++i) {
+            const DecodeUnit& u = ctx->units[i];
+            ctx->unit_order[(size_t)cnt[(size_t)(max_len - (u.page_end - u.page_begin))]++] = (int32_t)i;
+        }
+    }
     std::stable_sort(ctx->tiles.begin(), ctx->tiles.end(),
                      [](const PrefillTile& x, const PrefillTile& y) { return x.pages > y.pages; });
     const int32_t n_bins = assign_bins(ctx, bins_max, pair_cus);
@@ -1337,8 +1334,6 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     }
     rc = ensure_pinned(&ctx->staging[slot], &ctx->staging_words[slot], words, ctx->upload_done[slot],
                        &ctx->upload_pending[slot]);
-    if (!rc && words > ctx->d_step_words[slot])  // no upload may still write the old buffer
-        rc = check_hip(hipStreamSynchronize(ctx->copy_stream), "hipStreamSynchronize(copy)");
     if (!rc) rc = ensure_device(ctx, &ctx->d_step_slot[slot], &ctx->d_step_words[slot], words, false);
     // The split workspace for any group up to the decode tile, so that a
     // captured gsp_attention_step of this step never has to grow it.
@@ -1349,7 +1344,11 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, (size_t)total_q * H, true);
     if (rc) return rc;
 
-    int32_t* st = ctx->staging[slot];
+    // The step image is written in cached host memory and copied into the
+    // pinned slot in one pass: element-wise stores straight into the pinned
+    // buffer measured several times slower.
+    ctx->stage_host.resize(words);
+    int32_t* st = ctx->stage_host.data();
     std::memset(st, 0, kHdrWords * sizeof(int32_t));
     int32_t max_id = -1;
     {
@@ -1385,7 +1384,10 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         }
     }
     if (total_q) std::memcpy(st + off_ctx, ctx->q_ctx.data(), (size_t)total_q * sizeof(int32_t));
-    if (n_units) std::memcpy(st + off_units, ctx->units.data(), n_units * sizeof(DecodeUnit));
+    {
+        DecodeUnit* dst = reinterpret_cast<DecodeUnit*>(st + off_units);
+        for (size_t j = 0; j < n_units; ++j) dst[j] = ctx->units[(size_t)ctx->unit_place[j]];
+    }
     if (n_tiles) std::memcpy(st + off_tiles, ctx->tiles.data(), n_tiles * sizeof(PrefillTile));
     std::memcpy(st + off_bins, ctx->bin_units.data(), ((size_t)n_bins + 1) * sizeof(int32_t));
     st[kHdrRows] = B;
@@ -1400,22 +1402,17 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     st[kHdrTiles] = (int32_t)n_tiles;
     st[kHdrBins] = n_bins;
 
-    // One copy for the whole step, on the copy stream, once the kernels that
-    // read this slot's previous step are done.  They are marked by the first
-    // kernel call of the step after them; without such a call (two packs in a
-    // row), everything enqueued so far is marked here.
-    if (ctx->step_fresh)
-        rc = check_hip(hipEventRecord(ctx->kernel_done[slot], ctx->stream), "hipEventRecord(step kernels)");
-    if (!rc) rc = check_hip(hipStreamWaitEvent(ctx->copy_stream, ctx->kernel_done[slot], 0), "hipStreamWaitEvent(copy)");
-    if (!rc)
-        rc = check_hip(hipMemcpyAsync(ctx->d_step_slot[slot], st, words * sizeof(int32_t), hipMemcpyHostToDevice,
-                                      ctx->copy_stream),
-                       "hipMemcpyAsync(step)");
-    if (!rc) rc = check_hip(hipEventRecord(ctx->upload_done[slot], ctx->copy_stream), "hipEventRecord");
+    // One copy for the whole step, on the context's stream (behind the
+    // kernels that read this slot's previous step), then the event that frees
+    // the pinned buffer.
+    std::memcpy(ctx->staging[slot], st, words * sizeof(int32_t));
+    rc = check_hip(hipMemcpyAsync(ctx->d_step_slot[slot], ctx->staging[slot], words * sizeof(int32_t),
+                                  hipMemcpyHostToDevice, ctx->stream),
+                   "hipMemcpyAsync(step)");
+    if (!rc) rc = check_hip(hipEventRecord(ctx->upload_done[slot], ctx->stream), "hipEventRecord");
     if (rc) return rc;
     ctx->upload_pending[slot] = true;
     ctx->upload_synced[slot] = false;
-    ctx->step_fresh = true;
     ctx->slot = slot;
     ctx->d_step = ctx->d_step_slot[slot];
 

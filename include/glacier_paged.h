@@ -339,15 +339,15 @@ int gsp_set_prefill_path(gsp_ctx* ctx, int32_t path);
  * Rows with q_len >= 16 run as prefill tiles when head_dim == v_head_dim is 64
  * or 128 with 16-token pages, else as per-query decode units.  GSP_DECODE_DPP
  * serves head_dim 64 or 128, 16-token pages and groups up to 8 only.  Work is
- * enqueued on the context's stream.  A step with both
- * decode units and prefill tiles runs the tiles on a second stream of the
- * context, forked from and joined back into that stream, so the call is still
- * ordered as a whole on the context's stream.
+ * enqueued on the context's stream.  A step with both decode units and
+ * prefill tiles runs them in one kernel (with GSP_DECODE_DPP: the tiles on
+ * second streams of the context, forked from and joined back into that
+ * stream, so the call is still ordered as a whole on the context's stream).
  *
  * Step uploads: gsp_step_pack alternates between two device slots and copies
- * the step on a copy stream of the context, so the upload of step i+1
- * overlaps the kernels of step i; the kernels of a step wait for its upload,
- * and a slot is rewritten only after the kernels that read it are done.
+ * the step with one copy on the context's stream, behind the kernels that
+ * read the slot's previous step and before the kernels of the step; its
+ * pinned host buffer is rewritten two packs later, once that copy is done.
  * Graph capture: the call can be captured on the context's stream once the
  * packed step's upload is known complete (gsp_sync after gsp_step_pack;
  * otherwise GSP_E_STATE).  The graph holds the step's kernels only and reads
