@@ -147,7 +147,7 @@ def describe(step, layers: int) -> dict:
 
 
 def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: float, layers: int = 4,
-                 decode_path: str = "auto", profile_only: bool = False) -> dict:
+                 decode_path: str = "auto", profile_only: bool = False, prefill_split: str = "records") -> dict:
     import numpy as np
     import torch
 
@@ -159,6 +159,7 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     torch.cuda.synchronize()
     ctx = gsp.Context(0)
     ctx.set_decode_path({"auto": gsp.DECODE_AUTO, "dpp": gsp.DECODE_DPP, "mfma": gsp.DECODE_MFMA}[decode_path])
+    ctx.set_prefill_split({"records": gsp.SPLIT_RECORDS, "in_tile": gsp.SPLIT_IN_TILE}[prefill_split])
     # A dedicated torch stream: the library launches on it and the events below
     # are recorded on it (torch's default stream is the null handle).
     stream = torch.cuda.Stream()
@@ -237,6 +238,8 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
             "fp16_products_per_fp32_product": products,
             "fp32_attention_tflops": round(tfs, 2),
             "mean_launch_ms": round(pre_ms, 5),
+            # fp32 pages: "records" times the split-record kernel and the tiles together.
+            "prefill_split": prefill_split if step.kv_dtype == "f32" else "none",
         }
         if len(rows_d):
             sub_d, qi_d = step.subset(rows_d)
@@ -593,6 +596,8 @@ def main() -> int:
                     help="pool layers; step i attends layer i mod LAYERS (1 re-reads one layer every step)")
     ap.add_argument("--decode-path", default="auto", choices=["auto", "mfma", "dpp"],
                     help="decode kernel (auto = the matrix-core kernel)")
+    ap.add_argument("--prefill-split", default="records", choices=["records", "in_tile"],
+                    help="fp32 prefill tiles: split records written once per step (default) or split in each tile")
     ap.add_argument("--profile-only", action="store_true",
                     help="only the warmup and timed launches (plus each kernel alone for mixed steps)")
     ap.add_argument("--summarize-trace", metavar="CSV", help="summarize a rocprofv3 kernel-trace CSV and exit")
@@ -621,7 +626,7 @@ def main() -> int:
     for name in names:
         res = run_workload(name, args.steps, args.warmup, cpu=not (args.no_cpu or args.profile_only),
                            cpu_budget_s=args.cpu_budget, layers=args.layers, decode_path=args.decode_path,
-                           profile_only=args.profile_only)
+                           profile_only=args.profile_only, prefill_split=args.prefill_split)
         print(json.dumps(res), flush=True)
     if args.copy_calibration > 0:
         import torch

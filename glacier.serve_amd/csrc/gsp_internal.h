@@ -85,7 +85,7 @@ struct PrefillTile {
     int32_t token_count;  // the row's BlockTable.TokenCount
     int32_t pages;        // ceil(min(token_count, pos0 + ntok) / 16): pages the tile reads
     int32_t kvh;          // KV head
-    int32_t reserved;
+    int32_t rec0;         // first split record of the tile's row and KV head (fp32 pages)
 };
 static_assert(sizeof(PrefillTile) == 32, "PrefillTile is packed as 8 int32");
 
@@ -106,9 +106,41 @@ struct PrefillArgs {
     int32_t n_kv;
     int32_t group;         // query heads per KV head (any; grid.y covers them 8, or for groups up to 4, 4 at a time)
     float scale_log2;
+    // fp32 pages only: the step's split records (launch_prefill_split, this
+    // layer), PrefillTile.rec0 being the first record of the tile's row and KV
+    // head; null: each tile splits the pages it reads itself.
+    const unsigned char* records;
 };
 
-// Launches the MFMA prefill kernel for (head_dim, kv dtype).
+// One (row, KV head) of the split records: records rec0 .. rec0 + pairs - 1
+// hold its page pairs, pairs = ceil(ceil(ctx_last / 16) / 2).
+struct PrefillSplitItem {
+    int32_t bt_base;   // offset of the row's table inside the packed ids
+    int32_t ctx_last;  // tokens of the row its tiles read: min(TokenCount, pos + q_len)
+    int32_t kvh;
+    int32_t rec0;
+};
+static_assert(sizeof(PrefillSplitItem) == 16, "PrefillSplitItem is packed as 4 int32");
+
+struct PrefillSplitArgs {
+    const void* k_pool;
+    const void* v_pool;
+    int64_t block_stride;
+    int64_t layer_offset;
+    int64_t head_stride;
+    const PrefillSplitItem* items;
+    const int32_t* bt_ids;
+    unsigned char* records;
+};
+
+// Bytes of one split record (one page pair, one KV head) for head_dim 64 or 128 (else 0).
+int prefill_record_bytes(int head_dim);
+// Writes the split records of fp32 pages: grid (max_pairs, num_items).
+hipError_t launch_prefill_split(int head_dim, int num_items, int max_pairs, const PrefillSplitArgs& a,
+                                hipStream_t stream);
+
+// Launches the MFMA prefill kernel for (head_dim, kv dtype); with a.records
+// (fp32 pages) the tiles read the split records.
 hipError_t launch_prefill_mfma(int head_dim, int kv_f16, int num_tiles, const PrefillArgs& a, hipStream_t stream);
 
 // Launches a step with both decode bins and prefill tiles as one kernel (the

@@ -47,11 +47,24 @@
 //   result: lane holds O[token 4g + r][col].
 // The causal limit is per row (token); padding rows past the tile's tokens
 // keep finite scores and are never written.  Page pairs are staged through two
-// LDS buffers (register-prefetched a page at a time) with one barrier per pair;
-// V goes in transposed, so each PV B operand is one 16-byte LDS read, and the
-// K and V operands of the next matrix step are read while the current one runs.
+// LDS buffers with one barrier per pair; V goes in transposed, so each PV B
+// operand is one 16-byte LDS read, and the K and V operands of the next
+// matrix step are read while the current one runs.
+//
+// Two forms for fp32 pages.  Every tile of a row reads the same page pairs, so
+// by default (split records) prefill_split_kernel first writes each pair of
+// each tiled row and KV head once per step and layer as the finished image of
+// an LDS buffer (hi/lo K rows with one K exponent for the pair, transposed
+// hi/lo V with per-key exponents, the scales), and the tiles copy records into
+// LDS with direct-to-LDS loads: no staging registers, no split arithmetic in
+// the tile, and the score products of pair k overlap the softmax of pair
+// k - 1 (prefill_tile_body_rec).  Without records (the allocation-free entry
+// point, fp16 pages) each tile stages and splits the pages it reads through
+// registers, a page at a time (prefill_tile_body).
 // The roofline of these rows is the matrix peak.
 #include "gsp_decode_body.h"
+
+#include <type_traits>
 
 namespace gsp {
 namespace {
@@ -146,16 +159,47 @@ __device__ __forceinline__ constexpr int vt_row(int col) { return col * kVtStrid
 template <int D, typename KT>
 struct PfLds;
 
-// Each buffer's arrays sit together, so every offset within a buffer fits the
-// 16-bit immediate of an LDS instruction.
+// A buffer of fp32 pages is two halves: the K half (the hi and lo rows) and
+// the V half (the transposed V pairs and the scales of both K and V).  Each
+// half's arrays sit together, so every offset within a half fits the 16-bit
+// immediate of an LDS instruction.  Both halves are 128 (D + 8) bytes, whole
+// kilobytes (the span of one wave's 16-byte-per-lane direct-to-LDS load), and
+// a buffer is also the layout of a split record (one page pair of one row and
+// KV head, written once per step by prefill_split_kernel), so a tile copies a
+// record, or either half of one, into LDS with no registers and no arithmetic.
+constexpr int kRecordChunk = 64 * 16;
 template <int D>
-struct alignas(16) PfLdsBuf32 {
+constexpr int kHalfBytes = 2 * kPairKeys * (D + 8) * 2;
+template <int D>
+constexpr int kRecordBytes = 2 * kHalfBytes<D>;
+
+template <int D>
+struct alignas(16) PfKHalf {
     _Float16 kh[kPairKeys * (D + 8)], kl[kPairKeys * (D + 8)];
+};
+
+template <int D>
+struct alignas(16) PfVHalfBody {
     _Float16 vt[kVtLen<D, true>];
     float ks[kPairKeys];  // 2^e of each key's K pair
     int ev[kPairKeys];    // exponent of each key's V pair
     int evw[2 * kDecodeWaves];          // largest V exponent of each wave's four keys, per page
 };
+
+template <int D>
+struct alignas(16) PfVHalf : PfVHalfBody<D> {
+    unsigned char pad[kHalfBytes<D> - sizeof(PfVHalfBody<D>)];
+};
+
+template <int D>
+struct alignas(16) PfLdsBuf32 {
+    PfKHalf<D> k;
+    PfVHalf<D> v;
+};
+static_assert(sizeof(PfKHalf<128>) == kHalfBytes<128> && sizeof(PfVHalf<128>) == kHalfBytes<128> &&
+                  sizeof(PfKHalf<64>) == kHalfBytes<64> && sizeof(PfVHalf<64>) == kHalfBytes<64>,
+              "each half is whole kilobytes");
+static_assert(kHalfBytes<128> % kRecordChunk == 0 && kHalfBytes<64> % kRecordChunk == 0, "whole chunks");
 
 template <int D>
 struct alignas(16) PfLds<D, float> {
@@ -259,28 +303,33 @@ __device__ __forceinline__ int swap32_max_i32(int x) {
     return max((int)r[0], (int)r[1]);
 }
 
-template <int D>
-__device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D, float>& sh, int buf, int slot) {
+// K rows take one exponent per key (PAIR_K false) or ek_pair for the whole
+// page pair (split records: the scores then need one factor per tile).
+template <int D, bool PAIR_K = false>
+__device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLdsBuf32<D>& b, int slot, int ek_pair = 0) {
     constexpr int kRow = PfLds<D, float>::kRow;
     constexpr int W = kVW<D>;
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     typedef float f2 __attribute__((ext_vector_type(2)));
     const int key = threadIdx.x >> 4;
     const int part = threadIdx.x & 15;
-    uint32_t mk = 0;
+    int ek = ek_pair;
+    if constexpr (!PAIR_K) {
+        uint32_t mk = 0;
 #pragma unroll
-    for (int i = 0; i < kStageChunks<D>; ++i) mk = max(mk, max_abs_bits(sr.k[i]));
-    const int ek = pair_exponent_bits(row16_max_u32(mk));
+        for (int i = 0; i < kStageChunks<D>; ++i) mk = max(mk, max_abs_bits(sr.k[i]));
+        ek = pair_exponent_bits(row16_max_u32(mk));
+    }
     const float dk = ldexpf(1.0f, -ek);
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
         const int at = (slot * kBlockSize + key) * kRow + 64 * i + 4 * part;
         h4 hi, lo;
         split_pair(sr.k[i] * dk, hi, lo);
-        *reinterpret_cast<h4*>(&sh.b[buf].kh[at]) = hi;
-        *reinterpret_cast<h4*>(&sh.b[buf].kl[at]) = lo;
+        *reinterpret_cast<h4*>(&b.k.kh[at]) = hi;
+        *reinterpret_cast<h4*>(&b.k.kl[at]) = lo;
     }
-    if (part == 0) sh.b[buf].ks[slot * kBlockSize + key] = ldexpf(1.0f, ek);
+    if (part == 0) b.v.ks[slot * kBlockSize + key] = ldexpf(1.0f, ek);
 
     // V, transposed: each of the lane's columns takes its key pair as one
     // word of hi halves and one of lo halves.
@@ -299,21 +348,21 @@ __device__ __forceinline__ void stage_store(const PfStage<D, float>& sr, PfLds<D
         const int at = vt_row<true>(W * vpart + c) + pos;
         h2 hi, lo;
         split_pair(f2{sr.v[0][c] * dv[0], sr.v[1][c] * dv[1]}, hi, lo);
-        *reinterpret_cast<h2*>(&sh.b[buf].vt[at]) = hi;
-        *reinterpret_cast<h2*>(&sh.b[buf].vt[at + kPairKeys]) = lo;
+        *reinterpret_cast<h2*>(&b.v.vt[at]) = hi;
+        *reinterpret_cast<h2*>(&b.v.vt[at + kPairKeys]) = lo;
     }
     if (vpart == 0) {
-        sh.b[buf].ev[slot * kBlockSize + 2 * kg] = ev[0];
-        sh.b[buf].ev[slot * kBlockSize + 2 * kg + 1] = ev[1];
+        b.v.ev[slot * kBlockSize + 2 * kg] = ev[0];
+        b.v.ev[slot * kBlockSize + 2 * kg + 1] = ev[1];
     }
     // The page's largest V exponent: this wave's four keys (two per half-wave),
     // then one slot per wave.
     const int evw = swap32_max_i32(max(ev[0], ev[1]));
-    if ((threadIdx.x & 63) == 0) sh.b[buf].evw[slot * kDecodeWaves + (threadIdx.x >> 6)] = evw;
+    if ((threadIdx.x & 63) == 0) b.v.evw[slot * kDecodeWaves + (threadIdx.x >> 6)] = evw;
 }
 
 template <int D>
-__device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLds<D, _Float16>& sh, int buf, int slot) {
+__device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLdsBuf16<D>& b, int slot) {
     constexpr int kRow = PfLds<D, _Float16>::kRow;
     constexpr int W = kVW<D>;
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -322,19 +371,107 @@ __device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLd
 #pragma unroll
     for (int i = 0; i < kStageChunks<D>; ++i) {
         const int at = (slot * kBlockSize + key) * kRow + 64 * i + 4 * part;
-        *reinterpret_cast<h4*>(&sh.b[buf].k[at]) = sr.k[i];
+        *reinterpret_cast<h4*>(&b.k[at]) = sr.k[i];
     }
     const int kg = threadIdx.x >> 5;
     const int vpart = threadIdx.x & 31;
     const int pos = 8 * (kg >> 1) + 4 * slot + 2 * (kg & 1);
 #pragma unroll
     for (int c = 0; c < W; ++c)
-        *reinterpret_cast<h2*>(&sh.b[buf].v[vt_row<false>(W * vpart + c) + pos]) = h2{sr.v[0][c], sr.v[1][c]};
+        *reinterpret_cast<h2*>(&b.v[vt_row<false>(W * vpart + c) + pos]) = h2{sr.v[0][c], sr.v[1][c]};
+}
+
+// Split records of fp32 pages.  Every tile of a row walks the row's pages from
+// page 0 in the same pairs, so the hi/lo split of pair i (for one KV head) is
+// the same for all of them: prefill_split_kernel writes it once per step as
+// the image of one LDS buffer (K half, then V half), and a tile copies the
+// halves it needs into LDS with direct-to-LDS loads.  The record of a row's
+// pair covers the row's tokens up to min(TokenCount, pos + q_len); keys of it
+// past a tile's own limit are masked like any other.
+
+// 16 bytes per lane from r at voffset into LDS at lds + 16 * lane (lds uniform over the wave).
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, int voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+}
+
+// As lds_load16, from r at soffset + voffset (soffset uniform).
+__device__ __forceinline__ void lds_load16s(__amdgpu_buffer_rsrc_t r, void* lds, int voffset, int soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0,
+                                             0);
+}
+
+// One half (kHalfBytes) of the record r (a resource over that one record) from
+// byte `off` into `dst`: lane l of wave w moves bytes 1024 (4 c + w) + 16 l of
+// the half for c = 0, 1, ...; each wave's kilobyte lands contiguously at the
+// same offset of dst.  The lane's part of the offset is the same for every
+// chunk; the rest is uniform and goes in the scalar offset.
+template <int D>
+__device__ __forceinline__ void half_load(void* dst, __amdgpu_buffer_rsrc_t r, int off) {
+    constexpr int kChunks = kHalfBytes<D> / kRecordChunk;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane_off = 16 * (threadIdx.x & 63);
+    unsigned char* base = static_cast<unsigned char*>(dst);
+#pragma unroll
+    for (int c0 = 0; c0 < kChunks; c0 += kDecodeWaves) {
+        const int c = c0 + w;
+        if (c0 + kDecodeWaves <= kChunks || c < kChunks)  // only the last round may be partial
+            lds_load16s(r, base + kRecordChunk * c, lane_off, off + kRecordChunk * c);
+    }
+}
+
+// The direct-to-LDS loads of this wave have landed (the barrier after it
+// publishes them to the other waves).
+__device__ __forceinline__ void record_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// One workgroup per (page pair, row and KV head): stages the pair exactly as
+// a tile would (stage_load, stage_store) and writes the buffer out as record
+// item.rec0 + pair.  Pairs past the row's pages exit at once.
+template <int D>
+__global__ __launch_bounds__(kDecodeThreads) void prefill_split_kernel(PrefillSplitArgs a) {
+    __shared__ PfLdsBuf32<D> sh;
+    const PrefillSplitItem it = a.items[blockIdx.y];
+    const int pages = (it.ctx_last + kBlockSize - 1) / kBlockSize;
+    const int pair = blockIdx.x;
+    if (2 * pair >= pages) return;
+    const float* kbase = static_cast<const float*>(a.k_pool) + a.layer_offset + (int64_t)it.kvh * a.head_stride;
+    const float* vbase = static_cast<const float*>(a.v_pool) + a.layer_offset + (int64_t)it.kvh * a.head_stride;
+    const int32_t* bt = a.bt_ids + it.bt_base;
+    PfStage<D, float> sr[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int pg = 2 * pair + h;
+        const bool have = pg < pages;
+        const int64_t blk = have ? bt[pg] : 0;
+        stage_load<D>(sr[h], kbase + blk * a.block_stride, vbase + blk * a.block_stride,
+                      have ? min(kBlockSize, it.ctx_last - pg * kBlockSize) : 0);
+    }
+    // One K exponent for the pair: its largest |K| over both pages (wave
+    // maxima, then the four waves through LDS).
+    __shared__ uint32_t wave_max[kDecodeWaves];
+    uint32_t mk = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < kStageChunks<D>; ++i) mk = max(mk, max_abs_bits(sr[h].k[i]));
+    mk = (uint32_t)swap32_max_i32((int)swap16_max_u32(row16_max_u32(mk)));  // bits of |x| < 2^31
+    if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = mk;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) mk = max(mk, wave_max[w]);
+    const int ek = pair_exponent_bits(mk);
+    stage_store<D, true>(sr[0], sh, 0, ek);
+    stage_store<D, true>(sr[1], sh, 1, ek);
+    __syncthreads();
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const u4* src = reinterpret_cast<const u4*>(&sh);
+    u4* dst = reinterpret_cast<u4*>(a.records + ((int64_t)it.rec0 + pair) * kRecordBytes<D>);
+    for (int i = threadIdx.x; i < kRecordBytes<D> / 16; i += kDecodeThreads) dst[i] = src[i];
 }
 
 // Q operands of one tile for the K = 32 matrix cores, q[j] = Q[token n][32j + 8g
-// .. +7] as a scaled fp16 pair, and the lane's score factor 2^e_token * scale
-// (log2 units).
+// .. +7] as a scaled fp16 pair, and the lane's score factor 2^e_token * |scale|
+// (log2 units).  Q carries the scale's sign (an exact negation), so the factor
+// is positive and the largest score times it is the largest scaled score.
 template <int D>
 struct TileQ {
     h8 hi[D / 32];
@@ -355,7 +492,7 @@ __device__ __forceinline__ void load_tile_q(TileQ<D>& tq, const float* qrow, boo
     mx = fmaxf(mx, __shfl_xor(mx, 16));  // token n's elements live in lanes n + 16g
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const int e = pair_exponent(mx);
-    const float down = ldexpf(1.0f, -e);
+    const float down = scale < 0.f ? -ldexpf(1.0f, -e) : ldexpf(1.0f, -e);
 #pragma unroll
     for (int j = 0; j < D / 32; ++j) {
         h4 h0, l0, h1, l1;
@@ -364,7 +501,7 @@ __device__ __forceinline__ void load_tile_q(TileQ<D>& tq, const float* qrow, boo
         tq.hi[j] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
         tq.lo[j] = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
     }
-    tq.sc = ldexpf(scale, e);
+    tq.sc = ldexpf(fabsf(scale), e);
 }
 
 // Per-tile softmax state: O (in the wave's units, see eo below), the max m (log2 units) that
@@ -448,6 +585,8 @@ __device__ __forceinline__ void pair_softmax(TileState<D>& st, f4& s0, f4& s1, b
 // 4 heads, else 1.  Every tile of a wave is computed on every page, so the
 // hot loop has no branches; a tile past the group (zero Q) is simply not
 // stored.  It costs no time: the page barrier waits for the busiest wave.
+// This form splits the fp32 pages it reads itself (fp16 pages need no split);
+// prefill_tile_body_rec below reads the step's split records instead.
 template <int D, typename KT, int TILES>
 __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D, KT>& sh, int bx, int by) {
     constexpr int kPrefillTiles = TILES;
@@ -495,10 +634,11 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
         stage_load<D>(sr, kbase + blk * a.block_stride, vbase + blk * a.block_stride,
                       have ? min(kBlockSize, ctx_last - pg * kBlockSize) : 0);
     };
+    const int pairs = (t.pages + 1) >> 1;
     load_regs(0);
-    stage_store<D>(sr, sh, 0, 0);
+    stage_store<D>(sr, sh.b[0], 0);
     load_regs(1);
-    stage_store<D>(sr, sh, 0, 1);
+    stage_store<D>(sr, sh.b[0], 1);
     __syncthreads();
 
     // Pages go in pairs (32 keys, one v_mfma_f32_16x16x32_f16 step of P.V).
@@ -507,7 +647,6 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
     // O is kept in units of 2^(eo - 12), eo the largest V exponent so far; it is
     // the same for every tile of the wave, which all see the same pages.
     int eo = -1000;  // below any page's V exponent: the first page sets it
-    const int pairs = (t.pages + 1) >> 1;
     for (int i = 0; i < pairs; ++i) {
         const int buf = i & 1;
         const bool more = i + 1 < pairs;
@@ -522,14 +661,14 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
         if constexpr (kSplitKV) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                ks0[r] = sh.b[buf].ks[4 * g + r];
-                ks1[r] = sh.b[buf].ks[kBlockSize + 4 * g + r];
-                evk[r] = sh.b[buf].ev[4 * g + r];
-                evk[4 + r] = sh.b[buf].ev[kBlockSize + 4 * g + r];
+                ks0[r] = sh.b[buf].v.ks[4 * g + r];
+                ks1[r] = sh.b[buf].v.ks[kBlockSize + 4 * g + r];
+                evk[r] = sh.b[buf].v.ev[4 * g + r];
+                evk[4 + r] = sh.b[buf].v.ev[kBlockSize + 4 * g + r];
             }
-            evmax = sh.b[buf].evw[0];
+            evmax = sh.b[buf].v.evw[0];
 #pragma unroll
-            for (int w = 1; w < 2 * kDecodeWaves; ++w) evmax = max(evmax, sh.b[buf].evw[w]);
+            for (int w = 1; w < 2 * kDecodeWaves; ++w) evmax = max(evmax, sh.b[buf].v.evw[w]);
         }
         // P' = P * pv[key]: 2^(e_v(key) - eo + 12) for fp32 pages (a pair with larger
         // V exponents raises eo first, and O takes the factor eo_down), 2^12 for
@@ -574,8 +713,8 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
         auto read_k = [&](int t, h8& kh, h8& kl) {
             const int at = kq + (t & 1) * kBlockSize * kRow + 32 * (t >> 1);
             if constexpr (kSplitKV) {
-                kh = *reinterpret_cast<const h8*>(&sh.b[buf].kh[at]);
-                kl = *reinterpret_cast<const h8*>(&sh.b[buf].kl[at]);
+                kh = *reinterpret_cast<const h8*>(&sh.b[buf].k.kh[at]);
+                kl = *reinterpret_cast<const h8*>(&sh.b[buf].k.kl[at]);
             } else {
                 kh = *reinterpret_cast<const h8*>(&sh.b[buf].k[at]);
             }
@@ -638,7 +777,7 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
         // The first page of the next pair goes to the other buffer (free since
         // the last barrier), and its second page starts loading.
         if (more) {
-            stage_store<D>(sr, sh, buf ^ 1, 0);
+            stage_store<D>(sr, sh.b[buf ^ 1], 0);
             load_regs(2 * i + 3);
         }
 
@@ -649,8 +788,8 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
         auto read_v = [&](int b, h8& bh, h8& bl) {
             const int at = vq + vt_row<kSplitKV>(64 * (b >> 2)) + kVtStride<kSplitKV> * (b & 3);
             if constexpr (kSplitKV) {
-                bh = *reinterpret_cast<const h8*>(&sh.b[buf].vt[at]);
-                bl = *reinterpret_cast<const h8*>(&sh.b[buf].vt[at + kPairKeys]);
+                bh = *reinterpret_cast<const h8*>(&sh.b[buf].v.vt[at]);
+                bl = *reinterpret_cast<const h8*>(&sh.b[buf].v.vt[at + kPairKeys]);
             } else {
                 bh = *reinterpret_cast<const h8*>(&sh.b[buf].v[at]);
             }
@@ -674,7 +813,7 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
                     st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bl, st[s].o[b], 0, 0, 0);
             }
         }
-        if (more) stage_store<D>(sr, sh, buf ^ 1, 1);
+        if (more) stage_store<D>(sr, sh.b[buf ^ 1], 1);
         __syncthreads();
     }
 
@@ -707,10 +846,339 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
     }
 }
 
-template <int D, typename KT, int TILES>
+// Records form, software-pipelined.  Iteration k runs the score products of
+// pair k while the same wave's vector ALUs run the softmax of pair k - 1 (two
+// independent instruction streams, interleaved below so that the vector work
+// issues while the matrix cores run), then the P.V products of pair k - 1.
+// K and V halves have their own double buffers: iteration k reads K(k) and
+// V(k - 1) and loads K(k + 1) and V(k) behind them, so LDS holds four halves,
+// the two buffers of the form above.  The arithmetic is that of
+// prefill_tile_body; the softmax is written without branches, the rare O
+// rescale being the one branch, between the two groups of products.
+template <int D>
+struct alignas(16) PfLdsPipe {
+    PfKHalf<D> k[2];
+    PfVHalf<D> v[2];
+};
+
+// Largest of eight floats and of a row's four lane groups, without the
+// quieting that fmaxf adds to loaded values (scores are never NaN here).
+__device__ __forceinline__ float max8(const f4& a, const f4& b) {
+    float m;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(m) : "v"(a[0]), "v"(a[1]), "v"(a[2]));
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(m) : "v"(m), "v"(a[3]), "v"(b[0]));
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(m) : "v"(m), "v"(b[1]), "v"(b[2]));
+    asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(m), "v"(b[3]));
+    return m;
+}
+
+__device__ __forceinline__ float cross_row_max_raw(float x) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    asm("v_max_f32 %0, %1, %2" : "=v"(x) : "v"(__uint_as_float(r16[0])), "v"(__uint_as_float(r16[1])));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    asm("v_max_f32 %0, %1, %2" : "=v"(x) : "v"(__uint_as_float(r32[0])), "v"(__uint_as_float(r32[1])));
+    return x;
+}
+
+// pair_softmax of raw scores s (their log2-unit value is t = s * c, c > 0:
+// the tile's Q carries the scale's sign), without branches or lane exchanges
+// beyond the row max: m moves for every lane when some row of the wave grew
+// by more than kLazyLog2 (`grew`); alpha is token n's factor (1 where m did
+// not move), which the O rows take only when something grew.  P = 2^(t - m)
+// with t rounded first: m is a rounded t, so the largest score gives exactly
+// 2^0 however large the scores are (a fused s * c - m would keep up to half an
+// ulp of t, which for scores near 2^40 overflows exp2).
+template <bool MASK>
+__device__ __forceinline__ void pair_softmax_rec(float& m, float& l, f4& s0, f4& s1, float c, int key0, int row_ctx,
+                                                 float& alpha, bool& grew) {
+    if constexpr (MASK) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s0[r] = key0 + r >= row_ctx ? -INFINITY : s0[r];
+            s1[r] = key0 + kBlockSize + r >= row_ctx ? -INFINITY : s1[r];
+        }
+    }
+    s0 *= c;
+    s1 *= c;
+    const float mp = cross_row_max_raw(max8(s0, s1));
+    grew = __any(mp > m + kLazyLog2);  // true on the first pair (m = -inf)
+    const float mn = grew ? fmaxf(m, mp) : m;  // finite: the first pair holds key 0 for every row
+    alpha = fast_exp2(m - mn);  // 1 where m stays, 0 on the first pair
+    m = mn;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        s0[r] = fast_exp2(s0[r] - mn);
+        s1[r] = fast_exp2(s1[r] - mn);
+    }
+    l = l * alpha + (((s0[0] + s0[1]) + (s0[2] + s0[3])) + ((s1[0] + s1[1]) + (s1[2] + s1[3])));
+}
+
+template <int D, int TILES>
+__device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLdsPipe<D>& sh, int bx, int by) {
+    constexpr int kRow = D + 8;
+    constexpr int kSteps = D / 16;  // score steps per pair (32 head dims of one page each), = output blocks
+    const PrefillTile t = a.tiles[bx];
+    const int hc = by * kDecodeWaves * TILES;
+    const int G = min(kDecodeWaves * TILES, a.group - hc);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int h0 = t.kvh * a.group + hc;
+    const bool row_live = n < t.ntok;
+    const int row_ctx = row_live ? min(t.token_count, t.pos0 + n + 1) : 0x7fffffff;
+
+    // Pair i of the tile is record t.rec0 + i.
+    const int pairs = (t.pages + 1) >> 1;
+    auto record = [&](int i) {
+        return prefill_rsrc(a.records + ((int64_t)t.rec0 + i) * kRecordBytes<D>, kRecordBytes<D>);
+    };
+    auto load_k = [&](int i) { half_load<D>(&sh.k[i & 1], record(i), 0); };
+    auto load_v = [&](int i) { half_load<D>(&sh.v[i & 1], record(i), kHalfBytes<D>); };
+    load_k(0);
+
+    TileQ<D> q[TILES];
+    TileState<D> st[TILES];
+#pragma unroll
+    for (int s = 0; s < TILES; ++s) {
+        const int T = wave + 4 * s;
+        const float* qrow = a.q + ((int64_t)(t.qi0 + (row_live ? n : 0)) * a.n_heads + h0 + (T < G ? T : 0)) * D;
+        load_tile_q<D>(q[s], qrow, T < G && row_live, g, a.scale_log2);
+#pragma unroll
+        for (int j = 0; j < kSteps; ++j) st[s].o[j] = f4{0.f, 0.f, 0.f, 0.f};
+        st[s].m = -INFINITY;
+        st[s].l = 0.f;
+    }
+    const int kq = n * kRow + 8 * g;              // the lane's K word in a K half (halves)
+    const int vq = vt_row<true>(4 * n) + 8 * g;   // its V word in a V half
+
+    // S^T = K . Q^T of pair i for every tile: step u takes page u & 1's head
+    // dims 32 (u >> 1) .. + 31; the tiles' chains alternate within a step.
+    auto scores = [&](int i, f4 (&sc)[2][TILES]) {
+        const _Float16* kh = sh.k[i & 1].kh;
+        const _Float16* kl = sh.k[i & 1].kl;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int s = 0; s < TILES; ++s) sc[h][s] = f4{0.f, 0.f, 0.f, 0.f};
+        auto read_k = [&](int u, h8& khv, h8& klv) {
+            const int at = kq + (u & 1) * kBlockSize * kRow + 32 * (u >> 1);
+            khv = *reinterpret_cast<const h8*>(&kh[at]);
+            klv = *reinterpret_cast<const h8*>(&kl[at]);
+        };
+        h8 nkh, nkl;
+        read_k(0, nkh, nkl);
+#pragma unroll
+        for (int u = 0; u < kSteps; ++u) {
+            const h8 khv = nkh, klv = nkl;
+            if (u + 1 < kSteps) read_k(u + 1, nkh, nkl);
+            __builtin_amdgcn_sched_barrier(0);  // one step's reads ahead, no more
+            const int j = u >> 1, h = u & 1;
+#pragma unroll
+            for (int s = 0; s < TILES; ++s)
+                sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khv, q[s].hi[j], sc[h][s], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < TILES; ++s)
+                sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khv, q[s].lo[j], sc[h][s], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < TILES; ++s)
+                sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(klv, q[s].hi[j], sc[h][s], 0, 0, 0);
+        }
+    };
+
+    // The scales of pair i, from its V half: the pair's one K factor (records
+    // carry one K exponent per pair) and the V exponents of the lane's eight keys.
+    struct PairScales {
+        float ks;
+        int evk[8];
+        int evw[2 * kDecodeWaves];
+    };
+    auto read_scales = [&](int i, PairScales& ps) {
+        const PfVHalfBody<D>& vb = sh.v[i & 1];
+        ps.ks = vb.ks[0];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            ps.evk[r] = vb.ev[4 * g + r];
+            ps.evk[4 + r] = vb.ev[kBlockSize + 4 * g + r];
+        }
+#pragma unroll
+        for (int w = 0; w < 2 * kDecodeWaves; ++w) ps.evw[w] = vb.evw[w];
+    };
+
+    // Softmax of pair i (its scores in sc) for every tile, into P' as fp16
+    // pairs; need[s]: tile s's O rows must take alpha[s] (token n's factor) and
+    // eo_down before P'.V is added.
+    int eo = -1000;  // O is kept in units of 2^(eo - 12), eo the largest V exponent so far
+    float eo_down = 1.f;
+    auto softmax = [&](auto masked, int i, f4 (&sc)[2][TILES], const PairScales& ps, h8 (&ph)[TILES],
+                       h8 (&pl)[TILES], float (&alpha)[TILES], bool (&need)[TILES]) {
+        const float ks = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ps.ks)));  // one per pair
+        const int* evk = ps.evk;
+        int evmax = ps.evw[0];
+#pragma unroll
+        for (int w = 1; w < 2 * kDecodeWaves; ++w) evmax = max(evmax, ps.evw[w]);
+        const bool eo_up = evmax > eo;
+        eo_down = ldexpf(1.0f, min(0, eo - evmax));  // 0 on the first pair
+        eo = max(eo, evmax);
+        f4 pv0, pv1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pv0[r] = ldexpf(1.0f, evk[r] - eo + kPScaleLog2);
+            pv1[r] = ldexpf(1.0f, evk[4 + r] - eo + kPScaleLog2);
+        }
+        const int key0 = i * kPairKeys + 4 * g;
+#pragma unroll
+        for (int s = 0; s < TILES; ++s) {
+            f4 p0 = sc[0][s];
+            f4 p1 = sc[1][s];
+            bool grew;
+            pair_softmax_rec<decltype(masked)::value>(st[s].m, st[s].l, p0, p1, q[s].sc * ks, key0, row_ctx, alpha[s],
+                                                      grew);
+            need[s] = grew || eo_up;
+            p0 *= pv0;
+            p1 *= pv1;
+            h4 hi0, lo0, hi1, lo1;
+            split_pair(p0, hi0, lo0);
+            split_pair(p1, hi1, lo1);
+            ph[s] = __builtin_shufflevector(hi0, hi1, 0, 1, 2, 3, 4, 5, 6, 7);
+            pl[s] = __builtin_shufflevector(lo0, lo1, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
+
+    // O += P'.V over pair i: block b takes B = V[keys][64 (b >> 2) + 4 n + (b & 3)].
+    auto values = [&](int i, const h8 (&ph)[TILES], const h8 (&pl)[TILES]) {
+        const _Float16* vt = sh.v[i & 1].vt;
+        auto read_v = [&](int b, h8& bh, h8& bl) {
+            const int at = vq + vt_row<true>(64 * (b >> 2)) + kVtStride<true> * (b & 3);
+            bh = *reinterpret_cast<const h8*>(&vt[at]);
+            bl = *reinterpret_cast<const h8*>(&vt[at + kPairKeys]);
+        };
+        h8 nbh, nbl;
+        read_v(0, nbh, nbl);
+#pragma unroll
+        for (int b = 0; b < kSteps; ++b) {
+            const h8 bh = nbh, bl = nbl;
+            if (b + 1 < kSteps) read_v(b + 1, nbh, nbl);
+            __builtin_amdgcn_sched_barrier(0);  // one block's reads ahead, no more
+#pragma unroll
+            for (int s = 0; s < TILES; ++s)
+                st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bh, st[s].o[b], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < TILES; ++s)
+                st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s], bh, st[s].o[b], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < TILES; ++s)
+                st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bl, st[s].o[b], 0, 0, 0);
+        }
+    };
+
+    // O rows are tokens 4g + r: their factors come from the lanes of those tokens.
+    auto rescale = [&](const float (&alpha)[TILES], const bool (&need)[TILES]) {
+#pragma unroll
+        for (int s = 0; s < TILES; ++s) {
+            if (need[s]) {
+                f4 rows;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) rows[r] = __shfl(alpha[s], 4 * g + r) * eo_down;
+#pragma unroll
+                for (int b = 0; b < kSteps; ++b) st[s].o[b] *= rows;
+            }
+        }
+    };
+
+    record_wait();
+    __syncthreads();
+    if (pairs > 1) load_k(1);
+    load_v(0);
+    f4 sa[2][TILES], sb[2][TILES];  // scores of the pair before the current one, and of the current one
+    scores(0, sa);
+    record_wait();
+    __syncthreads();
+
+    // Iteration k: scores of pair k into sout while the softmax of pair k - 1
+    // (scores in sin) runs, then P'.V of pair k - 1.  Pair i needs the causal
+    // mask when some row of the tile may stop inside it.
+    const int first_diag = min(pairs, min(t.pos0 + 1, t.token_count) / kPairKeys);
+    auto iteration = [&](auto masked, int k, f4 (&sin)[2][TILES], f4 (&sout)[2][TILES]) {
+        if (k + 1 < pairs) load_k(k + 1);
+        load_v(k);
+        h8 ph[TILES], pl[TILES];
+        float alpha[TILES];
+        bool need[TILES];
+        PairScales ps;
+        read_scales(k - 1, ps);
+        scores(k, sout);
+        softmax(masked, k - 1, sin, ps, ph, pl, alpha, need);
+        rescale(alpha, need);
+        values(k - 1, ph, pl);
+        record_wait();
+        __syncthreads();
+    };
+    int k = 1;
+    for (const int k_plain = min(pairs, first_diag + 1); k < k_plain; ++k) {
+        iteration(std::false_type{}, k, sa, sb);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int s = 0; s < TILES; ++s) sa[h][s] = sb[h][s];
+    }
+    for (; k < pairs; ++k) {
+        iteration(std::true_type{}, k, sa, sb);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int s = 0; s < TILES; ++s) sa[h][s] = sb[h][s];
+    }
+    {
+        h8 ph[TILES], pl[TILES];
+        float alpha[TILES];
+        bool need[TILES];
+        PairScales ps;
+        read_scales(pairs - 1, ps);
+        softmax(std::true_type{}, pairs - 1, sa, ps, ph, pl, alpha, need);
+        rescale(alpha, need);
+        values(pairs - 1, ph, pl);
+    }
+
+    // O rows are tokens 4g + r of head T; l of token n lives in lanes n (+16k).
+#pragma unroll
+    for (int s = 0; s < TILES; ++s) {
+        const int T = wave + 4 * s;
+        if (T >= G) continue;
+        float ls = st[s].l;
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        const float unit = ldexpf(1.0f, eo - kPScaleLog2);
+        f4 inv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) inv[r] = unit / __shfl(ls, 4 * g + r);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = 4 * g + r;
+            if (tok < t.ntok) {
+                float* orow = a.out + ((int64_t)(t.qi0 + tok) * a.n_heads + h0 + T) * D;
+#pragma unroll
+                for (int c = 0; c < D / 64; ++c) {
+                    f4 v;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = st[s].o[4 * c + i][r] * inv[r];
+                    *reinterpret_cast<f4*>(orow + 64 * c + 4 * n) = v;
+                }
+            }
+        }
+    }
+}
+
+template <int D, typename KT, int TILES, bool REC>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(PrefillArgs a) {
-    __shared__ PfLds<D, KT> sh;
-    prefill_tile_body<D, KT, TILES>(a, sh, blockIdx.x, blockIdx.y);
+    if constexpr (REC) {
+        __shared__ PfLdsPipe<D> sh;
+        prefill_tile_body_rec<D, TILES>(a, sh, blockIdx.x, blockIdx.y);
+    } else {
+        __shared__ PfLds<D, KT> sh;
+        prefill_tile_body<D, KT, TILES>(a, sh, blockIdx.x, blockIdx.y);
+    }
 }
 
 // A step with both decode units and prefill tiles in one launch: workgroups
@@ -721,19 +1189,20 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(P
 // takes a tile: HBM-bound and matrix-bound waves share the CUs in one kernel,
 // with no second stream (streams share the device's few hardware queues, and
 // two kernels on one queue run one after the other).
-template <int D, typename KT, int TILES>
+template <int D, typename KT, int TILES, bool REC>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_mixed_mfma_kernel(DecodeArgs da, PrefillArgs pa, int num_bins,
                                                                           int decode_y, int tile_y) {
     __shared__ union {
         EpilogueLds<D, kMaxGroupMfma> d;
-        PfLds<D, KT> p;
+        typename std::conditional<REC, PfLdsPipe<D>, PfLds<D, KT>>::type p;
     } sh;
     const int bx = blockIdx.x;
     const int by = blockIdx.y;
     if (bx < num_bins) {
         if (by < decode_y) decode_bins_body<D, KT, kExact>(da, sh.d, bx, by);
     } else if (by < tile_y) {
-        prefill_tile_body<D, KT, TILES>(pa, sh.p, bx - num_bins, by);
+        if constexpr (REC) prefill_tile_body_rec<D, TILES>(pa, sh.p, bx - num_bins, by);
+        else prefill_tile_body<D, KT, TILES>(pa, sh.p, bx - num_bins, by);
     }
 }
 
@@ -744,12 +1213,18 @@ hipError_t launch_mixed(int num_bins, int num_tiles, const DecodeArgs& da, const
     const int decode_y = (da.group + kDecodeTileHeads - 1) / kDecodeTileHeads;
     const int tile_y = (pa.group + per_wg - 1) / per_wg;
     const dim3 grid(num_bins + num_tiles, max(decode_y, tile_y));
-    if (tiles == 2)
-        hipLaunchKernelGGL((paged_mixed_mfma_kernel<D, KT, 2>), grid, dim3(kDecodeThreads), 0, stream, da, pa, num_bins,
-                           decode_y, tile_y);
-    else
-        hipLaunchKernelGGL((paged_mixed_mfma_kernel<D, KT, 1>), grid, dim3(kDecodeThreads), 0, stream, da, pa, num_bins,
-                           decode_y, tile_y);
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(kDecodeThreads), 0, stream, da, pa, num_bins, decode_y, tile_y);
+    };
+    if constexpr (sizeof(KT) == 4) {
+        if (pa.records) {
+            if (tiles == 2) go(paged_mixed_mfma_kernel<D, KT, 2, true>);
+            else go(paged_mixed_mfma_kernel<D, KT, 1, true>);
+            return hipGetLastError();
+        }
+    }
+    if (tiles == 2) go(paged_mixed_mfma_kernel<D, KT, 2, false>);
+    else go(paged_mixed_mfma_kernel<D, KT, 1, false>);
     return hipGetLastError();
 }
 
@@ -759,18 +1234,40 @@ hipError_t launch_tiles(int num_tiles, const PrefillArgs& a, hipStream_t stream)
     const int per_wg = kDecodeWaves * tiles;
     static_assert(kPrefillHeads == 2 * kDecodeWaves, "a workgroup covers at most kPrefillHeads heads");
     const dim3 grid(num_tiles, (a.group + per_wg - 1) / per_wg);
-    if (tiles == 2)
-        hipLaunchKernelGGL((paged_prefill_mfma_kernel<D, KT, 2>), grid, dim3(kDecodeThreads), 0, stream, a);
-    else
-        hipLaunchKernelGGL((paged_prefill_mfma_kernel<D, KT, 1>), grid, dim3(kDecodeThreads), 0, stream, a);
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kDecodeThreads), 0, stream, a); };
+    if constexpr (sizeof(KT) == 4) {
+        if (a.records) {
+            if (tiles == 2) go(paged_prefill_mfma_kernel<D, KT, 2, true>);
+            else go(paged_prefill_mfma_kernel<D, KT, 1, true>);
+            return hipGetLastError();
+        }
+    }
+    if (tiles == 2) go(paged_prefill_mfma_kernel<D, KT, 2, false>);
+    else go(paged_prefill_mfma_kernel<D, KT, 1, false>);
     return hipGetLastError();
 }
 
 }  // namespace
 
+int prefill_record_bytes(int head_dim) {
+    return head_dim == 128 ? kRecordBytes<128> : head_dim == 64 ? kRecordBytes<64> : 0;
+}
+
+hipError_t launch_prefill_split(int head_dim, int num_items, int max_pairs, const PrefillSplitArgs& a,
+                                hipStream_t stream) {
+    if (num_items <= 0 || max_pairs <= 0) return hipSuccess;
+    if (!a.records || !a.items || num_items > 65535) return hipErrorInvalidValue;
+    const dim3 grid(max_pairs, num_items);
+    if (head_dim == 128) hipLaunchKernelGGL(prefill_split_kernel<128>, grid, dim3(kDecodeThreads), 0, stream, a);
+    else if (head_dim == 64) hipLaunchKernelGGL(prefill_split_kernel<64>, grid, dim3(kDecodeThreads), 0, stream, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t launch_mixed_mfma(int head_dim, int kv_f16, int num_bins, int num_tiles, const DecodeArgs& da,
                              const PrefillArgs& pa, hipStream_t stream) {
     if (num_bins <= 0 || num_tiles <= 0 || da.group < 1 || pa.group != da.group) return hipErrorInvalidValue;
+    if (kv_f16 && pa.records) return hipErrorInvalidValue;
     if (da.head_dim != head_dim || da.v_head_dim != head_dim || da.block_size != kBlockSize) return hipErrorInvalidValue;
     if (head_dim == 128) return kv_f16 ? launch_mixed<128, _Float16>(num_bins, num_tiles, da, pa, stream)
                                        : launch_mixed<128, float>(num_bins, num_tiles, da, pa, stream);
@@ -781,7 +1278,7 @@ hipError_t launch_mixed_mfma(int head_dim, int kv_f16, int num_bins, int num_til
 
 hipError_t launch_prefill_mfma(int head_dim, int kv_f16, int num_tiles, const PrefillArgs& a, hipStream_t stream) {
     if (num_tiles <= 0) return hipSuccess;
-    if (a.group < 1) return hipErrorInvalidValue;
+    if (a.group < 1 || (kv_f16 && a.records)) return hipErrorInvalidValue;
     if (head_dim == 128) return kv_f16 ? launch_tiles<128, _Float16>(num_tiles, a, stream)
                                        : launch_tiles<128, float>(num_tiles, a, stream);
     if (head_dim == 64) return kv_f16 ? launch_tiles<64, _Float16>(num_tiles, a, stream)

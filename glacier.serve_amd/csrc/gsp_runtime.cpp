@@ -180,6 +180,7 @@ struct gsp_ctx {
     gsp_step_info info{};
     int32_t max_id = -1;
     size_t off_rows = 0, off_ids = 0, off_ctx = 0, off_wr = 0, off_units = 0, off_tiles = 0, off_bins = 0;
+    size_t off_split = 0;
     int32_t num_units = 0;      // decode units of the packed step
     int32_t num_bins = 0;       // decode workgroups (bins of units) of the packed step
     int32_t num_tiles = 0;      // prefill tiles of the packed step
@@ -188,6 +189,15 @@ struct gsp_ctx {
     int32_t step_blocks = 0;
     int32_t step_block_size = 0;
     bool step_tileable = false;
+    // Split records of the packed step's fp32 prefill tiles (records_head_dim
+    // 0: none, the tiles split their pages themselves): one per page pair of
+    // each tiled row and KV head, written by gsp_attention_step per layer.
+    int32_t num_split_items = 0;
+    int32_t split_max_pairs = 0;
+    int64_t num_records = 0;
+    int32_t records_head_dim = 0;
+    unsigned char* d_records = nullptr;
+    size_t d_records_bytes = 0;
 
     // Split-KV workspace: partials and per-(query, KV head) split counters.
     float* part = nullptr;
@@ -199,6 +209,7 @@ struct gsp_ctx {
     int32_t decode_bins_override = 0;
     int32_t decode_path = GSP_DECODE_AUTO;
     int32_t prefill_path = GSP_PREFILL_AUTO;
+    int32_t prefill_split = GSP_SPLIT_RECORDS;
 
     // Split size chosen for the last step shape (reused while the work drifts < 3%).
     int32_t cached_target = 0;
@@ -219,6 +230,7 @@ struct gsp_ctx {
     std::vector<int32_t> bin_cursor;
     std::vector<int64_t> bin_load;
     std::vector<PrefillTile> tiles;
+    std::vector<gsp::PrefillSplitItem> split_items;
     std::vector<int32_t> q_ctx;
     std::vector<int32_t> query_pages;
     std::vector<int64_t> sim_count, sim_heap;
@@ -460,6 +472,7 @@ void gsp_shutdown(gsp_ctx* ctx) {
     if (ctx->d_mmcnt) (void)hipFree(ctx->d_mmcnt);
     if (ctx->part) (void)hipFree(ctx->part);
     if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->d_records) (void)hipFree(ctx->d_records);
     if (ctx->aux_done) (void)hipEventDestroy(ctx->aux_done);
     for (int j = 0; j < 2; ++j)
         if (ctx->side_stream[j]) (void)hipStreamSynchronize(ctx->side_stream[j]);
@@ -530,6 +543,15 @@ int gsp_set_prefill_path(gsp_ctx* ctx, int32_t path) {
     if (path != GSP_PREFILL_AUTO && path != GSP_PREFILL_TILES && path != GSP_PREFILL_PER_TOKEN)
         return gsp::fail(GSP_E_INVALID_ARG, "unknown prefill path %d", path);
     ctx->prefill_path = path;
+    return GSP_OK;
+}
+
+int gsp_set_prefill_split(gsp_ctx* ctx, int32_t mode) {
+    gsp::clear_error();
+    if (!ctx) return gsp::fail(GSP_E_INVALID_ARG, "ctx is NULL");
+    if (mode != GSP_SPLIT_RECORDS && mode != GSP_SPLIT_IN_TILE)
+        return gsp::fail(GSP_E_INVALID_ARG, "unknown prefill split mode %d", mode);
+    ctx->prefill_split = mode;
     return GSP_OK;
 }
 
@@ -1208,7 +1230,15 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     }
     ctx->units.clear();
     ctx->tiles.clear();
+    ctx->split_items.clear();
     ctx->q_ctx.assign((size_t)total_q, 0);
+    // fp32 tiles read split records (one per page pair of each tiled row and
+    // KV head) unless the caller asked the tiles to split their own pages.
+    const bool records = tileable && pd.kv_dtype == GSP_KV_F32 && ctx->prefill_split == GSP_SPLIT_RECORDS;
+    int64_t n_records = 0;
+    int32_t split_max_pairs = 0;
+    // grid.y of the split kernel holds one (row, KV head) each.
+    constexpr size_t kMaxSplitItems = 65535;
     int64_t slots = 0, pairs_split = 0, tiled_queries = 0, tiled_pairs = 0;
     {
         int64_t qi = 0, bt_base = 0;
@@ -1223,6 +1253,16 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                 for (int32_t i = 0; i < ql; ++i)
                     ctx->q_ctx[qi + i] = (int32_t)std::min<int64_t>(tc, (int64_t)pos + i + 1);
                 if (tc > 0) {
+                    // The row's page pairs: every tile of the row reads a prefix of them.
+                    const int32_t row_pairs = (int32_t)(((total_last + bs - 1) / bs + 1) / 2);
+                    const int64_t rec_row = n_records;
+                    if (records) {
+                        for (int32_t kvh = 0; kvh < H; ++kvh)
+                            ctx->split_items.push_back(gsp::PrefillSplitItem{
+                                (int32_t)bt_base, (int32_t)total_last, kvh, (int32_t)(rec_row + (int64_t)kvh * row_pairs)});
+                        n_records += (int64_t)H * row_pairs;
+                        split_max_pairs = std::max(split_max_pairs, row_pairs);
+                    }
                     for (int32_t t0 = 0; t0 < ql; t0 += gsp::kPrefillTileTokens) {
                         PrefillTile t;
                         t.qi0 = (int32_t)(qi + t0);
@@ -1232,9 +1272,9 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                         t.token_count = tc;
                         const int64_t last = std::min<int64_t>(tc, (int64_t)t.pos0 + t.ntok);
                         t.pages = (int32_t)((last + bs - 1) / bs);
-                        t.reserved = 0;
                         for (int32_t kvh = 0; kvh < H; ++kvh) {
                             t.kvh = kvh;
+                            t.rec0 = records ? (int32_t)(rec_row + (int64_t)kvh * row_pairs) : 0;
                             ctx->tiles.push_back(t);
                         }
                     }
@@ -1296,6 +1336,11 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
             ctx->unit_order[(size_t)cnt[(size_t)(max_len - (u.page_end - u.page_begin))]++] = (int32_t)i;
         }
     }
+    if (ctx->split_items.size() > kMaxSplitItems) {  // the tiles split their own pages
+        ctx->split_items.clear();
+        n_records = 0;
+        split_max_pairs = 0;
+    }
     std::stable_sort(ctx->tiles.begin(), ctx->tiles.end(),
                      [](const PrefillTile& x, const PrefillTile& y) { return x.pages > y.pages; });
     const int32_t n_bins = assign_bins(ctx, bins_max, pair_cus);
@@ -1319,6 +1364,9 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     off += n_units * (sizeof(DecodeUnit) / sizeof(int32_t));
     const size_t off_tiles = off;
     off += n_tiles * (sizeof(PrefillTile) / sizeof(int32_t));
+    const size_t n_split = ctx->split_items.size();
+    const size_t off_split = off;
+    off += n_split * (sizeof(gsp::PrefillSplitItem) / sizeof(int32_t));
     const size_t off_bins = off;
     off += (size_t)n_bins + 1;
     const size_t words = off;
@@ -1342,6 +1390,10 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
                            (size_t)slots * gsp::kMaxGroupMfma * (size_t)(pd.v_head_dim + 2), false);
     if (!rc && slots > 0)
         rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, (size_t)total_q * H, true);
+    // The split records, so that a captured gsp_attention_step never grows them.
+    if (!rc && n_records > 0)
+        rc = ensure_device(ctx, &ctx->d_records, &ctx->d_records_bytes,
+                           (size_t)n_records * (size_t)gsp::prefill_record_bytes(pd.head_dim), false);
     if (rc) return rc;
 
     // The step image is written in cached host memory and copied into the
@@ -1389,6 +1441,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         for (size_t j = 0; j < n_units; ++j) dst[j] = ctx->units[(size_t)ctx->unit_place[j]];
     }
     if (n_tiles) std::memcpy(st + off_tiles, ctx->tiles.data(), n_tiles * sizeof(PrefillTile));
+    if (n_split) std::memcpy(st + off_split, ctx->split_items.data(), n_split * sizeof(gsp::PrefillSplitItem));
     std::memcpy(st + off_bins, ctx->bin_units.data(), ((size_t)n_bins + 1) * sizeof(int32_t));
     st[kHdrRows] = B;
     st[kHdrTotalQ] = (int32_t)total_q;
@@ -1422,7 +1475,12 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->off_wr = off_wr;
     ctx->off_units = off_units;
     ctx->off_tiles = off_tiles;
+    ctx->off_split = off_split;
     ctx->off_bins = off_bins;
+    ctx->num_split_items = (int32_t)n_split;
+    ctx->split_max_pairs = split_max_pairs;
+    ctx->num_records = n_records;
+    ctx->records_head_dim = n_records > 0 ? pd.head_dim : 0;
     ctx->num_bins = n_bins;
     ctx->max_id = max_id;
     ctx->num_slots = (int32_t)slots;
@@ -1446,7 +1504,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->info.prefill_queries = (int32_t)tiled_queries;
     ctx->info.prefill_pairs = tiled_pairs;
     ctx->info.decode_bins = n_bins;
-    ctx->info.reserved = 0;
+    ctx->info.split_records = (int32_t)n_records;
     ctx->info.pack_host_ns =
         std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t_pack0).count();
     ctx->step_valid = true;
@@ -1616,14 +1674,38 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     p.n_kv = d.heads_kv;
     p.group = group;
     p.scale_log2 = a.scale_log2;
+    p.records = nullptr;
+    // fp32 tiles read the step's split records, written here for this layer
+    // just before the tiles on the tiles' stream (the allocation-free entry
+    // point has no room for them: its tiles split their own pages).
+    const bool use_records = !fixed && ctx->num_tiles > 0 && ctx->num_records > 0 && !f16 &&
+                             ctx->records_head_dim == d.head_dim &&
+                             ctx->d_records_bytes >= (size_t)ctx->num_records * (size_t)gsp::prefill_record_bytes(d.head_dim);
+    auto launch_split = [&](hipStream_t s) -> int {
+        if (!use_records) return GSP_OK;
+        gsp::PrefillSplitArgs sa;
+        sa.k_pool = p.k_pool;
+        sa.v_pool = p.v_pool;
+        sa.block_stride = p.block_stride;
+        sa.layer_offset = p.layer_offset;
+        sa.head_stride = p.head_stride;
+        sa.items = reinterpret_cast<const gsp::PrefillSplitItem*>(ctx->d_step + ctx->off_split);
+        sa.bt_ids = p.bt_ids;
+        sa.records = ctx->d_records;
+        p.records = ctx->d_records;
+        return check_hip(gsp::launch_prefill_split(d.head_dim, ctx->num_split_items, ctx->split_max_pairs, sa, s),
+                         "prefill split launch");
+    };
     // Decode units stream from HBM and prefill tiles keep the matrix cores
     // busy.  With both in the step and the matrix-core decode (tiles exist
     // only for its fixed shapes), one kernel runs both kinds of workgroup side
     // by side.  With the DPP decode, each kernel goes to its own side stream,
     // forked here and joined back below.
     if (use_mfma && ctx->num_units > 0 && ctx->num_tiles > 0) {
-        rc = check_hip(gsp::launch_mixed_mfma(d.head_dim, f16, ctx->num_bins, ctx->num_tiles, a, p, ctx->stream),
-                       "mixed step launch");
+        rc = launch_split(ctx->stream);
+        if (!rc)
+            rc = check_hip(gsp::launch_mixed_mfma(d.head_dim, f16, ctx->num_bins, ctx->num_tiles, a, p, ctx->stream),
+                           "mixed step launch");
         const int rd = step_done(ctx, capturing);
         return rc ? rc : rd;
     }
@@ -1648,8 +1730,11 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
         }
         if (rc) return rc;
     }
-    if (ctx->num_tiles > 0)
-        rc = check_hip(gsp::launch_prefill_mfma(d.head_dim, f16, ctx->num_tiles, p, tile_stream), "prefill launch");
+    if (ctx->num_tiles > 0) {
+        rc = launch_split(tile_stream);
+        if (!rc)
+            rc = check_hip(gsp::launch_prefill_mfma(d.head_dim, f16, ctx->num_tiles, p, tile_stream), "prefill launch");
+    }
     if (fork) {
         for (int j = 0; j < 2; ++j) {
             const int jc = check_hip(hipEventRecord(ctx->join_ev[j], ctx->side_stream[j]), "hipEventRecord(join)");

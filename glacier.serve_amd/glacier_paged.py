@@ -48,6 +48,8 @@ DECODE_MFMA = 2
 PREFILL_AUTO = 0
 PREFILL_TILES = 1
 PREFILL_PER_TOKEN = 2
+SPLIT_RECORDS = 0
+SPLIT_IN_TILE = 1
 ROPE_PAIRS = 0
 ROPE_HALVES = 1
 WTYPE_F32, WTYPE_Q8_0 = 0, 8  # GGUF tensor type ids (gsp_matmul_batch)
@@ -137,7 +139,7 @@ class StepInfo(ctypes.Structure):
         ("prefill_queries", i32),
         ("prefill_pairs", ctypes.c_int64),
         ("decode_bins", i32),
-        ("reserved", i32),
+        ("split_records", i32),
         ("pack_host_ns", ctypes.c_int64),
     ]
 
@@ -187,6 +189,7 @@ _SIGNATURES = {
     "gsp_set_split_pages": (ctypes.c_int, [vp, i32]),
     "gsp_set_decode_path": (ctypes.c_int, [vp, i32]),
     "gsp_set_prefill_path": (ctypes.c_int, [vp, i32]),
+    "gsp_set_prefill_split": (ctypes.c_int, [vp, i32]),
     "gsp_set_decode_bins": (ctypes.c_int, [vp, i32]),
     "gsp_attention_step": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, ctypes.c_float, fp]),
     "gsp_attention_step_noalloc": (ctypes.c_int, [vp, vp, i32, i32, vp, vp, ctypes.c_float, fp]),
@@ -315,6 +318,11 @@ class Context:
     def set_prefill_path(self, path: int) -> None:
         """Route prefill rows for the next pack_step (PREFILL_AUTO / TILES / PER_TOKEN)."""
         _check(self._lib.gsp_set_prefill_path(self._h, int(path)))
+
+    def set_prefill_split(self, mode: int) -> None:
+        """How fp32 prefill tiles of the next pack_step get their pages' hi/lo split:
+        SPLIT_RECORDS (once per step and layer, the default) or SPLIT_IN_TILE."""
+        _check(self._lib.gsp_set_prefill_split(self._h, int(mode)))
 
     # ---- step packing -------------------------------------------------
     def pack_step(

@@ -274,7 +274,7 @@ typedef struct gsp_step_info {
     int32_t prefill_queries;     /* query tokens served by those tiles */
     int64_t prefill_pairs;       /* sum over tiled query tokens of total (causal key count) */
     int32_t decode_bins;         /* decode workgroups: each runs one bin of units back to back */
-    int32_t reserved;
+    int32_t split_records;       /* page-pair split records of fp32 tiles (0: the tiles split their pages) */
     int64_t pack_host_ns;        /* host time of the gsp_step_pack call that made the step:
                                     validation, scheduling, staging and the copy's enqueue */
 } gsp_step_info;
@@ -317,6 +317,19 @@ int gsp_set_decode_path(gsp_ctx* ctx, int32_t path);
 #define GSP_PREFILL_TILES 1
 #define GSP_PREFILL_PER_TOKEN 2
 int gsp_set_prefill_path(gsp_ctx* ctx, int32_t path);
+
+/* How prefill tiles over fp32 pages get the fp16 hi/lo split of the pages
+ * they read, for the next gsp_step_pack (tuning and tests).
+ * GSP_SPLIT_RECORDS (the default): gsp_attention_step first writes each page
+ * pair of each tiled row and KV head once as a split record (a device
+ * workspace of about 17 KB per page and KV head at head_dim 128, sized by
+ * gsp_step_pack), and the tiles copy records into LDS.  GSP_SPLIT_IN_TILE:
+ * every tile splits the pages it reads (no workspace; the form
+ * gsp_attention_step_noalloc always uses).  Both give results within the
+ * same bound; fp16 pools are not affected. */
+#define GSP_SPLIT_RECORDS 0
+#define GSP_SPLIT_IN_TILE 1
+int gsp_set_prefill_split(gsp_ctx* ctx, int32_t mode);
 
 /* ------------------------------------------------------------------------ */
 /* Attention                                                                 */
@@ -364,7 +377,10 @@ int gsp_attention_step(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_
  * Same arguments, kernels and results as gsp_attention_step, but the split-KV
  * workspace (partial outputs and per-(query, KV head) counters) lives in a
  * fixed device array of GSP_NOALLOC_SCRATCH_BYTES per GPU instead of context
- * memory: the call never allocates or frees, whatever the step's size.  The
+ * memory: the call never allocates or frees, whatever the step's size.  Its
+ * fp32 prefill tiles always split their own pages (GSP_SPLIT_IN_TILE), so its
+ * results equal gsp_attention_step's bit for bit when the step was packed
+ * with that mode, and within the fp32 bound otherwise.  The
  * array's first GSP_NOALLOC_COUNTERS int32 words are counters (a step may use
  * total_q * heads_kv of them) and the rest holds partials (a step uses
  * partial_slots * (n_heads / heads_kv) * (v_head_dim + 2) floats); a step that

@@ -6,7 +6,9 @@ cover 16 query tokens x one KV head x up to 8 query heads; these cases pin the
 ragged last tile (q_len % 16), tiles that straddle page boundaries, the first
 chunk of a sequence (pos 0), token counts below pos + q_len, rows with
 TokenCount 0, GQA groups above 8 (several head chunks per tile) and steps that
-mix decode units with tiles.  Bar: max abs error <= 1e-4 (fp32 KV), <= 2e-3 (fp16 KV).
+mix decode units with tiles.  Tiles over fp32 pages run both ways: from the
+split records written once per step (the default) and splitting their pages
+themselves.  Bar: max abs error <= 1e-4 (fp32 KV), <= 2e-3 (fp16 KV).
 """
 import numpy as np
 import pytest
@@ -18,6 +20,7 @@ from gpu_helpers import TOL, max_err, oracle_step, to_device_pool
 pytestmark = pytest.mark.gpu
 
 PREFILL_PATHS = {"tiles": 1, "auto": 0, "per_token": 2}
+SPLITS = {"records": 0, "in_tile": 1}
 
 GEOMS = [
     (28, 4, 128, "f32"),  # group 7
@@ -31,9 +34,10 @@ GEOMS = [
 ]
 
 
-def run_step(torch, gsp, ctx, step, q, pool, prefill_path, layer=0, split_pages=0, fill=np.nan):
+def run_step(torch, gsp, ctx, step, q, pool, prefill_path, layer=0, split_pages=0, fill=np.nan, split="records"):
     ctx.set_split_pages(split_pages)
     ctx.set_prefill_path(prefill_path)
+    ctx.set_prefill_split(SPLITS[split])
     try:
         ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
                       q_lens=step.q_lens)
@@ -48,6 +52,7 @@ def run_step(torch, gsp, ctx, step, q, pool, prefill_path, layer=0, split_pages=
     finally:
         ctx.set_split_pages(0)
         ctx.set_prefill_path(0)
+        ctx.set_prefill_split(0)
 
 
 def expected_tiles(step, min_q):
@@ -57,15 +62,18 @@ def expected_tiles(step, min_q):
 
 @pytest.mark.parametrize("geom", GEOMS, ids=lambda g: f"{g[0]}q{g[1]}kv_d{g[2]}_{g[3]}")
 @pytest.mark.parametrize("path", list(PREFILL_PATHS))
-def test_prefill_tiles_match_oracle(torch_mod, gsp, ctx, geom, path):
+@pytest.mark.parametrize("split", list(SPLITS))
+def test_prefill_tiles_match_oracle(torch_mod, gsp, ctx, geom, path, split):
     nh, nkv, d, dt = geom
-    print(f"case prefill {geom} path={path}", flush=True)
+    if split == "in_tile" and (dt == "f16" or path == "per_token"):
+        pytest.skip("the split mode only concerns tiles over fp32 pages")
+    print(f"case prefill {geom} path={path} split={split}", flush=True)
     q_lens = np.array([2, 15, 16, 17, 33, 64, 1, 5, 48, 31], np.int32)
     step = workloads.small_step(seed=nh * 17 + nkv * 3 + d, rows=len(q_lens), n_heads=nh, n_kv=nkv, head_dim=d,
                                 kv_dtype=dt, ctx_lo=0, ctx_hi=150, total_blocks=256, q_lens=q_lens)
     q, k, v = workloads.host_values(step)
     pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
-    got, info = run_step(torch_mod, gsp, ctx, step, q, pool, PREFILL_PATHS[path])
+    got, info = run_step(torch_mod, gsp, ctx, step, q, pool, PREFILL_PATHS[path], split=split)
     ref = oracle_step(step, q, k, v, threads=threads())
     pool.destroy()
     min_q = {"tiles": 2, "auto": 16, "per_token": 1 << 30}[path]
@@ -96,8 +104,9 @@ def test_first_chunk_and_clamped_token_counts(torch_mod, gsp, ctx):
     assert max_err(got, ref) <= 1e-4
 
 
-def test_stale_slots_past_token_count_do_not_leak(torch_mod, gsp, ctx):
-    """Slots past a prefill row's TokenCount may hold NaN / Inf; tiles never read them."""
+@pytest.mark.parametrize("split", list(SPLITS))
+def test_stale_slots_past_token_count_do_not_leak(torch_mod, gsp, ctx, split):
+    """Slots past a prefill row's TokenCount may hold NaN / Inf; tiles (and split records) never read them."""
     q_lens = np.array([20, 37, 16], np.int32)
     step = workloads.small_step(seed=44, rows=3, n_heads=28, n_kv=4, head_dim=128, ctx_lo=0, ctx_hi=60,
                                 total_blocks=64, q_lens=q_lens)
@@ -109,14 +118,15 @@ def test_stale_slots_past_token_count_do_not_leak(torch_mod, gsp, ctx):
         kn[last, :, :, used:] = np.nan
         vn[last, :, :, used:] = np.inf
     pool, keep = to_device_pool(torch_mod, gsp, ctx, step, kn, vn)
-    got, _ = run_step(torch_mod, gsp, ctx, step, q, pool, 1)
+    got, _ = run_step(torch_mod, gsp, ctx, step, q, pool, 1, split=split)
     pool.destroy()
     assert max_err(got, oracle_step(step, q, k, v)) <= 1e-4
 
 
-@pytest.mark.parametrize("dt", ["f32", "f16"])
-def test_mixed_decode_and_prefill_step(torch_mod, gsp, ctx, dt):
-    """Decode units (split-KV) and prefill tiles of one packed step, over two layers."""
+@pytest.mark.parametrize("dt,split", [("f32", "records"), ("f32", "in_tile"), ("f16", "records")])
+def test_mixed_decode_and_prefill_step(torch_mod, gsp, ctx, dt, split):
+    """Decode units (split-KV) and prefill tiles of one packed step, over two layers (the
+    records of the second layer overwrite the first's)."""
     rng = np.random.default_rng(12)
     q_lens = np.array([1, 1, 96, 1, 19, 1, 1, 250, 1], np.int32)
     step = workloads.small_step(seed=12, rows=len(q_lens), n_heads=28, n_kv=4, head_dim=128, kv_dtype=dt,
@@ -129,7 +139,7 @@ def test_mixed_decode_and_prefill_step(torch_mod, gsp, ctx, dt):
         k, v = k.astype(np.float16), v.astype(np.float16)
     pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
     for layer, sp in ((0, 0), (1, 3)):
-        got, info = run_step(torch_mod, gsp, ctx, step, q, pool, 0, layer=layer, split_pages=sp)
+        got, info = run_step(torch_mod, gsp, ctx, step, q, pool, 0, layer=layer, split_pages=sp, split=split)
         assert info.prefill_tiles == expected_tiles(step, 16) and info.decode_units > 0
         ref = oracle_step(step, q, k.astype(np.float32), v.astype(np.float32), layer=layer, threads=threads())
         assert max_err(got, ref) <= TOL[dt]
@@ -167,7 +177,8 @@ def fp64_reference(step, q, k, v):
 
 
 @pytest.mark.parametrize("case", ["peaked_scores", "mixed_v_pages", "beyond_fp16_range", "small_v", "tiny_values"])
-def test_prefill_tiles_hold_fp32_range(torch_mod, gsp, ctx, case):
+@pytest.mark.parametrize("split", list(SPLITS))
+def test_prefill_tiles_hold_fp32_range(torch_mod, gsp, ctx, case, split):
     """fp32 pages enter the fp16 matrix cores as scaled hi + lo pairs.  Values far outside fp16's
     range, pages whose V magnitudes differ by 1e9, tiny values and near-one-hot softmaxes stay
     within 4x of fp32 arithmetic's own error against float64 (the fp32 oracle's error; for
@@ -190,7 +201,7 @@ def test_prefill_tiles_hold_fp32_range(torch_mod, gsp, ctx, case):
         q, k, v = q * 1e-6, k * 1e-7, v * 1e-30
     q, k, v = q.astype(np.float32), k.astype(np.float32), v.astype(np.float32)
     pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
-    got, info = run_step(torch_mod, gsp, ctx, step, q, pool, 1)
+    got, info = run_step(torch_mod, gsp, ctx, step, q, pool, 1, split=split)
     pool.destroy()
     assert info.prefill_tiles > 0
     exact = fp64_reference(step, q, k, v)
@@ -198,3 +209,24 @@ def test_prefill_tiles_hold_fp32_range(torch_mod, gsp, ctx, case):
     mag = float(np.abs(exact).max())
     assert np.isfinite(got).all()
     assert max_err(got, exact) <= 4.0 * fp32_err + 1e-6 * mag
+
+
+def test_split_records_equal_in_tile_split(torch_mod, gsp, ctx):
+    """Records and in-tile splitting agree to the fp32 bar, and records are what the default
+    pack selects for fp32 pools.  Rows of several tiles share records; rows end mid-pair
+    (odd page counts) as well as on a pair."""
+    q_lens = np.array([130, 47, 16, 200], np.int32)
+    step = workloads.small_step(seed=77, rows=4, n_heads=28, n_kv=4, head_dim=128, ctx_lo=0, ctx_hi=700,
+                                total_blocks=256, q_lens=q_lens)
+    q, k, v = workloads.host_values(step)
+    pool, keep = to_device_pool(torch_mod, gsp, ctx, step, k, v)
+    rec, info_rec = run_step(torch_mod, gsp, ctx, step, q, pool, 1, split="records")
+    own, info_own = run_step(torch_mod, gsp, ctx, step, q, pool, 1, split="in_tile")
+    pool.destroy()
+    pairs = [(-(-min(int(tc), int(p) + int(ql)) // 16) + 1) // 2
+             for tc, p, ql in zip(step.token_counts, step.positions, q_lens) if tc > 0]
+    assert info_rec.split_records == sum(pairs) * step.n_kv and info_own.split_records == 0
+    assert any(-(-min(int(tc), int(p) + int(ql)) // 16) % 2 for tc, p, ql in
+               zip(step.token_counts, step.positions, q_lens))
+    assert max_err(rec, own) <= 1e-4
+    assert max_err(rec, oracle_step(step, q, k, v, threads=threads())) <= 1e-4

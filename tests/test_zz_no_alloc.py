@@ -1,9 +1,12 @@
 """gsp_attention_step_noalloc against gsp_attention_step.
 
 The allocation-free entry point runs the same kernels with the split-KV
-partials and counters in the library's fixed per-GPU scratch array.  Its
-output must equal gsp_attention_step's bit for bit (same schedule, same
-merge order) and stay within the oracle's tolerance, on two calls in a row,
+partials and counters in the library's fixed per-GPU scratch array; its fp32
+prefill tiles split their pages themselves (the step's split records are not
+in the array).  Its output must equal gsp_attention_step's bit for bit when
+that runs the same kernels (same schedule, same merge order; for fp32 tiles,
+a pack told to split in the tiles), stay within the oracle's tolerance and,
+against the records form, within it too, on two calls in a row,
 the second with a smaller step; a captured noalloc step must replay equal to
 the eager one; a step whose workspace exceeds the array is refused before
 anything is enqueued.
@@ -17,13 +20,15 @@ from gpu_helpers import TOL, max_err, oracle_step, to_device_pool
 pytestmark = pytest.mark.gpu
 
 
-def _pack(ctx, pool, step, split_pages=0):
+def _pack(ctx, pool, step, split_pages=0, prefill_split=0):
     ctx.set_split_pages(split_pages)
+    ctx.set_prefill_split(prefill_split)
     try:
         return ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids,
                              step.max_seq_len, q_lens=step.q_lens)
     finally:
         ctx.set_split_pages(0)
+        ctx.set_prefill_split(0)
 
 
 def _both(torch, ctx, pool, step, qd):
@@ -72,9 +77,13 @@ def test_noalloc_mixed_step_and_repeat(torch_mod, gsp, ctx):
     q, k, v = workloads.host_values(step)
     pool, keep = to_device_pool(torch, gsp, ctx, step, k, v)
     try:
-        info = _pack(ctx, pool, step, 2)
-        assert info.prefill_tiles > 0 and info.split_pairs > 0
         qd = torch.from_numpy(q).cuda()
+        info = _pack(ctx, pool, step, 2)
+        assert info.prefill_tiles > 0 and info.split_pairs > 0 and info.split_records > 0
+        records, got = _both(torch, ctx, pool, step, qd)
+        assert max_err(got, records) <= TOL["f32"]
+        info = _pack(ctx, pool, step, 2, prefill_split=1)  # the tiles split their pages, as noalloc's do
+        assert info.split_records == 0
         ref, got = _both(torch, ctx, pool, step, qd)
         assert np.array_equal(got, ref, equal_nan=True)
         again = torch.full_like(torch.from_numpy(got).cuda(), float("nan"))
