@@ -445,14 +445,41 @@ def kv_write_timing(gsp, torch, ctx, stream, step, pool, layers: int, calls: int
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / calls * 1e3
 
-    us_step = timed(lambda i: pool.rope_write_step(i % layers, step.n_heads, base, style, q.data_ptr(), k.data_ptr(),
-                                                   v.data_ptr()))
+    def write_step(i):
+        pool.rope_write_step(i % layers, step.n_heads, base, style, q.data_ptr(), k.data_ptr(), v.data_ptr())
+
+    us_step = timed(write_step)
     us_host = timed(lambda i: pool.rope_write_tokens(i % layers, pos, blocks, slots, step.n_heads, base, style,
                                                      q.data_ptr(), k.data_ptr(), v.data_ptr()))
+    # The same calls captured once and replayed as a graph: the device's own
+    # cost per call, without the Python loop's pace (the eager figure above
+    # can be bound by the host issuing the calls).
+    us_graph = None
+    try:
+        ctx.sync()  # a capture reads the packed step only once its upload is known complete
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(calls):
+                write_step(i)
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        with torch.cuda.stream(stream):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us_graph = round(e0.elapsed_time(e1) / calls * 1e3, 2)
+        del graph
+    except Exception as exc:  # the eager figures stand alone
+        us_graph = "graph capture failed: " + str(exc)
     elem = 2 if step.kv_dtype == "f16" else 4
     moved = n * (2 * step.n_heads * step.head_dim * 4 + 2 * step.n_kv * step.head_dim * 4
                  + 2 * step.n_kv * step.head_dim * elem)
-    return {"tokens": n, "us_per_layer_call": round(us_step, 2), "bytes_per_call": moved,
+    return {"tokens": n, "us_per_layer_call": round(us_step, 2), "us_per_layer_call_graph": us_graph,
+            "bytes_per_call": moved,
             "gbs": round(moved / (us_step * 1e-6) / 1e9, 1), "us_per_call_host_arrays": round(us_host, 2),
             "note": "gsp_rope_write_step: Q rotated in place, K rotated and stored, V stored, slots from the "
                     "packed step; the host-array form restages ids per call"}

@@ -103,6 +103,7 @@ __device__ __forceinline__ void decode_unit(const DecodeArgs& a, const DecodeUni
     const float scale = a.scale_log2;
 
     for (int p = u.page_begin + wave; p < u.page_end; p += kDecodeWaves) {
+#pragma clang fp contract(off)  // the max and the exponents see the same rounded scores
         const int64_t blk = a.bt_ids[u.bt_base + p];
         const KT* kp = kbase + blk * a.block_stride + lane_off;
         const KT* vp = vbase + blk * a.block_stride + lane_off;

@@ -342,6 +342,7 @@ __device__ __forceinline__ void page_pv(WaveState<D>& st, const PageRegs<D, _Flo
 template <int D, typename KT>
 __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D, KT>& pr, const QRegs<D, KT>& qr,
                                              int ntok, int g) {
+#pragma clang fp contract(off)  // the max and the exponents see the same rounded scores
     f4 s = page_scores<D>(pr, qr);
     if (ntok < kTileTokens) {
 #pragma unroll

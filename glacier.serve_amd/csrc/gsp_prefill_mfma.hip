@@ -527,6 +527,7 @@ constexpr float kLazyLog2 = 3.0f;
 template <int D>
 __device__ __forceinline__ f4 page_softmax(TileState<D>& st, f4 s, bool diag, int key0, int row_ctx, int g,
                                            f4& alpha_rows, bool& rescale) {
+#pragma clang fp contract(off)  // the max and the exponents see the same rounded scores
     if (diag) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -555,6 +556,7 @@ __device__ __forceinline__ f4 page_softmax(TileState<D>& st, f4 s, bool diag, in
 template <int D>
 __device__ __forceinline__ void pair_softmax(TileState<D>& st, f4& s0, f4& s1, bool diag, int key0, int row_ctx,
                                              int g, f4& alpha_rows, bool& rescale) {
+#pragma clang fp contract(off)  // the max and the exponents see the same rounded scores
     if (diag) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -891,6 +893,9 @@ __device__ __forceinline__ float cross_row_max_raw(float x) {
 template <bool MASK>
 __device__ __forceinline__ void pair_softmax_rec(float& m, float& l, f4& s0, f4& s1, float c, int key0, int row_ctx,
                                                  float& alpha, bool& grew) {
+    // No multiply-add contraction here: the max and the exponents must see the
+    // same rounded scores (a fused s * c - m keeps the product unrounded).
+#pragma clang fp contract(off)
     if constexpr (MASK) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
