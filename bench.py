@@ -326,7 +326,7 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         "seq_steps_per_s": round(step.num_rows / (t_step_ms * 1e-3), 1),
         "t_step_ms": round(t_step_ms, 5),
         "t_step_breakdown": {
-            "definition": "seq_steps_per_s = B / t_step; t_step = one engine step: host pack (one H2D copy) + "
+            "definition": "seq_steps_per_s = B / t_step; t_step = one engine step: host pack (one upload) + "
                           "one layer's attention, issued back to back through the Python binding; median period",
             "t_step_ms_mean": round(t_step_mean_ms, 5),
             "t_step_ms_p90": round(float(np.percentile(periods[n_step // 4:], 90)) * 1e3, 5),

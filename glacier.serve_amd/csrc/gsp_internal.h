@@ -262,6 +262,10 @@ hipError_t launch_copy_block(int kv_f16, const CopyBlockArgs& a, hipStream_t str
 // Sets n int32 words at p to `value` with a kernel (capturable, unlike hipMemsetAsync).
 hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t value, hipStream_t stream);
 
+// Copies n16 16-byte words from src (device-visible pinned host memory, both
+// 16-byte aligned) to dst with a kernel on `stream`.
+hipError_t launch_upload_step(const void* src, void* dst, int64_t n16, hipStream_t stream);
+
 // Fixed device scratch of the allocation-free attention entry point
 // (gsp_noalloc.hip): one array per GPU, its address looked up once per device.
 hipError_t noalloc_setup(int device);

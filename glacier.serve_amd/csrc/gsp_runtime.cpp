@@ -136,15 +136,17 @@ struct gsp_ctx {
 
     // Step staging, double-buffered: successive packs alternate between two
     // slots, each a pinned host buffer and its device mirror.  A step's upload
-    // is one copy on the context's stream, so stream order puts it after the
-    // kernels that read the slot's previous step and before the kernels of
-    // this one; no event crosses streams.  upload_done (recorded after the
-    // copy) tells the host when the pinned buffer may be written again: the
-    // pack two steps later usually finds it done, since the GPU is at most a
-    // step behind.
+    // is one copy kernel on the context's stream (upload_step_kernel, reading
+    // the fine-grained pinned buffer over the bus), so stream order puts it
+    // after the kernels that read the slot's previous step and before the
+    // kernels of this one; no event crosses streams.  upload_done (recorded
+    // after the copy) tells the host when the pinned buffer may be written
+    // again: the pack two steps later usually finds it done, since the GPU is
+    // at most a step behind.
     static constexpr int kSlots = 2;
     int32_t* staging[kSlots] = {};
     size_t staging_words[kSlots] = {};
+    const void* staging_dev[kSlots] = {};  // staging[j] as the device addresses it
     int32_t* d_step_slot[kSlots] = {};
     size_t d_step_words[kSlots] = {};
     hipEvent_t upload_done[kSlots] = {};
@@ -302,7 +304,9 @@ int host_wait(hipEvent_t ev, const char* what) {
 }
 
 // Grows a pinned host buffer (waiting for the upload that last used it).
-int ensure_pinned(int32_t** buf, size_t* cap, size_t words, hipEvent_t done, bool* pending) {
+// `flags` are hipHostMalloc's.
+int ensure_pinned(int32_t** buf, size_t* cap, size_t words, hipEvent_t done, bool* pending,
+                  unsigned flags = hipHostMallocDefault) {
     if (*pending) {
         int rc = host_wait(done, "hipEventSynchronize(staging)");
         if (rc) return rc;
@@ -313,8 +317,7 @@ int ensure_pinned(int32_t** buf, size_t* cap, size_t words, hipEvent_t done, boo
     if (*buf) (void)hipHostFree(*buf);
     *buf = nullptr;
     *cap = 0;
-    int rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(buf), n * sizeof(int32_t),
-                                     hipHostMallocDefault),
+    int rc = check_hip(hipHostMalloc(reinterpret_cast<void**>(buf), n * sizeof(int32_t), flags),
                        "hipHostMalloc(staging)");
     if (rc) return rc;
     *cap = n;
@@ -1370,6 +1373,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     const size_t off_bins = off;
     off += (size_t)n_bins + 1;
     const size_t words = off;
+    const size_t words16 = align_up(words, 4);  // the upload moves 16-byte words
 
     int rc = set_device(ctx);
     if (rc) return rc;
@@ -1380,9 +1384,17 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         if (rc) return rc;
         ctx->slot_captured[slot] = false;
     }
-    rc = ensure_pinned(&ctx->staging[slot], &ctx->staging_words[slot], words, ctx->upload_done[slot],
-                       &ctx->upload_pending[slot]);
-    if (!rc) rc = ensure_device(ctx, &ctx->d_step_slot[slot], &ctx->d_step_words[slot], words, false);
+    {
+        const size_t had = ctx->staging_words[slot];  // changes when the buffer is replaced
+        rc = ensure_pinned(&ctx->staging[slot], &ctx->staging_words[slot], words16, ctx->upload_done[slot],
+                           &ctx->upload_pending[slot], hipHostMallocMapped | hipHostMallocCoherent);
+        if (!rc && (ctx->staging_words[slot] != had || !ctx->staging_dev[slot])) {
+            void* dp = nullptr;
+            rc = check_hip(hipHostGetDevicePointer(&dp, ctx->staging[slot], 0), "hipHostGetDevicePointer(staging)");
+            ctx->staging_dev[slot] = rc ? nullptr : dp;
+        }
+    }
+    if (!rc) rc = ensure_device(ctx, &ctx->d_step_slot[slot], &ctx->d_step_words[slot], words16, false);
     // The split workspace for any group up to the decode tile, so that a
     // captured gsp_attention_step of this step never has to grow it.
     if (!rc && slots > 0)
@@ -1457,11 +1469,12 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
 
     // One copy for the whole step, on the context's stream (behind the
     // kernels that read this slot's previous step), then the event that frees
-    // the pinned buffer.
+    // the pinned buffer.  The pad words up to a 16-byte word are zeroed.
     std::memcpy(ctx->staging[slot], st, words * sizeof(int32_t));
-    rc = check_hip(hipMemcpyAsync(ctx->d_step_slot[slot], ctx->staging[slot], words * sizeof(int32_t),
-                                  hipMemcpyHostToDevice, ctx->stream),
-                   "hipMemcpyAsync(step)");
+    for (size_t j = words; j < words16; ++j) ctx->staging[slot][j] = 0;
+    rc = check_hip(gsp::launch_upload_step(ctx->staging_dev[slot], ctx->d_step_slot[slot], (int64_t)(words16 / 4),
+                                           ctx->stream),
+                   "step upload launch");
     if (!rc) rc = check_hip(hipEventRecord(ctx->upload_done[slot], ctx->stream), "hipEventRecord");
     if (rc) return rc;
     ctx->upload_pending[slot] = true;

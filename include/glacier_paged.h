@@ -358,9 +358,10 @@ int gsp_set_prefill_split(gsp_ctx* ctx, int32_t mode);
  * stream, so the call is still ordered as a whole on the context's stream).
  *
  * Step uploads: gsp_step_pack alternates between two device slots and copies
- * the step with one copy on the context's stream, behind the kernels that
- * read the slot's previous step and before the kernels of the step; its
- * pinned host buffer is rewritten two packs later, once that copy is done.
+ * the step with one copy kernel on the context's stream (it reads the pinned
+ * host buffer over the bus), behind the kernels that read the slot's previous
+ * step and before the kernels of the step; its pinned host buffer is
+ * rewritten two packs later, once that copy is done.
  * Graph capture: the call can be captured on the context's stream once the
  * packed step's upload is known complete (gsp_sync after gsp_step_pack;
  * otherwise GSP_E_STATE).  The graph holds the step's kernels only and reads
