@@ -109,9 +109,12 @@ struct VecW {
     typedef T type __attribute__((ext_vector_type(W)));
 };
 
-template <typename V>
+// STREAM: the non-temporal hint for data read once (16-byte loads only; see
+// kStreamLoad).
+template <typename V, bool STREAM = false>
 __device__ __forceinline__ V buffer_load(__amdgpu_buffer_rsrc_t r, int off) {
-    if constexpr (sizeof(V) == 16) return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    if constexpr (sizeof(V) == 16)
+        return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, STREAM ? kStreamLoad : 0));
     else if constexpr (sizeof(V) == 8) return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
     else return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
@@ -225,7 +228,8 @@ __device__ __forceinline__ int stage_offset(int j) {
     return (threadIdx.x >> 4) * D + 64 * j + 4 * (threadIdx.x & 15);
 }
 
-template <int D, typename KT>
+// STREAM: the pages are read once (the split pass), not by every tile of a row.
+template <int D, typename KT, bool STREAM = false>
 __device__ __forceinline__ void stage_load(PfStage<D, KT>& sr, const KT* kpage, const KT* vpage, int ntok) {
     typedef typename PfStage<D, KT>::kvec kvec;
     typedef typename PfStage<D, KT>::vvec vvec;
@@ -234,11 +238,11 @@ __device__ __forceinline__ void stage_load(PfStage<D, KT>& sr, const KT* kpage, 
     const __amdgpu_buffer_rsrc_t rk = prefill_rsrc(kpage, bytes);
     const __amdgpu_buffer_rsrc_t rv = prefill_rsrc(vpage, bytes);
 #pragma unroll
-    for (int i = 0; i < kStageChunks<D>; ++i) sr.k[i] = buffer_load<kvec>(rk, kE * stage_offset<D>(i));
+    for (int i = 0; i < kStageChunks<D>; ++i) sr.k[i] = buffer_load<kvec, STREAM>(rk, kE * stage_offset<D>(i));
     const int kg = threadIdx.x >> 5;
     const int vpart = threadIdx.x & 31;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) sr.v[kk] = buffer_load<vvec>(rv, kE * ((2 * kg + kk) * D + kVW<D> * vpart));
+    for (int kk = 0; kk < 2; ++kk) sr.v[kk] = buffer_load<vvec, STREAM>(rv, kE * ((2 * kg + kk) * D + kVW<D> * vpart));
 }
 
 // Max of x over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four rows of a wave),
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(kDecodeThreads) void prefill_split_kernel(PrefillSp
         const int pg = 2 * pair + h;
         const bool have = pg < pages;
         const int64_t blk = have ? bt[pg] : 0;
-        stage_load<D>(sr[h], kbase + blk * a.block_stride, vbase + blk * a.block_stride,
+        stage_load<D, float, true>(sr[h], kbase + blk * a.block_stride, vbase + blk * a.block_stride,
                       have ? min(kBlockSize, it.ctx_last - pg * kBlockSize) : 0);
     }
     // One K exponent for the pair: its largest |K| over both pages (wave
