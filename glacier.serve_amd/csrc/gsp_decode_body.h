@@ -100,27 +100,30 @@ struct PageRegs<D, _Float16> {
 
 template <typename KT>
 struct Raw4;
-// fp32 page rows are read once per step, in 16-byte pieces, with the
-// non-temporal hint (cache policy bit nt = 2): a Qwen2.5-7B-shape decode step
-// (64 rows, fp32 pages, 329 MB read cache-cold) measured 63.3-63.9 us with it
-// against 67.6-68.2 us without.  The 8-byte fp16 loads keep the default
-// policy: the same hint made fp16 decode steps (Llama-3-8B shape, 1.7 GB; 16
-// rows of 16k-32k tokens, 1.5 GB) about 18% slower, and sc0 alone changed
-// nothing.
+// Pages are read once per step.  Loads that take whole 128-byte lines, or
+// whole halves of them, get the non-temporal hint (cache policy bit nt = 2);
+// with it a Qwen2.5-7B-shape decode step (64 rows, fp32 pages, 329 MB read
+// cache-cold) measured 63.3-63.9 us against 67.6-68.2 us.  fp16 K rows are
+// read 32 bytes of a line per load (four loads per line): with the hint there
+// too, fp16 decode steps (Llama-3-8B shape, 1.7 GB; 16 rows of 16k-32k tokens,
+// 1.5 GB) were about 18% slower; with it on their V loads alone (whole lines)
+// they were 2.8% faster.
 constexpr int kStreamLoad = 2;
 
 template <>
 struct Raw4<float> {
     typedef f4 T;
+    template <int AUX = 0>
     __device__ static f4 load(__amdgpu_buffer_rsrc_t r, int off) {
-        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4, 0, kStreamLoad));
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4, 0, AUX));
     }
 };
 template <>
 struct Raw4<_Float16> {
     typedef h4 T;
+    template <int AUX = 0>
     __device__ static h4 load(__amdgpu_buffer_rsrc_t r, int off) {
-        return __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, off * 2, 0, 0));
+        return __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, off * 2, 0, AUX));
     }
 };
 
@@ -182,12 +185,14 @@ __device__ __forceinline__ void load_page(PageRegs<D, KT>& pr, const KT* kpage, 
     int kl = n * D + 4 * g;
     int vl = 4 * g * D + 4 * n;
     asm volatile("" : "+v"(kl), "+v"(vl));
+    constexpr int kAuxK = sizeof(KT) == 4 ? kStreamLoad : 0;  // 16-byte fp32 K pieces, half a line per row
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) pr.k[j] = Raw4<KT>::load(rk, kl + 16 * j);
+    for (int j = 0; j < D / 16; ++j) pr.k[j] = Raw4<KT>::template load<kAuxK>(rk, kl + 16 * j);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int c = 0; c < D / 64; ++c) pr.v[kk][c] = Raw4<KT>::load(rv, vl + kk * D + 64 * c);
+        for (int c = 0; c < D / 64; ++c)
+            pr.v[kk][c] = Raw4<KT>::template load<kStreamLoad>(rv, vl + kk * D + 64 * c);  // whole lines
 }
 
 // Q^T operand of a unit, q[j] = Q[head n][16j + 4g .. +3], and `sc`, the
