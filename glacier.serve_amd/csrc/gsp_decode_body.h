@@ -86,6 +86,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const void* base, in
 template <int D, typename KT>
 struct PageRegs;
 
+// Exact-shape fp16 pages take the K = 32 fp16 matrix step for the scores:
+// lane (n, g) holds K[key n][32 j + 8 g .. + 7] (one 16-byte load, half a
+// 128-byte line of the row) and Q[head n][the same dims].  Other fp16 shapes
+// use the K = 16 step with 8-byte pieces at 16 j + 4 g.
+template <typename KT, int MODE>
+constexpr bool kK32 = sizeof(KT) == 2 && MODE == kExact;
+
 template <int D>
 struct PageRegs<D, float> {
     f4 k[D / 16];
@@ -182,12 +189,23 @@ __device__ __forceinline__ void load_page(PageRegs<D, KT>& pr, const KT* kpage, 
     // keeps them from being hoisted out of the page loop), so each load takes
     // its constant part in the instruction's immediate offset.  Hoisted, the
     // sixteen offsets would each hold a register across the loop.
-    int kl = n * D + 4 * g;
+    int kl = n * D + (sizeof(KT) == 2 ? 8 : 4) * g;  // fp16: the K = 32 layout
     int vl = 4 * g * D + 4 * n;
     asm volatile("" : "+v"(kl), "+v"(vl));
-    constexpr int kAuxK = sizeof(KT) == 4 ? kStreamLoad : 0;  // 16-byte fp32 K pieces, half a line per row
+    if constexpr (sizeof(KT) == 2) {
+        // K = 32 layout: 16 bytes at 32 j + 8 g, half a line of the row.
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) pr.k[j] = Raw4<KT>::template load<kAuxK>(rk, kl + 16 * j);
+        for (int j = 0; j < D / 32; ++j) {
+            const h8 x = __builtin_bit_cast(
+                h8, __builtin_amdgcn_raw_buffer_load_b128(rk, (kl + 32 * j) * 2, 0, kStreamLoad));
+            pr.k[2 * j] = __builtin_shufflevector(x, x, 0, 1, 2, 3);
+            pr.k[2 * j + 1] = __builtin_shufflevector(x, x, 4, 5, 6, 7);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) pr.k[j] = Raw4<KT>::template load<kStreamLoad>(rk, kl + 16 * j);
+    }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
@@ -231,12 +249,14 @@ struct QRegs<D, _Float16> {
 
 // Q row of head `h` (the tile's head n, or its first head for padding
 // lanes); dims past head_dim are zero.
-template <int D, int MODE>
+template <int D, typename KT, int MODE>
 __device__ __forceinline__ void load_q(QRaw<D>& qr, const DecodeArgs& a, int qi, int h, int g, const Geo<D, MODE>& geo) {
     const float* qrow = a.q + ((int64_t)qi * a.n_heads + h) * geo.d;
 #pragma unroll
     for (int j = 0; j < D / 16; ++j) {
-        const int dim = 16 * j + 4 * g;
+        // q[j] holds dims 16 j + 4 g .. + 3, or for the K = 32 step dims
+        // 32 (j / 2) + 8 g + 4 (j % 2) .. + 3 (q[2j], q[2j + 1]: one operand).
+        const int dim = kK32<KT, MODE> ? 32 * (j >> 1) + 8 * g + 4 * (j & 1) : 16 * j + 4 * g;
         if constexpr (MODE == kExact) {
             qr.q[j] = *reinterpret_cast<const f4*>(qrow + dim);
         } else if constexpr (MODE == kVec4) {
@@ -289,7 +309,7 @@ struct WaveState {
 };
 
 // S^T = K . Q^T for one page; returns the lane's S[head n][token 4g + r] in log2 units.
-template <int D>
+template <int D, bool K32>
 __device__ __forceinline__ f4 page_scores(const PageRegs<D, float>& pr, const QRegs<D, float>& qr) {
     // 32 (d = 128) or 16 (d = 64) rank-4 steps, two accumulation chains.
     f4 s0 = {0.f, 0.f, 0.f, 0.f};
@@ -307,15 +327,28 @@ __device__ __forceinline__ f4 page_scores(const PageRegs<D, float>& pr, const QR
     return (s0 + s1) * qr.sc;
 }
 
-template <int D>
+template <int D, bool K32>
 __device__ __forceinline__ f4 page_scores(const PageRegs<D, _Float16>& pr, const QRegs<D, _Float16>& qr) {
-    // K . (q_hi + q_lo): one rank-16 step per 16 dims and half, fp32 accumulation.
+    // K . (q_hi + q_lo), fp32 accumulation: one rank-32 step per 32 dims and
+    // half (K32), else one rank-16 step per 16 dims and half.
     f4 s0 = {0.f, 0.f, 0.f, 0.f};
     f4 s1 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (K32) {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 #pragma unroll
-    for (int j = 0; j < D / 16; ++j) {
-        s0 = __builtin_amdgcn_mfma_f32_16x16x16f16(pr.k[j], qr.hi[j], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_16x16x16f16(pr.k[j], qr.lo[j], s1, 0, 0, 0);
+        for (int j = 0; j < D / 32; ++j) {
+            const h8 k = __builtin_shufflevector(pr.k[2 * j], pr.k[2 * j + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+            const h8 qh = __builtin_shufflevector(qr.hi[2 * j], qr.hi[2 * j + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+            const h8 ql = __builtin_shufflevector(qr.lo[2 * j], qr.lo[2 * j + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+            s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k, qh, s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k, ql, s1, 0, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < D / 16; ++j) {
+            s0 = __builtin_amdgcn_mfma_f32_16x16x16f16(pr.k[j], qr.hi[j], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x16f16(pr.k[j], qr.lo[j], s1, 0, 0, 0);
+        }
     }
     return (s0 + s1) * qr.sc;
 }
@@ -353,11 +386,11 @@ __device__ __forceinline__ void page_pv(WaveState<D>& st, const PageRegs<D, _Flo
         }
 }
 
-template <int D, typename KT>
+template <int D, typename KT, int MODE>
 __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D, KT>& pr, const QRegs<D, KT>& qr,
                                              int ntok, int g) {
 #pragma clang fp contract(off)  // the max and the exponents see the same rounded scores
-    f4 s = page_scores<D>(pr, qr);
+    f4 s = page_scores<D, kK32<KT, MODE>>(pr, qr);
     if (ntok < kTileTokens) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -489,7 +522,7 @@ __device__ __forceinline__ void decode_bins_body(const DecodeArgs& a, EpilogueLd
     {
         const DecodeUnit u0 = read_unit(a, first);
         const int blk0 = first_block(a, first, wave);
-        load_q<D, MODE>(qraw, a, u0.qi, u0.kvh * a.group + hq, g, geo);
+        load_q<D, KT, MODE>(qraw, a, u0.qi, u0.kvh * a.group + hq, g, geo);
         load_first_page<D, KT, MODE>(ra, a, u0, blk0, wave, n, g, geo);
     }
     const int rb0 = ld_meta(a.bin_rest + first);
@@ -536,7 +569,7 @@ __device__ __forceinline__ void decode_bins_body(const DecodeArgs& a, EpilogueLd
                                        min(geo.bs, u.ctx - pn * geo.bs), n, g, geo);
             }
             rb_ready = false;
-            compute_page<D, KT>(st, ra, q, min(geo.bs, u.ctx - p * geo.bs), g);
+            compute_page<D, KT, MODE>(st, ra, q, min(geo.bs, u.ctx - p * geo.bs), g);
             if (pn >= u.page_end) break;
             const int pnn = pn + kDecodeWaves;
             if (pnn < u.page_end) {
@@ -544,7 +577,7 @@ __device__ __forceinline__ void decode_bins_body(const DecodeArgs& a, EpilogueLd
                 load_page<D, KT, MODE>(ra, kbase + blk * a.block_stride, vbase + blk * a.v_block_stride,
                                        min(geo.bs, u.ctx - pnn * geo.bs), n, g, geo);
             }
-            compute_page<D, KT>(st, rb, q, min(geo.bs, u.ctx - pn * geo.bs), g);
+            compute_page<D, KT, MODE>(st, rb, q, min(geo.bs, u.ctx - pn * geo.bs), g);
             p = pnn;
         }
 
@@ -559,7 +592,7 @@ __device__ __forceinline__ void decode_bins_body(const DecodeArgs& a, EpilogueLd
         // per wave in flight.
         rb_ready = false;
         if (has_next) {
-            load_q<D, MODE>(qraw, a, un.qi, un.kvh * a.group + hq, g, geo);
+            load_q<D, KT, MODE>(qraw, a, un.qi, un.kvh * a.group + hq, g, geo);
             load_first_page<D, KT, MODE>(ra, a, un, blkn, wave, n, g, geo);
             if (has_n2) {
                 const int64_t koff = a.layer_offset + (int64_t)un.kvh * a.head_stride + (int64_t)blkn2 * a.block_stride;
