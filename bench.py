@@ -147,7 +147,8 @@ def describe(step, layers: int) -> dict:
 
 
 def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: float, layers: int = 4,
-                 decode_path: str = "auto", profile_only: bool = False, prefill_split: str = "records") -> dict:
+                 decode_path: str = "auto", profile_only: bool = False, prefill_split: str = "records",
+                 split_pages: int = 0, decode_bins: int = 0) -> dict:
     import numpy as np
     import torch
 
@@ -160,6 +161,8 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     ctx = gsp.Context(0)
     ctx.set_decode_path({"auto": gsp.DECODE_AUTO, "dpp": gsp.DECODE_DPP, "mfma": gsp.DECODE_MFMA}[decode_path])
     ctx.set_prefill_split({"records": gsp.SPLIT_RECORDS, "in_tile": gsp.SPLIT_IN_TILE}[prefill_split])
+    ctx.set_split_pages(split_pages)  # 0: the library's own choice
+    ctx.set_decode_bins(decode_bins)
     # A dedicated torch stream: the library launches on it and the events below
     # are recorded on it (torch's default stream is the null handle).
     stream = torch.cuda.Stream()
@@ -625,6 +628,10 @@ def main() -> int:
                     help="decode kernel (auto = the matrix-core kernel)")
     ap.add_argument("--prefill-split", default="records", choices=["records", "in_tile"],
                     help="fp32 prefill tiles: split records written once per step (default) or split in each tile")
+    ap.add_argument("--split-pages", type=int, default=0,
+                    help="largest split-KV unit in pages (tuning; 0: the library's choice)")
+    ap.add_argument("--decode-bins", type=int, default=0,
+                    help="decode workgroups (tuning; 0: the library's choice)")
     ap.add_argument("--profile-only", action="store_true",
                     help="only the warmup and timed launches (plus each kernel alone for mixed steps)")
     ap.add_argument("--summarize-trace", metavar="CSV", help="summarize a rocprofv3 kernel-trace CSV and exit")
@@ -653,7 +660,8 @@ def main() -> int:
     for name in names:
         res = run_workload(name, args.steps, args.warmup, cpu=not (args.no_cpu or args.profile_only),
                            cpu_budget_s=args.cpu_budget, layers=args.layers, decode_path=args.decode_path,
-                           profile_only=args.profile_only, prefill_split=args.prefill_split)
+                           profile_only=args.profile_only, prefill_split=args.prefill_split,
+                           split_pages=args.split_pages, decode_bins=args.decode_bins)
         print(json.dumps(res), flush=True)
     if args.copy_calibration > 0:
         import torch
