@@ -593,7 +593,7 @@ __device__ __forceinline__ void pair_softmax(TileState<D>& st, f4& s0, f4& s1, b
 // stored.  It costs no time: the page barrier waits for the busiest wave.
 // This form splits the fp32 pages it reads itself (fp16 pages need no split);
 // prefill_tile_body_rec below reads the step's split records instead.
-template <int D, typename KT, int TILES>
+template <int D, typename KT, int TILES, int LIVE = TILES>
 __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D, KT>& sh, int bx, int by) {
     constexpr int kPrefillTiles = TILES;
     constexpr int kRow = PfLds<D, KT>::kRow;
@@ -616,7 +616,7 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
     TileQ<D> q[kPrefillTiles];
     TileState<D> st[kPrefillTiles];
 #pragma unroll
-    for (int s = 0; s < kPrefillTiles; ++s) {
+    for (int s = 0; s < LIVE; ++s) {
         const int T = wave + 4 * s;
         const float* qrow = a.q + ((int64_t)(t.qi0 + (row_live ? n : 0)) * a.n_heads + h0 + (T < G ? T : 0)) * D;
         load_tile_q<D>(q[s], qrow, T < G && row_live, g, a.scale_log2);
@@ -712,7 +712,7 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int s = 0; s < kPrefillTiles; ++s) sc[h][s] = f4{0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; s < LIVE; ++s) sc[h][s] = f4{0.f, 0.f, 0.f, 0.f};
         // Step t = 2j + h takes page h's head dims 32j .. 32j + 31; its K words
         // are read while step t - 1's products run.  Within a step the tiles'
         // chains alternate, so no product waits on the one just issued.
@@ -734,14 +734,14 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
             __builtin_amdgcn_sched_barrier(0);  // one step's reads ahead, no more
             const int j = t >> 1, h = t & 1;
 #pragma unroll
-            for (int s = 0; s < kPrefillTiles; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].hi[j], sc[h][s], 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < kPrefillTiles; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, q[s].lo[j], sc[h][s], 0, 0, 0);
             if constexpr (kSplitKV) {
 #pragma unroll
-                for (int s = 0; s < kPrefillTiles; ++s)
+                for (int s = 0; s < LIVE; ++s)
                     sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, q[s].hi[j], sc[h][s], 0, 0, 0);
             }
         }
@@ -751,7 +751,7 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
         // first page, 4..7 those of the second.
         h8 ph[kPrefillTiles], pl[kPrefillTiles];
 #pragma unroll
-        for (int s = 0; s < kPrefillTiles; ++s) {
+        for (int s = 0; s < LIVE; ++s) {
             TileState<D>& ts = st[s];
             f4 p0 = sc[0][s] * q[s].sc;  // lane: S[token n][keys key0 .. key0 + 3], log2 units
             f4 p1 = sc[1][s] * q[s].sc;
@@ -808,14 +808,14 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
             if (b + 1 < D / 16) read_v(b + 1, nbh, nbl);
             __builtin_amdgcn_sched_barrier(0);  // one block's reads ahead, no more
 #pragma unroll
-            for (int s = 0; s < kPrefillTiles; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bh, st[s].o[b], 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < kPrefillTiles; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s], bh, st[s].o[b], 0, 0, 0);
             if constexpr (kSplitKV) {
 #pragma unroll
-                for (int s = 0; s < kPrefillTiles; ++s)
+                for (int s = 0; s < LIVE; ++s)
                     st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bl, st[s].o[b], 0, 0, 0);
             }
         }
@@ -825,7 +825,7 @@ __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D,
 
     // O rows are tokens 4g + r of head T; l of token n lives in lanes n (+16k).
 #pragma unroll
-    for (int s = 0; s < kPrefillTiles; ++s) {
+    for (int s = 0; s < LIVE; ++s) {
         const int T = wave + 4 * s;
         if (T >= G) continue;
         float ls = st[s].l;
@@ -922,7 +922,7 @@ __device__ __forceinline__ void pair_softmax_rec(float& m, float& l, f4& s0, f4&
     l = l * alpha + (((s0[0] + s0[1]) + (s0[2] + s0[3])) + ((s1[0] + s1[1]) + (s1[2] + s1[3])));
 }
 
-template <int D, int TILES>
+template <int D, int TILES, int LIVE = TILES>
 __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLdsPipe<D>& sh, int bx, int by) {
     constexpr int kRow = D + 8;
     constexpr int kSteps = D / 16;  // score steps per pair (32 head dims of one page each), = output blocks
@@ -950,7 +950,7 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
     TileQ<D> q[TILES];
     TileState<D> st[TILES];
 #pragma unroll
-    for (int s = 0; s < TILES; ++s) {
+    for (int s = 0; s < LIVE; ++s) {
         const int T = wave + 4 * s;
         const float* qrow = a.q + ((int64_t)(t.qi0 + (row_live ? n : 0)) * a.n_heads + h0 + (T < G ? T : 0)) * D;
         load_tile_q<D>(q[s], qrow, T < G && row_live, g, a.scale_log2);
@@ -970,7 +970,7 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int s = 0; s < TILES; ++s) sc[h][s] = f4{0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; s < LIVE; ++s) sc[h][s] = f4{0.f, 0.f, 0.f, 0.f};
         auto read_k = [&](int u, h8& khv, h8& klv) {
             const int at = kq + (u & 1) * kBlockSize * kRow + 32 * (u >> 1);
             khv = *reinterpret_cast<const h8*>(&kh[at]);
@@ -985,13 +985,13 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
             __builtin_amdgcn_sched_barrier(0);  // one step's reads ahead, no more
             const int j = u >> 1, h = u & 1;
 #pragma unroll
-            for (int s = 0; s < TILES; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khv, q[s].hi[j], sc[h][s], 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < TILES; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khv, q[s].lo[j], sc[h][s], 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < TILES; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 sc[h][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(klv, q[s].hi[j], sc[h][s], 0, 0, 0);
         }
     };
@@ -1038,7 +1038,7 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
         }
         const int key0 = i * kPairKeys + 4 * g;
 #pragma unroll
-        for (int s = 0; s < TILES; ++s) {
+        for (int s = 0; s < LIVE; ++s) {
             f4 p0 = sc[0][s];
             f4 p1 = sc[1][s];
             bool grew;
@@ -1071,13 +1071,13 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
             if (b + 1 < kSteps) read_v(b + 1, nbh, nbl);
             __builtin_amdgcn_sched_barrier(0);  // one block's reads ahead, no more
 #pragma unroll
-            for (int s = 0; s < TILES; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bh, st[s].o[b], 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < TILES; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s], bh, st[s].o[b], 0, 0, 0);
 #pragma unroll
-            for (int s = 0; s < TILES; ++s)
+            for (int s = 0; s < LIVE; ++s)
                 st[s].o[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s], bl, st[s].o[b], 0, 0, 0);
         }
     };
@@ -1085,7 +1085,7 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
     // O rows are tokens 4g + r: their factors come from the lanes of those tokens.
     auto rescale = [&](const float (&alpha)[TILES], const bool (&need)[TILES]) {
 #pragma unroll
-        for (int s = 0; s < TILES; ++s) {
+        for (int s = 0; s < LIVE; ++s) {
             if (need[s]) {
                 f4 rows;
 #pragma unroll
@@ -1130,14 +1130,14 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int s = 0; s < TILES; ++s) sa[h][s] = sb[h][s];
+            for (int s = 0; s < LIVE; ++s) sa[h][s] = sb[h][s];
     }
     for (; k < pairs; ++k) {
         iteration(std::true_type{}, k, sa, sb);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int s = 0; s < TILES; ++s) sa[h][s] = sb[h][s];
+            for (int s = 0; s < LIVE; ++s) sa[h][s] = sb[h][s];
     }
     {
         h8 ph[TILES], pl[TILES];
@@ -1152,7 +1152,7 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
 
     // O rows are tokens 4g + r of head T; l of token n lives in lanes n (+16k).
 #pragma unroll
-    for (int s = 0; s < TILES; ++s) {
+    for (int s = 0; s < LIVE; ++s) {
         const int T = wave + 4 * s;
         if (T >= G) continue;
         float ls = st[s].l;
@@ -1179,14 +1179,34 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
     }
 }
 
+// Runs tile workgroup (bx, by) of either body.  With two tiles per wave, a
+// wave whose second head is past the group (wave + 4 >= G: groups of 5 to 7
+// heads, or a partial last head chunk) computes its first tile only; its
+// barriers and copies are the same, so the workgroup stays in step.  Skipping
+// the padding tile's products took a Qwen2.5-7B-shape batch of sixteen prefill
+// chunks (group 7) from 268-273 us to 260-263 us.
+template <int D, typename KT, int TILES, bool REC, typename Sh>
+__device__ __forceinline__ void prefill_tile(const PrefillArgs& a, Sh& sh, int bx, int by) {
+    const int G = min(kDecodeWaves * TILES, a.group - by * kDecodeWaves * TILES);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool one = TILES == 2 && wave + kDecodeWaves >= G;
+    if constexpr (REC) {
+        if (one) prefill_tile_body_rec<D, TILES, 1>(a, sh, bx, by);
+        else prefill_tile_body_rec<D, TILES>(a, sh, bx, by);
+    } else {
+        if (one) prefill_tile_body<D, KT, TILES, 1>(a, sh, bx, by);
+        else prefill_tile_body<D, KT, TILES>(a, sh, bx, by);
+    }
+}
+
 template <int D, typename KT, int TILES, bool REC>
 __global__ __launch_bounds__(kDecodeThreads, 2) void paged_prefill_mfma_kernel(PrefillArgs a) {
     if constexpr (REC) {
         __shared__ PfLdsPipe<D> sh;
-        prefill_tile_body_rec<D, TILES>(a, sh, blockIdx.x, blockIdx.y);
+        prefill_tile<D, KT, TILES, true>(a, sh, blockIdx.x, blockIdx.y);
     } else {
         __shared__ PfLds<D, KT> sh;
-        prefill_tile_body<D, KT, TILES>(a, sh, blockIdx.x, blockIdx.y);
+        prefill_tile<D, KT, TILES, false>(a, sh, blockIdx.x, blockIdx.y);
     }
 }
 
@@ -1210,8 +1230,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void paged_mixed_mfma_kernel(Dec
     if (bx < num_bins) {
         if (by < decode_y) decode_bins_body<D, KT, kExact>(da, sh.d, bx, by);
     } else if (by < tile_y) {
-        if constexpr (REC) prefill_tile_body_rec<D, TILES>(pa, sh.p, bx - num_bins, by);
-        else prefill_tile_body<D, KT, TILES>(pa, sh.p, bx - num_bins, by);
+        prefill_tile<D, KT, TILES, REC>(pa, sh.p, bx - num_bins, by);
     }
 }
 
