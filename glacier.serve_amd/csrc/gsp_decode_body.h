@@ -107,14 +107,14 @@ struct PageRegs<D, _Float16> {
 
 template <typename KT>
 struct Raw4;
-// Pages are read once per step.  Loads that take whole 128-byte lines, or
-// whole halves of them, get the non-temporal hint (cache policy bit nt = 2);
-// with it a Qwen2.5-7B-shape decode step (64 rows, fp32 pages, 329 MB read
-// cache-cold) measured 63.3-63.9 us against 67.6-68.2 us.  fp16 K rows are
-// read 32 bytes of a line per load (four loads per line): with the hint there
-// too, fp16 decode steps (Llama-3-8B shape, 1.7 GB; 16 rows of 16k-32k tokens,
-// 1.5 GB) were about 18% slower; with it on their V loads alone (whole lines)
-// they were 2.8% faster.
+// Pages are read once per step.  The exact-shape page loads (load_page) each
+// take a whole 128-byte line or a contiguous half of one, and carry the
+// non-temporal hint (cache policy bit nt = 2): a Qwen2.5-7B-shape decode step
+// (64 rows, fp32 pages, 329 MB read cache-cold) measured 63.3-63.9 us with it
+// against 67.6-68.2 us without.  On 8-byte fp16 K pieces (a quarter line per
+// load) the same hint made fp16 decode steps about 18% slower, which is why
+// fp16 K rows are read in the K = 32 layout (16-byte pieces, half a line):
+// with it, a Llama-3-8B-shape step (1.7 GB) went from 287.6 to 271.1 us.
 constexpr int kStreamLoad = 2;
 
 template <>
