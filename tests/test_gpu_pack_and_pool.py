@@ -193,9 +193,9 @@ def test_cow_fork_copies_page_on_device(torch_mod, gsp, ctx):
 
 
 def test_back_to_back_packs_without_host_sync(torch_mod, gsp, ctx):
-    """Packs alternate between two device slots whose uploads run on the library's
-    copy stream: a pack may overwrite a slot only after the kernels of the step
-    packed two calls earlier have read it.  Nine packs of three different steps,
+    """Packs alternate between two device slots, each uploaded by one copy kernel on
+    the context's stream: a pack may overwrite a slot only after the kernels of the
+    step packed two calls earlier have read it.  Nine packs of three different steps,
     each followed by its attention and its KV write, with no host sync between
     them: every output must match the oracle."""
     from gpu_helpers import TOL, max_err, oracle_step, to_device_pool
@@ -285,3 +285,25 @@ def test_concurrent_cow_forks_copy_pages_on_device(torch_mod, gsp, ctx):
     assert alloc.free_blocks_count == 64
     alloc.attach_pool(None, None)
     pool.destroy()
+
+
+def test_step_upload_through_growing_staging(gsp):
+    """A fresh context packs steps whose images grow and shrink, so that each slot's pinned
+    buffer is reallocated (and its device address looked up again) while the other slot
+    holds the previous step; every upload is checked bit for bit by downloading it."""
+    ctx2 = gsp.Context(0)
+    try:
+        sizes = [(3, 40), (40, 900), (5, 60), (64, 2000), (64, 2000), (2, 16), (80, 3000)]
+        for i, (rows, hi) in enumerate(sizes):
+            step = workloads.small_step(seed=300 + i, rows=rows, n_heads=8, n_kv=2, head_dim=64, ctx_hi=hi,
+                                        total_blocks=8192)
+            pool = gsp.Pool.create(ctx2, total_blocks=step.total_blocks, layers=1, heads_kv=step.n_kv, head_dim=4)
+            info = ctx2.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids,
+                                  step.max_seq_len)
+            pool.destroy()
+            print(f"case upload pack {i}: rows={rows} staging_bytes={info.staging_bytes}", flush=True)
+            rows_d, ids_d, ctx_d = ctx2.download_step()
+            er, ei, ec = expected_packing(step)
+            assert np.array_equal(rows_d, er) and np.array_equal(ids_d, ei) and np.array_equal(ctx_d, ec), i
+    finally:
+        ctx2.close()
