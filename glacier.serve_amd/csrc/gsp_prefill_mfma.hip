@@ -393,12 +393,8 @@ __device__ __forceinline__ void stage_store(const PfStage<D, _Float16>& sr, PfLd
 // pair covers the row's tokens up to min(TokenCount, pos + q_len); keys of it
 // past a tile's own limit are masked like any other.
 
-// 16 bytes per lane from r at voffset into LDS at lds + 16 * lane (lds uniform over the wave).
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, int voffset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
-}
-
-// As lds_load16, from r at soffset + voffset (soffset uniform).
+// 16 bytes per lane from r at soffset + voffset into LDS at lds + 16 * lane
+// (lds and soffset uniform over the wave).
 __device__ __forceinline__ void lds_load16s(__amdgpu_buffer_rsrc_t r, void* lds, int voffset, int soffset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0,
                                              0);
