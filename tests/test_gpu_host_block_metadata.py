@@ -1,4 +1,4 @@
-"""On the GPU box: the free stack, refcounts and BlockTable against the reference's KATs and the oracle (test_block_metadata.py).
+"""Under the gpu mark: the free stack, refcounts and BlockTable against the reference's KATs and the oracle (test_block_metadata.py).
 
 These tests call only host entry points, so they also run without a GPU; this
 module collects them again under the gpu mark, so that the library the GPU run

@@ -1,4 +1,4 @@
-"""On the GPU box: the host metadata under concurrent threads (test_host_meta_concurrency.py).
+"""Under the gpu mark: the host metadata under concurrent threads (test_host_meta_concurrency.py).
 
 These tests call only host entry points, so they also run without a GPU; this
 module collects them again under the gpu mark, so that the library the GPU run

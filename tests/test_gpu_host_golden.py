@@ -1,4 +1,4 @@
-"""On the GPU box: the committed golden fixtures: oracle vectors and the block-table op log (test_golden.py).
+"""Under the gpu mark: the committed golden fixtures: oracle vectors and the block-table op log (test_golden.py).
 
 These tests call only host entry points, so they also run without a GPU; this
 module collects them again under the gpu mark, so that the library the GPU run
