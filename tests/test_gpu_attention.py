@@ -144,6 +144,36 @@ def test_zero_total_rows_leave_out_untouched(torch_mod, gsp, ctx):
     pool.destroy()
 
 
+def test_steps_with_nothing_to_attend(torch_mod, gsp, ctx):
+    """A step of no rows, and one whose rows all have TokenCount 0, launch nothing and write nothing;
+    the context then runs an ordinary step."""
+    torch = torch_mod
+    rng = np.random.default_rng(12)
+    ctxs = np.array([20, 40, 33], np.int32)
+    step = workloads.decode_step("empty", rng, ctxs, 8, 2, 64, "f32", 64, 4096, 12)
+    q, k, v = workloads.host_values(step)
+    pool, keep = to_device_pool(torch, gsp, ctx, step, k, v)
+    qd = torch.from_numpy(np.ascontiguousarray(q, dtype=np.float32)).cuda()
+
+    info = ctx.pack_step(pool, [], [], [0], [], 4096)
+    assert info.num_rows == 0 and info.decode_units == 0 and info.prefill_tiles == 0
+    out = torch.full((3, 8, 64), 7.0, dtype=torch.float32, device="cuda")
+    ctx.attention_step(pool, 0, 8, qd.data_ptr(), out.data_ptr(), step.scale)
+    ctx.sync()
+    assert bool((out == 7.0).all())
+
+    idle = workloads.Step(step.name, step.n_heads, step.n_kv, step.head_dim, step.kv_dtype, step.total_blocks,
+                          step.max_seq_len, step.positions, np.zeros(3, np.int32), step.bt_offsets, step.bt_ids,
+                          step.q_lens, step.seed, dict(step.notes), step.block_size, step.v_head_dim)
+    got = gpu_step(torch, gsp, ctx, idle, q, pool, fill=7.0)
+    assert ctx.step_info().decode_units == 0
+    assert np.all(got == 7.0)
+
+    got = gpu_step(torch, gsp, ctx, step, q, pool)
+    assert max_err(got, oracle_step(step, q, k, v)) <= 1e-4
+    pool.destroy()
+
+
 @pytest.mark.parametrize("dt", ["f32", "f16"])
 def test_prefill_rows_are_causal(torch_mod, gsp, ctx, dt):
     """Rows with q_len > 1: query i attends to min(TokenCount, pos + i + 1) tokens."""
