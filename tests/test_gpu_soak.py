@@ -9,6 +9,8 @@ pair) and 1 to 1000 workgroups (so pieces of one pair land on different CUs and
 XCDs, in every order), over several geometries, fp32 and fp16 pages, decode and
 prefill rows, and stops at the first output that differs from the oracle.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -25,7 +27,8 @@ GEOMS = [
     (64, 8, 128, 128, 16, "f16"),
     (32, 1, 96, 80, 8, "f32"),
 ]
-STEPS_PER_GEOM = 60
+# GSP_SOAK_STEPS lengthens the soak (steps per geometry).
+STEPS_PER_GEOM = int(os.environ.get("GSP_SOAK_STEPS", "60"))
 
 
 @pytest.mark.parametrize("geom", GEOMS, ids=lambda g: f"{g[0]}q{g[1]}kv_d{g[2]}_dv{g[3]}_bs{g[4]}_{g[5]}")
