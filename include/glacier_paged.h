@@ -244,18 +244,18 @@ typedef struct gsp_step_desc {
 } gsp_step_desc;
 
 /* Validates and packs one engine step for `pool` (its KV-head count and
- * block count) and uploads it with a single host-to-device copy on the
- * context's stream; the packed step serves every layer of that pool.  Query
+ * block count) and uploads it in one copy (a copy kernel that reads the
+ * pinned staging buffer) on the context's stream; the packed step serves every layer of that pool.  Query
  * token i of row b sits at pos = positions[b] + i and attends to
  *     total = min(token_counts[b], pos + 1)           (PagedAttentionKernel.cs:41)
  * tokens (causal for q_lens[b] > 1, PagedTransformerRunner.cs:454-474); a row
  * whose every query token has total == 0 is skipped and its out rows are left
- * untouched (PagedAttentionKernel.cs:42).  Only the first ceil(total/16) table
- * entries of a row are packed.  Errors (GSP_E_INVALID_ARG):
+ * untouched (PagedAttentionKernel.cs:42).  Only the first ceil(total/block_size)
+ * table entries of a row are packed.  Errors (GSP_E_INVALID_ARG):
  *   max_seq_len <= 0; pos < 0 or pos + q_len - 1 >= max_seq_len
  *   (PagedAttentionKernel.cs:34-37); token_counts[b] > max_seq_len (:38-39);
  *   bt_offsets outside [0, n_bt_ids] or decreasing; a row's table shorter
- *   than ceil(total/16); a block id outside the pool. */
+ *   than ceil(total/block_size); a block id outside the pool. */
 int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc);
 
 /* Sizes of the packed step (for tests and the bench). */
