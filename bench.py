@@ -22,6 +22,10 @@ left in the 256 MB Infinity Cache.  Prints ONE JSON line (per workload with
                operand pairs, 3 fp16 products per fp32 product (2 for fp16
                pages): its roofline is those fp16 products against the
                2.5 PFLOP/s dense fp16 matrix peak.
+  stream_ceiling  (decode-only steps) a plain non-temporal streaming read of
+               the same bytes, over L buffers in turn and timed the same way,
+               on the same GPU in the same run: what this GPU streams cold at
+               all, and the decode kernel's rate as a share of it
   cpu_baseline the CPU oracle (C++ restatement of the reference kernel) timed
                on this host on the same inputs
 --profile-only runs only the packed step's warmup and timed launches (and, for
@@ -358,6 +362,10 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         "roofline": roofline,
     })
     result.update(extra)
+    if not len(tiled):
+        ceiling = stream_ceiling(torch, stream, kv_bytes, layers, steps)
+        ceiling["decode_vs_ceiling"] = round(gbs / ceiling["gbs"], 4)
+        result["stream_ceiling"] = ceiling
     if cpu:
         result["cpu_baseline"], ref = cpu_baseline(step, q, k, v, cpu_budget_s)
         err = float(np.nanmax(np.abs(got.astype(np.float64) - ref.astype(np.float64))))
@@ -370,6 +378,53 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     pool.destroy()
     ctx.close()
     return result
+
+
+def stream_ceiling(torch, stream, nbytes: int, layers: int, steps: int) -> dict:
+    """A plain non-temporal 16-byte streaming read of nbytes (libglacier_probe.so),
+    over `layers` buffers in turn as the decode steps rotate layers, with one
+    untimed launch ahead of the first event and `steps` launches back to back:
+    the decode timing's bracket around a kernel that only streams.  Best of two
+    grid sizes."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(ROOT / "glacier.serve_amd" / "libglacier_probe.so"))
+    fn = lib.gsp_probe_stream_read
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    n = (nbytes + 15) // 16 * 16
+    grids = (1024, 2048)
+    bufs = [torch.zeros(n, dtype=torch.uint8, device="cuda") for _ in range(layers)]
+    sink = torch.zeros(max(grids), dtype=torch.int32, device="cuda")
+
+    def launch(i: int, grid: int) -> None:
+        rc = fn(bufs[i % layers].data_ptr(), n, grid, sink.data_ptr(), stream.cuda_stream)
+        if rc:
+            raise RuntimeError(f"stream probe launch failed (code {rc})")
+
+    best = None
+    for grid in grids:
+        for i in range(layers):
+            launch(i, grid)
+        launch(layers - 1, grid)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            launch(i, grid)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / steps * 1e3
+        if best is None or us < best[0]:
+            best = (us, grid)
+    del bufs, sink
+    torch.cuda.empty_cache()
+    us, grid = best
+    gbs = n / us / 1e3
+    return {"us": round(us, 2), "gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "grid": grid,
+            "bytes": n, "note": f"plain non-temporal 16-byte streaming read of the step's KV bytes over {layers} "
+                                f"buffers in turn, {steps} launches back to back, same GPU and run; best of grids "
+                                f"{grids[0]} and {grids[1]}"}
 
 
 def matmul_timing(gsp, torch, ctx, stream, step, calls: int = 50) -> dict:

@@ -1,4 +1,5 @@
-"""Builds libglacier_paged.so (gfx950 kernels + host runtime + C ABI) in-tree.
+"""Builds libglacier_paged.so (gfx950 kernels + host runtime + C ABI) in-tree, and
+libglacier_probe.so, the streaming-read probe that bench.py times beside it.
 
     python glacier.serve_amd/build.py
 
@@ -16,6 +17,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libglacier_paged.so"
+PROBE_LIB = PKG / "libglacier_probe.so"
+PROBE_SOURCES = [CSRC / "gsp_stream_probe.hip"]
 
 SOURCES = [
     CSRC / "gsp_decode.hip",
@@ -48,7 +51,13 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    tmp = LIB.with_suffix(".so.tmp")
+    _compile(SOURCES, LIB, verbose)
+    _compile(PROBE_SOURCES, PROBE_LIB, verbose)
+    return LIB
+
+
+def _compile(sources, lib: Path, verbose: bool) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [
         hipcc(),
         f"--offload-arch={ARCH}",
@@ -64,7 +73,7 @@ def build(verbose: bool = False) -> Path:
         *DEVICE_FLAGS,
         "-x",
         "hip",
-        *[str(s) for s in SOURCES],
+        *[str(s) for s in sources],
         "-o",
         str(tmp),
     ]
@@ -79,8 +88,7 @@ def build(verbose: bool = False) -> Path:
         lines = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln]
         if lines:
             print("\n".join(lines))
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
 
 
 if __name__ == "__main__":
