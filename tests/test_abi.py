@@ -52,3 +52,13 @@ def test_abi_version_and_error_string():
     rc = lib.gsp_block_allocator_create(0, 16, ctypes.byref(h))
     assert rc == gp.GSP_E_INVALID_ARG
     assert b"totalBlocks" in lib.gsp_last_error()
+
+
+def test_probe_library_exports_only_the_stream_probe():
+    """libglacier_probe.so (bench.py's streaming-read ceiling) is separate from the boundary."""
+    probe = Path(gp.LIB_PATH).with_name("libglacier_probe.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", str(probe)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    assert {n for n in exported if n.startswith("gsp_")} == {"gsp_probe_stream_read"}
+    assert "gsp_probe_stream_read" not in declared_functions()
