@@ -384,47 +384,50 @@ def stream_ceiling(torch, stream, nbytes: int, layers: int, steps: int) -> dict:
     """A plain non-temporal 16-byte streaming read of nbytes (libglacier_probe.so),
     over `layers` buffers in turn as the decode steps rotate layers, with one
     untimed launch ahead of the first event and `steps` launches back to back:
-    the decode timing's bracket around a kernel that only streams.  Best of two
-    grid sizes."""
+    the decode timing's bracket around a kernel that only streams.  Best of nine
+    launch shapes (grids 512, 1024, 2048 x 2, 4, 8 loads in flight per lane)."""
     import ctypes
 
     lib = ctypes.CDLL(str(ROOT / "glacier.serve_amd" / "libglacier_probe.so"))
     fn = lib.gsp_probe_stream_read
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     fn.restype = ctypes.c_int
     n = (nbytes + 15) // 16 * 16
-    grids = (1024, 2048)
+    grids = (512, 1024, 2048)
+    depths = (2, 4, 8)
     bufs = [torch.zeros(n, dtype=torch.uint8, device="cuda") for _ in range(layers)]
     sink = torch.zeros(max(grids), dtype=torch.int32, device="cuda")
 
-    def launch(i: int, grid: int) -> None:
-        rc = fn(bufs[i % layers].data_ptr(), n, grid, sink.data_ptr(), stream.cuda_stream)
+    def launch(i: int, grid: int, depth: int) -> None:
+        rc = fn(bufs[i % layers].data_ptr(), n, grid, depth, sink.data_ptr(), stream.cuda_stream)
         if rc:
             raise RuntimeError(f"stream probe launch failed (code {rc})")
 
     best = None
     for grid in grids:
-        for i in range(layers):
-            launch(i, grid)
-        launch(layers - 1, grid)
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(steps):
-            launch(i, grid)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) / steps * 1e3
-        if best is None or us < best[0]:
-            best = (us, grid)
+        for depth in depths:
+            for i in range(layers):
+                launch(i, grid, depth)
+            launch(layers - 1, grid, depth)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(steps):
+                launch(i, grid, depth)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / steps * 1e3
+            if best is None or us < best[0]:
+                best = (us, grid, depth)
     del bufs, sink
     torch.cuda.empty_cache()
-    us, grid = best
+    us, grid, depth = best
     gbs = n / us / 1e3
     return {"us": round(us, 2), "gbs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "grid": grid,
-            "bytes": n, "note": f"plain non-temporal 16-byte streaming read of the step's KV bytes over {layers} "
-                                f"buffers in turn, {steps} launches back to back, same GPU and run; best of grids "
-                                f"{grids[0]} and {grids[1]}"}
+            "loads_in_flight_per_lane": depth, "bytes": n,
+            "note": f"plain non-temporal 16-byte streaming read of the step's KV bytes over {layers} buffers in turn, "
+                    f"{steps} launches back to back, same GPU and run; best of grids {'/'.join(map(str, grids))} x "
+                    f"{'/'.join(map(str, depths))} loads in flight per lane"}
 
 
 def matmul_timing(gsp, torch, ctx, stream, step, calls: int = 50) -> dict:
