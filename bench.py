@@ -50,7 +50,8 @@ sys.path.insert(0, str(ROOT / "glacier.serve_amd"))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged-attn decode KV GB/s (% HBM peak) + seq-steps/sec, Qwen2.5-7B shape"
-WORKLOADS = ["qwen05b_decode", "qwen7b_decode", "llama8b_decode", "qwen7b_mixed", "longctx_decode"]
+WORKLOADS = ["qwen05b_decode", "qwen7b_decode", "llama8b_decode", "qwen7b_mixed", "longctx_decode",
+             "refmodel_decode"]
 DEFAULT_WORKLOAD = "qwen7b_decode"
 KERNEL_NAME = "paged_decode_mfma_kernel"
 PREFILL_KERNEL_NAME = "paged_prefill_mfma_kernel"
@@ -62,6 +63,7 @@ PREFILL_TILE_MIN_Q = 16     # rows the library runs as prefill tiles by default
 # Host threads a job may use per GPU on the measurement hosts: their CPU share
 # is 16 cores per GPU, whatever sched_getaffinity shows.
 HOST_CPU_SHARE = 16
+CPU_WARMUP_STEPS = 5  # untimed CPU baseline steps before the timed ones
 
 
 def visible_cores() -> int:
@@ -136,8 +138,9 @@ def describe(step, layers: int) -> dict:
         "heads_q": step.n_heads,
         "heads_kv": step.n_kv,
         "head_dim": step.head_dim,
+        "v_head_dim": step.dv,
         "kv_dtype": step.kv_dtype,
-        "block_size": 16,
+        "block_size": step.block_size,
         "pool_blocks": step.total_blocks,
         "pool_layers": layers,
         "layer_per_step": "step i attends layer i mod pool_layers",
@@ -177,8 +180,9 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     torch.cuda.set_stream(stream)
     ctx.set_stream(stream.cuda_stream)
     pool = gsp.Pool.wrap(ctx, k.data_ptr(), v.data_ptr(), step.total_blocks, layers, step.n_kv, step.head_dim,
-                         gsp.KV_F16 if step.kv_dtype == "f16" else gsp.KV_F32)
-    out = torch.empty((step.total_q, step.n_heads, step.head_dim), device="cuda", dtype=torch.float32)
+                         gsp.KV_F16 if step.kv_dtype == "f16" else gsp.KV_F32, v_head_dim=step.dv,
+                         block_size=step.block_size)
+    out = torch.empty((step.total_q, step.n_heads, step.dv), device="cuda", dtype=torch.float32)
 
     def pack():
         return ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
@@ -305,7 +309,7 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
     for i in range(5):
         pack()
         attend(i % layers)
-    pack_ns, periods = [], []
+    pack_ns, wait_ns, periods = [], [], []
     torch.cuda.synchronize()
     t0 = t_prev = time.perf_counter()
     for i in range(n_step):
@@ -315,9 +319,24 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
         periods.append(t_now - t_prev)
         t_prev = t_now
         pack_ns.append(info_i.pack_host_ns)
+        wait_ns.append(info_i.pack_wait_ns)
     torch.cuda.synchronize()
     t_step_mean_ms = (time.perf_counter() - t0) * 1e3 / n_step
     t_step_ms = float(np.median(periods[n_step // 4:])) * 1e3
+    # The step's upload on the device: events around the pack's copy kernel, each enqueued
+    # behind a running attention step (the host packs while that kernel runs), so the interval
+    # is the copy kernel with its launch and the two events' own latency, not the host's packing.
+    ups = []
+    for i in range(20):
+        attend(i % layers)
+        u0 = torch.cuda.Event(enable_timing=True)
+        u1 = torch.cuda.Event(enable_timing=True)
+        u0.record(stream)
+        pack()
+        u1.record(stream)
+        ups.append((u0, u1))
+    torch.cuda.synchronize()
+    upload_us = float(np.median([a.elapsed_time(b) for a, b in ups])) * 1e3
 
     # Distribution of single steps: each between its own events on the launch
     # stream and waited for alone, so it includes one launch's start-up that the
@@ -347,7 +366,17 @@ def run_workload(name: str, steps: int, warmup: int, cpu: bool, cpu_budget_s: fl
             "t_step_ms_p90": round(float(np.percentile(periods[n_step // 4:], 90)) * 1e3, 5),
             "t_step_ms_max": round(max(periods) * 1e3, 3),
             "pack_host_us_median": round(float(np.median(pack_ns)) / 1e3, 2),
+            "pack_wait_us_median": round(float(np.median(wait_ns)) / 1e3, 2),
+            "pack_work_us_median": round(float(np.median(np.array(pack_ns) - np.array(wait_ns))) / 1e3, 2),
+            "upload_interval_us_median": round(upload_us, 2),
             "kernel_ms": round(kernel_ms, 5),
+            "step_overhead_us": round(t_step_ms * 1e3 - kernel_ms * 1e3, 2),
+            "notes": "pack_host = pack_work (validation, plan, staging; on the host while the previous step's "
+                     "kernel runs) + pack_wait (the host, ahead of the GPU, waiting for the staging slot's "
+                     "upload of two steps before: back-pressure, off the device's path); step_overhead = "
+                     "t_step - kernel_ms is what the device spends per step beyond the attention kernel (the "
+                     "upload copy kernel and launch gaps); upload_interval brackets the copy kernel with two "
+                     "events and so also holds their latency",
             "steps": n_step,
         },
         "seq_steps_per_s_kernel_only": round(step.num_rows / (ms_per_step * 1e-3), 1),
@@ -490,15 +519,15 @@ def kv_write_timing(gsp, torch, ctx, stream, step, pool, layers: int, calls: int
     gen = torch.Generator(device="cuda").manual_seed(step.seed)
     q = torch.randn((n, step.n_heads, step.head_dim), device="cuda", generator=gen)
     k = torch.randn((n, step.n_kv, step.head_dim), device="cuda", generator=gen)
-    v = torch.randn((n, step.n_kv, step.head_dim), device="cuda", generator=gen)
+    v = torch.randn((n, step.n_kv, step.dv), device="cuda", generator=gen)
     base, style = 1000000.0, gsp.ROPE_HALVES
     pos, blocks, slots = [], [], []
     for b in range(step.num_rows):
         for i in range(int(step.lens[b])):
             p = int(step.positions[b]) + i
             pos.append(p)
-            blocks.append(int(step.table(b)[p // 16]))
-            slots.append(p % 16)
+            blocks.append(int(step.table(b)[p // step.block_size]))
+            slots.append(p % step.block_size)
     pos, blocks, slots = (np.array(x, np.int32) for x in (pos, blocks, slots))
     torch.cuda.synchronize()
 
@@ -545,8 +574,8 @@ def kv_write_timing(gsp, torch, ctx, stream, step, pool, layers: int, calls: int
     except Exception as exc:  # the eager figures stand alone
         us_graph = "graph capture failed: " + str(exc)
     elem = 2 if step.kv_dtype == "f16" else 4
-    moved = n * (2 * step.n_heads * step.head_dim * 4 + 2 * step.n_kv * step.head_dim * 4
-                 + 2 * step.n_kv * step.head_dim * elem)
+    moved = n * (2 * step.n_heads * step.head_dim * 4 + step.n_kv * (step.head_dim + step.dv) * 4
+                 + step.n_kv * (step.head_dim + step.dv) * elem)
     return {"tokens": n, "us_per_layer_call": round(us_step, 2), "us_per_layer_call_graph": us_graph,
             "bytes_per_call": moved,
             "gbs": round(moved / (us_step * 1e-6) / 1e9, 1), "us_per_call_host_arrays": round(us_host, 2),
@@ -599,15 +628,23 @@ def cpu_baseline(step, q, k, v, budget_s: float):
     vh = v.index_select(0, idx)[:, :1].float().cpu().numpy()
     qh = q.cpu().numpy()
     ids = inv.astype(np.int32)
-    pool = orc.HostPool(kh, vh)
+    pool = orc.HostPool(kh, vh, block_size=step.block_size)
     nt = cpu_threads()
-    out = np.zeros((step.total_q, step.n_heads, step.head_dim), np.float32)
+    out = np.zeros((step.total_q, step.n_heads, step.dv), np.float32)
 
     def one():
         orc.attention_step(pool, 0, step.positions, step.token_counts, step.bt_offsets, ids, qh, step.n_heads,
                            step.scale, step.max_seq_len, q_lens=step.q_lens, out=out, n_threads=nt)
 
-    one()  # warm-up (also the parity reference)
+    # Five warm-up steps, as the reference benchmark warms up (Program.cs:101-115); the first is also
+    # the parity reference.  Fewer when one step would eat a tenth of the budget.
+    warm = 0
+    t_warm = time.perf_counter()
+    while warm < CPU_WARMUP_STEPS:
+        one()
+        warm += 1
+        if time.perf_counter() - t_warm > budget_s / 10:
+            break
     times = []
     t_start = time.perf_counter()
     while len(times) < 20 and (time.perf_counter() - t_start) < budget_s:
@@ -620,8 +657,8 @@ def cpu_baseline(step, q, k, v, budget_s: float):
         "unit": "GB/s",
         "cores": nt,
         "kind": "port",
-        "sample": f"whole {step.name} step ({step.num_rows} rows), median of {len(times)} steps "
-                  f"(budget {budget_s:.0f} s), {nt} threads on '{cpu_model()}' ({visible_cores()} cores visible "
+        "sample": f"whole {step.name} step ({step.num_rows} rows), median of {len(times)} steps after {warm} "
+                  f"warm-up steps (budget {budget_s:.0f} s), {nt} threads on '{cpu_model()}' ({visible_cores()} cores visible "
                   f"to the process, {HOST_CPU_SHARE} per GPU allotted to a job on this host), ISA level "
                   f"{orc.host_isa()} (2=AVX-512, 1=AVX2); C++ restatement of the reference C# kernel",
         "ms_per_step": round(med * 1e3, 3),

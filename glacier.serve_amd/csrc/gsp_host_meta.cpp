@@ -159,7 +159,7 @@ int gsp_block_table_attach_prefix(gsp_block_table* t, const int32_t* ids, int32_
 
 int gsp_block_table_append_token(gsp_block_table* t, int32_t* block_id, int32_t* offset) {
     gsp::clear_error();
-    if (!t || !block_id || !offset) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument"), 0;
+    if (!t || !block_id || !offset) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument"), -1;
     gsp_block_allocator* a = t->alloc;
     const int32_t bs = a->block_size;
     if (t->token_count % bs == 0) {

@@ -8,6 +8,7 @@
 // host code never passes it to a kernel or a copy: gsp_init looks the device
 // address up once per device (with that device current) through
 // hipGetSymbolAddress, and every later use goes through that pointer.
+#include <atomic>
 #include <mutex>
 
 #include "../../include/glacier_paged.h"
@@ -20,8 +21,11 @@ static_assert(GSP_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size is a multiple 
 static __device__ __align__(256) unsigned char scratch[GSP_NOALLOC_SCRATCH_BYTES];
 
 constexpr int kMaxDevices = 64;
+// The lookup runs once per device under the mutex; the per-call read of the
+// pointer (noalloc_scratch) takes no lock: the pointer is published with a
+// release store and read with an acquire load, and never changes afterwards.
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
+std::atomic<void*> g_scratch_ptr[kMaxDevices];  // static storage: zero (nullptr) before any store
 
 }  // namespace
 
@@ -30,19 +34,18 @@ namespace gsp {
 hipError_t noalloc_setup(int device) {
     if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if (g_scratch_ptr[device]) return hipSuccess;
+    if (g_scratch_ptr[device].load(std::memory_order_acquire)) return hipSuccess;
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return e;
     if (!p) return hipErrorInvalidSymbol;
-    g_scratch_ptr[device] = p;
+    g_scratch_ptr[device].store(p, std::memory_order_release);
     return hipSuccess;
 }
 
 void* noalloc_scratch(int device) {
     if (device < 0 || device >= kMaxDevices) return nullptr;
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    return g_scratch_ptr[device];
+    return g_scratch_ptr[device].load(std::memory_order_acquire);
 }
 
 }  // namespace gsp

@@ -589,6 +589,8 @@ __device__ __forceinline__ void pair_softmax(TileState<D>& st, f4& s0, f4& s1, b
 // stored.  It costs no time: the page barrier waits for the busiest wave.
 // This form splits the fp32 pages it reads itself (fp16 pages need no split);
 // prefill_tile_body_rec below reads the step's split records instead.
+// LIVE (<= TILES) is the number of tiles this wave computes; it bounds only
+// the per-tile loops, never a barrier (see prefill_tile).
 template <int D, typename KT, int TILES, int LIVE = TILES>
 __device__ __forceinline__ void prefill_tile_body(const PrefillArgs& a, PfLds<D, KT>& sh, int bx, int by) {
     constexpr int kPrefillTiles = TILES;
@@ -918,6 +920,7 @@ __device__ __forceinline__ void pair_softmax_rec(float& m, float& l, f4& s0, f4&
     l = l * alpha + (((s0[0] + s0[1]) + (s0[2] + s0[3])) + ((s1[0] + s1[1]) + (s1[2] + s1[3])));
 }
 
+// LIVE bounds only the per-tile loops, never a barrier (see prefill_tile).
 template <int D, int TILES, int LIVE = TILES>
 __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLdsPipe<D>& sh, int bx, int by) {
     constexpr int kRow = D + 8;
@@ -1178,7 +1181,13 @@ __device__ __forceinline__ void prefill_tile_body_rec(const PrefillArgs& a, PfLd
 // Runs tile workgroup (bx, by) of either body.  With two tiles per wave, a
 // wave whose second head is past the group (wave + 4 >= G: groups of 5 to 7
 // heads, or a partial last head chunk) computes its first tile only; its
-// barriers and copies are the same, so the workgroup stays in step.  Skipping
+// barriers and copies are the same, so the workgroup stays in step.  The
+// waves of one workgroup then run different instantiations (LIVE = 1 and
+// LIVE = TILES), which is correct only because LIVE bounds nothing but the
+// unrolled per-tile loops of straight-line arithmetic: every barrier, LDS
+// copy and page load of the bodies sits outside those loops and runs the same
+// number of times in both.  Keep it so: a barrier inside a LIVE-bounded loop
+// would leave the workgroup's waves at different barriers.  Skipping
 // the padding tile's products took a Qwen2.5-7B-shape batch of sixteen prefill
 // chunks (group 7) from 268-273 us to 260-263 us.
 template <int D, typename KT, int TILES, bool REC, typename Sh>

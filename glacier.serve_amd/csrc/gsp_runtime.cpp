@@ -1379,6 +1379,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     if (rc) return rc;
     // The other slot than the step packed last: its kernels may still run.
     const int slot = ctx->slot ^ 1;
+    const auto t_wait0 = std::chrono::steady_clock::now();
     if (ctx->slot_captured[slot]) {  // replays of a graph that read this slot
         rc = check_hip(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
         if (rc) return rc;
@@ -1388,6 +1389,8 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
         const size_t had = ctx->staging_words[slot];  // changes when the buffer is replaced
         rc = ensure_pinned(&ctx->staging[slot], &ctx->staging_words[slot], words16, ctx->upload_done[slot],
                            &ctx->upload_pending[slot], hipHostMallocMapped | hipHostMallocCoherent);
+        ctx->info.pack_wait_ns =
+            std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t_wait0).count();
         if (!rc && (ctx->staging_words[slot] != had || !ctx->staging_dev[slot])) {
             void* dp = nullptr;
             rc = check_hip(hipHostGetDevicePointer(&dp, ctx->staging[slot], 0), "hipHostGetDevicePointer(staging)");

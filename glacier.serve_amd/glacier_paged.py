@@ -141,6 +141,7 @@ class StepInfo(ctypes.Structure):
         ("decode_bins", i32),
         ("split_records", i32),
         ("pack_host_ns", ctypes.c_int64),
+        ("pack_wait_ns", ctypes.c_int64),
     ]
 
 

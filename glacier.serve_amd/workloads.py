@@ -15,6 +15,8 @@ The five measured shapes:
   qwen7b_mixed     28/4 heads, d=128, 48 decode rows ctx U[256,4096] + 16 prefill rows
                    (prior U[0,2048], chunk U[32,512], causal), 32768 blocks, fp32
   longctx_decode   64/8 heads, d=128, 16 rows, ctx U[16384,32768], fp16, 32768 blocks
+Beside them, refmodel_decode: the reference's test-model attention (2/1 heads, d=32,
+8-token pages) at 256 rows, ctx log-uniform [128,4096], fp32, 65536 blocks.
 """
 from __future__ import annotations
 
@@ -238,6 +240,16 @@ def llama8b_decode(seed: int = SEED_BASE + 3, make_alloc: Optional[Callable] = N
                 notes={"admit_evict_steps": steps, "p_admit": 0.55, "sigma": 1.0})
     step.notes["allocated_blocks"] = total_blocks - int(alloc.free_blocks_count)
     return step
+
+
+def refmodel_decode(seed: int = SEED_BASE + 6) -> Step:
+    """The attention geometry of the reference's own GPU test model (2 query / 1 KV heads, head_dim 32,
+    8-token pages; PhaseCServeRemediationTests.cs:330-352), at serving batch: 256 rows, contexts
+    log-uniform in [128, 4096], fp32, a 65536-block pool.  It runs the decode kernel's general form
+    (run-time widths and page size)."""
+    rng = np.random.default_rng(seed)
+    ctx = np.rint(np.exp(rng.uniform(math.log(128), math.log(4096), size=256))).astype(np.int32)
+    return decode_step("refmodel_decode", rng, ctx, 2, 1, 32, "f32", 65536, 4096, seed, block_size=8)
 
 
 CONFIGS = {

@@ -277,6 +277,9 @@ typedef struct gsp_step_info {
     int32_t split_records;       /* page-pair split records of fp32 tiles (0: the tiles split their pages) */
     int64_t pack_host_ns;        /* host time of the gsp_step_pack call that made the step:
                                     validation, scheduling, staging and the copy's enqueue */
+    int64_t pack_wait_ns;        /* the part of pack_host_ns spent waiting for the staging
+                                    slot: the upload that used it two packs earlier (and, after a
+                                    capture read the slot, the context's stream) */
 } gsp_step_info;
 
 int gsp_step_get_info(const gsp_ctx* ctx, gsp_step_info* out);
@@ -364,7 +367,11 @@ int gsp_set_prefill_split(gsp_ctx* ctx, int32_t mode);
  * rewritten two packs later, once that copy is done.
  * Graph capture: the call can be captured on the context's stream once the
  * packed step's upload is known complete (gsp_sync after gsp_step_pack;
- * otherwise GSP_E_STATE).  The graph holds the step's kernels only and reads
+ * otherwise GSP_E_STATE).  gsp_step_pack sizes the split-KV workspace for
+ * GQA groups up to 16 (it does not know n_heads); a larger group needs
+ * ceil(group / 16) times that, which the first eager call with that group
+ * allocates: run one before capturing (a captured call that would have to
+ * grow the workspace fails with GSP_E_STATE and enqueues nothing).  The graph holds the step's kernels only and reads
  * the packed step's slot: it is valid until the next gsp_step_pack.  The pack
  * after that reuses the slot and first waits on the host for the context's
  * stream; replays launched on other streams must have finished by then. */
@@ -469,9 +476,10 @@ int gsp_block_table_attach_prefix(gsp_block_table* t, const int32_t* ids, int32_
                                   int32_t token_count);
 /* AppendToken (BlockTable.cs:46-80): 1 on success, 0 on pool exhaustion with
  * the table unchanged and *block_id = *offset = -1.  -1 with GSP_E_INVALID_ARG
- * set (table unchanged) where the reference throws: TokenCount is inside a
- * page but the table holds no page (an empty prefix attached with a nonzero
- * token count; `_physicalBlockIds[^1]`, BlockTable.cs:60). */
+ * set (table unchanged) for a NULL argument, and where the reference throws:
+ * TokenCount is inside a page but the table holds no page (an empty prefix
+ * attached with a nonzero token count; `_physicalBlockIds[^1]`,
+ * BlockTable.cs:60). */
 int gsp_block_table_append_token(gsp_block_table* t, int32_t* block_id, int32_t* offset);
 /* AppendToken n times, as a prefill chunk reserves its slots
  * (PagedTransformerRunner.cs:383-401); stops at the first failure.  Returns

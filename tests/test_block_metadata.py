@@ -285,3 +285,19 @@ def test_append_token_on_an_empty_partial_table_raises():
     t2.attach_prefix_blocks([], 16)
     ok, b, off = t2.append_token()
     assert ok and b == 0 and off == 0 and t2.token_count == 17
+
+
+def test_append_token_null_arguments_are_errors_not_exhaustion():
+    """A NULL output pointer is an invalid argument (-1 with GSP_E_INVALID_ARG), never the 0 that
+    means the pool is exhausted; the table and the pool stay unchanged."""
+    import ctypes
+
+    a = gp.BlockAllocator(4, 16)
+    t = gp.BlockTable(a)
+    lib = gp.load()
+    b = ctypes.c_int32()
+    assert lib.gsp_block_table_append_token(t._h, None, ctypes.byref(b)) == -1
+    assert lib.gsp_block_table_append_token(t._h, ctypes.byref(b), None) == -1
+    assert lib.gsp_block_table_append_token(None, ctypes.byref(b), ctypes.byref(b)) == -1
+    assert t.token_count == 0 and t.block_count == 0 and a.free_blocks_count == 4
+    assert t.append_token()[0]

@@ -16,13 +16,18 @@ from gpu_helpers import TOL, max_err, oracle_step, to_device_pool
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("kind", ["mixed", "decode_split"])
+@pytest.mark.parametrize("kind", ["mixed", "decode_split", "decode_group32"])
 def test_captured_step_replays_match_eager(torch_mod, gsp, ctx, kind):
+    """For a GQA group above 16 (two head tiles) the eager call before the capture grows the split
+    workspace to the step's tiles, as the header asks."""
     torch = torch_mod
     if kind == "mixed":
         q_lens = np.array([1, 24, 1, 40, 1, 3, 1, 17], np.int32)
         step = workloads.small_step(seed=41, rows=8, n_heads=28, n_kv=4, head_dim=128, ctx_hi=300,
                                     total_blocks=512, q_lens=q_lens)
+    elif kind == "decode_group32":
+        step = workloads.small_step(seed=43, rows=9, n_heads=32, n_kv=1, head_dim=128, ctx_lo=100, ctx_hi=900,
+                                    total_blocks=1024)
     else:
         step = workloads.small_step(seed=42, rows=16, n_heads=28, n_kv=4, head_dim=128, ctx_lo=100, ctx_hi=900,
                                     total_blocks=1024)
@@ -32,7 +37,7 @@ def test_captured_step_replays_match_eager(torch_mod, gsp, ctx, kind):
     stream = torch.cuda.Stream()
     ctx.set_stream(stream.cuda_stream)
     try:
-        ctx.set_split_pages(3 if kind == "decode_split" else 0)
+        ctx.set_split_pages(3 if kind.startswith("decode") else 0)
         info = ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
                              q_lens=step.q_lens)
         ctx.set_split_pages(0)
@@ -68,6 +73,43 @@ def test_captured_step_replays_match_eager(torch_mod, gsp, ctx, kind):
     finally:
         ctx.set_stream(None)  # back to the context's own stream
         pool.destroy()
+
+
+def test_capture_that_would_grow_the_workspace_fails_cleanly(torch_mod, gsp):
+    """A fresh context packs a group-32 step (workspace sized for one head tile) and captures its
+    first gsp_attention_step: the call must refuse with a state error before enqueuing anything,
+    and an eager call afterwards must work."""
+    torch = torch_mod
+    step = workloads.small_step(seed=44, rows=6, n_heads=32, n_kv=1, head_dim=128, ctx_lo=100, ctx_hi=600,
+                                total_blocks=512)
+    print("graph case capture-without-eager group 32", flush=True)
+    q, k, v = workloads.host_values(step)
+    with gsp.Context(0) as fresh:
+        pool, keep = to_device_pool(torch, gsp, fresh, step, k, v)
+        stream = torch.cuda.Stream()
+        fresh.set_stream(stream.cuda_stream)
+        try:
+            fresh.set_split_pages(3)
+            info = fresh.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids,
+                                   step.max_seq_len)
+            assert info.split_pairs > 0
+            qd = torch.from_numpy(q).cuda()
+            out = torch.full((step.total_q, step.n_heads, step.head_dim), float("nan"), device="cuda")
+            fresh.sync()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with pytest.raises(gsp.StateError):
+                with torch.cuda.graph(graph, stream=stream):
+                    fresh.attention_step(pool, 0, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
+            del graph
+            torch.cuda.synchronize()
+            with torch.cuda.stream(stream):
+                fresh.attention_step(pool, 0, step.n_heads, qd.data_ptr(), out.data_ptr(), step.scale)
+            stream.synchronize()
+            assert max_err(out.cpu().numpy(), oracle_step(step, q, k, v)) <= TOL[step.kv_dtype]
+        finally:
+            fresh.set_stream(None)
+            pool.destroy()
 
 
 def _graph_node_types(graph) -> list:

@@ -24,6 +24,8 @@ SPLITS = {"records": 0, "in_tile": 1}
 
 GEOMS = [
     (28, 4, 128, "f32"),  # group 7
+    (20, 4, 128, "f32"),  # group 5: waves 1-3 compute one tile, wave 0 two
+    (24, 4, 64, "f32"),   # group 6: waves 2-3 compute one tile
     (14, 2, 64, "f32"),   # group 7, d64
     (32, 8, 128, "f16"),  # group 4
     (8, 1, 128, "f32"),   # group 8: one full head chunk

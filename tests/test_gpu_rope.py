@@ -216,3 +216,65 @@ def test_step_writes_match_the_explicit_writes(torch_mod, gsp, ctx, dt):
     small.destroy()
     for p in pools:
         p.destroy()
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_engine_tick_sequence_over_layers(torch_mod, gsp, ctx, dt):
+    """The per-tick sequence the integration prescribes (PagedTransformerRunner.cs:605-659 per layer):
+    one gsp_step_pack for the tick, then for every layer gsp_rope_write_step (Q rotated in place, K
+    rotated and stored, V stored at each query token's own slot) followed by gsp_attention_step on
+    that layer.  Three layers, decode rows plus a prefill chunk (stored whole before its causal
+    attention), each layer with its own Q/K/V, against the oracle doing the same rotation, store and
+    attention layer by layer on the host arenas."""
+    torch = torch_mod
+    nh, nkv, d, base, layers = 28, 4, 128, 1000000.0, 3
+    q_lens = np.array([1, 1, 23, 1, 1], np.int32)
+    step = workloads.small_step(seed=131, rows=5, n_heads=nh, n_kv=nkv, head_dim=d, kv_dtype=dt, ctx_lo=10,
+                                ctx_hi=300, total_blocks=256, q_lens=q_lens)
+    # Decode rows attend their newest token: position = TokenCount - 1 (the slot the tick allocated).
+    for b in range(step.num_rows):
+        if step.lens[b] == 1:
+            step.positions[b] = step.token_counts[b] - 1
+    print(f"case engine tick {dt} layers={layers}", flush=True)
+    rng = np.random.default_rng(132)
+    _, k, v = workloads.host_values(step, layers=layers)
+    pool, keep = to_device_pool(torch, gsp, ctx, step, k, v)
+    nq = step.total_q
+    qs = [rng.standard_normal((nq, nh, d)).astype(np.float32) for _ in range(layers)]
+    ks = [rng.standard_normal((nq, nkv, d)).astype(np.float32) for _ in range(layers)]
+    vs = [rng.standard_normal((nq, nkv, d)).astype(np.float32) for _ in range(layers)]
+    ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
+                  q_lens=step.q_lens)
+    outs = []
+    for l in range(layers):
+        qd = torch.from_numpy(qs[l]).cuda()
+        kd = torch.from_numpy(ks[l]).cuda()
+        vd = torch.from_numpy(vs[l]).cuda()
+        out = torch.full((nq, nh, d), float("nan"), device="cuda")
+        torch.cuda.synchronize()  # torch fills on its own stream, the library on the context's
+        pool.rope_write_step(l, nh, base, 1, qd.data_ptr(), kd.data_ptr(), vd.data_ptr())
+        ctx.attention_step(pool, l, nh, qd.data_ptr(), out.data_ptr(), step.scale)
+        ctx.sync()
+        outs.append(out.cpu().numpy())
+        del qd, kd, vd
+    pool.destroy()
+    # Oracle: the same rotation and store per layer on the host arenas (fp16 pools keep the rotated
+    # K and the V rounded once), then the reference attention of that layer.
+    npdt = np.float16 if dt == "f16" else np.float32
+    k2, v2 = k.copy(), v.copy()
+    for l in range(layers):
+        qr = np.empty_like(qs[l])
+        i = 0
+        for b in range(step.num_rows):
+            for t in range(int(step.lens[b])):
+                p = int(step.positions[b]) + t
+                qr[i] = orc.rope(qs[l][i], p, base, 1)
+                blk = int(step.table(b)[p // 16])
+                k2[blk, l, :, p % 16] = orc.rope(ks[l][i], p, base, 1).astype(npdt).astype(np.float32)
+                v2[blk, l, :, p % 16] = vs[l][i].astype(npdt).astype(np.float32)
+                i += 1
+        ref = oracle_step(step, qr, k2, v2, layer=l)
+        err = max_err(outs[l], ref)
+        print(f"layer {l}: max abs err {err:.3e}", flush=True)
+        assert not np.isnan(outs[l]).any()
+        assert err <= (1e-4 if dt == "f32" else 2e-3)
