@@ -28,6 +28,7 @@ SOURCES = [
     CSRC / "gsp_matmul.hip",
     CSRC / "gsp_noalloc.hip",
     CSRC / "gsp_runtime.cpp",
+    CSRC / "gsp_step_plan.cpp",
     CSRC / "gsp_host_meta.cpp",
     CSRC / "gsp_status.cpp",
 ]

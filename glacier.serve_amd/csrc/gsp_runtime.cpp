@@ -18,100 +18,13 @@
 #include "gsp_host_meta.h"
 #include "gsp_internal.h"
 #include "gsp_status.h"
+#include "gsp_step_plan.h"
 
 using gsp::DecodeUnit;
 using gsp::PrefillTile;
 namespace {
 
-// Packed step layout, in int32 elements from the start of the staging buffer.
-enum : int {
-    kHdrRows = 0,
-    kHdrTotalQ,
-    kHdrPages,
-    kHdrUnits,
-    kHdrTarget,
-    kHdrSlots,
-    kHdrMaxId,
-    kHdrPairsSplit,
-    kHdrHeadsKv,
-    kHdrTiles,
-    kHdrBins,
-    kHdrWords = 16
-};
-
-// Decode schedule.  The decode kernel is persistent: one workgroup per bin,
-// and each bin's units run back to back while the next unit's first pages
-// are already in flight.  The host packs units into bins longest first (LPT
-// list scheduling).  Within a bin, split pieces go first and whole pairs
-// last, so split merges finish while other work still streams rather than in
-// the kernel's tail.  Two bins per CU (the decode kernels' occupancy) keep a
-// second workgroup streaming while the first one is in a unit epilogue; one
-// workgroup alone can draw the CU's full share of HBM bandwidth, so the split
-// size is scored per CU.  A unit costs its pages plus a fixed transition; a
-// split piece also pays for publishing its partial and for its share of the
-// merge.
-constexpr int kDecodeBinsPerCu = 2;
-constexpr int64_t kUnitCostPages = 1;
-constexpr int64_t kSplitCostPages = 3;
-constexpr int32_t kSplitCandidates[] = {8,   12,  16,  20,  24,  32,  40,  48,  64,  80,   96,
-                                        128, 160, 192, 256, 384, 512, 768, 1024, 1536, 2048};
-
-// A step with few pages per workgroup is latency-bound: a unit of at most
-// four pages per wave streams in about two round trips, and a split would add
-// its publish, count and merge round trips for nothing (config 1 measured
-// 6.8 us whole against 7.6 us split).
-constexpr int64_t kWholePairMaxPages = 4 * gsp::kDecodeWaves;
-constexpr int64_t kUnderloadPagesPerBin = 4;
-
-int64_t unit_cost(int64_t pages, bool split) { return pages + kUnitCostPages + (split ? kSplitCostPages : 0); }
-
-// Makespan (in pages) of LPT-packing the units that `target` produces from
-// the per-query page counts into `bins` bins.
-int64_t simulate_split(const std::vector<int32_t>& pages, int32_t heads_kv, int32_t target, int64_t bins,
-                       std::vector<int64_t>& count, std::vector<int64_t>& heap) {
-    // count[2s] whole pairs of s pages, count[2s + 1] split pieces of s pages.
-    count.assign(2 * ((size_t)target + 1), 0);
-    int32_t longest = 0;
-    for (int32_t P : pages) {
-        const int32_t ns = std::min((P + target - 1) / target, gsp::kMaxSplits);
-        const int32_t base = P / ns, extra = P % ns;
-        const int sp = ns > 1 ? 1 : 0;
-        count[2 * ((size_t)base + 1) + sp] += (int64_t)extra * heads_kv;
-        count[2 * (size_t)base + sp] += (int64_t)(ns - extra) * heads_kv;
-        longest = std::max(longest, base + (extra ? 1 : 0));
-    }
-    heap.clear();
-    for (int32_t s = longest; s >= 1; --s) {
-        for (int sp = 1; sp >= 0; --sp) {
-            const int64_t cost = unit_cost(s, sp == 1);
-            for (int64_t c = count[2 * (size_t)s + sp]; c > 0; --c) {
-                if ((int64_t)heap.size() < bins) {
-                    heap.push_back(-cost);  // min-heap through negated loads
-                    std::push_heap(heap.begin(), heap.end());
-                } else {
-                    std::pop_heap(heap.begin(), heap.end());
-                    heap.back() -= cost;
-                    std::push_heap(heap.begin(), heap.end());
-                }
-            }
-        }
-    }
-    int64_t worst = 0;
-    for (int64_t x : heap) worst = std::max(worst, -x);
-    return worst;
-}
-
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
-// Rows of at least this many query tokens run as prefill tiles by default:
-// a tile reads each K/V page once for 16 query tokens, while shorter rows keep
-// the decode kernel's split-KV parallelism over long prefixes.
-constexpr int32_t kPrefillAutoMinQ = 16;
-
-bool row_is_tiled(int32_t path, int32_t q_len, bool tileable) {
-    if (!tileable || path == GSP_PREFILL_PER_TOKEN || q_len < 2) return false;
-    return path == GSP_PREFILL_TILES || q_len >= kPrefillAutoMinQ;
-}
 
 bool is_oom(hipError_t e) { return e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation; }
 
@@ -213,29 +126,10 @@ struct gsp_ctx {
     int32_t prefill_path = GSP_PREFILL_AUTO;
     int32_t prefill_split = GSP_SPLIT_RECORDS;
 
-    // Split size chosen for the last step shape (reused while the work drifts < 3%).
-    int32_t cached_target = 0;
-    int64_t cached_tasks = 0;
-    int32_t cached_heads_kv = 0;
-    int64_t cached_queries = 0;
-    int64_t cached_bins = 0;
-
-    // Host scratch reused across steps.
-    std::vector<DecodeUnit> units;    // in the order they were built
-    std::vector<int32_t> unit_order;  // unit indices, longest first (stable)
-    std::vector<int32_t> unit_place;  // unit indices in their packed order (assign_bins)
-    std::vector<int32_t> len_count;   // counting sort of unit_order
-    std::vector<int32_t> stage_host;  // the step image, built in cached memory, then copied to the pinned slot
-    std::vector<int32_t> bin_units;   // [num_bins + 1] offsets of each bin's units after its first
-    std::vector<int32_t> unit_bin;
-    std::vector<std::pair<int64_t, int32_t>> bin_heap;
-    std::vector<int32_t> bin_cursor;
-    std::vector<int64_t> bin_load;
-    std::vector<PrefillTile> tiles;
-    std::vector<gsp::PrefillSplitItem> split_items;
-    std::vector<int32_t> q_ctx;
-    std::vector<int32_t> query_pages;
-    std::vector<int64_t> sim_count, sim_heap;
+    // The host packer and the plan of the packed step (its image, copied into
+    // the pinned slot, and the sizes the launches need).
+    gsp::StepPlanner planner;
+    gsp::StepPlan plan;
 };
 
 struct gsp_pool {
@@ -1012,89 +906,6 @@ int gsp_pool_download(gsp_ctx* ctx, gsp_pool* pool, int32_t which, size_t offset
 
 /* ---------------------------------------------------------------- steps */
 
-// Packs the longest-first units into bins, one decode workgroup each.
-//  - LPT: each unit goes to the least-loaded bin (ties to the lowest).  With
-//    `pair` (a grid of two workgroups per CU) the LPT runs over `nb / 2` CU
-//    bins and each CU bin's units are then dealt to its workgroups c and
-//    c + nb / 2, each unit to the lighter of the two.  In-order dispatch puts
-//    those two workgroups on one CU, where they share its bandwidth, so what
-//    must balance is their sum; should they land apart, each still holds
-//    about half of a balanced CU bin.  Pairing needs two units per CU bin.
-//  - Within a bin, split pieces run first and whole pairs last, each group
-//    keeping the longest-first order, so merges finish before the tail.
-// Works on unit indices: unit_order (longest first) in, unit_place out.
-// Layout: unit_place[b] is bin b's first unit; the other units follow, bin by
-// bin, with bin b's at [bin_units[b], bin_units[b + 1]).  No bin is empty.
-// Returns the bin count.
-static int32_t assign_bins(gsp_ctx* ctx, int64_t bins_max, bool pair) {
-    const std::vector<int32_t>& ord = ctx->unit_order;
-    const size_t n = ord.size();
-    const int32_t nb = (int32_t)std::min<int64_t>(bins_max, (int64_t)n);
-    ctx->bin_units.assign((size_t)nb + 1, 0);
-    if (nb == 0) return 0;
-    pair = pair && nb == bins_max && nb % 2 == 0;
-    const int32_t nl = pair ? nb / 2 : nb;  // bins of the LPT
-    auto& heap = ctx->bin_heap;
-    heap.clear();
-    for (int32_t b = 0; b < nl; ++b) heap.emplace_back(0, b);
-    const std::greater<std::pair<int64_t, int32_t>> later;
-    std::make_heap(heap.begin(), heap.end(), later);
-    ctx->unit_bin.resize(n);
-    auto& count = ctx->bin_cursor;
-    count.assign((size_t)nl, 0);
-    for (size_t i = 0; i < n; ++i) {
-        const DecodeUnit& u = ctx->units[(size_t)ord[i]];
-        std::pop_heap(heap.begin(), heap.end(), later);
-        const int32_t b = heap.back().second;
-        ctx->unit_bin[i] = b;
-        count[(size_t)b] += 1;
-        heap.back().first += unit_cost(u.page_end - u.page_begin, (u.split_info >> 16) > 1);
-        std::push_heap(heap.begin(), heap.end(), later);
-    }
-    if (pair) {
-        for (int32_t b = 0; b < nl; ++b)
-            if (count[(size_t)b] < 2) return assign_bins(ctx, bins_max, false);
-        auto& load = ctx->bin_load;
-        load.assign((size_t)nb, 0);
-        for (int pass = 0; pass < 2; ++pass)
-            for (size_t i = 0; i < n; ++i) {
-                const DecodeUnit& u = ctx->units[(size_t)ord[i]];
-                const bool split = (u.split_info >> 16) > 1;
-                if (split != (pass == 0)) continue;
-                const int32_t c = ctx->unit_bin[i];
-                const int32_t w = load[(size_t)c] <= load[(size_t)(c + nl)] ? c : c + nl;
-                ctx->unit_bin[i] = w;
-                load[(size_t)w] += unit_cost(u.page_end - u.page_begin, split);
-            }
-        for (size_t i = 0; i < n; ++i) ctx->bin_units[(size_t)ctx->unit_bin[i] + 1] += 1;
-    } else {
-        for (int32_t b = 0; b < nb; ++b) ctx->bin_units[(size_t)b + 1] = count[(size_t)b];
-    }
-    // bin_units[b + 1] holds bin b's unit count: its first unit goes to slot b,
-    // the rest to the bin's run after the nb first units.
-    ctx->bin_units[0] = nb;
-    for (int32_t b = 0; b < nb; ++b) ctx->bin_units[(size_t)b + 1] += ctx->bin_units[(size_t)b] - 1;
-    auto& cursor = ctx->bin_cursor;
-    cursor.assign((size_t)nb, -1);  // -1: the bin's first unit is still to place
-    ctx->unit_place.resize(n);
-    for (int pass = 0; pass < 2; ++pass) {
-        const bool want_split = pass == 0;
-        for (size_t i = 0; i < n; ++i) {
-            const DecodeUnit& u = ctx->units[(size_t)ord[i]];
-            if (((u.split_info >> 16) > 1) != want_split) continue;
-            const int32_t b = ctx->unit_bin[i];
-            int32_t& cur = cursor[(size_t)b];
-            if (cur < 0) {
-                ctx->unit_place[(size_t)b] = ord[i];
-                cur = ctx->bin_units[(size_t)b];
-            } else {
-                ctx->unit_place[(size_t)cur++] = ord[i];
-            }
-        }
-    }
-    return nb;
-}
-
 int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc) {
     gsp::clear_error();
     if (!ctx || !pool || !desc) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool/desc is NULL");
@@ -1111,271 +922,27 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     }
     ctx->step_valid = false;
     const gsp_pool_desc& pd = pool->desc;
-    const int32_t B = desc->num_rows;
-    if (B < 0) return gsp::fail(GSP_E_INVALID_ARG, "num_rows must be >= 0 (got %d)", B);
-    if (desc->max_seq_len <= 0)
-        return gsp::fail(GSP_E_INVALID_ARG, "maxSeqLen must be positive (got %d)", desc->max_seq_len);
-    if (B > 0 && (!desc->positions || !desc->token_counts || !desc->bt_offsets || !desc->bt_ids))
-        return gsp::fail(GSP_E_INVALID_ARG, "positions/token_counts/bt_offsets/bt_ids must not be NULL");
-    const int32_t L = desc->max_seq_len;
+    gsp::PlanPool pp;
+    pp.total_blocks = pd.total_blocks;
+    pp.heads_kv = pd.heads_kv;
+    pp.head_dim = pd.head_dim;
+    pp.v_head_dim = pd.v_head_dim;
+    pp.block_size = pd.block_size;
+    pp.kv_dtype = pd.kv_dtype;
+    gsp::PlanOptions po;
+    po.num_cus = ctx->num_cus;
+    po.split_pages_override = ctx->split_pages_override;
+    po.decode_bins_override = ctx->decode_bins_override;
+    po.prefill_path = ctx->prefill_path;
+    po.prefill_split = ctx->prefill_split;
+    gsp::StepPlan& plan = ctx->plan;
+    int rc = ctx->planner.plan(pp, desc, po, plan);
+    if (rc) return rc;
     const int32_t H = pd.heads_kv;
-    const int32_t bs = pd.block_size;
-    // Prefill tiles serve 16-token pages of equal K and V widths 64 or 128;
-    // rows of other pools run as per-query decode units.
-    const bool tileable = bs == 16 && pd.head_dim == pd.v_head_dim && (pd.head_dim == 64 || pd.head_dim == 128);
-
-    // Pass 1: validate rows (the reference's throws, PagedAttentionKernel.cs:34-39,
-    // plus the table and pool bounds) and size the packed arrays.
-    int64_t total_q = 0, packed_pages = 0, kv_tokens = 0, pair_pages = 0, max_pages = 0;
-    bool any_tiles = false;
-    if (desc->n_bt_ids < 0) return gsp::fail(GSP_E_INVALID_ARG, "n_bt_ids must be >= 0 (got %d)", desc->n_bt_ids);
-    // The CSR must stay inside the caller's id array: every row span is read
-    // through bt_offsets, so they are checked before any id is.
-    for (int32_t b = 0; b < B; ++b) {
-        const int32_t o0 = desc->bt_offsets[b], o1 = desc->bt_offsets[b + 1];
-        if (o0 < 0 || o1 < o0 || o1 > desc->n_bt_ids)
-            return gsp::fail(GSP_E_INVALID_ARG, "row %d: bt_offsets [%d, %d) outside [0, n_bt_ids = %d] or decreasing",
-                             b, o0, o1, desc->n_bt_ids);
-    }
-    for (int32_t b = 0; b < B; ++b) {
-        const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
-        const int32_t pos = desc->positions[b];
-        const int32_t tc = desc->token_counts[b];
-        if (ql < 0) return gsp::fail(GSP_E_INVALID_ARG, "row %d: q_len must be >= 0 (got %d)", b, ql);
-        const int64_t last = (int64_t)pos + std::max(ql, 1) - 1;
-        if (pos < 0 || last >= L)
-            return gsp::fail(GSP_E_INVALID_ARG, "row %d: token position %lld exceeds valid sequence range [0, %d]", b,
-                             (long long)(pos < 0 ? pos : last), L - 1);
-        if (tc < 0) return gsp::fail(GSP_E_INVALID_ARG, "row %d: token count %d is negative", b, tc);
-        if (tc > L) return gsp::fail(GSP_E_INVALID_ARG, "row %d: BlockTable token count %d exceeds maxSeqLen %d", b, tc, L);
-        const int32_t span = desc->bt_offsets[b + 1] - desc->bt_offsets[b];
-        const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
-        const int64_t pages = (total_last + bs - 1) / bs;
-        if (pages > span)
-            return gsp::fail(GSP_E_INVALID_ARG, "row %d: %lld tokens need %lld blocks but the table holds %d", b,
-                             (long long)total_last, (long long)pages, span);
-        const int32_t* ids = desc->bt_ids + desc->bt_offsets[b];
-        for (int64_t i = 0; i < pages; ++i)
-            if (ids[i] < 0 || ids[i] >= pd.total_blocks)
-                return gsp::fail(GSP_E_INVALID_ARG, "row %d: block id %d out of range [0, %d)", b, ids[i],
-                                 pd.total_blocks);
-        total_q += ql;
-        packed_pages += pages;
-        kv_tokens += total_last;
-        if (row_is_tiled(ctx->prefill_path, ql, tileable)) {  // tiles, not split-KV units
-            any_tiles = any_tiles || tc > 0;
-            continue;
-        }
-        max_pages = std::max(max_pages, pages);
-        for (int32_t i = 0; i < ql; ++i) {
-            const int64_t tot = std::min<int64_t>(tc, (int64_t)pos + i + 1);
-            pair_pages += (tot + bs - 1) / bs;
-        }
-    }
-    if (total_q > INT32_MAX / 4 || packed_pages > INT32_MAX / 4 || pair_pages * H > INT32_MAX / 2)
-        return gsp::fail(GSP_E_INVALID_ARG, "step too large");
-
-    // Pass 2: split-KV units.  Each query token is cut into nsplit near-equal
-    // page ranges of at most `target` pages; a unit is one (query token, KV
-    // head, page range) and one workgroup.  Units are sorted longest first, so
-    // in-order dispatch schedules them longest-processing-time first.
-    const int64_t T = pair_pages * H;
-    // A pair is cut into at most kMaxSplits pieces.
-    const int64_t min_target = std::max<int64_t>(1, (max_pages + gsp::kMaxSplits - 1) / gsp::kMaxSplits);
-    // Default grid: two workgroups per CU, bins balanced per CU (assign_bins).
-    // A step that also has prefill tiles runs them beside the decode units
-    // (gsp_attention_step): the HBM-bound decode grid then takes one
-    // workgroup per four CUs and leaves the other slots to the matrix-bound
-    // tiles, which take several times longer (config 4 measured 428 us this
-    // way, against 452 us with one per two CUs and 487 us with one per CU).
-    const bool pair_cus = ctx->decode_bins_override <= 0 && !any_tiles;
-    const int64_t bins_max = ctx->decode_bins_override > 0 ? (int64_t)ctx->decode_bins_override
-                             : pair_cus                    ? (int64_t)kDecodeBinsPerCu * std::max(1, ctx->num_cus)
-                                                           : (int64_t)std::max(1, ctx->num_cus / 4);
-    const int64_t sim_bins = pair_cus ? bins_max / kDecodeBinsPerCu : bins_max;
-    int64_t target = 1;
-    if (T > 0) {
-        if (ctx->split_pages_override > 0) {
-            target = std::max<int64_t>(ctx->split_pages_override, min_target);
-        } else if (max_pages <= kWholePairMaxPages && T <= kUnderloadPagesPerBin * bins_max) {
-            target = std::max<int64_t>(1, max_pages);  // whole pairs
-        } else if (ctx->cached_target > 0 && ctx->cached_heads_kv == H && ctx->cached_queries == total_q &&
-                   ctx->cached_bins == bins_max && T * 100 >= ctx->cached_tasks * 97 &&
-                   T * 100 <= ctx->cached_tasks * 103) {
-            target = std::max<int64_t>(ctx->cached_target, min_target);  // engine steps drift slowly
-        } else {
-            ctx->query_pages.clear();
-            for (int32_t b = 0; b < B; ++b) {
-                const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
-                if (row_is_tiled(ctx->prefill_path, ql, tileable)) continue;
-                for (int32_t i = 0; i < ql; ++i) {
-                    const int64_t tot = std::min<int64_t>(desc->token_counts[b], (int64_t)desc->positions[b] + i + 1);
-                    if (tot > 0) ctx->query_pages.push_back((int32_t)((tot + bs - 1) / bs));
-                }
-            }
-            int64_t best_cost = INT64_MAX;
-            for (int32_t cand : kSplitCandidates) {
-                if (cand < min_target) continue;
-                if (T / cand > 16 * bins_max) continue;  // far too many units to be competitive
-                const int64_t c = simulate_split(ctx->query_pages, H, cand, sim_bins, ctx->sim_count, ctx->sim_heap);
-                if (c <= best_cost) {  // ties go to the larger split (fewer units)
-                    best_cost = c;
-                    target = cand;
-                }
-                if (cand >= max_pages) break;  // larger candidates give the same units
-            }
-            ctx->cached_target = (int32_t)target;
-            ctx->cached_tasks = T;
-            ctx->cached_heads_kv = H;
-            ctx->cached_queries = total_q;
-            ctx->cached_bins = bins_max;
-        }
-    }
-    ctx->units.clear();
-    ctx->tiles.clear();
-    ctx->split_items.clear();
-    ctx->q_ctx.assign((size_t)total_q, 0);
-    // fp32 tiles read split records (one per page pair of each tiled row and
-    // KV head) unless the caller asked the tiles to split their own pages.
-    const bool records = tileable && pd.kv_dtype == GSP_KV_F32 && ctx->prefill_split == GSP_SPLIT_RECORDS;
-    int64_t n_records = 0;
-    int32_t split_max_pairs = 0;
-    // grid.y of the split kernel holds one (row, KV head) each.
-    constexpr size_t kMaxSplitItems = 65535;
-    int64_t slots = 0, pairs_split = 0, tiled_queries = 0, tiled_pairs = 0;
-    {
-        int64_t qi = 0, bt_base = 0;
-        for (int32_t b = 0; b < B; ++b) {
-            const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
-            const int32_t pos = desc->positions[b];
-            const int32_t tc = desc->token_counts[b];
-            const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
-            if (row_is_tiled(ctx->prefill_path, ql, tileable)) {
-                // Causal tiles of 16 query tokens; a row with TokenCount 0 has
-                // total 0 for every token and gets none (out left untouched).
-                for (int32_t i = 0; i < ql; ++i)
-                    ctx->q_ctx[qi + i] = (int32_t)std::min<int64_t>(tc, (int64_t)pos + i + 1);
-                if (tc > 0) {
-                    // The row's page pairs: every tile of the row reads a prefix of them.
-                    const int32_t row_pairs = (int32_t)(((total_last + bs - 1) / bs + 1) / 2);
-                    const int64_t rec_row = n_records;
-                    if (records) {
-                        for (int32_t kvh = 0; kvh < H; ++kvh)
-                            ctx->split_items.push_back(gsp::PrefillSplitItem{
-                                (int32_t)bt_base, (int32_t)total_last, kvh, (int32_t)(rec_row + (int64_t)kvh * row_pairs)});
-                        n_records += (int64_t)H * row_pairs;
-                        split_max_pairs = std::max(split_max_pairs, row_pairs);
-                    }
-                    for (int32_t t0 = 0; t0 < ql; t0 += gsp::kPrefillTileTokens) {
-                        PrefillTile t;
-                        t.qi0 = (int32_t)(qi + t0);
-                        t.bt_base = (int32_t)bt_base;
-                        t.pos0 = pos + t0;
-                        t.ntok = std::min(gsp::kPrefillTileTokens, ql - t0);
-                        t.token_count = tc;
-                        const int64_t last = std::min<int64_t>(tc, (int64_t)t.pos0 + t.ntok);
-                        t.pages = (int32_t)((last + bs - 1) / bs);
-                        for (int32_t kvh = 0; kvh < H; ++kvh) {
-                            t.kvh = kvh;
-                            t.rec0 = records ? (int32_t)(rec_row + (int64_t)kvh * row_pairs) : 0;
-                            ctx->tiles.push_back(t);
-                        }
-                    }
-                    for (int32_t i = 0; i < ql; ++i) tiled_pairs += ctx->q_ctx[qi + i];
-                    tiled_queries += ql;
-                }
-                qi += ql;
-                bt_base += (total_last + bs - 1) / bs;
-                continue;
-            }
-            for (int32_t i = 0; i < ql; ++i, ++qi) {
-                const int32_t tot = (int32_t)std::min<int64_t>(tc, (int64_t)pos + i + 1);
-                ctx->q_ctx[qi] = tot;
-                if (tot <= 0) continue;
-                const int32_t pages = (tot + bs - 1) / bs;
-                const int32_t nsplit = (int32_t)std::min<int64_t>((pages + target - 1) / target, gsp::kMaxSplits);
-                const int32_t base = pages / nsplit, extra = pages % nsplit;
-                for (int32_t kvh = 0; kvh < H; ++kvh) {
-                    for (int32_t s = 0; s < nsplit; ++s) {
-                        DecodeUnit u;
-                        u.qi = (int32_t)qi;
-                        u.bt_base = (int32_t)bt_base;
-                        u.page_begin = s * base + std::min(s, extra);
-                        u.page_end = u.page_begin + base + (s < extra ? 1 : 0);
-                        u.ctx = tot;
-                        u.kvh = kvh;
-                        u.slot = nsplit > 1 ? (int32_t)slots : -1;
-                        u.split_info = s | (nsplit << 16);
-                        const int32_t* row_ids = desc->bt_ids + desc->bt_offsets[b];
-                        for (int w = 0; w < gsp::kDecodeWaves; ++w) {
-                            const int32_t p = u.page_begin + w;
-                            const int32_t p2 = p + gsp::kDecodeWaves;
-                            u.first_blk[w] = p < u.page_end ? row_ids[p] : -1;
-                            u.second_blk[w] = p2 < u.page_end ? row_ids[p2] : -1;
-                        }
-                        ctx->units.push_back(u);
-                    }
-                    if (nsplit > 1) {
-                        slots += nsplit;
-                        ++pairs_split;
-                    }
-                }
-            }
-            bt_base += (total_last + bs - 1) / bs;
-        }
-    }
-    // Longest first, ties in build order: a counting sort of unit indices by
-    // page count (the records themselves move once, into the step image).
-    {
-        int32_t max_len = 0;
-        for (const DecodeUnit& u : ctx->units) max_len = std::max(max_len, u.page_end - u.page_begin);
-        auto& cnt = ctx->len_count;
-        cnt.assign((size_t)max_len + 2, 0);
-        for (const DecodeUnit& u : ctx->units) cnt[(size_t)(max_len - (u.page_end - u.page_begin)) + 1] += 1;
-        for (size_t l = 1; l < cnt.size(); ++l) cnt[l] += cnt[l - 1];
-        ctx->unit_order.resize(ctx->units.size());
-        for (size_t i = 0; i < ctx->units.size(); ++i) {
-            const DecodeUnit& u = ctx->units[i];
-            ctx->unit_order[(size_t)cnt[(size_t)(max_len - (u.page_end - u.page_begin))]++] = (int32_t)i;
-        }
-    }
-    if (ctx->split_items.size() > kMaxSplitItems) {  // the tiles split their own pages
-        ctx->split_items.clear();
-        n_records = 0;
-        split_max_pairs = 0;
-    }
-    std::stable_sort(ctx->tiles.begin(), ctx->tiles.end(),
-                     [](const PrefillTile& x, const PrefillTile& y) { return x.pages > y.pages; });
-    const int32_t n_bins = assign_bins(ctx, bins_max, pair_cus);
-
-    // Pass 3: write the staging buffer and upload it with one copy.
-    const size_t n_units = ctx->units.size();
-    const size_t n_tiles = ctx->tiles.size();
-    size_t off = kHdrWords;
-    const size_t off_rows = off;
-    off += (size_t)B + 1;
-    const size_t off_ids = off;
-    off += (size_t)packed_pages;
-    const size_t off_ctx = off;
-    off += (size_t)total_q;
-    // Where each query token's own K/V goes (gsp_*_write_step): its position,
-    // and the block and slot of that position, or block -1 without a slot.
-    const size_t off_wr = off;
-    off += 3 * (size_t)total_q;
-    off = align_up(off, 8);
-    const size_t off_units = off;
-    off += n_units * (sizeof(DecodeUnit) / sizeof(int32_t));
-    const size_t off_tiles = off;
-    off += n_tiles * (sizeof(PrefillTile) / sizeof(int32_t));
-    const size_t n_split = ctx->split_items.size();
-    const size_t off_split = off;
-    off += n_split * (sizeof(gsp::PrefillSplitItem) / sizeof(int32_t));
-    const size_t off_bins = off;
-    off += (size_t)n_bins + 1;
-    const size_t words = off;
+    const size_t words = plan.image.size();
     const size_t words16 = align_up(words, 4);  // the upload moves 16-byte words
 
-    int rc = set_device(ctx);
+    rc = set_device(ctx);
     if (rc) return rc;
     // The other slot than the step packed last: its kernels may still run.
     const int slot = ctx->slot ^ 1;
@@ -1400,80 +967,21 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     if (!rc) rc = ensure_device(ctx, &ctx->d_step_slot[slot], &ctx->d_step_words[slot], words16, false);
     // The split workspace for any group up to the decode tile, so that a
     // captured gsp_attention_step of this step never has to grow it.
-    if (!rc && slots > 0)
+    if (!rc && plan.num_slots > 0)
         rc = ensure_device(ctx, &ctx->part, &ctx->part_floats,
-                           (size_t)slots * gsp::kMaxGroupMfma * (size_t)(pd.v_head_dim + 2), false);
-    if (!rc && slots > 0)
-        rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, (size_t)total_q * H, true);
+                           (size_t)plan.num_slots * gsp::kMaxGroupMfma * (size_t)(pd.v_head_dim + 2), false);
+    if (!rc && plan.num_slots > 0)
+        rc = ensure_device(ctx, &ctx->counters, &ctx->counter_words, (size_t)plan.total_q * H, true);
     // The split records, so that a captured gsp_attention_step never grows them.
-    if (!rc && n_records > 0)
+    if (!rc && plan.num_records > 0)
         rc = ensure_device(ctx, &ctx->d_records, &ctx->d_records_bytes,
-                           (size_t)n_records * (size_t)gsp::prefill_record_bytes(pd.head_dim), false);
+                           (size_t)plan.num_records * (size_t)gsp::prefill_record_bytes(pd.head_dim), false);
     if (rc) return rc;
-
-    // The step image is written in cached host memory and copied into the
-    // pinned slot in one pass: element-wise stores straight into the pinned
-    // buffer measured several times slower.
-    ctx->stage_host.resize(words);
-    int32_t* st = ctx->stage_host.data();
-    std::memset(st, 0, kHdrWords * sizeof(int32_t));
-    int32_t max_id = -1;
-    {
-        int32_t* rows = st + off_rows;
-        int32_t* ids = st + off_ids;
-        int32_t* wr_pos = st + off_wr;
-        int32_t* wr_blk = wr_pos + total_q;
-        int32_t* wr_slot = wr_blk + total_q;
-        int64_t w = 0, qi = 0;
-        rows[0] = 0;
-        for (int32_t b = 0; b < B; ++b) {
-            const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
-            const int32_t pos = desc->positions[b];
-            const int32_t tc = desc->token_counts[b];
-            const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
-            const int64_t pages = (total_last + bs - 1) / bs;
-            const int32_t* src = desc->bt_ids + desc->bt_offsets[b];
-            for (int64_t i = 0; i < pages; ++i) {
-                ids[w++] = src[i];
-                max_id = std::max(max_id, src[i]);
-            }
-            rows[b + 1] = (int32_t)w;
-            // A query token at p < TokenCount has its slot in the packed pages
-            // (p < total_last); the reference stores its K/V there before
-            // attending (PagedTransformerRunner.cs:620-634, :437-452).
-            for (int32_t i = 0; i < ql; ++i, ++qi) {
-                const int64_t p = (int64_t)pos + i;
-                wr_pos[qi] = (int32_t)p;
-                const bool has = p < tc;
-                wr_blk[qi] = has ? src[p / bs] : -1;
-                wr_slot[qi] = has ? (int32_t)(p % bs) : 0;
-            }
-        }
-    }
-    if (total_q) std::memcpy(st + off_ctx, ctx->q_ctx.data(), (size_t)total_q * sizeof(int32_t));
-    {
-        DecodeUnit* dst = reinterpret_cast<DecodeUnit*>(st + off_units);
-        for (size_t j = 0; j < n_units; ++j) dst[j] = ctx->units[(size_t)ctx->unit_place[j]];
-    }
-    if (n_tiles) std::memcpy(st + off_tiles, ctx->tiles.data(), n_tiles * sizeof(PrefillTile));
-    if (n_split) std::memcpy(st + off_split, ctx->split_items.data(), n_split * sizeof(gsp::PrefillSplitItem));
-    std::memcpy(st + off_bins, ctx->bin_units.data(), ((size_t)n_bins + 1) * sizeof(int32_t));
-    st[kHdrRows] = B;
-    st[kHdrTotalQ] = (int32_t)total_q;
-    st[kHdrPages] = (int32_t)packed_pages;
-    st[kHdrUnits] = (int32_t)n_units;
-    st[kHdrTarget] = (int32_t)target;
-    st[kHdrSlots] = (int32_t)slots;
-    st[kHdrMaxId] = max_id;
-    st[kHdrPairsSplit] = (int32_t)pairs_split;
-    st[kHdrHeadsKv] = H;
-    st[kHdrTiles] = (int32_t)n_tiles;
-    st[kHdrBins] = n_bins;
 
     // One copy for the whole step, on the context's stream (behind the
     // kernels that read this slot's previous step), then the event that frees
     // the pinned buffer.  The pad words up to a 16-byte word are zeroed.
-    std::memcpy(ctx->staging[slot], st, words * sizeof(int32_t));
+    std::memcpy(ctx->staging[slot], plan.image.data(), words * sizeof(int32_t));
     for (size_t j = words; j < words16; ++j) ctx->staging[slot][j] = 0;
     rc = check_hip(gsp::launch_upload_step(ctx->staging_dev[slot], ctx->d_step_slot[slot], (int64_t)(words16 / 4),
                                            ctx->stream),
@@ -1485,42 +993,42 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->slot = slot;
     ctx->d_step = ctx->d_step_slot[slot];
 
-    ctx->off_rows = off_rows;
-    ctx->off_ids = off_ids;
-    ctx->off_ctx = off_ctx;
-    ctx->off_wr = off_wr;
-    ctx->off_units = off_units;
-    ctx->off_tiles = off_tiles;
-    ctx->off_split = off_split;
-    ctx->off_bins = off_bins;
-    ctx->num_split_items = (int32_t)n_split;
-    ctx->split_max_pairs = split_max_pairs;
-    ctx->num_records = n_records;
-    ctx->records_head_dim = n_records > 0 ? pd.head_dim : 0;
-    ctx->num_bins = n_bins;
-    ctx->max_id = max_id;
-    ctx->num_slots = (int32_t)slots;
-    ctx->num_units = (int32_t)n_units;
-    ctx->num_tiles = (int32_t)n_tiles;
+    ctx->off_rows = plan.off_rows;
+    ctx->off_ids = plan.off_ids;
+    ctx->off_ctx = plan.off_ctx;
+    ctx->off_wr = plan.off_wr;
+    ctx->off_units = plan.off_units;
+    ctx->off_tiles = plan.off_tiles;
+    ctx->off_split = plan.off_split;
+    ctx->off_bins = plan.off_bins;
+    ctx->num_split_items = plan.num_split_items;
+    ctx->split_max_pairs = plan.split_max_pairs;
+    ctx->num_records = plan.num_records;
+    ctx->records_head_dim = plan.num_records > 0 ? pd.head_dim : 0;
+    ctx->num_bins = plan.num_bins;
+    ctx->max_id = plan.max_id;
+    ctx->num_slots = (int32_t)plan.num_slots;
+    ctx->num_units = plan.num_units;
+    ctx->num_tiles = plan.num_tiles;
     ctx->step_heads_kv = H;
     ctx->step_blocks = pd.total_blocks;
-    ctx->step_block_size = bs;
-    ctx->step_tileable = tileable;
-    ctx->info.num_rows = B;
-    ctx->info.total_q = (int32_t)total_q;
-    ctx->info.packed_pages = (int32_t)packed_pages;
+    ctx->step_block_size = pd.block_size;
+    ctx->step_tileable = plan.tileable;
+    ctx->info.num_rows = plan.num_rows;
+    ctx->info.total_q = (int32_t)plan.total_q;
+    ctx->info.packed_pages = (int32_t)plan.packed_pages;
     ctx->info.heads_kv = H;
-    ctx->info.decode_units = (int32_t)n_units;
-    ctx->info.split_pairs = (int32_t)pairs_split;
-    ctx->info.partial_slots = (int32_t)slots;
-    ctx->info.pages_per_split = (int32_t)target;
-    ctx->info.kv_tokens = kv_tokens;
+    ctx->info.decode_units = plan.num_units;
+    ctx->info.split_pairs = (int32_t)plan.pairs_split;
+    ctx->info.partial_slots = (int32_t)plan.num_slots;
+    ctx->info.pages_per_split = plan.target;
+    ctx->info.kv_tokens = plan.kv_tokens;
     ctx->info.staging_bytes = (int64_t)(words * sizeof(int32_t));
-    ctx->info.prefill_tiles = (int32_t)n_tiles;
-    ctx->info.prefill_queries = (int32_t)tiled_queries;
-    ctx->info.prefill_pairs = tiled_pairs;
-    ctx->info.decode_bins = n_bins;
-    ctx->info.split_records = (int32_t)n_records;
+    ctx->info.prefill_tiles = plan.num_tiles;
+    ctx->info.prefill_queries = (int32_t)plan.tiled_queries;
+    ctx->info.prefill_pairs = plan.tiled_pairs;
+    ctx->info.decode_bins = plan.num_bins;
+    ctx->info.split_records = (int32_t)plan.num_records;
     ctx->info.pack_host_ns =
         std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t_pack0).count();
     ctx->step_valid = true;

@@ -75,6 +75,7 @@ def test_captured_step_replays_match_eager(torch_mod, gsp, ctx, kind):
         pool.destroy()
 
 
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
 def test_capture_that_would_grow_the_workspace_fails_cleanly(torch_mod, gsp):
     """A fresh context packs a group-32 step (workspace sized for one head tile) and captures its
     first gsp_attention_step: the call must refuse with a state error before enqueuing anything,
