@@ -103,6 +103,7 @@ struct gsp_ctx {
     int32_t step_heads_kv = 0;  // pool geometry the step was packed for
     int32_t step_blocks = 0;
     int32_t step_block_size = 0;
+    int32_t step_page_tokens = 0;  // tokens per kernel page (the pool's page, or a part of it above 16)
     bool step_tileable = false;
     // Split records of the packed step's fp32 prefill tiles (records_head_dim
     // 0: none, the tiles split their pages themselves): one per page pair of
@@ -924,6 +925,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     const gsp_pool_desc& pd = pool->desc;
     gsp::PlanPool pp;
     pp.total_blocks = pd.total_blocks;
+    pp.layers = pd.layers;
     pp.heads_kv = pd.heads_kv;
     pp.head_dim = pd.head_dim;
     pp.v_head_dim = pd.v_head_dim;
@@ -1013,6 +1015,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->step_heads_kv = H;
     ctx->step_blocks = pd.total_blocks;
     ctx->step_block_size = pd.block_size;
+    ctx->step_page_tokens = plan.page_tokens;
     ctx->step_tileable = plan.tileable;
     ctx->info.num_rows = plan.num_rows;
     ctx->info.total_q = (int32_t)plan.total_q;
@@ -1108,7 +1111,7 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     const bool use_mfma = ctx->decode_path != GSP_DECODE_DPP;
     if (!use_mfma && ctx->num_units > 0 &&
         (group > gsp::kMaxGroup || d.head_dim != d.v_head_dim || (d.head_dim != 64 && d.head_dim != 128) ||
-         d.block_size != gsp::kBlockSize))
+         ctx->step_page_tokens != gsp::kBlockSize))
         return gsp::fail(GSP_E_UNSUPPORTED,
                          "the DPP decode kernel serves headDim 64 or 128, 16-token pages and groups up to %d",
                          gsp::kMaxGroup);
@@ -1159,10 +1162,13 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     gsp::DecodeArgs a;
     a.k_pool = pool->k;
     a.v_pool = pool->v;
-    a.block_stride = pool->block_stride_k;
+    // Pool pages above 16 tokens are read as kernel pages of step_page_tokens
+    // tokens whose ids count in kernel page strides (gsp_step_plan.h).
+    const bool kernel_pages = ctx->step_page_tokens != d.block_size;
+    a.block_stride = kernel_pages ? (int64_t)ctx->step_page_tokens * d.head_dim : pool->block_stride_k;
     a.layer_offset = (int64_t)layer * pool->layer_stride_k;
     a.head_stride = pool->head_stride_k;
-    a.v_block_stride = pool->block_stride_v;
+    a.v_block_stride = kernel_pages ? (int64_t)ctx->step_page_tokens * d.v_head_dim : pool->block_stride_v;
     a.v_layer_offset = (int64_t)layer * pool->layer_stride_v;
     a.v_head_stride = pool->head_stride_v;
     a.units = reinterpret_cast<const DecodeUnit*>(ctx->d_step + ctx->off_units);
@@ -1179,7 +1185,7 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     a.scale_log2 = attn_scale * 1.4426950408889634f;
     a.head_dim = d.head_dim;
     a.v_head_dim = d.v_head_dim;
-    a.block_size = d.block_size;
+    a.block_size = ctx->step_page_tokens;
     a.total_q = ctx->info.total_q;
     a.num_slots = slots;
     a.slot_heads = slot_heads;

@@ -185,7 +185,22 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
         return fail(GSP_E_INVALID_ARG, "positions/token_counts/bt_offsets/bt_ids must not be NULL");
     const int32_t L = desc->max_seq_len;
     const int32_t H = pd.heads_kv;
-    const int32_t bs = pd.block_size;
+    if (pd.block_size < 1) return fail(GSP_E_INVALID_ARG, "blockSize must be >= 1 (got %d)", pd.block_size);
+    // The kernels read pages of at most 16 tokens.  A pool page of pbs > 16
+    // tokens is read as r = pbs / bs kernel pages of bs tokens (bs the largest
+    // divisor of pbs up to 16): kernel page k of a row is sub-page k % r of
+    // pool page k / r, and its id b * (layers * heads_kv * r) + k % r times a
+    // kernel page stride of bs * head_dim addresses exactly that sub-page in
+    // the reference layout [block][layer][head][slot][dim]
+    // (PagedBlockPool.cs:77-83).  Validation below is in pool pages.
+    const int32_t pbs = pd.block_size;
+    int32_t bs = std::min(pbs, kBlockSize);
+    while (pbs % bs) --bs;
+    const int32_t r = pbs / bs;
+    const int64_t vfactor = (int64_t)std::max(1, pd.layers) * H * r;
+    if (r > 1 && ((int64_t)pd.total_blocks - 1) * vfactor + (r - 1) > INT32_MAX)
+        return fail(GSP_E_UNSUPPORTED, "%d blocks of %d-token pages: too many kernel pages for 32-bit ids",
+                    pd.total_blocks, pbs);
     // Prefill tiles serve 16-token pages of equal K and V widths 64 or 128;
     // rows of other pools run as per-query decode units.
     const bool tileable = bs == 16 && pd.head_dim == pd.v_head_dim && (pd.head_dim == 64 || pd.head_dim == 128);
@@ -193,6 +208,7 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
     // Pass 1: validate rows (the reference's throws, PagedAttentionKernel.cs:34-39,
     // plus the table and pool bounds) and size the packed arrays.
     int64_t total_q = 0, packed_pages = 0, kv_tokens = 0, pair_pages = 0, max_pages = 0;
+    int32_t max_id = -1;  // largest pool block id the step reads
     bool any_tiles = false;
     if (desc->n_bt_ids < 0) return fail(GSP_E_INVALID_ARG, "n_bt_ids must be >= 0 (got %d)", desc->n_bt_ids);
     // The CSR must stay inside the caller's id array: every row span is read
@@ -216,15 +232,18 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
         if (tc > L) return fail(GSP_E_INVALID_ARG, "row %d: BlockTable token count %d exceeds maxSeqLen %d", b, tc, L);
         const int32_t span = desc->bt_offsets[b + 1] - desc->bt_offsets[b];
         const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
-        const int64_t pages = (total_last + bs - 1) / bs;
-        if (pages > span)
+        const int64_t ppages = (total_last + pbs - 1) / pbs;  // pool pages
+        if (ppages > span)
             return fail(GSP_E_INVALID_ARG, "row %d: %lld tokens need %lld blocks but the table holds %d", b,
-                             (long long)total_last, (long long)pages, span);
+                             (long long)total_last, (long long)ppages, span);
         const int32_t* ids = desc->bt_ids + desc->bt_offsets[b];
-        for (int64_t i = 0; i < pages; ++i)
+        for (int64_t i = 0; i < ppages; ++i) {
             if (ids[i] < 0 || ids[i] >= pd.total_blocks)
                 return fail(GSP_E_INVALID_ARG, "row %d: block id %d out of range [0, %d)", b, ids[i],
                                  pd.total_blocks);
+            max_id = std::max(max_id, ids[i]);
+        }
+        const int64_t pages = (total_last + bs - 1) / bs;  // kernel pages
         total_q += ql;
         packed_pages += pages;
         kv_tokens += total_last;
@@ -240,6 +259,30 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
     }
     if (total_q > INT32_MAX / 4 || packed_pages > INT32_MAX / 4 || pair_pages * H > INT32_MAX / 2)
         return fail(GSP_E_INVALID_ARG, "step too large");
+    // From here on the tables are in kernel pages: for pool pages above 16
+    // tokens, each row's table is expanded into kernel page ids.  The write
+    // slots (pass 3) keep pool blocks and slots.
+    const gsp_step_desc* const pdesc = desc;
+    gsp_step_desc vdesc;
+    if (r > 1) {
+        voffs_.resize((size_t)B + 1);
+        vids_.resize((size_t)packed_pages);
+        int64_t w = 0;
+        voffs_[0] = 0;
+        for (int32_t b = 0; b < B; ++b) {
+            const int32_t ql = desc->q_lens ? desc->q_lens[b] : 1;
+            const int64_t total_last = ql > 0 ? std::min<int64_t>(desc->token_counts[b], (int64_t)desc->positions[b] + ql) : 0;
+            const int64_t pages = (total_last + bs - 1) / bs;
+            const int32_t* ids = desc->bt_ids + desc->bt_offsets[b];
+            for (int64_t k = 0; k < pages; ++k) vids_[(size_t)w++] = (int32_t)(ids[k / r] * vfactor + k % r);
+            voffs_[(size_t)b + 1] = (int32_t)w;
+        }
+        vdesc = *desc;
+        vdesc.bt_offsets = voffs_.data();
+        vdesc.bt_ids = vids_.data();
+        vdesc.n_bt_ids = (int32_t)w;
+        desc = &vdesc;
+    }
 
     // Pass 2: split-KV units.  Each query token is cut into nsplit near-equal
     // page ranges of at most `target` pages; a unit is one (query token, KV
@@ -446,7 +489,6 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
     out.image.resize(words);
     int32_t* st = out.image.data();
     std::memset(st, 0, kHdrWords * sizeof(int32_t));
-    int32_t max_id = -1;
     {
         int32_t* rows = st + off_rows;
         int32_t* ids = st + off_ids;
@@ -462,10 +504,8 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
             const int64_t total_last = ql > 0 ? std::min<int64_t>(tc, (int64_t)pos + ql) : 0;
             const int64_t pages = (total_last + bs - 1) / bs;
             const int32_t* src = desc->bt_ids + desc->bt_offsets[b];
-            for (int64_t i = 0; i < pages; ++i) {
-                ids[w++] = src[i];
-                max_id = std::max(max_id, src[i]);
-            }
+            const int32_t* psrc = pdesc->bt_ids + pdesc->bt_offsets[b];  // pool blocks
+            for (int64_t i = 0; i < pages; ++i) ids[w++] = src[i];
             rows[b + 1] = (int32_t)w;
             // A query token at p < TokenCount has its slot in the packed pages
             // (p < total_last); the reference stores its K/V there before
@@ -474,8 +514,8 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
                 const int64_t p = (int64_t)pos + i;
                 wr_pos[qi] = (int32_t)p;
                 const bool has = p < tc;
-                wr_blk[qi] = has ? src[p / bs] : -1;
-                wr_slot[qi] = has ? (int32_t)(p % bs) : 0;
+                wr_blk[qi] = has ? psrc[p / pbs] : -1;
+                wr_slot[qi] = has ? (int32_t)(p % pbs) : 0;
             }
         }
     }
@@ -524,6 +564,8 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
     out.tiled_pairs = tiled_pairs;
     out.max_id = max_id;
     out.tileable = tileable;
+    out.page_tokens = bs;
+    out.pool_page_split = r;
     return GSP_OK;
 }
 

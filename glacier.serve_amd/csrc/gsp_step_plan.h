@@ -18,6 +18,7 @@ namespace gsp {
 // The pool geometry a step is planned for.
 struct PlanPool {
     int32_t total_blocks = 0;
+    int32_t layers = 1;
     int32_t heads_kv = 0;
     int32_t head_dim = 0;
     int32_t v_head_dim = 0;
@@ -59,8 +60,15 @@ struct StepPlan {
     int64_t num_records = 0;       // split records (fp32 prefill tiles)
     int64_t tiled_queries = 0;
     int64_t tiled_pairs = 0;
-    int32_t max_id = -1;           // largest block id the step reads
+    int32_t max_id = -1;           // largest pool block id the step reads
     bool tileable = false;         // the pool's shape takes prefill tiles
+    // Kernel pages: the packed ids and the units count pages of page_tokens
+    // (<= 16) tokens.  pool_page_split == 1: they are the pool's pages and
+    // blocks.  Above 1, each pool page is that many kernel pages, with ids
+    // block * (layers * heads_kv * pool_page_split) + sub-page, so the kernels
+    // take a page stride of page_tokens * head_dim (v_head_dim for V).
+    int32_t page_tokens = 0;
+    int32_t pool_page_split = 1;
 };
 
 class StepPlanner {
@@ -68,7 +76,8 @@ public:
     // Validates `desc` for `pool` (the reference's throws,
     // PagedAttentionKernel.cs:34-39, plus the table and pool bounds) and plans
     // it into `out`.  GSP_OK, or GSP_E_INVALID_ARG with the message set and
-    // `out` unspecified.
+    // `out` unspecified (GSP_E_UNSUPPORTED for pool pages above 16 tokens whose
+    // kernel page ids would not fit 32 bits).
     int plan(const PlanPool& pool, const gsp_step_desc* desc, const PlanOptions& opt, StepPlan& out);
 
 private:
@@ -95,6 +104,7 @@ private:
     std::vector<PrefillSplitItem> split_items_;
     std::vector<int32_t> q_ctx_;
     std::vector<int32_t> query_pages_;
+    std::vector<int32_t> voffs_, vids_;  // row tables in kernel pages (pool pages above 16 tokens)
     std::vector<int64_t> sim_count_, sim_heap_;
 };
 

@@ -42,7 +42,7 @@ extern "C" {
 
 #define GSP_ABI_VERSION 8
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
-#define GSP_MAX_BLOCK_SIZE 16 /* largest page size of a device pool */
+#define GSP_MAX_BLOCK_SIZE 4096 /* largest page size of a device pool */
 
 typedef enum gsp_status {
     GSP_OK = 0,
@@ -122,7 +122,8 @@ typedef struct gsp_pool_desc {
     int32_t heads_kv;
     int32_t head_dim;
     int32_t v_head_dim;  /* <= 0 means head_dim (PagedBlockPool.cs:73) */
-    int32_t block_size;  /* tokens per page, 1 .. GSP_MAX_BLOCK_SIZE */
+    int32_t block_size;  /* tokens per page, 1 .. GSP_MAX_BLOCK_SIZE (PagedBlockPool.cs:61-67
+                            takes any blockSize >= 1) */
     int32_t kv_dtype;    /* gsp_kv_dtype */
 } gsp_pool_desc;
 
@@ -350,11 +351,15 @@ int gsp_set_prefill_split(gsp_ctx* ctx, int32_t mode);
  * (CudaPagedTransformerRunner.cs:402-412) and then some: head_dim and
  * v_head_dim even and at most 256 (v_head_dim may differ from head_dim, as
  * in the CPU kernel's generic path, PagedAttentionKernel.cs:326-370); any
- * GQA group (n_heads % heads_kv == 0); pages of 1..16 tokens.  The pool must
- * have the KV heads, block count and page size the step was packed for.
+ * GQA group (n_heads % heads_kv == 0); pages of 1 to GSP_MAX_BLOCK_SIZE
+ * tokens.  The kernels read pages of at most 16 tokens: a pool page of more
+ * is read as equal parts of the largest size up to 16 that divides it (32 and
+ * 64 as 16-token parts, 24 as 12, a prime size as single tokens).  The pool
+ * must have the KV heads, block count and page size the step was packed for.
  * Rows with q_len >= 16 run as prefill tiles when head_dim == v_head_dim is 64
- * or 128 with 16-token pages, else as per-query decode units.  GSP_DECODE_DPP
- * serves head_dim 64 or 128, 16-token pages and groups up to 8 only.  Work is
+ * or 128 and the parts have 16 tokens, else as per-query decode units.
+ * GSP_DECODE_DPP serves head_dim 64 or 128, 16-token parts and groups up to 8
+ * only.  Work is
  * enqueued on the context's stream.  A step with both decode units and
  * prefill tiles runs them in one kernel (with GSP_DECODE_DPP: the tiles on
  * second streams of the context, forked from and joined back into that

@@ -52,8 +52,8 @@ bool read_steps(const char* path, std::vector<Step>& out) {
     int32_t magic = 0, count = 0;
     if (!rd(&magic, 1) || magic != 0x53505347 || !rd(&count, 1)) return false;
     for (int32_t s = 0; s < count; ++s) {
-        int32_t h[10];
-        if (!rd(h, 10)) return false;
+        int32_t h[11];
+        if (!rd(h, 11)) return false;
         Step st;
         st.pool.total_blocks = h[0];
         st.pool.heads_kv = h[1];
@@ -65,6 +65,7 @@ bool read_steps(const char* path, std::vector<Step>& out) {
         st.max_seq_len = h[7];
         st.has_qlens = h[8] != 0;
         const int32_t n_ids = h[9];
+        st.pool.layers = h[10];
         st.positions.resize((size_t)B);
         st.token_counts.resize((size_t)B);
         st.offsets.resize((size_t)B + 1);
@@ -98,8 +99,17 @@ void check_image(const Step& st, const gsp::StepPlan& p, const std::string& ctx)
     const int32_t* im = p.image.data();
     const size_t words = p.image.size();
     const int32_t B = st.rows();
-    const int32_t bs = st.pool.block_size;
+    const int32_t pbs = st.pool.block_size;  // pool page
+    int32_t bs = std::min(pbs, 16);          // kernel page: the largest divisor of pbs up to 16
+    while (pbs % bs) --bs;
+    const int32_t r = pbs / bs;
     const int32_t H = st.pool.heads_kv;
+    if (p.page_tokens != bs || p.pool_page_split != r) return failf("kernel page size", ctx);
+    // Kernel page k of a row: sub-page k % r of pool page k / r.
+    auto kernel_id = [&](int32_t b, int64_t k) -> int64_t {
+        const int64_t blk = st.ids[(size_t)st.offsets[(size_t)b] + (size_t)(k / r)];
+        return r == 1 ? blk : blk * ((int64_t)st.pool.layers * H * r) + k % r;
+    };
     auto in_image = [&](size_t off, size_t n) { return off <= words && n <= words - off; };
     if (!in_image(0, gsp::kHdrWords) || im[gsp::kHdrRows] != B || im[gsp::kHdrUnits] != p.num_units ||
         im[gsp::kHdrTiles] != p.num_tiles || im[gsp::kHdrBins] != p.num_bins || im[gsp::kHdrHeadsKv] != H ||
@@ -125,7 +135,7 @@ void check_image(const Step& st, const gsp::StepPlan& p, const std::string& ctx)
         q += ql;
         if (rows[b + 1] - rows[b] != pages) return failf("row span", ctx);
         for (int64_t i = 0; i < pages; ++i)
-            if (ids[rows[b] + i] != st.ids[(size_t)st.offsets[(size_t)b] + (size_t)i]) return failf("packed id", ctx);
+            if (ids[rows[b] + i] != kernel_id(b, i)) return failf("packed id", ctx);
     }
     if (q != p.total_q) return failf("total_q", ctx);
     // Write slots.
@@ -138,7 +148,8 @@ void check_image(const Step& st, const gsp::StepPlan& p, const std::string& ctx)
             const int64_t pos = (int64_t)st.positions[(size_t)b] + i;
             if (wr_pos[qi] != pos) return failf("write position", ctx);
             const bool has = pos < st.token_counts[(size_t)b];
-            if (has ? (wr_blk[qi] != ids[rows[b] + pos / bs] || wr_slot[qi] != pos % bs) : wr_blk[qi] != -1)
+            const int32_t pool_blk = has ? st.ids[(size_t)st.offsets[(size_t)b] + (size_t)(pos / pbs)] : -1;
+            if (has ? (wr_blk[qi] != pool_blk || wr_slot[qi] != pos % pbs) : wr_blk[qi] != -1)
                 return failf("write slot", ctx);
         }
     // Units: pages of each (query, KV head) covered once; splits consistent.
@@ -345,7 +356,8 @@ void fuzz(gsp::StepPlanner& planner, std::mt19937& rng, int iters) {
     for (int it = 0; it < iters; ++it) {
         auto u = [&](int64_t lo, int64_t hi) { return (int32_t)(lo + (int64_t)(rng() % (uint64_t)(hi - lo + 1))); };
         Step st;
-        st.pool.block_size = u(1, 16);
+        st.pool.block_size = u(0, 3) ? u(1, 16) : u(17, 64);
+        st.pool.layers = u(1, 4);
         st.pool.heads_kv = u(1, 8);
         st.pool.head_dim = 2 * u(1, 128);
         st.pool.v_head_dim = u(0, 3) ? st.pool.head_dim : 2 * u(1, 128);
@@ -388,7 +400,7 @@ void fuzz(gsp::StepPlanner& planner, std::mt19937& rng, int iters) {
         if (rc == GSP_OK) {
             ++accepted;
             check_image(st, out, "fuzz " + std::to_string(it));
-        } else if (rc != GSP_E_INVALID_ARG) {
+        } else if (rc != GSP_E_INVALID_ARG && !(rc == GSP_E_UNSUPPORTED && st.pool.block_size > 16)) {
             failf("unexpected status", "fuzz " + std::to_string(it));
         }
     }

@@ -218,8 +218,8 @@ def test_step_writes_match_the_explicit_writes(torch_mod, gsp, ctx, dt):
         p.destroy()
 
 
-@pytest.mark.parametrize("dt", ["f32", "f16"])
-def test_engine_tick_sequence_over_layers(torch_mod, gsp, ctx, dt):
+@pytest.mark.parametrize("dt,bs", [("f32", 16), ("f16", 16), ("f32", 32)])
+def test_engine_tick_sequence_over_layers(torch_mod, gsp, ctx, dt, bs):
     """The per-tick sequence the integration prescribes (PagedTransformerRunner.cs:605-659 per layer):
     one gsp_step_pack for the tick, then for every layer gsp_rope_write_step (Q rotated in place, K
     rotated and stored, V stored at each query token's own slot) followed by gsp_attention_step on
@@ -230,12 +230,12 @@ def test_engine_tick_sequence_over_layers(torch_mod, gsp, ctx, dt):
     nh, nkv, d, base, layers = 28, 4, 128, 1000000.0, 3
     q_lens = np.array([1, 1, 23, 1, 1], np.int32)
     step = workloads.small_step(seed=131, rows=5, n_heads=nh, n_kv=nkv, head_dim=d, kv_dtype=dt, ctx_lo=10,
-                                ctx_hi=300, total_blocks=256, q_lens=q_lens)
+                                ctx_hi=300, total_blocks=256, q_lens=q_lens, block_size=bs)
     # Decode rows attend their newest token: position = TokenCount - 1 (the slot the tick allocated).
     for b in range(step.num_rows):
         if step.lens[b] == 1:
             step.positions[b] = step.token_counts[b] - 1
-    print(f"case engine tick {dt} layers={layers}", flush=True)
+    print(f"case engine tick {dt} bs={bs} layers={layers}", flush=True)
     rng = np.random.default_rng(132)
     _, k, v = workloads.host_values(step, layers=layers)
     pool, keep = to_device_pool(torch, gsp, ctx, step, k, v)
@@ -269,9 +269,9 @@ def test_engine_tick_sequence_over_layers(torch_mod, gsp, ctx, dt):
             for t in range(int(step.lens[b])):
                 p = int(step.positions[b]) + t
                 qr[i] = orc.rope(qs[l][i], p, base, 1)
-                blk = int(step.table(b)[p // 16])
-                k2[blk, l, :, p % 16] = orc.rope(ks[l][i], p, base, 1).astype(npdt).astype(np.float32)
-                v2[blk, l, :, p % 16] = vs[l][i].astype(npdt).astype(np.float32)
+                blk = int(step.table(b)[p // bs])
+                k2[blk, l, :, p % bs] = orc.rope(ks[l][i], p, base, 1).astype(npdt).astype(np.float32)
+                v2[blk, l, :, p % bs] = vs[l][i].astype(npdt).astype(np.float32)
                 i += 1
         ref = oracle_step(step, qr, k2, v2, layer=l)
         err = max_err(outs[l], ref)

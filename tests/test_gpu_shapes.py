@@ -9,7 +9,8 @@ head_dim (PagedAttentionKernel.cs:326-370), and no bound on the GQA group
     (PhaseCServeRemediationTests.cs:321-346) and head_dim 32 / v_head_dim 64
     with 4-token pages (:257-319);
   - head dims 2 .. 256, multiples of 4 and not (loads of 4 and of 2 dims);
-  - page sizes 1 .. 16;
+  - page sizes 1 .. 16, and above (17, 24, 32, 48, 64: each pool page read as
+    equal kernel pages of at most 16 tokens);
   - GQA groups 17 .. 32 (tiles of 16 heads over grid.y), with forced splits;
   - v_head_dim above and below head_dim;
   - prefill rows on pools the prefill tiles do not serve (per-query units);
@@ -53,6 +54,13 @@ CASES = [
     (14, 2, 64, 64, 4, "f32", 200, 3),
     (28, 4, 128, 128, 8, "f16", 700, 0),
     (28, 4, 128, 128, 12, "f32", 700, 4),
+    # Pool pages above 16 tokens, read as kernel pages (the largest divisor up to 16):
+    (28, 4, 128, 128, 32, "f32", 900, 0),  # 16-token parts: the fixed-shape kernel
+    (28, 4, 128, 128, 32, "f32", 900, 3),
+    (32, 8, 128, 128, 64, "f16", 900, 2),
+    (2, 1, 32, 64, 48, "f32", 300, 1),     # v_head_dim != head_dim, 16-token parts
+    (8, 2, 64, 64, 24, "f32", 300, 0),     # 12-token parts
+    (4, 2, 32, 32, 17, "f16", 100, 2),     # a prime page size: single-token parts
 ]
 
 
@@ -80,11 +88,13 @@ def test_general_shapes_match_oracle(torch_mod, gsp, ctx, case):
         pool.destroy()
 
 
-@pytest.mark.parametrize("shape", [(32, 64, 4, "f32"), (96, 80, 8, "f16"), (128, 128, 8, "f32"), (48, 48, 16, "f32")],
+@pytest.mark.parametrize("shape", [(32, 64, 4, "f32"), (96, 80, 8, "f16"), (128, 128, 8, "f32"), (48, 48, 16, "f32"),
+                                   (128, 128, 32, "f32"), (64, 64, 64, "f16"), (128, 128, 24, "f32")],
                          ids=lambda s: f"d{s[0]}_dv{s[1]}_bs{s[2]}_{s[3]}")
 def test_prefill_rows_outside_the_tile_shapes(torch_mod, gsp, ctx, shape):
     """Chunked-prefill rows of a pool the prefill tiles do not serve run as per-query
-    decode units, causal as the reference runs them (PagedTransformerRunner.cs:454-474)."""
+    decode units, causal as the reference runs them (PagedTransformerRunner.cs:454-474).  Pool
+    pages of 32 or 64 tokens are read as 16-token kernel pages, which the tiles do serve."""
     torch = torch_mod
     d, dv, bs, dt = shape
     print(f"case prefill shape d={d} dv={dv} bs={bs} {dt}", flush=True)
@@ -99,8 +109,11 @@ def test_prefill_rows_outside_the_tile_shapes(torch_mod, gsp, ctx, shape):
         info = ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids,
                              step.max_seq_len, q_lens=step.q_lens)
         ctx.set_split_pages(0)
-        if not (bs == 16 and d == dv and d in (64, 128)):
+        kernel_bs = max(x for x in range(1, 17) if bs % x == 0)
+        if not (kernel_bs == 16 and d == dv and d in (64, 128)):
             assert info.prefill_tiles == 0
+        else:
+            assert info.prefill_tiles > 0
         got = gpu_step(torch, gsp, ctx, step, q, pool)
         ref = oracle_step(step, q, k, v)
         assert max_err(got, ref) <= TOL[dt]
@@ -143,8 +156,8 @@ def test_compute_attention_with_asymmetric_v(torch_mod, gsp, ctx):
 def test_unsupported_shapes_are_refused(torch_mod, gsp, ctx):
     torch = torch_mod
     z = torch.zeros(4096, device="cuda")
-    with pytest.raises(gsp.Unsupported):  # pages above 16 tokens
-        gsp.Pool.wrap(ctx, z.data_ptr(), z.data_ptr(), 2, 1, 1, 32, block_size=32)
+    with pytest.raises(gsp.Unsupported):  # pages above GSP_MAX_BLOCK_SIZE (4096) tokens
+        gsp.Pool.wrap(ctx, z.data_ptr(), z.data_ptr(), 1, 1, 1, 2, block_size=4097)
     odd = gsp.Pool.wrap(ctx, z.data_ptr(), z.data_ptr(), 4, 1, 1, 33, block_size=4)
     big = gsp.Pool.wrap(ctx, z.data_ptr(), z.data_ptr(), 1, 1, 1, 258, block_size=2)
     try:
