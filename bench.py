@@ -464,8 +464,9 @@ def matmul_timing(gsp, torch, ctx, stream, step, calls: int = 50) -> dict:
     hidden = n_heads * head_dim in and out, one batch row per query token of the step, random
     weights as Q8_0 and as F32.  Each call takes the next of enough weight copies to span 512 MB,
     twice the Infinity Cache, as a model's layers do (`us_per_call`); `us_per_call_warm` repeats one
-    copy.  Q8_0 runs on the fp16 matrix cores (x as scaled fp16 pairs), F32 on the fp32 ones; the
-    bytes bound is the weights at 8 TB/s."""
+    copy.  Q8_0 runs on the fp16 matrix cores (x as scaled fp16 pairs), F32 and the K-quants (Q4_K,
+    Q6_K, timed when hidden is a multiple of 256) on the fp32 ones; the bytes bound is the weights at
+    8 TB/s."""
     hidden = step.n_heads * step.head_dim
     batch = int(step.total_q)
     gen = torch.Generator(device="cuda").manual_seed(step.seed)
@@ -477,6 +478,15 @@ def matmul_timing(gsp, torch, ctx, stream, step, calls: int = 50) -> dict:
     q8 = torch.cat([d, q], dim=2).contiguous()
     weights = {"q8_0": (gsp.WTYPE_Q8_0, q8, hidden * nb * 34),
                "f32": (gsp.WTYPE_F32, torch.randn((hidden, hidden), device="cuda", generator=gen), hidden * hidden * 4)}
+    if hidden % 256 == 0:
+        # K-quant super-blocks: random quant bytes with small finite fp16 scales.
+        nk = hidden // 256
+        q4 = torch.randint(0, 256, (hidden, nk, 144), device="cuda", generator=gen, dtype=torch.uint8)
+        q4[:, :, 0:4] = (torch.rand((hidden, nk, 2), device="cuda", generator=gen) * 0.01).half().view(torch.uint8)
+        q6 = torch.randint(0, 256, (hidden, nk, 210), device="cuda", generator=gen, dtype=torch.uint8)
+        q6[:, :, 208:210] = (torch.rand((hidden, nk, 1), device="cuda", generator=gen) * 1e-3).half().view(torch.uint8)
+        weights["q4_k"] = (gsp.WTYPE_Q4_K, q4.contiguous(), hidden * nk * 144)
+        weights["q6_k"] = (gsp.WTYPE_Q6_K, q6.contiguous(), hidden * nk * 210)
     torch.cuda.synchronize()
     flops = 2.0 * batch * hidden * hidden
     out = {"in_dim": hidden, "out_dim": hidden, "batch": batch}

@@ -156,6 +156,8 @@ hipError_t launch_rope_write(int kv_f16, const RopeWriteArgs& a, hipStream_t str
 // Projection GEMM (gsp_matmul.hip): y[b][o] = sum_i W[o][i] x[b][i].
 constexpr int kWeightF32 = 0;   // GGUF type ids
 constexpr int kWeightQ8_0 = 8;
+constexpr int kWeightQ4_K = 12;  // super-blocks of 256 weights, 144 bytes
+constexpr int kWeightQ6_K = 14;  // super-blocks of 256 weights, 210 bytes
 struct MatmulArgs {
     const void* w;       // out_dim rows of in_dim weights (F32, or Q8_0 blocks of 34 bytes)
     const float* x;      // [batch][in_dim]

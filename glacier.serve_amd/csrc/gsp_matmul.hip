@@ -2,8 +2,9 @@
 //   y[b][o] = sum_i W[o][i] * x[b][i]
 // the product QuantKernels.MatMulBatch(type, W, x, y, inDim, outDim, batch)
 // computes around the attention step (PagedTransformerRunner.cs:601-603,659).
-// W holds out_dim rows of in_dim weights (the GGUF [in, out] layout) as F32 or
-// Q8_0 (blocks of 32 int8 with an fp16 scale d: w = d * q).
+// W holds out_dim rows of in_dim weights (the GGUF [in, out] layout) as F32,
+// Q8_0 (blocks of 32 int8 with an fp16 scale d: w = d * q), or the K-quant
+// super-blocks Q4_K and Q6_K (256 weights each, decoded further down).
 //
 // Two forms.  The fp32 form (matmul_batch_kernel, every F32 product and small
 // Q8_0 ones): every weight is exact in fp32 (Q8_0's d * q has at most 19
@@ -96,6 +97,118 @@ __device__ __forceinline__ void expand(float (&w)[16], const WRaw<kWeightQ8_0>& 
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[4 * i + e] = fmaf((float)((qd >> (8 * e)) & 0xFFu), d, bias);
     }
+}
+
+// K-quants: super-blocks of 256 weights in the public GGML layouts.  A
+// 64-wide chunk lies inside one super-block; lane group g's 16 weights are
+// columns 16 g .. 16 g + 15 of the chunk.  Every weight is decoded to the
+// float32 value the layout defines, in its own order of operations, so the
+// products stay exact fp32 products as for F32 weights.
+//
+// Q4_K (144 bytes: fp16 d, fp16 dmin, 12 bytes of 6-bit scales and mins, 128
+// bytes of 4-bit quants): chunk p of the super-block is sub-blocks 2 p (the low
+// nibbles of quant bytes 32 p .. 32 p + 31) and 2 p + 1 (their high nibbles),
+// weight = (d * sc) * q - dmin * m with one rounding.  The lane reads the
+// header dword, the three scale dwords and the four dwords of its 16 quant
+// bytes (32 p + 16 (g % 2)); super-blocks are 4-byte aligned.
+template <>
+struct WRaw<kWeightQ4_K> {
+    uint32_t hdr;    // d | dmin << 16
+    uint32_t sc[3];  // the 12 packed scale/min bytes
+    uint32_t q[4];   // the lane's 16 quant bytes
+    int j;           // the lane's sub-block, 0..7
+};
+
+__device__ __forceinline__ void load_raw(WRaw<kWeightQ4_K>& r, const MatmulArgs& a, int o, int k0, int g) {
+    const int64_t row_bytes = (int64_t)(a.in_dim / 256) * 144;
+    const uint32_t* bw = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)o * row_bytes +
+                                                           (int64_t)(k0 / 256) * 144);
+    const int p = (k0 & 255) >> 6;
+    r.hdr = bw[0];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) r.sc[i] = bw[1 + i];
+    const int qw = 4 + 8 * p + 4 * (g & 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.q[i] = bw[qw + i];
+    r.j = 2 * p + (g >> 1);
+}
+
+__device__ __forceinline__ uint32_t sc_byte(const uint32_t (&sc)[3], int k) {
+    const uint32_t w = k < 4 ? sc[0] : k < 8 ? sc[1] : sc[2];
+    return (w >> (8 * (k & 3))) & 0xFFu;
+}
+
+__device__ __forceinline__ void expand(float (&w)[16], const WRaw<kWeightQ4_K>& r, int g) {
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.hdr & 0xFFFFu));
+    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.hdr >> 16));
+    const int j = r.j;
+    // The six-bit scale and min of sub-block j: bytes j and j + 4 for j < 4;
+    // else the nibbles of byte j + 4 with the top two bits of bytes j - 4
+    // (scale) and j (min).
+    uint32_t scv, mv;
+    if (j < 4) {
+        scv = sc_byte(r.sc, j) & 63u;
+        mv = sc_byte(r.sc, j + 4) & 63u;
+    } else {
+        scv = (sc_byte(r.sc, j + 4) & 0xFu) | ((sc_byte(r.sc, j - 4) >> 6) << 4);
+        mv = (sc_byte(r.sc, j + 4) >> 4) | ((sc_byte(r.sc, j) >> 6) << 4);
+    }
+    const float d1 = d * (float)scv;   // exact
+    const float m1 = dmin * (float)mv;  // exact
+    const int shift = 4 * (g >> 1);     // low nibbles for sub-block 2 p, high for 2 p + 1
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[4 * i + e] = fmaf(d1, (float)((r.q[i] >> (8 * e + shift)) & 0xFu), -m1);
+}
+
+// Q6_K (210 bytes: 128 bytes of the quants' low 4 bits, 64 bytes of their
+// high 2 bits, 16 int8 scales, fp16 d): chunk cc of the super-block is half
+// n = cc / 2, and lane group g takes quarter c = 2 (cc % 2) + g / 2, weights
+// l0 .. l0 + 15 of it (l0 = 16 (g % 2)): low bytes 64 n + 32 (c % 2) + l
+// (low nibble for c < 2, high for c >= 2), bits 2 c .. 2 c + 1 of high bytes
+// 32 n + l, scale 8 n + l / 16 + 2 c; weight = (d * scale) * (q - 32).
+// Super-blocks are only 2-byte aligned (210 bytes), so the lane reads 16-bit
+// words.
+template <>
+struct WRaw<kWeightQ6_K> {
+    uint32_t lo[4];  // the 16 low-nibble bytes (pairs of 16-bit words)
+    uint32_t hi[4];  // the 16 high-bit bytes
+    uint32_t sd;     // the scale byte | d << 16
+    int c;           // the lane's quarter, 0..3
+};
+
+__device__ __forceinline__ void load_raw(WRaw<kWeightQ6_K>& r, const MatmulArgs& a, int o, int k0, int g) {
+    const int64_t row_bytes = (int64_t)(a.in_dim / 256) * 210;
+    const uint8_t* blk = static_cast<const uint8_t*>(a.w) + (int64_t)o * row_bytes + (int64_t)(k0 / 256) * 210;
+    const uint16_t* bh = reinterpret_cast<const uint16_t*>(blk);
+    const int cc = (k0 & 255) >> 6;
+    const int n = cc >> 1;
+    const int c = 2 * (cc & 1) + (g >> 1);
+    const int l0 = 16 * (g & 1);
+    const int lo_h = (64 * n + 32 * (c & 1) + l0) >> 1;  // in 16-bit words
+    const int hi_h = (128 + 32 * n + l0) >> 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r.lo[i] = (uint32_t)bh[lo_h + 2 * i] | ((uint32_t)bh[lo_h + 2 * i + 1] << 16);
+        r.hi[i] = (uint32_t)bh[hi_h + 2 * i] | ((uint32_t)bh[hi_h + 2 * i + 1] << 16);
+    }
+    r.sd = (uint32_t)blk[192 + 8 * n + (l0 >> 4) + 2 * c] | ((uint32_t)bh[104] << 16);
+    r.c = c;
+}
+
+__device__ __forceinline__ void expand(float (&w)[16], const WRaw<kWeightQ6_K>& r, int) {
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.sd >> 16));
+    const float ds = d * (float)(int8_t)(r.sd & 0xFFu);  // exact
+    const int nib = 4 * (r.c >> 1);
+    const int hb = 2 * r.c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int q = (int)(((r.lo[i] >> (8 * e + nib)) & 0xFu) | (((r.hi[i] >> (8 * e + hb)) & 3u) << 4)) - 32;
+            w[4 * i + e] = ds * (float)q;
+        }
 }
 
 template <int WT>
@@ -670,6 +783,10 @@ hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream) {
         hipLaunchKernelGGL(matmul_q8_f16_kernel, grid, dim3(kMmThreads), 0, stream, a);
     } else if (a.w_type == kWeightQ8_0)
         hipLaunchKernelGGL(matmul_batch_kernel<kWeightQ8_0>, grid, dim3(kMmThreads), 0, stream, a);
+    else if (a.w_type == kWeightQ4_K && a.in_dim % 256 == 0)
+        hipLaunchKernelGGL(matmul_batch_kernel<kWeightQ4_K>, grid, dim3(kMmThreads), 0, stream, a);
+    else if (a.w_type == kWeightQ6_K && a.in_dim % 256 == 0)
+        hipLaunchKernelGGL(matmul_batch_kernel<kWeightQ6_K>, grid, dim3(kMmThreads), 0, stream, a);
     else
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();

@@ -747,12 +747,15 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
         return gsp::fail(GSP_E_INVALID_ARG, "negative size (inDim %d, outDim %d, batch %d)", in_dim, out_dim, batch);
     if (batch == 0 || out_dim == 0) return GSP_OK;
     if (!w_dev || !x_dev || !y_dev) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument");
-    if (w_type != GSP_WTYPE_F32 && w_type != GSP_WTYPE_Q8_0)
-        return gsp::fail(GSP_E_UNSUPPORTED, "weight type %d: only F32 (%d) and Q8_0 (%d) are supported", w_type,
-                         GSP_WTYPE_F32, GSP_WTYPE_Q8_0);
-    if (in_dim == 0 || in_dim % 64 != 0)
-        return gsp::fail(GSP_E_UNSUPPORTED, "inDim must be a positive multiple of 64 (got %d)", in_dim);
-    const uintptr_t walign = w_type == GSP_WTYPE_F32 ? 16 : 4;
+    if (w_type != GSP_WTYPE_F32 && w_type != GSP_WTYPE_Q8_0 && w_type != GSP_WTYPE_Q4_K && w_type != GSP_WTYPE_Q6_K)
+        return gsp::fail(GSP_E_UNSUPPORTED,
+                         "weight type %d: only F32 (%d), Q8_0 (%d), Q4_K (%d) and Q6_K (%d) are supported", w_type,
+                         GSP_WTYPE_F32, GSP_WTYPE_Q8_0, GSP_WTYPE_Q4_K, GSP_WTYPE_Q6_K);
+    const bool kquant = w_type == GSP_WTYPE_Q4_K || w_type == GSP_WTYPE_Q6_K;
+    if (in_dim == 0 || in_dim % (kquant ? 256 : 64) != 0)
+        return gsp::fail(GSP_E_UNSUPPORTED, "inDim must be a positive multiple of %d for weight type %d (got %d)",
+                         kquant ? 256 : 64, w_type, in_dim);
+    const uintptr_t walign = w_type == GSP_WTYPE_F32 ? 16 : w_type == GSP_WTYPE_Q6_K ? 2 : 4;
     if (reinterpret_cast<uintptr_t>(w_dev) % walign != 0 || reinterpret_cast<uintptr_t>(x_dev) % 16 != 0 ||
         reinterpret_cast<uintptr_t>(y_dev) % 4 != 0)
         return gsp::fail(GSP_E_INVALID_ARG, "weights must be %d-byte aligned, x 16-byte aligned, y 4-byte aligned",

@@ -52,7 +52,7 @@ SPLIT_RECORDS = 0
 SPLIT_IN_TILE = 1
 ROPE_PAIRS = 0
 ROPE_HALVES = 1
-WTYPE_F32, WTYPE_Q8_0 = 0, 8  # GGUF tensor type ids (gsp_matmul_batch)
+WTYPE_F32, WTYPE_Q8_0, WTYPE_Q4_K, WTYPE_Q6_K = 0, 8, 12, 14  # GGUF tensor type ids (gsp_matmul_batch)
 BLOCK_SIZE = 16
 NOALLOC_SCRATCH_BYTES = 16 << 20  # GSP_NOALLOC_SCRATCH_BYTES: fixed scratch of attention_step_noalloc per GPU
 NOALLOC_COUNTERS = 65536          # GSP_NOALLOC_COUNTERS: its leading int32 counters
@@ -301,7 +301,7 @@ class Context:
     def matmul_batch(self, w_type: int, w_ptr: int, x_ptr: int, y_ptr: int, in_dim: int, out_dim: int,
                      batch: int) -> None:
         """QuantKernels.MatMulBatch (PagedTransformerRunner.cs:601-603,659) on device pointers:
-        y[b][o] = sum_i W[o][i] x[b][i], W as F32 or Q8_0 rows (WTYPE_*)."""
+        y[b][o] = sum_i W[o][i] x[b][i], W as F32, Q8_0, Q4_K or Q6_K rows (WTYPE_*)."""
         _check(self._lib.gsp_matmul_batch(self._h, int(w_type), vp(w_ptr), vp(x_ptr), vp(y_ptr), int(in_dim),
                                           int(out_dim), int(batch)))
 

@@ -193,22 +193,31 @@ int gsp_rope_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_h
 /* Weight types of gsp_matmul_batch: the GGUF tensor type ids. */
 #define GSP_WTYPE_F32 0
 #define GSP_WTYPE_Q8_0 8
+#define GSP_WTYPE_Q4_K 12
+#define GSP_WTYPE_Q6_K 14
 
 /* QuantKernels.MatMulBatch(type, weight, x, y, inDim, outDim, batchSize, xBlockSums)
  * (PagedTransformerRunner.cs:601-603 for Q/K/V, :659 for the attention
  * output): y[b][o] = sum_i W[o][i] * x[b][i] for b < batch, o < out_dim.  w_dev
  * holds out_dim rows of in_dim weights (the GGUF [in, out] layout), as fp32
- * (GSP_WTYPE_F32, 16-byte aligned) or Q8_0 (GSP_WTYPE_Q8_0: per 32 weights a
- * little-endian fp16 scale d and 32 int8 q, w = d * q; 4-byte aligned).
- * x_dev is [batch][in_dim] fp32 (16-byte aligned), y_dev [batch][out_dim] fp32,
- * overwritten; all device pointers.  Every weight is used exactly and sums are
- * fp32.  Small products keep x in fp32.  Large Q8_0 products take x as a
- * scaled fp16 pair on the fp16 matrix cores: each element then carries an
- * absolute error of at most ~2^-22 of its row's largest |x| (~22 significant
- * bits for elements near the row max, fewer for much smaller ones; every
- * finite x stays finite).  in_dim must
- * be a multiple of 64 (GSP_E_UNSUPPORTED otherwise, as for other weight
- * types); the reference's block sums are not needed by these two types. */
+ * (GSP_WTYPE_F32, 16-byte aligned), Q8_0 (GSP_WTYPE_Q8_0: per 32 weights a
+ * little-endian fp16 scale d and 32 int8 q, w = d * q; 4-byte aligned), or
+ * the K-quant super-blocks the reference GPU runner batches
+ * (CudaPagedTransformerRunner.cs:470-473) in the public GGML layouts, 256
+ * weights each: Q4_K (GSP_WTYPE_Q4_K, 144 bytes: fp16 d, fp16 dmin, 12 bytes
+ * of 6-bit scales and mins, 128 bytes of 4-bit quants, w = d*sc*q - dmin*m;
+ * 4-byte aligned) and Q6_K (GSP_WTYPE_Q6_K, 210 bytes: 128 bytes of low 4
+ * bits, 64 of high 2 bits, 16 int8 scales, fp16 d, w = d*sc*(q - 32);
+ * 2-byte aligned).  x_dev is [batch][in_dim] fp32 (16-byte aligned), y_dev
+ * [batch][out_dim] fp32, overwritten; all device pointers.  Every weight is
+ * decoded to the float32 value its format defines and sums are fp32.  Small
+ * products keep x in fp32, and so do all F32 and K-quant products.  Large
+ * Q8_0 products take x as a scaled fp16 pair on the fp16 matrix cores: each
+ * element then carries an absolute error of at most ~2^-22 of its row's
+ * largest |x| (~22 significant bits for elements near the row max, fewer for
+ * much smaller ones; every finite x stays finite).  in_dim must be a multiple
+ * of 64 (256 for the K-quants; GSP_E_UNSUPPORTED otherwise, as for other
+ * weight types); the reference's block sums are not needed by these types. */
 int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const float* x_dev, float* y_dev,
                      int32_t in_dim, int32_t out_dim, int32_t batch);
 

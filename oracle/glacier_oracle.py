@@ -162,6 +162,77 @@ def q8_0_decode(data, rows: int, cols: int) -> np.ndarray:
     return (q * d[..., None]).reshape(rows, cols)
 
 
+# K-quant super-blocks of 256 weights (the GGUF tensor types Q4_K = 12 and Q6_K = 14), decoded as
+# the public GGML block layout defines them (block_q4_K / block_q6_K and their dequantisation in
+# ggml-quants.c).  The reference runner batches its GEMMs on these types
+# (CudaPagedTransformerRunner.cs:470-473) through closed code, so only the layout's arithmetic is
+# restated, in float32 in the layout's own order (the weights a dequantising runner would see).
+WTYPE_Q4_K, WTYPE_Q6_K = 12, 14
+QK_K = 256
+Q4_K_BYTES, Q6_K_BYTES = 144, 210
+
+
+def q4_k_scale_min(scales: np.ndarray):
+    """The eight 6-bit (scale, min) pairs of Q4_K super-blocks from their 12 packed bytes
+    ([..., 12] uint8 -> two [..., 8] int arrays): sub-block j < 4 keeps its scale in the low 6 bits of
+    byte j and its min in those of byte j + 4; j >= 4 keeps the low 4 bits of each in byte j + 4
+    (scale low nibble, min high nibble) and the top 2 bits in bits 6-7 of byte j - 4 (scale) and
+    byte j (min)."""
+    s = scales.astype(np.int32)
+    sc = np.empty(s.shape[:-1] + (8,), np.int32)
+    mn = np.empty_like(sc)
+    sc[..., :4] = s[..., 0:4] & 63
+    mn[..., :4] = s[..., 4:8] & 63
+    sc[..., 4:] = (s[..., 8:12] & 0xF) | ((s[..., 0:4] >> 6) << 4)
+    mn[..., 4:] = (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)
+    return sc, mn
+
+
+def q4_k_decode(data, rows: int, cols: int) -> np.ndarray:
+    """Q4_K rows (cols / 256 super-blocks of 144 bytes each: fp16 d, fp16 dmin, 12 bytes of 6-bit
+    scales and mins, 128 bytes of 4-bit quants) as float64 [rows, cols].  Weights 64 p .. 64 p + 31
+    are the low nibbles of quant bytes 32 p .. 32 p + 31 and weights 64 p + 32 .. 64 p + 63 their high
+    nibbles (sub-blocks 2 p and 2 p + 1); weight i of sub-block j is d * sc_j * q_i - dmin * m_j, with
+    d * sc_j and dmin * m_j formed in float32 (exact) and one rounding in the difference."""
+    b = np.ascontiguousarray(data, dtype=np.uint8).reshape(rows, cols // QK_K, Q4_K_BYTES)
+    d = np.ascontiguousarray(b[..., 0:2]).view(np.float16)[..., 0].astype(np.float32)
+    dmin = np.ascontiguousarray(b[..., 2:4]).view(np.float16)[..., 0].astype(np.float32)
+    sc, mn = q4_k_scale_min(b[..., 4:16])
+    qs = b[..., 16:144].astype(np.int32)
+    q = np.empty(b.shape[:2] + (QK_K,), np.float32)
+    for p in range(4):
+        q[..., 64 * p:64 * p + 32] = qs[..., 32 * p:32 * p + 32] & 0xF
+        q[..., 64 * p + 32:64 * p + 64] = qs[..., 32 * p:32 * p + 32] >> 4
+    d1 = np.repeat(d[..., None] * sc.astype(np.float32), 32, axis=-1)
+    m1 = np.repeat(dmin[..., None] * mn.astype(np.float32), 32, axis=-1)
+    w = d1 * q - m1  # float32: d1 * q is exact, the difference rounds once
+    return w.reshape(rows, cols).astype(np.float64)
+
+
+def q6_k_decode(data, rows: int, cols: int) -> np.ndarray:
+    """Q6_K rows (cols / 256 super-blocks of 210 bytes each: 128 bytes of the quants' low 4 bits,
+    64 bytes of their high 2 bits, 16 int8 scales, fp16 d) as float64 [rows, cols].  Half n (weights
+    128 n ..) reads low bytes 64 n .., high bytes 32 n .. and scales 8 n ..; its quarter c (weights
+    128 n + 32 c + l, l < 32) takes the low (c = 0, 1) or high (c = 2, 3) nibble of low byte
+    64 n + 32 (c % 2) + l, bits 2 c .. 2 c + 1 of high byte 32 n + l and scale 8 n + l / 16 + 2 c;
+    the quant is those six bits minus 32, the weight (d * scale) * q in float32."""
+    b = np.ascontiguousarray(data, dtype=np.uint8).reshape(rows, cols // QK_K, Q6_K_BYTES)
+    ql = b[..., 0:128].astype(np.int32)
+    qh = b[..., 128:192].astype(np.int32)
+    scl = np.ascontiguousarray(b[..., 192:208]).view(np.int8).astype(np.float32)
+    d = np.ascontiguousarray(b[..., 208:210]).view(np.float16)[..., 0].astype(np.float32)
+    w = np.empty(b.shape[:2] + (QK_K,), np.float32)
+    for n in range(2):
+        lo = ql[..., 64 * n:64 * n + 64]
+        hi = qh[..., 32 * n:32 * n + 32]
+        for c in range(4):
+            nib = (lo[..., 32 * (c % 2):32 * (c % 2) + 32] >> (4 * (c // 2))) & 0xF
+            q = (nib | (((hi >> (2 * c)) & 3) << 4)) - 32
+            scale = np.repeat(scl[..., 8 * n + 2 * c:8 * n + 2 * c + 2], 16, axis=-1)
+            w[..., 128 * n + 32 * c:128 * n + 32 * c + 32] = (d[..., None] * scale) * q.astype(np.float32)
+    return w.reshape(rows, cols).astype(np.float64)
+
+
 def matmul_batch(w_type: int, w, x, in_dim: int, out_dim: int) -> np.ndarray:
     """y[b][o] = sum_i W[o][i] * x[b][i] in float64: the product MatMulBatch computes (its own
     arithmetic is closed code, so only this definition is restated).  W holds out_dim rows of in_dim
@@ -170,6 +241,10 @@ def matmul_batch(w_type: int, w, x, in_dim: int, out_dim: int) -> np.ndarray:
         wm = np.asarray(w, dtype=np.float32).reshape(out_dim, in_dim).astype(np.float64)
     elif w_type == WTYPE_Q8_0:
         wm = q8_0_decode(w, out_dim, in_dim)
+    elif w_type == WTYPE_Q4_K:
+        wm = q4_k_decode(w, out_dim, in_dim)
+    elif w_type == WTYPE_Q6_K:
+        wm = q6_k_decode(w, out_dim, in_dim)
     else:
         raise ValueError(f"weight type {w_type} is not restated")
     xm = np.asarray(x, dtype=np.float32).reshape(-1, in_dim).astype(np.float64)

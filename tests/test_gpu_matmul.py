@@ -133,3 +133,68 @@ def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, bat
         bar = bar + 2.0 ** -21 * np.abs(x64).max(axis=1, keepdims=True) * np.abs(wm).sum(axis=1)[None, :]
     assert np.all(np.isfinite(got))
     assert np.all(np.abs(got - ref) <= bar)
+
+
+# ---- K-quant weights (Q4_K, Q6_K: super-blocks of 256 weights) -------------------------------------
+# Random super-blocks are valid encodings: every byte pattern decodes to finite weights once the
+# fp16 scales are finite, so the quants, 6-bit scales/mins and high bits are random bytes and only
+# d (and dmin) are set.  The device decodes each weight to the float32 value the oracle's decoder
+# gives (pinned by closed forms in tests/test_matmul_oracle.py), so the bar is fp32 summation error.
+
+KQ_SHAPES = [
+    (256, 16, 1),
+    (512, 40, 5),
+    (3584, 512, 64),   # Qwen2.5-7B hidden size: 14 super-blocks per row
+    (4096, 48, 17),
+    (256, 96, 100),
+    (512, 37, 3),
+    (1024, 4100, 17),
+    (3584, 3584, 64),  # the Q projection of a Qwen2.5-7B layer for 64 decode rows
+]
+
+
+def _kquant_weights(rng, w_type, out_dim, in_dim):
+    nb = in_dim // orc.QK_K
+    if w_type == orc.WTYPE_Q4_K:
+        b = rng.integers(0, 256, (out_dim, nb, orc.Q4_K_BYTES), dtype=np.uint8)
+        b[..., 0:2] = np.ascontiguousarray((rng.uniform(1e-4, 2e-2, (out_dim, nb, 1))).astype(np.float16)).view(np.uint8)
+        b[..., 2:4] = np.ascontiguousarray((rng.uniform(1e-4, 2e-2, (out_dim, nb, 1))).astype(np.float16)).view(np.uint8)
+        data = b.reshape(-1)
+        return data, orc.q4_k_decode(data, out_dim, in_dim)
+    b = rng.integers(0, 256, (out_dim, nb, orc.Q6_K_BYTES), dtype=np.uint8)
+    b[..., 208:210] = np.ascontiguousarray((rng.uniform(1e-5, 1e-3, (out_dim, nb, 1))).astype(np.float16)).view(np.uint8)
+    data = b.reshape(-1)
+    return data, orc.q6_k_decode(data, out_dim, in_dim)
+
+
+@pytest.mark.parametrize("w_type", [orc.WTYPE_Q4_K, orc.WTYPE_Q6_K], ids=["q4_k", "q6_k"])
+@pytest.mark.parametrize("shape", KQ_SHAPES, ids=lambda s: f"in{s[0]}_out{s[1]}_b{s[2]}")
+def test_kquant_matmul_matches_oracle(torch_mod, gsp, ctx, shape, w_type):
+    in_dim, out_dim, batch = shape
+    print(f"case matmul {shape} type={w_type}", flush=True)
+    rng = np.random.default_rng(in_dim * 3 + out_dim + batch + w_type)
+    data, wm = _kquant_weights(rng, w_type, out_dim, in_dim)
+    assert np.all(np.isfinite(wm))
+    x = rng.standard_normal((batch, in_dim)).astype(np.float32)
+    got = _run(torch_mod, gsp, ctx, w_type, data, x, in_dim, out_dim)
+    ref = orc.matmul_batch(w_type, data, x, in_dim, out_dim)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wm).T
+    assert np.all(np.isfinite(got))
+    assert np.all(np.abs(got - ref) <= 1e-5 * mag + 1e-7)
+    again = _run(torch_mod, gsp, ctx, w_type, data, x, in_dim, out_dim)
+    assert np.array_equal(got, again)
+
+
+def test_kquant_matmul_errors(torch_mod, gsp, ctx):
+    torch = torch_mod
+    w = torch.zeros(4096, device="cuda")
+    x = torch.zeros((4, 512), device="cuda")
+    y = torch.zeros((4, 16), device="cuda")
+    torch.cuda.synchronize()
+    for wt in (gsp.WTYPE_Q4_K, gsp.WTYPE_Q6_K):
+        with pytest.raises(gsp.Unsupported):  # in_dim not a multiple of a 256-weight super-block
+            ctx.matmul_batch(wt, w.data_ptr(), x.data_ptr(), y.data_ptr(), 128, 16, 4)
+    with pytest.raises(gsp.InvalidArgument):  # Q4_K super-blocks are read as 4-byte words
+        ctx.matmul_batch(gsp.WTYPE_Q4_K, w.data_ptr() + 2, x.data_ptr(), y.data_ptr(), 256, 16, 4)
+    with pytest.raises(gsp.InvalidArgument):  # Q6_K as 2-byte words
+        ctx.matmul_batch(gsp.WTYPE_Q6_K, w.data_ptr() + 1, x.data_ptr(), y.data_ptr(), 256, 16, 4)
