@@ -142,13 +142,16 @@ struct RopeWriteArgs {
     float* q;                  // [n][n_heads][d], rotated in place (n_heads 0: none)
     const float* k;            // [n][n_kv][d], rotated into the pool
     const float* v;            // [n][n_kv][v_head_dim], stored as is
-    double log2_base;          // log2(freq_base)
+    const double* freq;        // [rope_dim / 2] angle per position of each pair, or NULL:
+    double log2_base;          // then pair j turns by freq_base^(-2j / rope_dim), log2(freq_base) here
     int32_t n;
     int32_t n_heads;
     int32_t n_kv;
     int32_t head_dim;
     int32_t v_head_dim;
     int32_t style;             // GSP_ROPE_PAIRS or GSP_ROPE_HALVES
+    int32_t rope_dim;          // dims rotated (even, <= head_dim); the rest pass through
+    float mscale;              // scale of the rotated dims
 };
 
 hipError_t launch_rope_write(int kv_f16, const RopeWriteArgs& a, hipStream_t stream);

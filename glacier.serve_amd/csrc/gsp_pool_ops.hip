@@ -36,12 +36,19 @@ __global__ __launch_bounds__(128) void write_tokens_kernel(WriteTokensArgs a) {
     for (int e = e0 + 256; e < a.v_head_dim; e += 128) vd[e] = static_cast<KT>(vs[e]);
 }
 
-// The angle of pair j at position `pos` reduced to [-pi, pi] in fp64, then its
-// cosine and sine in fp32 (shared by both RoPE kernels).
-__device__ inline void rope_angle(double pos, int j, int d, double log2_base, float* c, float* s) {
-    const double ang = pos * exp2(-(2.0 * j / d) * log2_base);
+// Cosine and sine of pair j's angle at position `pos`, times the rotation's
+// scale (shared by both RoPE kernels).  The angle, pos times the pair's rate
+// (the table's, or freq_base^(-2j/rope_dim)), is formed and reduced to
+// [-pi, pi] in fp64, so it stays exact at long positions; cosine and sine are
+// fp32.  A scale of 1 leaves them exact.
+__device__ inline void rope_angle(const RopeWriteArgs& a, double pos, int j, float* c, float* s) {
+    const double rate = a.freq ? a.freq[j] : exp2(-(2.0 * j / a.rope_dim) * a.log2_base);
+    const double ang = pos * rate;
     const double r = ang - 6.283185307179586 * rint(ang * 0.15915494309189535);
-    sincosf((float)r, s, c);
+    float sn, cn;
+    sincosf((float)r, &sn, &cn);
+    *c = cn * a.mscale;
+    *s = sn * a.mscale;
 }
 
 __device__ inline void rope_turn(float x0, float x1, float c, float s, float* y0, float* y1) {
@@ -50,21 +57,20 @@ __device__ inline void rope_turn(float x0, float x1, float c, float s, float* y0
 }
 
 // QuantKernels.RoPE then PagedBlockPool.Store for n tokens
-// (PagedTransformerRunner.cs:253-267, 437-452, 620-634), one workgroup per
-// token.  Pair j of every head turns by pos * base^(-2j/d) (Su et al.,
-// RoFormer): the angle is formed and reduced to [-pi, pi] in fp64, so it
-// stays exact at long positions, and its cosine and sine are taken once per
-// token in fp32.  Q heads are rotated in place, K heads are rotated into the
-// pool slot and V is stored as is; fp16 pools round to nearest even.  A token
-// with block id -1 has no slot: its Q is rotated, its K and V are not stored.
+// (PagedTransformerRunner.cs:253-267, 436-449, 619-634), one workgroup per
+// token.  Pair j < rope_dim/2 of every head turns by its angle (Su et al.,
+// RoFormer; rope_angle), taken once per token; dims from rope_dim on pass
+// through.  Q heads are rotated in place, K heads are rotated into the pool
+// slot and V is stored as is; fp16 pools round to nearest even.  A token with
+// block id -1 has no slot: its Q is rotated, its K and V are not stored.
 template <typename KT>
 __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
     __shared__ float cs[kRopeMaxHalf][2];
     const int i = blockIdx.x;
     const int d = a.head_dim;
-    const int half = d >> 1;
+    const int half = a.rope_dim >> 1;
     const double pos = (double)a.positions[i];
-    for (int j = threadIdx.x; j < half; j += blockDim.x) rope_angle(pos, j, d, a.log2_base, &cs[j][0], &cs[j][1]);
+    for (int j = threadIdx.x; j < half; j += blockDim.x) rope_angle(a, pos, j, &cs[j][0], &cs[j][1]);
     __syncthreads();
     const bool stored = a.block_ids[i] >= 0;
     const int64_t dst = (int64_t)a.block_ids[i] * a.block_stride + a.layer_offset + (int64_t)a.slots[i] * d;
@@ -93,6 +99,14 @@ __global__ __launch_bounds__(256) void rope_write_kernel(RopeWriteArgs a) {
             kd[e1] = static_cast<KT>(x0 * s + x1 * c);
         }
     }
+    // K dims past rope_dim go to the pool as they are.
+    const int tail = d - a.rope_dim;
+    for (int idx = threadIdx.x; stored && idx < a.n_kv * tail; idx += blockDim.x) {
+        const int hk = idx / tail;
+        const int e = a.rope_dim + (idx - hk * tail);
+        static_cast<KT*>(a.k_pool)[dst + (int64_t)hk * a.head_stride + e] =
+            static_cast<KT>(a.k[((int64_t)i * a.n_kv + hk) * d + e]);
+    }
     for (int idx = threadIdx.x; stored && idx < a.n_kv * dv; idx += blockDim.x) {
         const int hk = idx / dv;
         const int e = idx - hk * dv;
@@ -113,20 +127,24 @@ __device__ inline void store4(KT* p, const float4& x) {
 }
 
 // The same RoPE and Store with 16-byte accesses, for head_dim % 8 == 0,
-// v_head_dim % 4 == 0 and 16-byte aligned buffers.  A token's work is a list
-// of items: per Q head and per K head, head_dim / 8 items of four rotation
-// pairs (two float4 of the head), then per V head v_head_dim / 4 items of one
-// float4.  Workgroup (token, y) takes items [256 y, 256 y + 256), one per
-// thread.  The item list does not depend on the token's block id (a token
-// with none skips its K and V stores at the end), so each thread issues its
-// loads together with the token's position, block and slot, before the angle
-// table is built: a workgroup costs about one memory round trip.
+// rope_dim % 8 == 0, v_head_dim % 4 == 0 and 16-byte aligned buffers.  A
+// token's work is a list of items: per Q head and per K head, head_dim / 8
+// items, the first rope_dim / 8 of four rotation pairs (two float4 of the
+// head) and the rest of eight dims past rope_dim (two float4 passed through:
+// nothing to do for Q, a copy into the pool for K), then per V head
+// v_head_dim / 4 items of one float4.  Workgroup (token, y) takes items
+// [256 y, 256 y + 256), one per thread.  The item list does not depend on the
+// token's block id (a token with none skips its K and V stores at the end),
+// so each thread issues its loads together with the token's position, block
+// and slot, before the angle table is built: a workgroup costs about one
+// memory round trip.
 template <typename KT>
 __global__ __launch_bounds__(256) void rope_write_vec_kernel(RopeWriteArgs a) {
     __shared__ float cs[kRopeMaxHalf][2];
     const int i = blockIdx.x;
     const int d = a.head_dim;
-    const int half = d >> 1;
+    const int half = a.rope_dim >> 1;
+    const int rot_items = a.rope_dim >> 3;
     const int dv = a.v_head_dim;
     const int per_head = d >> 3;
     const int nq = a.n_heads * per_head;
@@ -151,9 +169,13 @@ __global__ __launch_bounds__(256) void rope_write_vec_kernel(RopeWriteArgs a) {
         h = (t - nq - nk) / (dv >> 2);
         m = (t - nq - nk) - h * (dv >> 2);
     }
-    // halves: elements 4m.. and half+4m.., pairs 4m..4m+3; pairs: elements 8m.. and 8m+4.., pairs 4m..4m+3.
-    const int e0 = pairs ? 8 * m : 4 * m;
-    const int e1 = pairs ? 8 * m + 4 : 4 * m + half;
+    // Rotation items: halves, elements 4m.. and half+4m.., pairs 4m..4m+3;
+    // pairs, elements 8m.. and 8m+4.., pairs 4m..4m+3.  Items past rope_dim:
+    // elements 8m..8m+7, which Q keeps and K copies.
+    const bool turn = m < rot_items;
+    if (kind == 0 && !turn) kind = 3;
+    const int e0 = pairs || !turn ? 8 * m : 4 * m;
+    const int e1 = pairs || !turn ? 8 * m + 4 : 4 * m + half;
     const float* src = kind == 0 ? a.q + ((int64_t)i * a.n_heads + h) * d
                      : kind == 1 ? a.k + ((int64_t)i * a.n_kv + h) * d
                                  : a.v + ((int64_t)i * a.n_kv + h) * dv;
@@ -168,7 +190,7 @@ __global__ __launch_bounds__(256) void rope_write_vec_kernel(RopeWriteArgs a) {
     const double pos = (double)a.positions[i];
     const int64_t blk = a.block_ids[i];
     const int64_t slot = a.slots[i];
-    for (int j = threadIdx.x; j < half; j += 256) rope_angle(pos, j, d, a.log2_base, &cs[j][0], &cs[j][1]);
+    for (int j = threadIdx.x; j < half; j += 256) rope_angle(a, pos, j, &cs[j][0], &cs[j][1]);
     __syncthreads();
 
     if (kind == 3 || (kind != 0 && blk < 0)) return;
@@ -179,8 +201,10 @@ __global__ __launch_bounds__(256) void rope_write_vec_kernel(RopeWriteArgs a) {
         return;
     }
     const int j0 = 4 * m;
-    float4 y0, y1;
-    if (pairs) {
+    float4 y0 = x0, y1 = x1;
+    if (!turn) {
+        // K dims past rope_dim: stored as they are.
+    } else if (pairs) {
         rope_turn(x0.x, x0.y, cs[j0][0], cs[j0][1], &y0.x, &y0.y);
         rope_turn(x0.z, x0.w, cs[j0 + 1][0], cs[j0 + 1][1], &y0.z, &y0.w);
         rope_turn(x1.x, x1.y, cs[j0 + 2][0], cs[j0 + 2][1], &y1.x, &y1.y);
@@ -263,10 +287,12 @@ hipError_t launch_write_tokens(int kv_f16, const WriteTokensArgs& a, hipStream_t
 
 hipError_t launch_rope_write(int kv_f16, const RopeWriteArgs& a, hipStream_t stream) {
     if (a.n <= 0) return hipSuccess;
-    if (a.head_dim > 2 * kRopeMaxHalf || (a.head_dim & 1)) return hipErrorInvalidValue;
+    if (a.head_dim > 2 * kRopeMaxHalf || (a.head_dim & 1) || a.rope_dim < 2 || a.rope_dim > a.head_dim ||
+        (a.rope_dim & 1))
+        return hipErrorInvalidValue;
     const auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-    const bool vec = a.head_dim % 8 == 0 && a.v_head_dim % 4 == 0 && al16(a.q) && al16(a.k) && al16(a.v) &&
-                     al16(a.k_pool) && al16(a.v_pool);
+    const bool vec = a.head_dim % 8 == 0 && a.rope_dim % 8 == 0 && a.v_head_dim % 4 == 0 && al16(a.q) &&
+                     al16(a.k) && al16(a.v) && al16(a.k_pool) && al16(a.v_pool);
     if (vec) {
         const int items = (a.n_heads + a.n_kv) * (a.head_dim / 8) + a.n_kv * (a.v_head_dim / 4);
         const dim3 grid(a.n, (items + 255) / 256);

@@ -131,6 +131,22 @@ struct gsp_ctx {
     // the pinned slot, and the sizes the launches need).
     gsp::StepPlanner planner;
     gsp::StepPlan plan;
+
+    // RoPE angle-rate tables (gsp_rope_write_*_ex with inv_freq or
+    // freq_factors): kRopeTables entries of kRopeMaxHalf doubles in one device
+    // buffer, matched by content.  A new table takes the entry used least
+    // recently; its copy runs on the context's stream from the pinned
+    // staging, which rope_done guards.
+    static constexpr int kRopeTables = 16;
+    double* d_rope = nullptr;
+    size_t d_rope_count = 0;
+    int32_t* rope_staging = nullptr;
+    size_t rope_staging_words = 0;
+    hipEvent_t rope_done = nullptr;
+    bool rope_pending = false;
+    std::vector<double> rope_rates[kRopeTables];
+    uint64_t rope_used[kRopeTables] = {};
+    uint64_t rope_clock = 0;
 };
 
 struct gsp_pool {
@@ -336,6 +352,7 @@ int gsp_init(int device, gsp_ctx** out) {
         if (!rc) rc = check_hip(hipEventRecord(ctx->upload_done[j], ctx->own_stream), "hipEventRecord");
     }
     if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->aux_done, hipEventDisableTiming), "hipEventCreate");
+    if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->rope_done, hipEventDisableTiming), "hipEventCreate");
     for (int j = 0; j < 2 && !rc; ++j)
         rc = check_hip(hipStreamCreateWithFlags(&ctx->side_stream[j], hipStreamNonBlocking), "hipStreamCreate");
     if (!rc) rc = check_hip(hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming), "hipEventCreate");
@@ -372,6 +389,9 @@ void gsp_shutdown(gsp_ctx* ctx) {
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->d_records) (void)hipFree(ctx->d_records);
     if (ctx->aux_done) (void)hipEventDestroy(ctx->aux_done);
+    if (ctx->d_rope) (void)hipFree(ctx->d_rope);
+    if (ctx->rope_staging) (void)hipHostFree(ctx->rope_staging);
+    if (ctx->rope_done) (void)hipEventDestroy(ctx->rope_done);
     for (int j = 0; j < 2; ++j)
         if (ctx->side_stream[j]) (void)hipStreamSynchronize(ctx->side_stream[j]);
     if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
@@ -552,23 +572,105 @@ int store_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const i
     return check_hip(gsp::launch_write_tokens(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "write_tokens launch");
 }
 
-int check_rope_args(const gsp_pool* pool, int32_t n_heads, float freq_base, int32_t style, const float* q_dev) {
+// The rotation of a RoPE write, checked and resolved for the kernels: the
+// angle-rate table on the device (nullptr: freq_base's formula), rope_dim and
+// mscale.
+struct RopeSetup {
+    const double* freq = nullptr;
+    double log2_base = 0.0;
+    int32_t style = GSP_ROPE_PAIRS;
+    int32_t rope_dim = 0;
+    float mscale = 1.0f;
+};
+
+// Puts the rates `rates` on the device (an entry already holding them, else
+// the entry used least recently) and returns its address.
+int rope_table(gsp_ctx* ctx, const std::vector<double>& rates, const double** out) {
+    int hit = -1, lru = 0;
+    for (int e = 0; e < gsp_ctx::kRopeTables; ++e) {
+        if (ctx->rope_rates[e] == rates) hit = e;
+        if (ctx->rope_used[e] < ctx->rope_used[lru]) lru = e;
+    }
+    if (hit < 0) {
+        bool cap_on = false;
+        int rc = is_capturing(ctx->stream, &cap_on);
+        if (rc) return rc;
+        if (cap_on)
+            return gsp::fail(GSP_E_STATE,
+                             "a new RoPE table must be copied to the device, which cannot happen while the stream is "
+                             "capturing: make one call with this table outside the capture first");
+        rc = ensure_device(ctx, &ctx->d_rope, &ctx->d_rope_count,
+                           (size_t)gsp_ctx::kRopeTables * gsp::kRopeMaxHalf, false);
+        if (!rc) rc = ensure_pinned(&ctx->rope_staging, &ctx->rope_staging_words, 2 * (size_t)gsp::kRopeMaxHalf,
+                                    ctx->rope_done, &ctx->rope_pending);
+        if (rc) return rc;
+        hit = lru;
+        double* dst = ctx->d_rope + (size_t)hit * gsp::kRopeMaxHalf;
+        std::memcpy(ctx->rope_staging, rates.data(), rates.size() * sizeof(double));
+        rc = check_hip(hipMemcpyAsync(dst, ctx->rope_staging, rates.size() * sizeof(double), hipMemcpyHostToDevice,
+                                      ctx->stream),
+                       "hipMemcpyAsync(rope table)");
+        if (!rc) rc = check_hip(hipEventRecord(ctx->rope_done, ctx->stream), "hipEventRecord");
+        if (rc) {
+            ctx->rope_rates[hit].clear();
+            return rc;
+        }
+        ctx->rope_pending = true;
+        ctx->rope_rates[hit] = rates;
+    }
+    ctx->rope_used[hit] = ++ctx->rope_clock;
+    *out = ctx->d_rope + (size_t)hit * gsp::kRopeMaxHalf;
+    return GSP_OK;
+}
+
+// Checks a rotation against the pool (QuantKernels.RoPE's arguments,
+// PagedTransformerRunner.cs:253-264) and resolves it; with `ctx` (after
+// set_device) it also places its table on the device.
+int check_rope(gsp_ctx* ctx, const gsp_pool* pool, int32_t n_heads, const gsp_rope_spec* spec, const float* q_dev,
+               RopeSetup* out) {
+    if (!spec) return gsp::fail(GSP_E_INVALID_ARG, "RoPE spec is NULL");
     if (n_heads < 0) return gsp::fail(GSP_E_INVALID_ARG, "nHeads must be >= 0 (got %d)", n_heads);
     if (n_heads > 0 && !q_dev) return gsp::fail(GSP_E_INVALID_ARG, "q is NULL with nHeads %d", n_heads);
-    if (style != GSP_ROPE_PAIRS && style != GSP_ROPE_HALVES)
-        return gsp::fail(GSP_E_INVALID_ARG, "unknown RoPE pairing %d", style);
-    if (!(freq_base > 0.0f) || !std::isfinite(freq_base))
-        return gsp::fail(GSP_E_INVALID_ARG, "RoPE frequency base must be positive and finite");
+    if (spec->style != GSP_ROPE_PAIRS && spec->style != GSP_ROPE_HALVES)
+        return gsp::fail(GSP_E_INVALID_ARG, "unknown RoPE pairing %d", spec->style);
     const gsp_pool_desc& d = pool->desc;
     if (d.head_dim % 2 != 0 || d.head_dim > 2 * gsp::kRopeMaxHalf)
         return gsp::fail(GSP_E_UNSUPPORTED, "RoPE needs an even headDim <= %d (got %d)", 2 * gsp::kRopeMaxHalf, d.head_dim);
-    return GSP_OK;
+    const int32_t rope_dim = spec->rope_dim == 0 ? d.head_dim : spec->rope_dim;
+    if (rope_dim < 2 || rope_dim > d.head_dim || rope_dim % 2 != 0)
+        return gsp::fail(GSP_E_INVALID_ARG, "ropeDim must be even and in [2, headDim %d] (got %d)", d.head_dim,
+                         spec->rope_dim);
+    const float mscale = spec->mscale == 0.0f ? 1.0f : spec->mscale;
+    if (!(mscale > 0.0f) || !std::isfinite(mscale))
+        return gsp::fail(GSP_E_INVALID_ARG, "RoPE mscale must be positive and finite");
+    if (!spec->inv_freq && (!(spec->freq_base > 0.0f) || !std::isfinite(spec->freq_base)))
+        return gsp::fail(GSP_E_INVALID_ARG, "RoPE frequency base must be positive and finite");
+    const int32_t half = rope_dim / 2;
+    for (int32_t j = 0; spec->inv_freq && j < half; ++j)
+        if (!(spec->inv_freq[j] >= 0.0f) || !std::isfinite(spec->inv_freq[j]))
+            return gsp::fail(GSP_E_INVALID_ARG, "invFreqTable[%d] must be finite and >= 0", j);
+    for (int32_t j = 0; spec->freq_factors && j < half; ++j)
+        if (!(spec->freq_factors[j] > 0.0f) || !std::isfinite(spec->freq_factors[j]))
+            return gsp::fail(GSP_E_INVALID_ARG, "ropeFreqs[%d] must be positive and finite", j);
+    out->style = spec->style;
+    out->rope_dim = rope_dim;
+    out->mscale = mscale;
+    out->freq = nullptr;
+    out->log2_base = spec->inv_freq ? 0.0 : std::log2((double)spec->freq_base);
+    if (!ctx || (!spec->inv_freq && !spec->freq_factors)) return GSP_OK;
+    std::vector<double> rates((size_t)half);
+    for (int32_t j = 0; j < half; ++j) {
+        double r = spec->inv_freq ? (double)spec->inv_freq[j] : std::exp2(-(2.0 * j / rope_dim) * out->log2_base);
+        if (spec->freq_factors) r /= (double)spec->freq_factors[j];
+        rates[j] = r;
+    }
+    return rope_table(ctx, rates, &out->freq);
 }
 
 // RoPE then Store of n tokens whose positions, block ids and slots are already on the device.
 int rope_store_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const int32_t* d_pos,
-                      const int32_t* d_blocks, const int32_t* d_slots, int32_t n_heads, float freq_base,
-                      int32_t style, float* q_dev, const float* k_dev, const float* v_dev) {
+                      const int32_t* d_blocks, const int32_t* d_slots, int32_t n_heads, const RopeSetup& r,
+                      float* q_dev, const float* k_dev, const float* v_dev) {
     const gsp_pool_desc& d = pool->desc;
     gsp::RopeWriteArgs a;
     a.k_pool = pool->k;
@@ -585,14 +687,24 @@ int rope_store_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, co
     a.q = q_dev;
     a.k = k_dev;
     a.v = v_dev;
-    a.log2_base = std::log2((double)freq_base);
+    a.freq = r.freq;
+    a.log2_base = r.log2_base;
     a.n = n;
     a.n_heads = n_heads;
     a.n_kv = d.heads_kv;
     a.head_dim = d.head_dim;
     a.v_head_dim = d.v_head_dim;
-    a.style = style;
+    a.style = r.style;
+    a.rope_dim = r.rope_dim;
+    a.mscale = r.mscale;
     return check_hip(gsp::launch_rope_write(d.kv_dtype == GSP_KV_F16, a, ctx->stream), "rope_write launch");
+}
+
+gsp_rope_spec plain_rope(float freq_base, int32_t style) {
+    gsp_rope_spec s{};
+    s.freq_base = freq_base;
+    s.style = style;
+    return s;
 }
 
 }  // namespace
@@ -630,15 +742,16 @@ int gsp_pool_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
     return store_tokens(ctx, pool, layer, n, ctx->d_aux, ctx->d_aux + n, k_dev, v_dev);
 }
 
-int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const int32_t* positions,
-                          const int32_t* block_ids, const int32_t* slots, int32_t n_heads, float freq_base,
-                          int32_t style, float* q_dev, const float* k_dev, const float* v_dev) {
+int gsp_rope_write_tokens_ex(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const int32_t* positions,
+                             const int32_t* block_ids, const int32_t* slots, int32_t n_heads,
+                             const gsp_rope_spec* rope, float* q_dev, const float* k_dev, const float* v_dev) {
     gsp::clear_error();
     if (!ctx || !pool) return gsp::fail(GSP_E_INVALID_ARG, "ctx/pool is NULL");
     if (n < 0) return gsp::fail(GSP_E_INVALID_ARG, "n must be >= 0 (got %d)", n);
     if (n == 0) return GSP_OK;
     if (!positions || !block_ids || !slots || !k_dev || !v_dev) return gsp::fail(GSP_E_INVALID_ARG, "NULL argument");
-    int rc = check_rope_args(pool, n_heads, freq_base, style, q_dev);
+    RopeSetup r;
+    int rc = check_rope(nullptr, pool, n_heads, rope, q_dev, &r);
     if (rc) return rc;
     const gsp_pool_desc& d = pool->desc;
     if (layer < 0 || layer >= d.layers) return gsp::fail(GSP_E_INVALID_ARG, "layer %d out of range [0, %d)", layer, d.layers);
@@ -650,6 +763,7 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
             return gsp::fail(GSP_E_INVALID_ARG, "slot %d out of range [0, %d)", slots[i], d.block_size);
     }
     rc = set_device(ctx);
+    if (!rc) rc = check_rope(ctx, pool, n_heads, rope, q_dev, &r);
     if (rc) return rc;
     const size_t words = 3 * (size_t)n;
     rc = ensure_pinned(&ctx->aux, &ctx->aux_words, words, ctx->aux_done, &ctx->aux_pending);
@@ -663,8 +777,16 @@ int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
     if (!rc) rc = check_hip(hipEventRecord(ctx->aux_done, ctx->stream), "hipEventRecord");
     if (rc) return rc;
     ctx->aux_pending = true;
-    return rope_store_tokens(ctx, pool, layer, n, ctx->d_aux, ctx->d_aux + n, ctx->d_aux + 2 * (size_t)n, n_heads,
-                             freq_base, style, q_dev, k_dev, v_dev);
+    return rope_store_tokens(ctx, pool, layer, n, ctx->d_aux, ctx->d_aux + n, ctx->d_aux + 2 * (size_t)n, n_heads, r,
+                             q_dev, k_dev, v_dev);
+}
+
+int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n, const int32_t* positions,
+                          const int32_t* block_ids, const int32_t* slots, int32_t n_heads, float freq_base,
+                          int32_t style, float* q_dev, const float* k_dev, const float* v_dev) {
+    const gsp_rope_spec spec = plain_rope(freq_base, style);
+    return gsp_rope_write_tokens_ex(ctx, pool, layer, n, positions, block_ids, slots, n_heads, &spec, q_dev, k_dev,
+                                    v_dev);
 }
 
 }  // extern "C"
@@ -708,23 +830,30 @@ int gsp_pool_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, const float
     return rc ? rc : rd;
 }
 
-int gsp_rope_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_heads, float freq_base, int32_t style,
-                        float* q_dev, const float* k_dev, const float* v_dev) {
+int gsp_rope_write_step_ex(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_heads, const gsp_rope_spec* rope,
+                           float* q_dev, const float* k_dev, const float* v_dev) {
     gsp::clear_error();
     int rc = check_write_step(ctx, pool, layer, k_dev, v_dev);
     if (rc) return rc;
-    rc = check_rope_args(pool, n_heads, freq_base, style, q_dev);
+    RopeSetup r;
+    rc = check_rope(nullptr, pool, n_heads, rope, q_dev, &r);
     if (rc) return rc;
     const int32_t n = ctx->info.total_q;
     if (n == 0) return GSP_OK;
     bool cap = false;
     rc = step_begin(ctx, &cap);
+    if (!rc) rc = check_rope(ctx, pool, n_heads, rope, q_dev, &r);
     if (rc) return rc;
     const int32_t* wr = ctx->d_step + ctx->off_wr;
-    rc = rope_store_tokens(ctx, pool, layer, n, wr, wr + n, wr + 2 * (size_t)n, n_heads, freq_base, style, q_dev,
-                           k_dev, v_dev);
+    rc = rope_store_tokens(ctx, pool, layer, n, wr, wr + n, wr + 2 * (size_t)n, n_heads, r, q_dev, k_dev, v_dev);
     const int rd = step_done(ctx, cap);
     return rc ? rc : rd;
+}
+
+int gsp_rope_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_heads, float freq_base, int32_t style,
+                        float* q_dev, const float* k_dev, const float* v_dev) {
+    const gsp_rope_spec spec = plain_rope(freq_base, style);
+    return gsp_rope_write_step_ex(ctx, pool, layer, n_heads, &spec, q_dev, k_dev, v_dev);
 }
 
 // Q8_0 products with at least this many outputs (batch x out_dim) take the fp16

@@ -159,6 +159,19 @@ class DeviceInfo(ctypes.Structure):
     ]
 
 
+class RopeSpec(ctypes.Structure):
+    """gsp_rope_spec: QuantKernels.RoPE's freqBase, pairing, ropeDim, mscale, invFreqTable and
+    ropeFreqs (host tables of rope_dim / 2 floats, or NULL)."""
+    _fields_ = [
+        ("freq_base", ctypes.c_float),
+        ("style", i32),
+        ("rope_dim", i32),
+        ("mscale", ctypes.c_float),
+        ("inv_freq", ctypes.POINTER(ctypes.c_float)),
+        ("freq_factors", ctypes.POINTER(ctypes.c_float)),
+    ]
+
+
 # name -> (restype, argtypes); every symbol declared in include/glacier_paged.h.
 _SIGNATURES = {
     "gsp_last_error": (ctypes.c_char_p, []),
@@ -181,6 +194,11 @@ _SIGNATURES = {
     "gsp_matmul_batch": (ctypes.c_int, [vp, i32, vp, vp, vp, i32, i32, i32]),
     "gsp_pool_write_step": (ctypes.c_int, [vp, vp, i32, vp, vp]),
     "gsp_rope_write_step": (ctypes.c_int, [vp, vp, i32, i32, ctypes.c_float, i32, vp, vp, vp]),
+    "gsp_rope_write_tokens_ex": (
+        ctypes.c_int,
+        [vp, vp, i32, i32, i32p, i32p, i32p, i32, ctypes.POINTER(RopeSpec), vp, vp, vp],
+    ),
+    "gsp_rope_write_step_ex": (ctypes.c_int, [vp, vp, i32, i32, ctypes.POINTER(RopeSpec), vp, vp, vp]),
     "gsp_pool_copy_block": (ctypes.c_int, [vp, vp, i32, i32, i32]),
     "gsp_pool_upload": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
     "gsp_pool_download": (ctypes.c_int, [vp, vp, i32, ctypes.c_size_t, vp, ctypes.c_size_t]),
@@ -510,6 +528,25 @@ class Pool:
                                             int(n_heads), float(freq_base), int(style), vp(q_ptr), vp(k_ptr),
                                             vp(v_ptr)))
 
+    def rope_write_tokens_ex(self, layer: int, positions, block_ids, slots, n_heads: int, rope: "Rope",
+                             q_ptr: int, k_ptr: int, v_ptr: int) -> None:
+        """rope_write_tokens with the runner's optional RoPE arguments (gsp_rope_write_tokens_ex)."""
+        p = _i32(positions)
+        b = _i32(block_ids)
+        s = _i32(slots)
+        if not (len(p) == len(b) == len(s)):
+            raise ValueError("positions, block_ids and slots differ in length")
+        spec = rope.spec(self.desc.head_dim)
+        _check(load().gsp_rope_write_tokens_ex(self._ctx.handle, self._h, int(layer), len(b), _ptr(p), _ptr(b),
+                                               _ptr(s), int(n_heads), ctypes.byref(spec), vp(q_ptr), vp(k_ptr),
+                                               vp(v_ptr)))
+
+    def rope_write_step_ex(self, layer: int, n_heads: int, rope: "Rope", q_ptr: int, k_ptr: int, v_ptr: int) -> None:
+        """rope_write_step with the runner's optional RoPE arguments (gsp_rope_write_step_ex)."""
+        spec = rope.spec(self.desc.head_dim)
+        _check(load().gsp_rope_write_step_ex(self._ctx.handle, self._h, int(layer), int(n_heads), ctypes.byref(spec),
+                                             vp(q_ptr), vp(k_ptr), vp(v_ptr)))
+
     def write_step(self, layer: int, k_ptr: int, v_ptr: int) -> None:
         """Store of the packed step's own tokens (gsp_pool_write_step): query token i's K/V into the
         slot of its position, from the step's device copy (no host arrays, no upload)."""
@@ -524,6 +561,33 @@ class Pool:
     def copy_block_data(self, src: int, dst: int, valid_tokens: int) -> None:
         """PagedBlockPool.CopyBlockData (PagedBlockPool.cs:304-327) on the device."""
         _check(load().gsp_pool_copy_block(self._ctx.handle, self._h, int(src), int(dst), int(valid_tokens)))
+
+
+class Rope:
+    """The rotation QuantKernels.RoPE applies (PagedTransformerRunner.cs:253-264): freqBase, the
+    pairing (ROPE_PAIRS / ROPE_HALVES), ropeDim (0: the whole head), invFreqTable (YaRN), ropeFreqs
+    (frequency factors) and mscale (0: 1).  Holds its tables for the calls that use it."""
+
+    def __init__(self, freq_base: float, style: int = 0, rope_dim: int = 0, inv_freq=None, freq_factors=None,
+                 mscale: float = 0.0):
+        self.freq_base = float(freq_base)
+        self.style = int(style)
+        self.rope_dim = int(rope_dim)
+        self.mscale = float(mscale)
+        self.inv_freq = None if inv_freq is None else np.ascontiguousarray(inv_freq, dtype=np.float32)
+        self.freq_factors = None if freq_factors is None else np.ascontiguousarray(freq_factors, dtype=np.float32)
+
+    def spec(self, head_dim: int) -> RopeSpec:
+        """The C struct for a pool of `head_dim`; the tables must hold rope_dim / 2 entries, the
+        count the library reads."""
+        half = (self.rope_dim or head_dim) // 2
+        for name, t in (("inv_freq", self.inv_freq), ("freq_factors", self.freq_factors)):
+            if t is not None and t.size != half:
+                raise ValueError(f"{name} holds {t.size} entries; rope_dim / 2 = {half}")
+        fp32 = ctypes.POINTER(ctypes.c_float)
+        tab = lambda t: fp32() if t is None else t.ctypes.data_as(fp32)
+        return RopeSpec(self.freq_base, self.style, self.rope_dim, self.mscale, tab(self.inv_freq),
+                        tab(self.freq_factors))
 
 
 def prefix_hash(parent_hash: int, tokens) -> int:

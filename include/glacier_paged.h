@@ -40,7 +40,7 @@ extern "C" {
 #pragma GCC visibility push(default)
 #endif
 
-#define GSP_ABI_VERSION 8
+#define GSP_ABI_VERSION 9
 #define GSP_BLOCK_SIZE 16 /* PagedBlockPool.DefaultBlockSize (PagedBlockPool.cs:18) */
 #define GSP_MAX_BLOCK_SIZE 4096 /* largest page size of a device pool */
 
@@ -164,7 +164,8 @@ int gsp_pool_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n
  * rotated and stored, and v_dev stored as is, exactly where
  * gsp_pool_write_tokens stores them.  This is the domain of the reference's
  * GPU runner: RoPE over the full head, no frequency table, no YaRN
- * (CudaPagedTransformerRunner.cs:414-418); head_dim even and at most 256.  The
+ * (CudaPagedTransformerRunner.cs:414-418; gsp_rope_write_tokens_ex below takes
+ * the CPU runner's other arguments); head_dim even and at most 256.  The
  * reference's rotation lives in closed code, so `style` (GSP_ROPE_*) names the
  * pairing.  positions, block_ids and slots are host arrays. */
 int gsp_rope_write_tokens(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n,
@@ -189,6 +190,44 @@ int gsp_pool_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, const float
 int gsp_rope_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_heads,
                         float freq_base, int32_t style, float* q_dev, const float* k_dev,
                         const float* v_dev);
+
+/* The rotation with the optional arguments of the reference's CPU runner,
+ * QuantKernels.RoPE(..., ropeFreqs, ropeDim, invFreqTable, mscale)
+ * (PagedTransformerRunner.cs:253-264, :436-447 and :619-631; the YaRN table
+ * and mscale are made at :86-104).  A zeroed struct with freq_base and style
+ * set is gsp_rope_write_tokens's rotation.
+ *   rope_dim      dims rotated per head, even, 2 <= rope_dim <= head_dim (0:
+ *                 head_dim).  Pairs come from the first rope_dim dims (PAIRS:
+ *                 (x[2j], x[2j+1]); HALVES: (x[j], x[j + rope_dim/2])); dims
+ *                 from rope_dim on pass through, into the pool for K.
+ *   inv_freq      NULL, or rope_dim/2 floats (host): pair j turns by
+ *                 pos * inv_freq[j] (a YaRN table).  NULL: by
+ *                 pos * freq_base^(-2j/rope_dim).
+ *   freq_factors  NULL, or rope_dim/2 floats > 0 (host, the GGUF rope_freqs
+ *                 tensor): pair j's angle is divided by freq_factors[j].
+ *   mscale        the rotated pairs are scaled by it (YaRN's attention factor,
+ *                 applied to Q and K alike); 0 means 1.
+ * The angle rates (inv_freq / freq_factors, fp64) of the last table are kept
+ * on the device; a call with another table first copies it there on the
+ * context's stream, which a stream that is capturing into a graph refuses
+ * with GSP_E_STATE (make one eager call with the table before capturing). */
+typedef struct gsp_rope_spec {
+  float freq_base;
+  int32_t style;
+  int32_t rope_dim;
+  float mscale;
+  const float* inv_freq;
+  const float* freq_factors;
+} gsp_rope_spec;
+
+/* gsp_rope_write_tokens and gsp_rope_write_step with the rotation `rope`. */
+int gsp_rope_write_tokens_ex(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n,
+                             const int32_t* positions, const int32_t* block_ids,
+                             const int32_t* slots, int32_t n_heads, const gsp_rope_spec* rope,
+                             float* q_dev, const float* k_dev, const float* v_dev);
+int gsp_rope_write_step_ex(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_heads,
+                           const gsp_rope_spec* rope, float* q_dev, const float* k_dev,
+                           const float* v_dev);
 
 /* Weight types of gsp_matmul_batch: the GGUF tensor type ids. */
 #define GSP_WTYPE_F32 0

@@ -90,6 +90,7 @@ def load():
         "orc_alloc_find_prefix": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.POINTER(i32)]),
         "orc_alloc_bind_prefix": (ctypes.c_int, [vp, ctypes.c_uint64, i32]),
         "orc_rope": (None, [f32p, i32, i32, i32, ctypes.c_double, i32]),
+        "orc_rope_ex": (None, [f32p, i32, i32, i32, ctypes.c_double, i32, i32, f32p, f32p, ctypes.c_double]),
         "orc_btab_create": (vp, [vp]),
         "orc_btab_destroy": (None, [vp]),
         "orc_btab_attach_prefix": (None, [vp, i32p, i32, i32]),
@@ -129,6 +130,46 @@ def rope(x: np.ndarray, pos: int, freq_base: float, style: int = ROPE_PAIRS) -> 
     dim = y.shape[-1]
     load().orc_rope(y.ctypes.data_as(f32p), y.size // dim, dim, int(pos), float(freq_base), int(style))
     return y
+
+
+def rope_ex(x: np.ndarray, pos: int, freq_base: float, style: int = ROPE_PAIRS, rope_dim: int = 0,
+            inv_freq=None, freq_factors=None, mscale: float = 1.0) -> np.ndarray:
+    """QuantKernels.RoPE with ropeDim, invFreqTable, ropeFreqs and mscale (orc_rope_ex): only the
+    first rope_dim dims rotate (0: all), pair j by pos * inv_freq[j] (or freq_base^(-2j/rope_dim))
+    divided by freq_factors[j], scaled by mscale; a rotated copy of x."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    dim = y.shape[-1]
+    rd = int(rope_dim) or dim
+    tabs = [None if t is None else _f32(t) for t in (inv_freq, freq_factors)]
+    for t in tabs:
+        if t is not None and t.size != rd // 2:
+            raise ValueError(f"tables hold rope_dim / 2 = {rd // 2} entries (got {t.size})")
+    ptrs = [None if t is None else t.ctypes.data_as(f32p) for t in tabs]
+    load().orc_rope_ex(y.ctypes.data_as(f32p), y.size // dim, dim, int(pos), float(freq_base), int(style), rd,
+                       ptrs[0], ptrs[1], float(mscale))
+    return y
+
+
+def yarn_inv_freq(rope_dim: int, freq_base: float, factor: float, orig_ctx: int, beta_fast: float = 32.0,
+                  beta_slow: float = 1.0) -> np.ndarray:
+    """A YaRN inverse-frequency table (Peng et al., 2023, "YaRN: Efficient Context Window Extension
+    of Large Language Models", NTK-by-parts): pair j's base rate theta_j = base^(-2j/d) completes
+    r_j = orig_ctx * theta_j / (2 pi) turns over the original context; rates with r_j above
+    beta_fast keep theta_j, below beta_slow become theta_j / factor, and a linear ramp in r_j joins
+    them.  Used to make realistic tables for tests: the product takes any table as given, and how
+    the reference's closed QuantKernels.PrecomputeYarnFrequencies (PagedTransformerRunner.cs:91-96)
+    forms its table is unpinned."""
+    j = np.arange(rope_dim // 2, dtype=np.float64)
+    theta = float(freq_base) ** (-2.0 * j / rope_dim)
+    turns = orig_ctx * theta / (2.0 * np.pi)
+    keep = np.clip((turns - beta_slow) / (beta_fast - beta_slow), 0.0, 1.0)
+    return (keep * theta + (1.0 - keep) * theta / factor).astype(np.float32)
+
+
+def yarn_mscale(factor: float) -> float:
+    """YaRN's attention factor 0.1 ln(s) + 1 for a context scale s > 1 (1 otherwise), from the same
+    paper; a test input, like yarn_inv_freq."""
+    return 1.0 if factor <= 1.0 else 0.1 * float(np.log(factor)) + 1.0
 
 
 # Projection GEMM weights (QuantKernels.MatMulBatch, PagedTransformerRunner.cs:601-603,659).

@@ -505,11 +505,14 @@ void orc_btab_release_all(orc_btab* t) {  // BlockTable.cs:108-116
 
 /* ------------------------------------------------------------------ RoPE */
 
-extern "C" void orc_rope(float* x, int32_t n_vec, int32_t dim, int32_t pos, double freq_base, int32_t style) {
-    const int32_t half = dim / 2;
+extern "C" void orc_rope_ex(float* x, int32_t n_vec, int32_t dim, int32_t pos, double freq_base, int32_t style,
+                            int32_t rope_dim, const float* inv_freq, const float* freq_factors, double mscale) {
+    const int32_t half = rope_dim / 2;
     for (int32_t j = 0; j < half; ++j) {
-        const double ang = (double)pos * std::pow(freq_base, -2.0 * j / dim);
-        const double c = std::cos(ang), s = std::sin(ang);
+        double rate = inv_freq ? (double)inv_freq[j] : std::pow(freq_base, -2.0 * j / rope_dim);
+        if (freq_factors) rate /= (double)freq_factors[j];
+        const double ang = (double)pos * rate;
+        const double c = std::cos(ang) * mscale, s = std::sin(ang) * mscale;
         for (int32_t v = 0; v < n_vec; ++v) {
             float* p = x + (size_t)v * dim;
             float* a = style == ORC_ROPE_PAIRS ? p + 2 * j : p + j;
@@ -519,4 +522,8 @@ extern "C" void orc_rope(float* x, int32_t n_vec, int32_t dim, int32_t pos, doub
             *b = (float)(x0 * s + x1 * c);
         }
     }
+}
+
+extern "C" void orc_rope(float* x, int32_t n_vec, int32_t dim, int32_t pos, double freq_base, int32_t style) {
+    orc_rope_ex(x, n_vec, dim, pos, freq_base, style, dim, nullptr, nullptr, 1.0);
 }

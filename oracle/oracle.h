@@ -11,7 +11,8 @@
  *   PagedBlockPool free stack / refcounts   PagedBlockPool.cs:112-121,178-299,332-353
  *   BlockTable                              BlockTable.cs:13-117
  *   decode / prefill call order             PagedTransformerRunner.cs:521-656, 362-474
- *   RoPE before the store                   PagedTransformerRunner.cs:253-267, 437-452, 620-634
+ *   RoPE before the store                   PagedTransformerRunner.cs:253-267, 436-449, 619-634
+ *   YaRN / partial RoPE arguments           PagedTransformerRunner.cs:86-104, 253-264
  *
  * Parity status of each function is stated at its declaration.
  */
@@ -78,6 +79,19 @@ int orc_compute_attention(const orc_pool* pool, const orc_table* table, int32_t 
  * uses is unpinned. */
 enum { ORC_ROPE_PAIRS = 0, ORC_ROPE_HALVES = 1 };
 void orc_rope(float* x, int32_t n_vec, int32_t dim, int32_t pos, double freq_base, int32_t style);
+
+/* The same rotation with the runner's optional arguments, QuantKernels.RoPE(...,
+ * ropeFreqs, ropeDim, invFreqTable, mscale) (PagedTransformerRunner.cs:253-264,
+ * 436-447, 619-631): only the first rope_dim dims of each vector are paired
+ * (PAIRS: (x[2j], x[2j+1]); HALVES: (x[j], x[j + rope_dim/2])), the rest are
+ * left as they are; pair j's angle is pos * inv_freq[j] (freq_base^(-2j/rope_dim)
+ * when inv_freq is NULL), divided by freq_factors[j] when given; the rotated
+ * pair is multiplied by mscale.  All in fp64.  Parity: the rotation of a
+ * given table is pinned by closed forms (tests/test_rope.py); how the closed
+ * QuantKernels.RoPE combines a table with ropeFreqs, and whether it scales
+ * the dims past ropeDim, is unpinned (no reference test covers them). */
+void orc_rope_ex(float* x, int32_t n_vec, int32_t dim, int32_t pos, double freq_base, int32_t style,
+                 int32_t rope_dim, const float* inv_freq, const float* freq_factors, double mscale);
 
 /* One engine step the way the reference runner drives the kernel: rows in
  * order (PagedTransformerRunner.cs:605-656), query token i of a row at

@@ -46,7 +46,7 @@ def test_no_unexpected_exports():
 
 def test_abi_version_and_error_string():
     lib = gp.load()
-    assert lib.gsp_abi_version() == 8
+    assert lib.gsp_abi_version() == 9
     # A host-only call that fails sets the thread-local message.
     h = ctypes.c_void_p()
     rc = lib.gsp_block_allocator_create(0, 16, ctypes.byref(h))

@@ -278,3 +278,278 @@ def test_engine_tick_sequence_over_layers(torch_mod, gsp, ctx, dt, bs):
         print(f"layer {l}: max abs err {err:.3e}", flush=True)
         assert not np.isnan(outs[l]).any()
         assert err <= (1e-4 if dt == "f32" else 2e-3)
+
+
+# ---- The runner's optional RoPE arguments (gsp_rope_write_*_ex): ropeDim
+# (partial rotation), invFreqTable (YaRN), ropeFreqs (frequency factors) and
+# mscale, PagedTransformerRunner.cs:86-104 and :253-264, against orc_rope_ex.
+
+def _factors(n):
+    return np.linspace(1.0, 6.0, n).astype(np.float32)
+
+
+EX_CASES = [
+    # (n_heads, n_kv, head_dim, kv dtype, rope_dim, YaRN table, frequency factors, mscale)
+    (16, 2, 128, "f32", 64, False, False, 0.0),   # partial, 16-byte kernel
+    (16, 2, 128, "f16", 64, True, False, None),   # partial YaRN, fp16 pool
+    (28, 4, 128, "f32", 0, True, False, None),    # full-head YaRN
+    (8, 8, 64, "f32", 0, False, True, 0.0),       # frequency factors
+    (12, 4, 128, "f16", 96, True, True, 1.25),    # all of them
+    (6, 2, 64, "f32", 36, False, False, 0.0),     # rope_dim % 8 != 0: the per-element kernel
+    (6, 2, 64, "f16", 20, True, True, 1.5),       # the same with tables
+    (4, 2, 48, "f32", 16, True, False, None),     # 16-byte kernel, 48-dim heads
+]
+
+
+def _rope_of(gsp, case, style, base):
+    nh, nkv, d, dt, rd, yarn, fac, ms = case
+    half = (rd or d) // 2
+    inv = orc.yarn_inv_freq(rd or d, base, 8.0, 4096) if yarn else None
+    ff = _factors(half) if fac else None
+    if ms is None:
+        ms = orc.yarn_mscale(8.0)
+    return gsp.Rope(base, style, rd, inv_freq=inv, freq_factors=ff, mscale=ms)
+
+
+def _oracle_rot(x, pos, rope):
+    return orc.rope_ex(x, pos, rope.freq_base, rope.style, rope.rope_dim, rope.inv_freq, rope.freq_factors,
+                       rope.mscale or 1.0)
+
+
+@pytest.mark.parametrize("style", [0, 1], ids=["pairs", "halves"])
+@pytest.mark.parametrize("case", EX_CASES, ids=lambda c: f"{c[0]}q{c[1]}kv_d{c[2]}_r{c[4]}_{c[3]}"
+                         f"{'_yarn' if c[5] else ''}{'_ff' if c[6] else ''}")
+def test_rope_ex_write_matches_oracle(torch_mod, gsp, ctx, case, style):
+    """Rotated dims within 2e-6 x mscale of the fp64 oracle (fp32), one fp16 ulp (fp16 pools); dims
+    past rope_dim are Q's own values and K's values stored as they are, bit for bit; V bit-exact."""
+    torch = torch_mod
+    nh, nkv, d, dt, rd, yarn, fac, ms = case
+    base = 1000000.0
+    print(f"case rope_ex {case} style={style}", flush=True)
+    rope = _rope_of(gsp, case, style, base)
+    rng = np.random.default_rng(nh * 11 + d + rd + style)
+    n, total_blocks = 29, 64
+    positions, blocks, slots = _tokens(rng, n, total_blocks)
+    positions[3] = 131071  # far past the original context of the YaRN table
+    q = rng.standard_normal((n, nh, d)).astype(np.float32)
+    k = rng.standard_normal((n, nkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, nkv, d)).astype(np.float32)
+    pool = gsp.Pool.create(ctx, total_blocks=total_blocks, layers=2, heads_kv=nkv, head_dim=d,
+                           kv_dtype=gsp.KV_F16 if dt == "f16" else gsp.KV_F32)
+    qd = torch.from_numpy(q).cuda()
+    kd = torch.from_numpy(k).cuda()
+    vd = torch.from_numpy(v).cuda()
+    torch.cuda.synchronize()
+    pool.rope_write_tokens_ex(1, positions, blocks, slots, nh, rope, qd.data_ptr(), kd.data_ptr(), vd.data_ptr())
+    ctx.sync()
+    npdt = np.float16 if dt == "f16" else np.float32
+    _, _, kb, vb = pool.arenas()
+    K = pool.download(0, kb).view(npdt).reshape(total_blocks, 2, nkv, 16, d)
+    V = pool.download(1, vb).view(npdt).reshape(total_blocks, 2, nkv, 16, d)
+    got_q = qd.cpu().numpy()
+    r = rd or d
+    scale = max(1.0, rope.mscale)
+    tol = 2e-3 * scale if dt == "f16" else 2e-6 * scale
+    for i in range(n):
+        ref_q = _oracle_rot(q[i], int(positions[i]), rope)
+        ref_k = _oracle_rot(k[i], int(positions[i]), rope)
+        assert max_err(got_q[i][:, :r], ref_q[:, :r]) <= 2e-6 * scale, f"q of token {i} at {positions[i]}"
+        assert np.array_equal(got_q[i][:, r:], q[i][:, r:]), f"q tail of token {i}"
+        got_k = K[blocks[i], 1, :, slots[i]]
+        assert max_err(got_k[:, :r].astype(np.float32), ref_k[:, :r]) <= tol, f"k of token {i}"
+        assert np.array_equal(got_k[:, r:], k[i][:, r:].astype(npdt)), f"k tail of token {i}"
+        assert np.array_equal(V[blocks[i], 1, :, slots[i]], v[i].astype(npdt)), f"v of token {i}"
+    mask = np.ones(K.shape, bool)
+    mask[blocks, 1, :, slots] = False
+    assert not K[mask].any() and not V[mask].any()
+    pool.destroy()
+
+
+def test_rope_ex_plain_spec_is_the_plain_call(torch_mod, gsp, ctx):
+    """A spec with only freq_base and style set is gsp_rope_write_tokens, bit for bit."""
+    torch = torch_mod
+    rng = np.random.default_rng(201)
+    n, nh, nkv, d = 17, 8, 2, 128
+    positions, blocks, slots = _tokens(rng, n, 32)
+    q = rng.standard_normal((n, nh, d)).astype(np.float32)
+    k = rng.standard_normal((n, nkv, d)).astype(np.float32)
+    pools = [gsp.Pool.create(ctx, total_blocks=32, layers=1, heads_kv=nkv, head_dim=d) for _ in range(2)]
+    qs = [torch.from_numpy(q).cuda() for _ in range(2)]
+    kd = torch.from_numpy(k).cuda()
+    torch.cuda.synchronize()
+    pools[0].rope_write_tokens(0, positions, blocks, slots, nh, 5e5, 1, qs[0].data_ptr(), kd.data_ptr(), kd.data_ptr())
+    pools[1].rope_write_tokens_ex(0, positions, blocks, slots, nh, gsp.Rope(5e5, 1), qs[1].data_ptr(), kd.data_ptr(),
+                                  kd.data_ptr())
+    ctx.sync()
+    assert torch.equal(qs[0], qs[1])
+    _, _, kb, _ = pools[0].arenas()
+    assert np.array_equal(pools[0].download(0, kb), pools[1].download(0, kb))
+    for p in pools:
+        p.destroy()
+
+
+def test_rope_ex_errors_and_table_cache(torch_mod, gsp, ctx):
+    """Malformed rotations are refused before anything is enqueued; more distinct tables than the
+    context keeps on the device (16) still rotate by their own rates, each checked against the
+    oracle, including a table evicted and set again."""
+    torch = torch_mod
+    import ctypes
+
+    d = 64
+    pool = gsp.Pool.create(ctx, total_blocks=8, layers=1, heads_kv=2, head_dim=d)
+    k = torch.ones((2, 2, d), device="cuda")
+    q = torch.full((2, 4, d), 0.5, device="cuda")
+    torch.cuda.synchronize()
+    bad = [
+        gsp.Rope(1e4, 0, rope_dim=3), gsp.Rope(1e4, 0, rope_dim=66), gsp.Rope(1e4, 0, rope_dim=-2),
+        gsp.Rope(1e4, 0, mscale=-1.0), gsp.Rope(1e4, 0, mscale=float("nan")), gsp.Rope(1e4, 2),
+        gsp.Rope(0.0, 0), gsp.Rope(1e4, 0, inv_freq=np.full(32, np.nan)),
+        gsp.Rope(1e4, 0, inv_freq=np.full(32, -1.0)), gsp.Rope(1e4, 0, freq_factors=np.zeros(32)),
+        gsp.Rope(1e4, 0, freq_factors=np.full(32, np.inf)),
+    ]
+    for rope in bad:
+        with pytest.raises(gsp.InvalidArgument):
+            pool.rope_write_tokens_ex(0, [1], [0], [0], 4, rope, q.data_ptr(), k.data_ptr(), k.data_ptr())
+    with pytest.raises(ValueError):  # the wrapper checks the table length the library will read
+        pool.rope_write_tokens_ex(0, [1], [0], [0], 4, gsp.Rope(1e4, 0, inv_freq=np.ones(31)), q.data_ptr(),
+                                  k.data_ptr(), k.data_ptr())
+    rc = gsp.load().gsp_rope_write_tokens_ex(ctx.handle, pool.handle, 0, 1, (ctypes.c_int32 * 1)(1),
+                                             (ctypes.c_int32 * 1)(0), (ctypes.c_int32 * 1)(0), 0, None, None,
+                                             ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(k.data_ptr()))
+    assert rc == gsp.GSP_E_INVALID_ARG
+    # A table with inv_freq ignores freq_base, so a zero base is accepted with it.
+    rng = np.random.default_rng(202)
+    kv = rng.standard_normal((1, 2, d)).astype(np.float32)
+    kd = torch.from_numpy(kv).cuda()
+    torch.cuda.synchronize()
+    _, _, kb, _ = pool.arenas()
+    tables = [orc.yarn_inv_freq(d, 1e4, 1.0 + t, 2048) for t in range(18)] + [None]
+    tables.append(orc.yarn_inv_freq(d, 1e4, 1.0, 2048))  # evicted by now: set again
+    for t, tab in enumerate(tables):
+        rope = gsp.Rope(0.0 if tab is not None else 1e4, 1, inv_freq=tab)
+        pos = 1000 + 37 * t
+        pool.rope_write_tokens_ex(0, [pos], [t % 8], [t % 16], 0, rope, 0, kd.data_ptr(), kd.data_ptr())
+        ctx.sync()
+        K = pool.download(0, kb).view(np.float32).reshape(8, 1, 2, 16, d)
+        ref = orc.rope_ex(kv[0], pos, rope.freq_base, 1, inv_freq=tab)
+        assert max_err(K[t % 8, 0, :, t % 16], ref) <= 2e-6, f"table {t}"
+    pool.destroy()
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_yarn_engine_tick_over_layers(torch_mod, gsp, ctx, dt):
+    """The engine tick with the CPU runner's YaRN setup on a partial-RoPE head: one gsp_step_pack,
+    then per layer gsp_rope_write_step_ex (rope_dim 64 of 128, a YaRN table, mscale on Q and K) and
+    gsp_attention_step at scale 1/sqrt(head_dim) (PagedTransformerRunner.cs:100-103 keeps the scale),
+    against the oracle doing the same rotation, store and attention per layer; the step form's stores
+    equal gsp_rope_write_tokens_ex's bit for bit."""
+    torch = torch_mod
+    nh, nkv, d, base, layers, rd = 16, 2, 128, 1000000.0, 2, 64
+    rope = gsp.Rope(base, 1, rd, inv_freq=orc.yarn_inv_freq(rd, base, 4.0, 4096), mscale=orc.yarn_mscale(4.0))
+    q_lens = np.array([1, 1, 21, 1], np.int32)
+    step = workloads.small_step(seed=141, rows=4, n_heads=nh, n_kv=nkv, head_dim=d, kv_dtype=dt, ctx_lo=30,
+                                ctx_hi=400, total_blocks=256, q_lens=q_lens)
+    for b in range(step.num_rows):
+        if step.lens[b] == 1:
+            step.positions[b] = step.token_counts[b] - 1
+    print(f"case yarn tick {dt}", flush=True)
+    rng = np.random.default_rng(142)
+    _, k, v = workloads.host_values(step, layers=layers)
+    pool, keep = to_device_pool(torch, gsp, ctx, step, k, v)
+    twin, keep2 = to_device_pool(torch, gsp, ctx, step, k, v)
+    nq = step.total_q
+    qs = [rng.standard_normal((nq, nh, d)).astype(np.float32) for _ in range(layers)]
+    ks = [rng.standard_normal((nq, nkv, d)).astype(np.float32) for _ in range(layers)]
+    vs = [rng.standard_normal((nq, nkv, d)).astype(np.float32) for _ in range(layers)]
+    pos = np.concatenate([int(step.positions[b]) + np.arange(int(step.lens[b])) for b in range(step.num_rows)])
+    blk = np.array([int(step.table(b)[p // 16]) for b in range(step.num_rows)
+                    for p in int(step.positions[b]) + np.arange(int(step.lens[b]))], np.int32)
+    ctx.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len,
+                  q_lens=step.q_lens)
+    outs = []
+    for l in range(layers):
+        qd = torch.from_numpy(qs[l]).cuda()
+        q2 = torch.from_numpy(qs[l]).cuda()
+        kd = torch.from_numpy(ks[l]).cuda()
+        vd = torch.from_numpy(vs[l]).cuda()
+        out = torch.full((nq, nh, d), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        pool.rope_write_step_ex(l, nh, rope, qd.data_ptr(), kd.data_ptr(), vd.data_ptr())
+        twin.rope_write_tokens_ex(l, pos, blk, pos % 16, nh, rope, q2.data_ptr(), kd.data_ptr(), vd.data_ptr())
+        ctx.attention_step(pool, l, nh, qd.data_ptr(), out.data_ptr(), step.scale)
+        ctx.sync()
+        assert torch.equal(qd, q2)
+        outs.append(out.cpu().numpy())
+    npdt = np.float16 if dt == "f16" else np.float32
+    _, _, kb, vb = pool.arenas()
+    assert np.array_equal(pool.download(0, kb), twin.download(0, kb))
+    assert np.array_equal(pool.download(1, vb), twin.download(1, vb))
+    pool.destroy()
+    twin.destroy()
+    k2, v2 = k.copy(), v.copy()
+    for l in range(layers):
+        qr = np.empty_like(qs[l])
+        for i in range(nq):
+            p = int(pos[i])
+            qr[i] = _oracle_rot(qs[l][i], p, rope)
+            k2[blk[i], l, :, p % 16] = _oracle_rot(ks[l][i], p, rope).astype(npdt).astype(np.float32)
+            v2[blk[i], l, :, p % 16] = vs[l][i].astype(npdt).astype(np.float32)
+        ref = oracle_step(step, qr, k2, v2, layer=l)
+        err = max_err(outs[l], ref)
+        print(f"layer {l}: max abs err {err:.3e}", flush=True)
+        assert not np.isnan(outs[l]).any()
+        assert err <= (1e-4 if dt == "f32" else 2e-3)
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_rope_ex_step_capture(torch_mod, gsp):
+    """gsp_rope_write_step_ex captured into a graph: a table set by an eager call replays with its
+    rates (every replay equal to the eager write, eager work between replays); a table not yet on
+    the device is refused during the capture with a state error."""
+    torch = torch_mod
+    nkv, d, base = 2, 128, 1e6
+    step = workloads.small_step(seed=151, rows=6, n_heads=8, n_kv=nkv, head_dim=d, ctx_lo=20, ctx_hi=200,
+                                total_blocks=128)
+    for b in range(step.num_rows):
+        step.positions[b] = step.token_counts[b] - 1
+    rope = gsp.Rope(base, 1, 96, inv_freq=orc.yarn_inv_freq(96, base, 4.0, 4096), mscale=1.2)
+    other = gsp.Rope(base, 1, 96, inv_freq=orc.yarn_inv_freq(96, base, 2.0, 4096))
+    print("case rope_ex capture", flush=True)
+    rng = np.random.default_rng(152)
+    k = rng.standard_normal((step.total_q, nkv, d)).astype(np.float32)
+    v = rng.standard_normal((step.total_q, nkv, d)).astype(np.float32)
+    with gsp.Context(0) as fresh:
+        pool = gsp.Pool.create(fresh, total_blocks=step.total_blocks, layers=1, heads_kv=nkv, head_dim=d)
+        stream = torch.cuda.Stream()
+        fresh.set_stream(stream.cuda_stream)
+        try:
+            kd = torch.from_numpy(k).cuda()
+            vd = torch.from_numpy(v).cuda()
+            torch.cuda.synchronize()
+            fresh.pack_step(pool, step.positions, step.token_counts, step.bt_offsets, step.bt_ids, step.max_seq_len)
+            pool.rope_write_step_ex(0, 0, rope, 0, kd.data_ptr(), vd.data_ptr())
+            fresh.sync()
+            _, _, kb, _ = pool.arenas()
+            eager = pool.download(0, kb).copy()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                pool.rope_write_step_ex(0, 0, rope, 0, kd.data_ptr(), vd.data_ptr())
+            bad = torch.cuda.CUDAGraph()
+            with pytest.raises(gsp.StateError):
+                with torch.cuda.graph(bad, stream=stream):
+                    pool.rope_write_step_ex(0, 0, other, 0, kd.data_ptr(), vd.data_ptr())
+            del bad
+            torch.cuda.synchronize()
+            for rep in range(3):
+                pool.upload(0, np.zeros(kb // 4, np.float32))
+                fresh.sync()
+                graph.replay()
+                torch.cuda.synchronize()
+                assert np.array_equal(pool.download(0, kb), eager), f"replay {rep}"
+                # Eager work between replays, with the other table (now placed on the device too).
+                pool.rope_write_step_ex(0, 0, other, 0, kd.data_ptr(), vd.data_ptr())
+                fresh.sync()
+            del graph
+        finally:
+            fresh.set_stream(None)
+            pool.destroy()
