@@ -31,17 +31,18 @@
 //
 // Shapes.  The fixed-shape instantiations (kExact) take head_dim ==
 // v_head_dim == DP in {64, 128} and 16-token pages, all compile-time.  The
-// general ones take any even head_dim and v_head_dim up to DP (64, 128 or
-// 256) and pages of 1..16 tokens at run time, the domain of the reference GPU
-// runner (CudaPagedTransformerRunner.cs:402-412) and of the CPU kernel's
-// generic path (PagedAttentionKernel.cs:326-370):
+// general ones take any head_dim and v_head_dim up to DP (64, 128 or 256) and
+// pages of 1..16 tokens at run time, the domain of the reference GPU runner
+// (CudaPagedTransformerRunner.cs:402-412) and of the CPU kernel's generic
+// path, which takes odd widths too (PagedAttentionKernel.cs:326-370):
 //  - a page of bs < 16 tokens fills the tile's first bs rows; the rest read
 //    as zero (past the descriptor's range) and are masked like a short page;
 //  - dims past head_dim (v_head_dim) are loaded from an offset past the
 //    descriptor's range, so they read as zero without a fetch; Q's are zero,
 //    so padded dims add nothing to S, and padded O columns are never stored;
 //  - kVec4 loads 4 dims per piece (head_dim, v_head_dim multiples of 4);
-//    kVec2 loads 2 (any even widths), so a piece never straddles a row.
+//    kVec2 loads 2 (any even widths) and kVec1 one (odd widths, whose rows
+//    are not 8-byte aligned), so a piece never straddles a row.
 // A GQA group above 16 heads runs as tiles of 16 over grid.y, each tile
 // rereading the pages (the reference CPU kernel rereads them per head).
 #pragma once
@@ -56,7 +57,7 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-enum DecodeMode { kExact = 0, kVec4 = 1, kVec2 = 2 };
+enum DecodeMode { kExact = 0, kVec4 = 1, kVec2 = 2, kVec1 = 3 };
 
 constexpr int kTileTokens = 16;  // token rows of a page tile (MFMA M for S^T)
 // An element offset past any page's descriptor range: the load reads zero
@@ -152,11 +153,32 @@ struct Raw2<_Float16> {
     }
 };
 
+// One element at element offset `off`.
+template <typename KT>
+struct Raw1;
+template <>
+struct Raw1<float> {
+    __device__ static float load(__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off * 4, 0, 0));
+    }
+};
+template <>
+struct Raw1<_Float16> {
+    __device__ static _Float16 load(__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(r, off * 2, 0, 0));
+    }
+};
+
 // Four elements of a row at dims dim .. dim+3 (element offset `row + dim`),
-// zero past `width`, as one piece (kVec4) or two (kVec2).
+// zero past `width`, as one piece (kVec4), two (kVec2) or four (kVec1).
 template <typename KT, int MODE>
 __device__ __forceinline__ typename Raw4<KT>::T load4(__amdgpu_buffer_rsrc_t r, int row, int dim, int width) {
-    if constexpr (MODE == kVec2) {
+    if constexpr (MODE == kVec1) {
+        typename Raw4<KT>::T x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = Raw1<KT>::load(r, dim + i < width ? row + dim + i : kOutOfRange);
+        return x;
+    } else if constexpr (MODE == kVec2) {
         const auto lo = Raw2<KT>::load(r, dim < width ? row + dim : kOutOfRange);
         const auto hi = Raw2<KT>::load(r, dim + 2 < width ? row + dim + 2 : kOutOfRange);
         return typename Raw4<KT>::T{lo[0], lo[1], hi[0], hi[1]};
@@ -261,6 +283,9 @@ __device__ __forceinline__ void load_q(QRaw<D>& qr, const DecodeArgs& a, int qi,
             qr.q[j] = *reinterpret_cast<const f4*>(qrow + dim);
         } else if constexpr (MODE == kVec4) {
             qr.q[j] = dim < geo.d ? *reinterpret_cast<const f4*>(qrow + dim) : f4{0.f, 0.f, 0.f, 0.f};
+        } else if constexpr (MODE == kVec1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qr.q[j][i] = dim + i < geo.d ? qrow[dim + i] : 0.f;
         } else {
             const f2 lo = dim < geo.d ? *reinterpret_cast<const f2*>(qrow + dim) : f2{0.f, 0.f};
             const f2 hi = dim + 2 < geo.d ? *reinterpret_cast<const f2*>(qrow + dim + 2) : f2{0.f, 0.f};

@@ -24,9 +24,10 @@ hipError_t launch_typed(dim3 grid, const DecodeArgs& a, hipStream_t stream) {
             launch_one<128, KT, kExact>(grid, a, stream);
         else
             launch_one<64, KT, kExact>(grid, a, stream);
-    } else if (d % 2 || dv % 2 || d < 2 || dv < 2 || d > 256 || dv > 256 || a.block_size < 1 ||
-               a.block_size > kTileTokens) {
+    } else if (d < 1 || dv < 1 || d > 256 || dv > 256 || a.block_size < 1 || a.block_size > kTileTokens) {
         return hipErrorInvalidValue;
+    } else if (d % 2 || dv % 2) {
+        launch_one<256, KT, kVec1>(grid, a, stream);
     } else if (d % 4 == 0 && dv % 4 == 0) {
         const int w = max(d, dv);
         if (w <= 64)

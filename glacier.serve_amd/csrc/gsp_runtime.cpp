@@ -1225,9 +1225,10 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     if (!ctx->step_valid) return gsp::fail(GSP_E_STATE, "gsp_step_pack must succeed before gsp_attention_step");
     const gsp_pool_desc& d = pool->desc;
     if (sink_logit) return gsp::fail(GSP_E_UNSUPPORTED, "attention sinks are not supported on the GPU path");
-    // The reference GPU runner's domain (CudaPagedTransformerRunner.cs:408-412).
-    if (d.head_dim % 2 || d.v_head_dim % 2 || d.head_dim > 256 || d.v_head_dim > 256)
-        return gsp::fail(GSP_E_UNSUPPORTED, "headDim (%d) and vHeadDim (%d) must be even and at most 256", d.head_dim,
+    // The reference GPU runner's bound (CudaPagedTransformerRunner.cs:408-412);
+    // odd widths as in the CPU kernel's generic path (PagedAttentionKernel.cs:326-370).
+    if (d.head_dim > 256 || d.v_head_dim > 256)
+        return gsp::fail(GSP_E_UNSUPPORTED, "headDim (%d) and vHeadDim (%d) must be at most 256", d.head_dim,
                          d.v_head_dim);
     if (layer < 0 || layer >= d.layers) return gsp::fail(GSP_E_INVALID_ARG, "layer %d out of range [0, %d)", layer, d.layers);
     if (n_heads < 1 || n_heads % d.heads_kv != 0)

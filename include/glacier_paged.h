@@ -397,8 +397,8 @@ int gsp_set_prefill_split(gsp_ctx* ctx, int32_t mode);
  * unsupported on the GPU path, as in CudaPagedTransformerRunner.cs:431.
  * Supported, the domain of the reference GPU runner
  * (CudaPagedTransformerRunner.cs:402-412) and then some: head_dim and
- * v_head_dim even and at most 256 (v_head_dim may differ from head_dim, as
- * in the CPU kernel's generic path, PagedAttentionKernel.cs:326-370); any
+ * v_head_dim from 1 to 256, odd ones included, and v_head_dim may differ from
+ * head_dim, as in the CPU kernel's generic path (PagedAttentionKernel.cs:326-370); any
  * GQA group (n_heads % heads_kv == 0); pages of 1 to GSP_MAX_BLOCK_SIZE
  * tokens.  The kernels read pages of at most 16 tokens: a pool page of more
  * is read as equal parts of the largest size up to 16 that divides it (32 and

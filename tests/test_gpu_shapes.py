@@ -8,7 +8,7 @@ head_dim (PagedAttentionKernel.cs:326-370), and no bound on the GQA group
   - the reference's own model shapes: head_dim 32 with 8-token pages
     (PhaseCServeRemediationTests.cs:321-346) and head_dim 32 / v_head_dim 64
     with 4-token pages (:257-319);
-  - head dims 2 .. 256, multiples of 4 and not (loads of 4 and of 2 dims);
+  - head dims 1 .. 256, multiples of 4, even and odd (loads of 4, 2 and 1 dims);
   - page sizes 1 .. 16, and above (17, 24, 32, 48, 64: each pool page read as
     equal kernel pages of at most 16 tokens);
   - GQA groups 17 .. 32 (tiles of 16 heads over grid.y), with forced splits;
@@ -61,6 +61,14 @@ CASES = [
     (2, 1, 32, 64, 48, "f32", 300, 1),     # v_head_dim != head_dim, 16-token parts
     (8, 2, 64, 64, 24, "f32", 300, 0),     # 12-token parts
     (4, 2, 32, 32, 17, "f16", 100, 2),     # a prime page size: single-token parts
+    # Odd widths (the CPU kernel's generic path): loads of one dim.
+    (4, 2, 33, 33, 16, "f32", 200, 0),
+    (4, 2, 33, 35, 8, "f16", 200, 2),
+    (2, 1, 1, 1, 16, "f32", 100, 0),
+    (8, 2, 127, 129, 16, "f32", 300, 3),
+    (6, 3, 255, 255, 16, "f16", 200, 0),
+    (4, 2, 33, 64, 24, "f32", 300, 1),
+    (20, 1, 65, 63, 4, "f32", 120, 2),     # odd widths with two tiles of heads
 ]
 
 
@@ -125,12 +133,13 @@ def test_prefill_rows_outside_the_tile_shapes(torch_mod, gsp, ctx, shape):
         pool.destroy()
 
 
-def test_compute_attention_with_asymmetric_v(torch_mod, gsp, ctx):
+@pytest.mark.parametrize("dims", [(32, 64), (33, 37)], ids=["d32_dv64", "d33_dv37"])
+def test_compute_attention_with_asymmetric_v(torch_mod, gsp, ctx, dims):
     """ComputeAttention's argument list with vHeadDim != headDim and 4-token pages, the
-    reference's asymmetric model (PhaseCServeRemediationTests.cs:257-319): out is
-    [nHeads][vHeadDim]."""
+    reference's asymmetric model (PhaseCServeRemediationTests.cs:257-319), and odd widths,
+    which its generic path takes (PagedAttentionKernel.cs:326-370): out is [nHeads][vHeadDim]."""
     torch = torch_mod
-    nh, nkv, d, dv, bs = 2, 1, 32, 64, 4
+    (d, dv), nh, nkv, bs = dims, 2, 1, 4
     step = workloads.small_step(seed=5, rows=1, n_heads=nh, n_kv=nkv, head_dim=d, ctx_lo=6, ctx_hi=6,
                                 total_blocks=8, block_size=bs, v_head_dim=dv)
     q, k, v = workloads.host_values(step)
@@ -158,13 +167,11 @@ def test_unsupported_shapes_are_refused(torch_mod, gsp, ctx):
     z = torch.zeros(4096, device="cuda")
     with pytest.raises(gsp.Unsupported):  # pages above GSP_MAX_BLOCK_SIZE (4096) tokens
         gsp.Pool.wrap(ctx, z.data_ptr(), z.data_ptr(), 1, 1, 1, 2, block_size=4097)
-    odd = gsp.Pool.wrap(ctx, z.data_ptr(), z.data_ptr(), 4, 1, 1, 33, block_size=4)
     big = gsp.Pool.wrap(ctx, z.data_ptr(), z.data_ptr(), 1, 1, 1, 258, block_size=2)
     try:
-        for pool in (odd, big):
-            ctx.pack_step(pool, [0], [1], [0, 1], [0], 16)
-            with pytest.raises(gsp.Unsupported):  # odd or above 256, as the reference runner refuses
-                ctx.attention_step(pool, 0, 1, z.data_ptr(), z.data_ptr(), 0.1)
+        ctx.pack_step(big, [0], [1], [0, 1], [0], 16)
+        with pytest.raises(gsp.Unsupported):  # above 256, as the reference runner refuses
+            ctx.attention_step(big, 0, 1, z.data_ptr(), z.data_ptr(), 0.1)
         general = gsp.Pool.wrap(ctx, z.data_ptr(), z.data_ptr(), 4, 1, 1, 32, block_size=8)
         ctx.pack_step(general, [0], [1], [0, 1], [0], 16)
         ctx.set_decode_path(gsp.DECODE_DPP)
@@ -180,7 +187,6 @@ def test_unsupported_shapes_are_refused(torch_mod, gsp, ctx):
         general.destroy()
     finally:
         ctx.sync()
-        odd.destroy()
         big.destroy()
 
 
