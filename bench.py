@@ -121,7 +121,7 @@ def profiled_traffic(workload: str, kernel: str):
     try:
         for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
+                return int(float(line.split(":", 1)[1].split()[0]))
     except OSError:
         pass
     return None
