@@ -181,7 +181,8 @@ struct MatmulArgs {
 };
 hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream);
 // The small-batch Q8_0 form (batch <= 64): the x pre-pass in tile order
-// (xh: matmul_small_x_halves halves, xexp: batch exponents), then one product
+// (xh: matmul_small_x_halves halves, xexp: splits x batch exponents, one per
+// K range of each row), then one product
 // kernel that merges its K ranges itself.  Needs chunks_per_split <=
 // matmul_small_chunks(batch), splits <= matmul_small_max_splits(batch) and,
 // with splits > 1, split_out holding splits x batch x (64 * tiles) floats

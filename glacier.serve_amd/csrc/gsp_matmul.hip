@@ -315,12 +315,6 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_batch_kernel(MatmulArgs 
 // x of one batch row as scaled fp16 pairs: one workgroup per row, four
 // elements per access (in_dim is a multiple of 64, rows 16-byte aligned).
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
-// kTiled: both halves go to a.xh in the order the small-batch kernel's A
-// operands are read, tile by tile: for M tile t (batch rows 16 t ..) and chunk
-// c, 4096 bytes as [block][hi, lo][lane g * 16 + m][8 halves], the halves
-// x[16 t + m][64 c + 32 block + 8 g ..].  A wave then loads one operand of one
-// block as 1 KB in one instruction.
-template <bool kTiled>
 __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a) {
     __shared__ float red[kMmThreads / 64];
     const int b = blockIdx.x;
@@ -362,8 +356,6 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
     const float down = ldexpf(1.0f, -e);
     h4v* xh = reinterpret_cast<h4v*>(static_cast<_Float16*>(a.xh) + (int64_t)b * a.in_dim);
     h4v* xl = reinterpret_cast<h4v*>(static_cast<_Float16*>(a.xl) + (int64_t)b * a.in_dim);
-    _Float16* xt = static_cast<_Float16*>(a.xh);
-    const int64_t tile0 = (int64_t)(b >> 4) * (a.in_dim / 64);
     auto put = [&](int i, f4 raw) {
         const f4 v = raw * down;
         const h4v h = __builtin_convertvector(v, h4v);
@@ -373,16 +365,8 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
 #pragma unroll
         for (int c = 0; c < 4; ++c) l[c] = __builtin_isinf(v[c]) ? 0.f : l[c];
         const h4v lh = __builtin_convertvector(l, h4v);
-        if (kTiled) {
-            const int k = 4 * i;
-            const int64_t base = ((tile0 + (k >> 6)) * 2 + ((k >> 5) & 1)) * 2 * 512 +
-                                 (((k >> 3) & 3) * 16 + (b & 15)) * 8 + (k & 7);
-            *reinterpret_cast<h4v*>(xt + base) = h;
-            *reinterpret_cast<h4v*>(xt + base + 512) = lh;
-        } else {
-            xh[i] = h;
-            xl[i] = lh;
-        }
+        xh[i] = h;
+        xl[i] = lh;
     };
     if (held) {
 #pragma unroll
@@ -395,6 +379,56 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
         for (int i = threadIdx.x; i < n4; i += kMmThreads) put(i, xr[i]);
     }
     if (threadIdx.x == 0) a.xexp[b] = e;
+}
+
+// The small-batch form's pre-pass: workgroup (b, z) turns batch row b's K
+// range z (the product kernel's range, chunks_per_split chunks of 64) into
+// scaled fp16 pairs in the order the product kernel's A operands are read,
+// tile by tile: for M tile t (batch rows 16 t ..) and chunk c, 4096 bytes as
+// [block][hi, lo][lane g * 16 + m][8 halves], the halves
+// x[16 t + m][64 c + 32 block + 8 g ..], so that a wave loads one operand of
+// one block as 1 KB in one instruction.  Each range has an exponent of its
+// own, xexp[z][b]
+// (the product kernel scales each range's partial by it).  A range's largest
+// |x| is at most its row's, so every element keeps at least the per-row
+// form's precision.  One f4 per thread and a single load round trip: for
+// Qwen2.5-7B's 3584-wide rows at 64 batch rows that is 448 workgroups of 128
+// elements' worth each instead of 64 workgroups walking whole rows.
+__global__ __launch_bounds__(kMmThreads) void matmul_split_x_range_kernel(MatmulArgs a) {
+    __shared__ float red[kMmThreads / 64];
+    const int b = blockIdx.x;
+    const int z = blockIdx.y;
+    const int i0 = z * a.chunks_per_split * 16;  // first f4 of the range
+    const int n4 = min(a.in_dim / 4, i0 + a.chunks_per_split * 16) - i0;  // host: at most kMmThreads
+    const int t = threadIdx.x;
+    const f4* xr = reinterpret_cast<const f4*>(a.x + (int64_t)b * a.in_dim) + i0;
+    const f4 raw = t < n4 ? xr[t] : f4{0.f, 0.f, 0.f, 0.f};
+    float mx = fmaxf(fmaxf(fabsf(raw[0]), fabsf(raw[1])), fmaxf(fabsf(raw[2]), fabsf(raw[3])));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // As in matmul_split_x_kernel: mx * 2^-e in [2^12, 2^13), e clamped to [-126, 115].
+    int ex = 0;
+    if (mx > 0.f && mx <= FLT_MAX) (void)frexpf(mx, &ex);
+    const int e = mx > 0.f ? (mx <= FLT_MAX ? min(115, max(-126, ex - 13)) : 115) : 0;
+    if (t < n4) {
+        const f4 v = raw * ldexpf(1.0f, -e);
+        const h4v h = __builtin_convertvector(v, h4v);
+        f4 l = v - __builtin_convertvector(h, f4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) l[c] = __builtin_isinf(v[c]) ? 0.f : l[c];
+        const h4v lh = __builtin_convertvector(l, h4v);
+        _Float16* xt = static_cast<_Float16*>(a.xh);
+        const int k = 4 * (i0 + t);
+        const int64_t tile0 = (int64_t)(b >> 4) * (a.in_dim / 64);
+        const int64_t base = ((tile0 + (k >> 6)) * 2 + ((k >> 5) & 1)) * 2 * 512 +
+                             (((k >> 3) & 3) * 16 + (b & 15)) * 8 + (k & 7);
+        *reinterpret_cast<h4v*>(xt + base) = h;
+        *reinterpret_cast<h4v*>(xt + base + 512) = lh;
+    }
+    if (t == 0) a.xexp[z * a.batch + b] = e;
 }
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -542,7 +576,7 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
 //
 // matmul_q8_f16_small_kernel<NT, CH> is the fp16 form for batches of at most
 // 64 rows (NT M tiles of 16), laid out so that nothing waits in line:
-//   - x comes from the pre-pass in tile order (matmul_split_x_kernel<true>):
+//   - x comes from the pre-pass in tile order (matmul_split_x_range_kernel):
 //     a wave loads the A operands of its M tile straight into registers, one
 //     KB per instruction, every chunk of its range at once, with no LDS and no
 //     barrier between chunks;
@@ -664,14 +698,14 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
     }
 
     // Lane holds batch rows 16 mt + 4 g + q of weight rows 64 x + 16 (nt0 + j) + n,
-    // scaled by 2^-xexp of the batch row.
+    // scaled by 2^-xexp of the batch row's K range.
     float v[NT][4];
     int bq[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) bq[q] = 16 * mt + 4 * g + q;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int e = a.xexp[min(bq[q], a.batch - 1)];
+        const int e = a.xexp[blockIdx.z * a.batch + min(bq[q], a.batch - 1)];
 #pragma unroll
         for (int j = 0; j < NT; ++j) v[j][q] = ldexpf(acc[j][q], e);
     }
@@ -762,7 +796,8 @@ hipError_t launch_matmul_q8_small(const MatmulArgs& a, hipStream_t stream) {
         a.chunks_per_split > matmul_small_chunks(a.batch) || a.splits > matmul_small_max_splits(a.batch) ||
         (a.splits > 1 && (!a.split_out || !a.counters)))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(matmul_split_x_kernel<true>, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
+    if (a.chunks_per_split * 16 > kMmThreads) return hipErrorInvalidValue;  // one f4 per thread
+    hipLaunchKernelGGL(matmul_split_x_range_kernel, dim3(a.batch, a.splits), dim3(kMmThreads), 0, stream, a);
     const dim3 grid((a.out_dim + kMmRowsWg - 1) / kMmRowsWg, 1, a.splits);
     if (a.batch <= 16)
         hipLaunchKernelGGL((matmul_q8_f16_small_kernel<1, 8>), grid, dim3(kMmThreads), 0, stream, a);
@@ -779,7 +814,7 @@ hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream) {
     if (a.w_type == kWeightF32)
         hipLaunchKernelGGL(matmul_batch_kernel<kWeightF32>, grid, dim3(kMmThreads), 0, stream, a);
     else if (a.w_type == kWeightQ8_0 && a.xh) {
-        hipLaunchKernelGGL(matmul_split_x_kernel<false>, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
+        hipLaunchKernelGGL(matmul_split_x_kernel, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
         hipLaunchKernelGGL(matmul_q8_f16_kernel, grid, dim3(kMmThreads), 0, stream, a);
     } else if (a.w_type == kWeightQ8_0)
         hipLaunchKernelGGL(matmul_batch_kernel<kWeightQ8_0>, grid, dim3(kMmThreads), 0, stream, a);

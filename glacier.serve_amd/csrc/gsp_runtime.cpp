@@ -915,7 +915,7 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
         a.splits = (int32_t)splits;
         a.chunks_per_split = (int32_t)per;
         rc = ensure_device(ctx, &ctx->d_mmx, &ctx->d_mmx_halves, (size_t)gsp::matmul_small_x_halves(batch, in_dim), false);
-        if (!rc) rc = ensure_device(ctx, &ctx->d_mmexp, &ctx->d_mmexp_words, (size_t)batch, false);
+        if (!rc) rc = ensure_device(ctx, &ctx->d_mmexp, &ctx->d_mmexp_words, (size_t)splits * batch, false);
         if (!rc && splits > 1) rc = ensure_device(ctx, &ctx->d_mm, &ctx->d_mm_floats, (size_t)splits * batch * tiles * 64, false);
         if (!rc && splits > 1) rc = ensure_device(ctx, &ctx->d_mmcnt, &ctx->d_mmcnt_words, (size_t)tiles, true);
         if (rc) return rc;
