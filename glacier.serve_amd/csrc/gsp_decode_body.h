@@ -65,14 +65,16 @@ constexpr int kTileTokens = 16;  // token rows of a page tile (MFMA M for S^T)
 constexpr int kOutOfRange = 1 << 28;
 
 // Widths and page size of a launch: compile-time for kExact, run time otherwise.
+// A decode tile is m consecutive pages of bs tokens (tt = m bs <= 16 rows).
 template <int DP, int MODE>
 struct Geo {
-    int d, dv, bs;
-    __device__ explicit Geo(const DecodeArgs& a) : d(a.head_dim), dv(a.v_head_dim), bs(a.block_size) {}
+    int d, dv, bs, m, tt;
+    __device__ explicit Geo(const DecodeArgs& a)
+        : d(a.head_dim), dv(a.v_head_dim), bs(a.block_size), m(a.tile_pages), tt(a.block_size * a.tile_pages) {}
 };
 template <int DP>
 struct Geo<DP, kExact> {
-    static constexpr int d = DP, dv = DP, bs = kBlockSize;
+    static constexpr int d = DP, dv = DP, bs = kBlockSize, m = 1, tt = kBlockSize;
     __device__ explicit Geo(const DecodeArgs&) {}
 };
 
@@ -233,6 +235,90 @@ __device__ __forceinline__ void load_page(PageRegs<D, KT>& pr, const KT* kpage, 
 #pragma unroll
         for (int c = 0; c < D / 64; ++c)
             pr.v[kk][c] = Raw4<KT>::template load<kStreamLoad>(rv, vl + kk * D + 64 * c);  // whole lines
+}
+
+// Step metadata (unit records, bin offsets, block table) is read-only while
+// the kernel runs.  Reading it through the constant address space lets the
+// compiler use scalar loads even though the epilogue stores inside the bin
+// loop: a vector load there would be followed by a full vmcnt(0) wait that
+// also drains the page loads in flight.
+typedef __attribute__((address_space(4))) const int32_t const_i32;
+
+__device__ __forceinline__ int ld_meta(const int32_t* p) { return *(const_i32*)p; }
+
+// Four elements of a row at dims dim .. dim + 3 through a plain pointer: zero
+// past `width` and for a row that is not valid, in the pieces of MODE.
+template <typename KT, int MODE>
+__device__ __forceinline__ typename Raw4<KT>::T row4(const KT* row, int dim, int width, bool valid) {
+    typedef typename Raw4<KT>::T T4;
+    T4 x = {};
+    if constexpr (MODE == kVec4) {
+        if (valid && dim < width) x = *reinterpret_cast<const T4*>(row + dim);
+    } else if constexpr (MODE == kVec2) {
+        typedef KT T2 __attribute__((ext_vector_type(2)));
+        if (valid && dim < width) {
+            const T2 lo = *reinterpret_cast<const T2*>(row + dim);
+            x[0] = lo[0];
+            x[1] = lo[1];
+        }
+        if (valid && dim + 2 < width) {
+            const T2 hi = *reinterpret_cast<const T2*>(row + dim + 2);
+            x[2] = hi[0];
+            x[3] = hi[1];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (valid && dim + i < width) x[i] = row[dim + i];
+    }
+    return x;
+}
+
+// Tile t of a row made of m > 1 pages (bt: the row's block ids; blk: page
+// t m's block, already read): rows j bs .. j bs + bs - 1 come from block
+// bt[t m + j], read only for pages that hold rows below ntok.  Each lane reads
+// its K row and its four V rows through plain pointers, so every lane of a
+// load fetches (a page tile of 8 tokens leaves half of them idle).
+template <int D, typename KT, int MODE>
+__device__ __forceinline__ void load_small_pages(PageRegs<D, KT>& pr, const DecodeArgs& a, const KT* kbase,
+                                                 const KT* vbase, const int32_t* bt, int t, int64_t blk, int ntok,
+                                                 int n, int g, const Geo<D, MODE>& geo) {
+    const int bs = geo.bs;
+    const int sh = bs == 8 ? 3 : 2;  // m > 1 only for 4- and 8-token pages
+    const int* tb = bt + t * geo.m;
+    const int b1 = bs < ntok ? ld_meta(tb + 1) : 0;
+    const int b2 = geo.m > 2 && 2 * bs < ntok ? ld_meta(tb + 2) : 0;
+    const int b3 = geo.m > 3 && 3 * bs < ntok ? ld_meta(tb + 3) : 0;
+    auto block_of = [&](int j) -> int64_t { return j == 0 ? blk : j == 1 ? b1 : j == 2 ? b2 : b3; };
+    {
+        const int j = n >> sh;
+        const KT* krow = kbase + block_of(j) * a.block_stride + (int64_t)(n - (j << sh)) * geo.d;
+#pragma unroll
+        for (int jj = 0; jj < D / 16; ++jj) pr.k[jj] = row4<KT, MODE>(krow, 16 * jj + 4 * g, geo.d, n < ntok);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const int rv = 4 * g + kk;
+        const int j = rv >> sh;
+        const KT* vrow = vbase + block_of(j) * a.v_block_stride + (int64_t)(rv - (j << sh)) * geo.dv;
+#pragma unroll
+        for (int c = 0; c < D / 64; ++c) pr.v[kk][c] = row4<KT, MODE>(vrow, 64 * c + 4 * n, geo.dv, rv < ntok);
+    }
+}
+
+// Tile t of a unit's row: one page (block blk) read by load_page, or several
+// small pages (load_small_pages).
+template <int D, typename KT, int MODE>
+__device__ __forceinline__ void load_tile(PageRegs<D, KT>& pr, const DecodeArgs& a, const KT* kbase, const KT* vbase,
+                                          const int32_t* bt, int t, int64_t blk, int ntok, int n, int g,
+                                          const Geo<D, MODE>& geo) {
+    if constexpr (MODE != kExact) {
+        if (geo.m > 1) {
+            load_small_pages<D, KT, MODE>(pr, a, kbase, vbase, bt, t, blk, ntok, n, g, geo);
+            return;
+        }
+    }
+    load_page<D, KT, MODE>(pr, kbase + blk * a.block_stride, vbase + blk * a.v_block_stride, ntok, n, g, geo);
 }
 
 // Q^T operand of a unit, q[j] = Q[head n][16j + 4g .. +3], and `sc`, the
@@ -448,15 +534,6 @@ __device__ __forceinline__ void compute_page(WaveState<D>& st, const PageRegs<D,
     page_pv<D>(st, pr, p);
 }
 
-// Step metadata (unit records, bin offsets, block table) is read-only while
-// the kernel runs.  Reading it through the constant address space lets the
-// compiler use scalar loads even though the epilogue stores inside the bin
-// loop: a vector load there would be followed by a full vmcnt(0) wait that
-// also drains the page loads in flight.
-typedef __attribute__((address_space(4))) const int32_t const_i32;
-
-__device__ __forceinline__ int ld_meta(const int32_t* p) { return *(const_i32*)p; }
-
 // The scalar fields of unit `ui`; the block ids are read separately (first_block).
 __device__ __forceinline__ DecodeUnit read_unit(const DecodeArgs& a, int ui) {
     const int32_t* src = reinterpret_cast<const int32_t*>(a.units + ui);
@@ -491,10 +568,10 @@ __device__ __forceinline__ void load_first_page(PageRegs<D, KT>& pr, const Decod
                                                 int wave, int n, int g, const Geo<D, MODE>& geo) {
     const int p = u.page_begin + wave;
     if (p < u.page_end) {
-        const int64_t koff = a.layer_offset + (int64_t)u.kvh * a.head_stride + (int64_t)blk * a.block_stride;
-        const int64_t voff = a.v_layer_offset + (int64_t)u.kvh * a.v_head_stride + (int64_t)blk * a.v_block_stride;
-        load_page<D, KT, MODE>(pr, static_cast<const KT*>(a.k_pool) + koff, static_cast<const KT*>(a.v_pool) + voff,
-                               min(geo.bs, u.ctx - p * geo.bs), n, g, geo);
+        const KT* kbase = static_cast<const KT*>(a.k_pool) + a.layer_offset + (int64_t)u.kvh * a.head_stride;
+        const KT* vbase = static_cast<const KT*>(a.v_pool) + a.v_layer_offset + (int64_t)u.kvh * a.v_head_stride;
+        load_tile<D, KT, MODE>(pr, a, kbase, vbase, a.bt_ids + u.bt_base, p, blk, min(geo.tt, u.ctx - p * geo.tt), n,
+                               g, geo);
     }
 }
 
@@ -589,20 +666,19 @@ __device__ __forceinline__ void decode_bins_body(const DecodeArgs& a, EpilogueLd
         while (p < u.page_end) {
             const int pn = p + kDecodeWaves;
             if (pn < u.page_end && !rb_ready) {
-                const int64_t blk = ld_meta(bt + pn);
-                load_page<D, KT, MODE>(rb, kbase + blk * a.block_stride, vbase + blk * a.v_block_stride,
-                                       min(geo.bs, u.ctx - pn * geo.bs), n, g, geo);
+                const int64_t blk = ld_meta(bt + pn * geo.m);
+                load_tile<D, KT, MODE>(rb, a, kbase, vbase, bt, pn, blk, min(geo.tt, u.ctx - pn * geo.tt), n, g, geo);
             }
             rb_ready = false;
-            compute_page<D, KT, MODE>(st, ra, q, min(geo.bs, u.ctx - p * geo.bs), g);
+            compute_page<D, KT, MODE>(st, ra, q, min(geo.tt, u.ctx - p * geo.tt), g);
             if (pn >= u.page_end) break;
             const int pnn = pn + kDecodeWaves;
             if (pnn < u.page_end) {
-                const int64_t blk = ld_meta(bt + pnn);
-                load_page<D, KT, MODE>(ra, kbase + blk * a.block_stride, vbase + blk * a.v_block_stride,
-                                       min(geo.bs, u.ctx - pnn * geo.bs), n, g, geo);
+                const int64_t blk = ld_meta(bt + pnn * geo.m);
+                load_tile<D, KT, MODE>(ra, a, kbase, vbase, bt, pnn, blk, min(geo.tt, u.ctx - pnn * geo.tt), n, g,
+                                       geo);
             }
-            compute_page<D, KT, MODE>(st, rb, q, min(geo.bs, u.ctx - pn * geo.bs), g);
+            compute_page<D, KT, MODE>(st, rb, q, min(geo.tt, u.ctx - pn * geo.tt), g);
             p = pnn;
         }
 
@@ -620,12 +696,11 @@ __device__ __forceinline__ void decode_bins_body(const DecodeArgs& a, EpilogueLd
             load_q<D, KT, MODE>(qraw, a, un.qi, un.kvh * a.group + hq, g, geo);
             load_first_page<D, KT, MODE>(ra, a, un, blkn, wave, n, g, geo);
             if (has_n2) {
-                const int64_t koff = a.layer_offset + (int64_t)un.kvh * a.head_stride + (int64_t)blkn2 * a.block_stride;
-                const int64_t voff =
-                    a.v_layer_offset + (int64_t)un.kvh * a.v_head_stride + (int64_t)blkn2 * a.v_block_stride;
-                load_page<D, KT, MODE>(rb, static_cast<const KT*>(a.k_pool) + koff,
-                                       static_cast<const KT*>(a.v_pool) + voff, min(geo.bs, un.ctx - pn2 * geo.bs), n,
-                                       g, geo);
+                const KT* nkbase = static_cast<const KT*>(a.k_pool) + a.layer_offset + (int64_t)un.kvh * a.head_stride;
+                const KT* nvbase =
+                    static_cast<const KT*>(a.v_pool) + a.v_layer_offset + (int64_t)un.kvh * a.v_head_stride;
+                load_tile<D, KT, MODE>(rb, a, nkbase, nvbase, a.bt_ids + un.bt_base, pn2, blkn2,
+                                       min(geo.tt, un.ctx - pn2 * geo.tt), n, g, geo);
                 rb_ready = true;
             }
         }

@@ -19,6 +19,10 @@ void launch_one(dim3 grid, const DecodeArgs& a, hipStream_t stream) {
 template <typename KT>
 hipError_t launch_typed(dim3 grid, const DecodeArgs& a, hipStream_t stream) {
     const int d = a.head_dim, dv = a.v_head_dim;
+    // A tile of several pages only for 4- and 8-token pages (16 rows).
+    if (a.tile_pages < 1 || (a.tile_pages > 1 && ((a.block_size != 4 && a.block_size != 8) ||
+                                                  a.block_size * a.tile_pages != kTileTokens)))
+        return hipErrorInvalidValue;
     if (d == dv && a.block_size == kBlockSize && (d == 64 || d == 128)) {
         if (d == 128)
             launch_one<128, KT, kExact>(grid, a, stream);

@@ -42,6 +42,7 @@ struct DecodeArgs {
     int32_t head_dim;      // K/Q width
     int32_t v_head_dim;    // V/out width
     int32_t block_size;    // tokens per page, 1..16
+    int32_t tile_pages;    // pages per decode tile: 16 / block_size for 4- and 8-token pages, else 1
     int32_t total_q;
     int32_t num_slots;     // partial slots per tile
     int32_t slot_heads;    // heads per partial slot: min(group, 16)

@@ -1301,7 +1301,8 @@ hipError_t launch_mixed_mfma(int head_dim, int kv_f16, int num_bins, int num_til
                              const PrefillArgs& pa, hipStream_t stream) {
     if (num_bins <= 0 || num_tiles <= 0 || da.group < 1 || pa.group != da.group) return hipErrorInvalidValue;
     if (kv_f16 && pa.records) return hipErrorInvalidValue;
-    if (da.head_dim != head_dim || da.v_head_dim != head_dim || da.block_size != kBlockSize) return hipErrorInvalidValue;
+    if (da.head_dim != head_dim || da.v_head_dim != head_dim || da.block_size != kBlockSize || da.tile_pages != 1)
+        return hipErrorInvalidValue;
     if (head_dim == 128) return kv_f16 ? launch_mixed<128, _Float16>(num_bins, num_tiles, da, pa, stream)
                                        : launch_mixed<128, float>(num_bins, num_tiles, da, pa, stream);
     if (head_dim == 64) return kv_f16 ? launch_mixed<64, _Float16>(num_bins, num_tiles, da, pa, stream)

@@ -104,6 +104,7 @@ struct gsp_ctx {
     int32_t step_blocks = 0;
     int32_t step_block_size = 0;
     int32_t step_page_tokens = 0;  // tokens per kernel page (the pool's page, or a part of it above 16)
+    int32_t step_tile_pages = 1;   // kernel pages per decode tile (the units count tiles)
     bool step_tileable = false;
     // Split records of the packed step's fp32 prefill tiles (records_head_dim
     // 0: none, the tiles split their pages themselves): one per page pair of
@@ -1148,6 +1149,7 @@ int gsp_step_pack(gsp_ctx* ctx, const gsp_pool* pool, const gsp_step_desc* desc)
     ctx->step_blocks = pd.total_blocks;
     ctx->step_block_size = pd.block_size;
     ctx->step_page_tokens = plan.page_tokens;
+    ctx->step_tile_pages = plan.tile_pages;
     ctx->step_tileable = plan.tileable;
     ctx->info.num_rows = plan.num_rows;
     ctx->info.total_q = (int32_t)plan.total_q;
@@ -1319,6 +1321,7 @@ int attention_launch(gsp_ctx* ctx, const gsp_pool* pool, int32_t layer, int32_t 
     a.head_dim = d.head_dim;
     a.v_head_dim = d.v_head_dim;
     a.block_size = ctx->step_page_tokens;
+    a.tile_pages = ctx->step_tile_pages;
     a.total_q = ctx->info.total_q;
     a.num_slots = slots;
     a.slot_heads = slot_heads;

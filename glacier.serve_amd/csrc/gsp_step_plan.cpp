@@ -197,6 +197,12 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
     int32_t bs = std::min(pbs, kBlockSize);
     while (pbs % bs) --bs;
     const int32_t r = pbs / bs;
+    // Decode units count 16-token tiles: a tile of 4- or 8-token pages is the
+    // tile_pages = 16 / bs consecutive pages of the row (the general kernels
+    // read each from its own block), so a wave's tile carries no empty rows.
+    // Other page sizes take one page per tile.
+    const int32_t m = (r == 1 && (bs == 4 || bs == 8)) ? kBlockSize / bs : 1;
+    const int32_t tt = bs * m;  // tokens per decode tile
     const int64_t vfactor = (int64_t)std::max(1, pd.layers) * H * r;
     if (r > 1 && ((int64_t)pd.total_blocks - 1) * vfactor + (r - 1) > INT32_MAX)
         return fail(GSP_E_UNSUPPORTED, "%d blocks of %d-token pages: too many kernel pages for 32-bit ids",
@@ -251,10 +257,10 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
             any_tiles = any_tiles || tc > 0;
             continue;
         }
-        max_pages = std::max(max_pages, pages);
+        max_pages = std::max(max_pages, (total_last + tt - 1) / tt);
         for (int32_t i = 0; i < ql; ++i) {
             const int64_t tot = std::min<int64_t>(tc, (int64_t)pos + i + 1);
-            pair_pages += (tot + bs - 1) / bs;
+            pair_pages += (tot + tt - 1) / tt;
         }
     }
     if (total_q > INT32_MAX / 4 || packed_pages > INT32_MAX / 4 || pair_pages * H > INT32_MAX / 2)
@@ -319,7 +325,7 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
                 if (row_is_tiled(opt.prefill_path, ql, tileable)) continue;
                 for (int32_t i = 0; i < ql; ++i) {
                     const int64_t tot = std::min<int64_t>(desc->token_counts[b], (int64_t)desc->positions[b] + i + 1);
-                    if (tot > 0) query_pages_.push_back((int32_t)((tot + bs - 1) / bs));
+                    if (tot > 0) query_pages_.push_back((int32_t)((tot + tt - 1) / tt));
                 }
             }
             int64_t best_cost = INT64_MAX;
@@ -401,7 +407,7 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
                 const int32_t tot = (int32_t)std::min<int64_t>(tc, (int64_t)pos + i + 1);
                 q_ctx_[qi] = tot;
                 if (tot <= 0) continue;
-                const int32_t pages = (int32_t)(((int64_t)tot + bs - 1) / bs);
+                const int32_t pages = (int32_t)(((int64_t)tot + tt - 1) / tt);  // tiles
                 const int32_t nsplit = (int32_t)std::min<int64_t>((pages + target - 1) / target, kMaxSplits);
                 const int32_t base = pages / nsplit, extra = pages % nsplit;
                 for (int32_t kvh = 0; kvh < H; ++kvh) {
@@ -416,11 +422,12 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
                         u.slot = nsplit > 1 ? (int32_t)slots : -1;
                         u.split_info = s | (nsplit << 16);
                         const int32_t* row_ids = desc->bt_ids + desc->bt_offsets[b];
+                        // Each wave's first two tiles: their (first) pages' blocks.
                         for (int w = 0; w < kDecodeWaves; ++w) {
                             const int32_t p = u.page_begin + w;
                             const int32_t p2 = p + kDecodeWaves;
-                            u.first_blk[w] = p < u.page_end ? row_ids[p] : -1;
-                            u.second_blk[w] = p2 < u.page_end ? row_ids[p2] : -1;
+                            u.first_blk[w] = p < u.page_end ? row_ids[(int64_t)p * m] : -1;
+                            u.second_blk[w] = p2 < u.page_end ? row_ids[(int64_t)p2 * m] : -1;
                         }
                         units_.push_back(u);
                     }
@@ -565,6 +572,7 @@ int StepPlanner::plan(const PlanPool& pool, const gsp_step_desc* desc, const Pla
     out.max_id = max_id;
     out.tileable = tileable;
     out.page_tokens = bs;
+    out.tile_pages = m;
     out.pool_page_split = r;
     return GSP_OK;
 }

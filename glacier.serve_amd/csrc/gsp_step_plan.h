@@ -69,6 +69,10 @@ struct StepPlan {
     // take a page stride of page_tokens * head_dim (v_head_dim for V).
     int32_t page_tokens = 0;
     int32_t pool_page_split = 1;
+    // Decode units count tiles of tile_pages kernel pages (2 for 8-token and
+    // 4 for 4-token pages, else 1): their page_begin / page_end and
+    // first_blk / second_blk (the tile's first page) are in tiles.
+    int32_t tile_pages = 1;
 };
 
 class StepPlanner {

@@ -105,6 +105,10 @@ void check_image(const Step& st, const gsp::StepPlan& p, const std::string& ctx)
     const int32_t r = pbs / bs;
     const int32_t H = st.pool.heads_kv;
     if (p.page_tokens != bs || p.pool_page_split != r) return failf("kernel page size", ctx);
+    // Decode units count tiles of m pages (4- and 8-token pages: 16 tokens).
+    const int32_t m = (r == 1 && (bs == 4 || bs == 8)) ? 16 / bs : 1;
+    const int32_t tt = bs * m;
+    if (p.tile_pages != m) return failf("tile pages", ctx);
     // Kernel page k of a row: sub-page k % r of pool page k / r.
     auto kernel_id = [&](int32_t b, int64_t k) -> int64_t {
         const int64_t blk = st.ids[(size_t)st.offsets[(size_t)b] + (size_t)(k / r)];
@@ -165,14 +169,14 @@ void check_image(const Step& st, const gsp::StepPlan& p, const std::string& ctx)
         const int32_t b = q_of_row[(size_t)u.qi];
         const int64_t pos = (int64_t)st.positions[(size_t)b] + (u.qi - row_first_q[(size_t)b]);
         const int64_t tot = std::min<int64_t>(st.token_counts[(size_t)b], pos + 1);
-        const int64_t pages = (tot + bs - 1) / bs;
+        const int64_t pages = (tot + tt - 1) / tt;  // tiles
         if (u.ctx != tot || u.bt_base != rows[b] || u.page_begin < 0 || u.page_end > pages ||
             u.page_begin >= u.page_end)
             return failf("unit range", ctx);
         for (int w = 0; w < gsp::kDecodeWaves; ++w) {
             const int32_t p1 = u.page_begin + w, p2 = p1 + gsp::kDecodeWaves;
-            if (u.first_blk[w] != (p1 < u.page_end ? ids[rows[b] + p1] : -1) ||
-                u.second_blk[w] != (p2 < u.page_end ? ids[rows[b] + p2] : -1))
+            if (u.first_blk[w] != (p1 < u.page_end ? ids[rows[b] + (int64_t)p1 * m] : -1) ||
+                u.second_blk[w] != (p2 < u.page_end ? ids[rows[b] + (int64_t)p2 * m] : -1))
                 return failf("unit block ids", ctx);
         }
         covered[(size_t)u.qi * (size_t)H + (size_t)u.kvh] += u.page_end - u.page_begin;
@@ -194,7 +198,7 @@ void check_image(const Step& st, const gsp::StepPlan& p, const std::string& ctx)
         const int32_t b = q_of_row[(size_t)qi];
         const int64_t pos = (int64_t)st.positions[(size_t)b] + (qi - row_first_q[(size_t)b]);
         const int64_t tot = std::min<int64_t>(st.token_counts[(size_t)b], pos + 1);
-        const int64_t want = tiled[(size_t)b] || tot <= 0 ? 0 : (tot + bs - 1) / bs;
+        const int64_t want = tiled[(size_t)b] || tot <= 0 ? 0 : (tot + tt - 1) / tt;
         for (int32_t h = 0; h < H; ++h)
             if (covered[(size_t)qi * (size_t)H + (size_t)h] != want) return failf("unit coverage", ctx);
     }
