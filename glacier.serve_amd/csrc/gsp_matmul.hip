@@ -33,6 +33,7 @@ namespace gsp {
 namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMmThreads = 256;
 constexpr int kMmRowsWg = 64;  // weight rows per workgroup, 16 per wave
@@ -494,7 +495,6 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
     const int c_end = min(chunks, c_begin + a.chunks_per_split);
 
     // x staging: thread tid moves batch row tid / 4, halves 16 (tid % 4) .. + 15 of hi and lo.
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
     const int xr = tid >> 2;
     const int xq = tid & 3;
     const int64_t xoff = (int64_t)min(b0 + xr, a.batch - 1) * a.in_dim + 16 * xq;
@@ -629,10 +629,12 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
     // group gg) is eight values; thread tid takes units tid + 256 k, that is
     // one fixed (chunk, block, lane group) of rows tid / 64 + 4 k.  A wave's
     // units are one row's chunks, so its loads cover whole 68-byte windows.
-    // Every unit's four dwords load first (raw buffer loads whose lane offset
-    // is fixed per thread plus a row step): block 0's values sit at dwords
-    // 2 gg .. 2 gg + 2 shifted by 2 bytes, block 1's at 9 + 2 gg, 10 + 2 gg,
-    // and the scale is the low half of dword 0 or the high half of dword 8.
+    // Every unit's four dwords load first, one 16-byte raw buffer load each
+    // (dword aligned; lane offset fixed per thread plus a row step): block 0's
+    // values sit at dwords 2 gg .. 2 gg + 2 shifted by 2 bytes (the load
+    // covers 2 gg .. 2 gg + 3), block 1's at 9 + 2 gg, 10 + 2 gg (the load
+    // covers 7 + 2 gg .. 10 + 2 gg), and the scale is the low half of dword 0
+    // or the high half of dword 8, both in lane group 0's load.
     // Units of chunks past the range load the range's last chunk and store
     // nothing; rows past out_dim read as zero (past the buffer's end).
     {
@@ -646,18 +648,14 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
         const int i = (tid >> 3) & 7;
         const int blk = (tid >> 2) & 1;
         const int gg = tid & 3;
-        const int s0 = blk ? 9 + 2 * gg : 2 * gg;
+        const int s0 = blk ? 7 + 2 * gg : 2 * gg;  // the unit's four dwords: s0 .. s0 + 3, inside the chunk
         const int voff = r0 * row_bytes + (c_begin + min(i, nc - 1)) * 68;
-        uint32_t wdw[kU][4];
+        u4 wdw[kU];
 #pragma unroll
         for (int k = 0; k < kU; ++k) {
             // The row step stays in the lane offset: the range check covers the
             // lane offset, not the scalar one.
-            const int vk = voff + 4 * k * row_bytes;
-            wdw[k][0] = __builtin_amdgcn_raw_buffer_load_b32(wr, vk + 4 * s0, 0, 0);
-            wdw[k][1] = __builtin_amdgcn_raw_buffer_load_b32(wr, vk + 4 * s0 + 4, 0, 0);
-            wdw[k][2] = __builtin_amdgcn_raw_buffer_load_b32(wr, vk + 4 * min(s0 + 2, 16), 0, 0);
-            wdw[k][3] = __builtin_amdgcn_raw_buffer_load_b32(wr, vk + 32 * blk, 0, 0);
+            wdw[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 4 * k * row_bytes + 4 * s0, 0, 0);
         }
         const int sh = blk ? 0 : 2;
         _Float16* wdst = &wh[r0 * kSmRowHalves + i * 64 + blk * 32 + gg * 8];
@@ -665,11 +663,13 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
         if (i < nc) {
 #pragma unroll
             for (int k = 0; k < kU; ++k) {
-                const h8 q = q8_to_h8(__builtin_amdgcn_alignbyte(wdw[k][1], wdw[k][0], sh),
-                                      __builtin_amdgcn_alignbyte(wdw[k][2], wdw[k][1], sh));
-                const uint32_t sw = blk ? wdw[k][3] >> 16 : wdw[k][3];
+                const uint32_t d0 = blk ? wdw[k][2] : wdw[k][0];
+                const uint32_t d1 = blk ? wdw[k][3] : wdw[k][1];
+                const h8 q = q8_to_h8(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(wdw[k][2], d1, sh));
                 *reinterpret_cast<h8*>(wdst + 4 * k * kSmRowHalves) = q;
-                ddst[4 * k * (2 * CH + 1)] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xFFFFu));  // four lane groups store the same value
+                // Lane group 0 holds the block's scale: dword 0 (low half) or 8 (high half).
+                const uint32_t sw = blk ? wdw[k][1] >> 16 : wdw[k][0];
+                if (gg == 0) ddst[4 * k * (2 * CH + 1)] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xFFFFu));
             }
         }
     }
