@@ -11,7 +11,8 @@
 // significant bits), and the products run on v_mfma_f32_16x16x4f32 with fp32
 // accumulation, so no operand is rounded below fp32.  The fp16 form
 // (matmul_q8_f16_kernel, large Q8_0 products, described further down) runs
-// one Q8_0 block per fp16 matrix step with x as a scaled fp16 pair.
+// one Q8_0 block per fp16 matrix step with x as a scaled fp16 pair; its
+// small-batch variants (at most 64 batch rows) take Q8_0 and Q4_K weights.
 //
 // fp32 form:
 // A workgroup (four waves) owns 64 weight rows (16 per wave, MFMA M) and 64
@@ -139,21 +140,24 @@ __device__ __forceinline__ uint32_t sc_byte(const uint32_t (&sc)[3], int k) {
     return (w >> (8 * (k & 3))) & 0xFFu;
 }
 
+// The six-bit scale and min of sub-block j: bytes j and j + 4 for j < 4;
+// else the nibbles of byte j + 4 with the top two bits of bytes j - 4
+// (scale) and j (min).
+__device__ __forceinline__ void q4k_scale_min(const uint32_t (&sc)[3], int j, uint32_t& scv, uint32_t& mv) {
+    if (j < 4) {
+        scv = sc_byte(sc, j) & 63u;
+        mv = sc_byte(sc, j + 4) & 63u;
+    } else {
+        scv = (sc_byte(sc, j + 4) & 0xFu) | ((sc_byte(sc, j - 4) >> 6) << 4);
+        mv = (sc_byte(sc, j + 4) >> 4) | ((sc_byte(sc, j) >> 6) << 4);
+    }
+}
+
 __device__ __forceinline__ void expand(float (&w)[16], const WRaw<kWeightQ4_K>& r, int g) {
     const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.hdr & 0xFFFFu));
     const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(r.hdr >> 16));
-    const int j = r.j;
-    // The six-bit scale and min of sub-block j: bytes j and j + 4 for j < 4;
-    // else the nibbles of byte j + 4 with the top two bits of bytes j - 4
-    // (scale) and j (min).
     uint32_t scv, mv;
-    if (j < 4) {
-        scv = sc_byte(r.sc, j) & 63u;
-        mv = sc_byte(r.sc, j + 4) & 63u;
-    } else {
-        scv = (sc_byte(r.sc, j + 4) & 0xFu) | ((sc_byte(r.sc, j - 4) >> 6) << 4);
-        mv = (sc_byte(r.sc, j + 4) >> 4) | ((sc_byte(r.sc, j) >> 6) << 4);
-    }
+    q4k_scale_min(r.sc, r.j, scv, mv);
     const float d1 = d * (float)scv;   // exact
     const float m1 = dmin * (float)mv;  // exact
     const int shift = 4 * (g >> 1);     // low nibbles for sub-block 2 p, high for 2 p + 1
@@ -395,6 +399,10 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
 // form's precision.  One f4 per thread and a single load round trip: for
 // Qwen2.5-7B's 3584-wide rows at 64 batch rows that is 448 workgroups of 128
 // elements' worth each instead of 64 workgroups walking whole rows.
+// With kSums (Q4_K weights) it also writes each 32-wide block's sum of the
+// scaled x, xsum[(z * 2 chunks_per_split + block of the range) * 64 + b], for
+// the weights' min term.
+template <bool kSums>
 __global__ __launch_bounds__(kMmThreads) void matmul_split_x_range_kernel(MatmulArgs a) {
     __shared__ float red[kMmThreads / 64];
     const int b = blockIdx.x;
@@ -414,8 +422,15 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_range_kernel(Matmul
     int ex = 0;
     if (mx > 0.f && mx <= FLT_MAX) (void)frexpf(mx, &ex);
     const int e = mx > 0.f ? (mx <= FLT_MAX ? min(115, max(-126, ex - 13)) : 115) : 0;
+    const f4 v = raw * ldexpf(1.0f, -e);
+    if constexpr (kSums) {
+        // Eight threads hold a block's 32 values: a tree over the group.
+        float s = (v[0] + v[1]) + (v[2] + v[3]);
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) s += __shfl_xor(s, off);
+        if (t < n4 && (t & 7) == 0) a.xsum[((int64_t)z * 2 * a.chunks_per_split + (t >> 3)) * 64 + b] = s;
+    }
     if (t < n4) {
-        const f4 v = raw * ldexpf(1.0f, -e);
         const h4v h = __builtin_convertvector(v, h4v);
         f4 l = v - __builtin_convertvector(h, f4);
 #pragma unroll
@@ -593,30 +608,17 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
 constexpr int kSmMaxPartials = 32;  // K ranges x tiles per lane the merge holds at most
 constexpr int kSmRowHalves = 8 * 64 + 8;  // an LDS weight row: 8 chunks of 64 halves, +16 bytes
 
-template <int NT, int CH>
-__global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(MatmulArgs a) {
-    static_assert(CH <= 8, "an LDS weight row holds 8 chunks");
-    __shared__ _Float16 wh[kMmRowsWg * kSmRowHalves];  // [weight row][chunk][64 halves]
-    __shared__ float wd[kMmRowsWg][2 * CH + 1];        // block scales [weight row][2 chunk + block]
-    __shared__ int last;
+// The small forms' shared steps.  Wave w of a workgroup takes M tile
+// mt = w NT / 4 (batch rows 16 mt ..) against N tiles nt0 .. nt0 + NT - 1
+// (weight rows 64 blockIdx.x + 16 nt0 ..); lane (g = lane / 16, n = lane % 16).
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int n = lane & 15;
-    const int g = lane >> 4;
-    const int chunks = a.in_dim / 64;
-    const int c_begin = blockIdx.z * a.chunks_per_split;
-    const int nc = min(chunks, c_begin + a.chunks_per_split) - c_begin;  // 1..CH (host)
-    constexpr int kWavesPerM = 4 / NT;
-    const int mt = wave / kWavesPerM;           // the wave's M tile
-    const int nt0 = (wave % kWavesPerM) * NT;   // its first N tile
-
-    // A operands of the wave's M tile, all chunks at once: [chunk][block][hi, lo].
-    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+// A operands of the wave's M tile, every chunk of the range at once:
+// [chunk][block][hi, lo], one KB per load from the pre-pass's tile order.
+template <int CH>
+__device__ __forceinline__ void small_load_x(h8 (&ax)[CH][2][2], const MatmulArgs& a, int mt, int chunks, int c_begin,
+                                             int nc, int lane) {
     const h8* xt = reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.xh)) +
                    ((int64_t)mt * chunks + c_begin) * 256 + lane;
-    h8 ax[CH][2][2];
 #pragma unroll
     for (int i = 0; i < CH; ++i)
         if (i < nc)
@@ -624,58 +626,13 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
             for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
                 for (int part = 0; part < 2; ++part) ax[i][blk][part] = xt[i * 256 + (blk * 2 + part) * 64];
+}
 
-    // Weights to fp16: unit u = 64 r + 8 i + 4 block + gg (row r, chunk i, lane
-    // group gg) is eight values; thread tid takes units tid + 256 k, that is
-    // one fixed (chunk, block, lane group) of rows tid / 64 + 4 k.  A wave's
-    // units are one row's chunks, so its loads cover whole 68-byte windows.
-    // Every unit's four dwords load first, one 16-byte raw buffer load each
-    // (dword aligned; lane offset fixed per thread plus a row step): block 0's
-    // values sit at dwords 2 gg .. 2 gg + 2 shifted by 2 bytes (the load
-    // covers 2 gg .. 2 gg + 3), block 1's at 9 + 2 gg, 10 + 2 gg (the load
-    // covers 7 + 2 gg .. 10 + 2 gg), and the scale is the low half of dword 0
-    // or the high half of dword 8, both in lane group 0's load.
-    // Units of chunks past the range load the range's last chunk and store
-    // nothing; rows past out_dim read as zero (past the buffer's end).
-    {
-        constexpr int kU = (kMmRowsWg * 64) / kMmThreads;
-        const int row_bytes = chunks * 68;
-        const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
-        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes),
-            (short)0, rows_here * row_bytes, 0x00020000);
-        const int r0 = tid >> 6;
-        const int i = (tid >> 3) & 7;
-        const int blk = (tid >> 2) & 1;
-        const int gg = tid & 3;
-        const int s0 = blk ? 7 + 2 * gg : 2 * gg;  // the unit's four dwords: s0 .. s0 + 3, inside the chunk
-        const int voff = r0 * row_bytes + (c_begin + min(i, nc - 1)) * 68;
-        u4 wdw[kU];
-#pragma unroll
-        for (int k = 0; k < kU; ++k) {
-            // The row step stays in the lane offset: the range check covers the
-            // lane offset, not the scalar one.
-            wdw[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 4 * k * row_bytes + 4 * s0, 0, 0);
-        }
-        const int sh = blk ? 0 : 2;
-        _Float16* wdst = &wh[r0 * kSmRowHalves + i * 64 + blk * 32 + gg * 8];
-        float* ddst = &wd[r0][2 * i + blk];
-        if (i < nc) {
-#pragma unroll
-            for (int k = 0; k < kU; ++k) {
-                const uint32_t d0 = blk ? wdw[k][2] : wdw[k][0];
-                const uint32_t d1 = blk ? wdw[k][3] : wdw[k][1];
-                const h8 q = q8_to_h8(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(wdw[k][2], d1, sh));
-                *reinterpret_cast<h8*>(wdst + 4 * k * kSmRowHalves) = q;
-                // Lane group 0 holds the block's scale: dword 0 (low half) or 8 (high half).
-                const uint32_t sw = blk ? wdw[k][1] >> 16 : wdw[k][0];
-                if (gg == 0) ddst[4 * k * (2 * CH + 1)] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xFFFFu));
-            }
-        }
-    }
-    __syncthreads();
-
-    f4 acc[NT];
+// The range's products: per block, hi and lo into a fresh accumulator, which
+// the block's scale (wd: [weight row][2 chunk + block]) adds into the sum.
+template <int NT, int CH>
+__device__ __forceinline__ void small_products(f4 (&acc)[NT], const h8 (&ax)[CH][2][2], const _Float16* wh,
+                                               const float (*wd)[2 * CH + 1], int nc, int nt0, int n, int g) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -696,7 +653,15 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
             }
         }
     }
+}
 
+// The tile's end: scale by 2^xexp of each batch row's K range, then either
+// store y (one range) or store the partial coherently, count the tile and, in
+// the last workgroup of the tile, add the ranges in z order (every load issued
+// before the first add) and reset the counter.
+template <int NT>
+__device__ __forceinline__ void small_finish(const MatmulArgs& a, const f4 (&acc)[NT], int mt, int nt0, int n, int g,
+                                             int tid, int& last) {
     // Lane holds batch rows 16 mt + 4 g + q of weight rows 64 x + 16 (nt0 + j) + n,
     // scaled by 2^-xexp of the batch row's K range.
     float v[NT][4];
@@ -756,6 +721,233 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
     if (tid == 0) __hip_atomic_store(a.counters + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+template <int NT, int CH>
+__global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(MatmulArgs a) {
+    static_assert(CH <= 8, "an LDS weight row holds 8 chunks");
+    __shared__ _Float16 wh[kMmRowsWg * kSmRowHalves];  // [weight row][chunk][64 halves]
+    __shared__ float wd[kMmRowsWg][2 * CH + 1];        // block scales [weight row][2 chunk + block]
+    __shared__ int last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int chunks = a.in_dim / 64;
+    const int c_begin = blockIdx.z * a.chunks_per_split;
+    const int nc = min(chunks, c_begin + a.chunks_per_split) - c_begin;  // 1..CH (host)
+    constexpr int kWavesPerM = 4 / NT;
+    const int mt = wave / kWavesPerM;           // the wave's M tile
+    const int nt0 = (wave % kWavesPerM) * NT;   // its first N tile
+
+    h8 ax[CH][2][2];
+    small_load_x<CH>(ax, a, mt, chunks, c_begin, nc, lane);
+
+    // Weights to fp16: unit u = 64 r + 8 i + 4 block + gg (row r, chunk i, lane
+    // group gg) is eight values; thread tid takes units tid + 256 k, that is
+    // one fixed (chunk, block, lane group) of rows tid / 64 + 4 k.  A wave's
+    // units are one row's chunks, so its loads cover whole 68-byte windows.
+    // Every unit's four dwords load first, one 16-byte raw buffer load each
+    // (dword aligned; lane offset fixed per thread plus a row step): block 0's
+    // values sit at dwords 2 gg .. 2 gg + 2 shifted by 2 bytes (the load
+    // covers 2 gg .. 2 gg + 3), block 1's at 9 + 2 gg, 10 + 2 gg (the load
+    // covers 7 + 2 gg .. 10 + 2 gg), and the scale is the low half of dword 0
+    // or the high half of dword 8, both in lane group 0's load.
+    // Units of chunks past the range load the range's last chunk and store
+    // nothing; rows past out_dim read as zero (past the buffer's end).
+    {
+        constexpr int kU = (kMmRowsWg * 64) / kMmThreads;
+        const int row_bytes = chunks * 68;
+        const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes),
+            (short)0, rows_here * row_bytes, 0x00020000);
+        const int r0 = tid >> 6;
+        const int i = (tid >> 3) & 7;
+        const int blk = (tid >> 2) & 1;
+        const int gg = tid & 3;
+        const int s0 = blk ? 7 + 2 * gg : 2 * gg;  // the unit's four dwords: s0 .. s0 + 3, inside the chunk
+        const int voff = r0 * row_bytes + (c_begin + min(i, nc - 1)) * 68;
+        u4 wdw[kU];
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            // The row step stays in the lane offset: the range check covers the
+            // lane offset, not the scalar one.
+            wdw[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 4 * k * row_bytes + 4 * s0, 0, 0);
+        }
+        const int sh = blk ? 0 : 2;
+        _Float16* wdst = &wh[r0 * kSmRowHalves + i * 64 + blk * 32 + gg * 8];
+        float* ddst = &wd[r0][2 * i + blk];
+        if (i < nc) {
+#pragma unroll
+            for (int k = 0; k < kU; ++k) {
+                const uint32_t d0 = blk ? wdw[k][2] : wdw[k][0];
+                const uint32_t d1 = blk ? wdw[k][3] : wdw[k][1];
+                const h8 q = q8_to_h8(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(wdw[k][2], d1, sh));
+                *reinterpret_cast<h8*>(wdst + 4 * k * kSmRowHalves) = q;
+                // Lane group 0 holds the block's scale: dword 0 (low half) or 8 (high half).
+                const uint32_t sw = blk ? wdw[k][1] >> 16 : wdw[k][0];
+                if (gg == 0) ddst[4 * k * (2 * CH + 1)] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xFFFFu));
+            }
+        }
+    }
+    __syncthreads();
+
+    f4 acc[NT];
+    small_products<NT, CH>(acc, ax, wh, wd, nc, nt0, n, g);
+    small_finish<NT>(a, acc, mt, nt0, n, g, tid, last);
+}
+
+// Four nibbles per dword (one per byte, 0..15) as fp16: the half 0x6400 | q is
+// 1024 + q, so subtracting 1024 leaves q exactly.
+__device__ __forceinline__ h8 nib_to_h8(uint32_t d0, uint32_t d1) {
+    h8 r;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t u = k ? d1 : d0;
+        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0, 64, u1, 64
+        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2, 64, u3, 64
+        const h2 a0 = __builtin_bit_cast(h2, p0) - h2{(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2 a1 = __builtin_bit_cast(h2, p1) - h2{(_Float16)1024.0f, (_Float16)1024.0f};
+        r[4 * k + 0] = a0[0];
+        r[4 * k + 1] = a0[1];
+        r[4 * k + 2] = a1[0];
+        r[4 * k + 3] = a1[1];
+    }
+    return r;
+}
+
+// ---- Q4_K weights, batches of up to 64 rows ---------------------------------
+//
+// matmul_q4k_f16_small_kernel<NT> is the Q8_0 small form with Q4_K weights.
+// A weight is w = d1 q - m1 per 32-wide sub-block (d1 = d * sc and
+// m1 = dmin * m, both exact in fp32; q = 0..15, exact in fp16), so
+//   y[b][o] = sum over blocks of  d1 * sum_k q_k x_k  -  m1 * sum_k x_k.
+// The first term is the Q8_0 form's: the quants go to LDS as fp16 and each
+// block is one hi/lo pair of 16x16x32 fp16 matrix steps scaled by d1.  The
+// second needs only the blocks' sums of x, which the pre-pass writes (of the
+// scaled x, so both terms carry the range's 2^-xexp): per four blocks one
+// v_mfma_f32_16x16x4f32 of the x sums (A: batch rows x blocks) against the
+// m1 values (B: blocks x weight rows) into a second accumulator, subtracted
+// before the scaling.  A chunk of 64 weights is one quarter p of a 256-weight
+// super-block: sub-blocks 2 p (low nibbles of quant bytes 32 p ..) and 2 p + 1
+// (their high nibbles), so ranges need not start on a super-block.
+template <int NT>
+__global__ __launch_bounds__(kMmThreads, 2) void matmul_q4k_f16_small_kernel(MatmulArgs a) {
+    constexpr int CH = 8;
+    __shared__ _Float16 wh[kMmRowsWg * kSmRowHalves];  // quants [weight row][chunk][64 halves]
+    __shared__ float wd[kMmRowsWg][2 * CH + 1];        // d1 = d * sc [weight row][2 chunk + block]
+    __shared__ float wm[kMmRowsWg][2 * CH + 1];        // m1 = dmin * m, the same way
+    __shared__ __attribute__((aligned(16))) float xs[2 * CH][64];  // block sums of scaled x [block][batch row]
+    __shared__ int last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int chunks = a.in_dim / 64;
+    const int c_begin = blockIdx.z * a.chunks_per_split;
+    const int nc = min(chunks, c_begin + a.chunks_per_split) - c_begin;  // 1..CH (host)
+    constexpr int kWavesPerM = 4 / NT;
+    const int mt = wave / kWavesPerM;
+    const int nt0 = (wave % kWavesPerM) * NT;
+
+    h8 ax[CH][2][2];
+    small_load_x<CH>(ax, a, mt, chunks, c_begin, nc, lane);
+
+    // Weights: unit (row r, chunk i) is one super-block quarter, 64 quants in 32
+    // bytes plus the super-block's 16-byte head (d, dmin, the 12 scale bytes);
+    // thread tid takes chunk tid % 8 of rows tid / 8 and tid / 8 + 32, three
+    // 16-byte raw buffer loads each (super-blocks are 144 bytes, so every load
+    // is dword aligned), all issued before the first is used.  Units of chunks
+    // past the range load the range's last chunk and store zero scales; rows
+    // past out_dim read as zero (past the buffer's end).
+    {
+        const int row_bytes = (a.in_dim / 256) * 144;
+        const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes),
+            (short)0, rows_here * row_bytes, 0x00020000);
+        const int i = tid & 7;
+        const int r0 = tid >> 3;
+        const int c = c_begin + min(i, nc - 1);
+        const int p = c & 3;
+        const int voff = r0 * row_bytes + (c >> 2) * 144;
+        u4 hd[2], qa[2], qb[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int off = voff + 32 * k * row_bytes;
+            hd[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
+            qa[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 16 + 32 * p, 0, 0);
+            qb[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 32 + 32 * p, 0, 0);
+        }
+        // The range's block sums, loaded after the weights (the memory counter
+        // drains in order, so the weights need not wait for them) and stored
+        // after the expansion: thread tid takes block tid / 16, batch rows
+        // 4 (tid % 16) .. + 3; blocks past the range and rows past the batch are 0.
+        const int sblk = tid >> 4;
+        const int b4 = 4 * (tid & 15);
+        f4 xsv = f4{0.f, 0.f, 0.f, 0.f};
+        if (sblk < 2 * nc)
+            xsv = *reinterpret_cast<const f4*>(a.xsum + ((int64_t)blockIdx.z * 2 * a.chunks_per_split + sblk) * 64 + b4);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int r = r0 + 32 * k;
+            float d1[2] = {0.f, 0.f}, m1[2] = {0.f, 0.f};
+            if (i < nc) {
+                const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd[k][0] & 0xFFFFu));
+                const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd[k][0] >> 16));
+                const uint32_t sc[3] = {hd[k][1], hd[k][2], hd[k][3]};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    uint32_t scv, mv;
+                    q4k_scale_min(sc, 2 * p + h, scv, mv);
+                    d1[h] = d * (float)scv;   // exact
+                    m1[h] = dmin * (float)mv;  // exact
+                }
+                const uint32_t q[8] = {qa[k][0], qa[k][1], qa[k][2], qa[k][3], qb[k][0], qb[k][1], qb[k][2], qb[k][3]};
+                _Float16* dst = &wh[r * kSmRowHalves + i * 64];
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    *reinterpret_cast<h8*>(dst + 8 * s) = nib_to_h8(q[2 * s] & 0x0F0F0F0Fu, q[2 * s + 1] & 0x0F0F0F0Fu);
+                    *reinterpret_cast<h8*>(dst + 32 + 8 * s) =
+                        nib_to_h8((q[2 * s] >> 4) & 0x0F0F0F0Fu, (q[2 * s + 1] >> 4) & 0x0F0F0F0Fu);
+                }
+            }
+            wd[r][2 * i] = d1[0];
+            wd[r][2 * i + 1] = d1[1];
+            wm[r][2 * i] = m1[0];
+            wm[r][2 * i + 1] = m1[1];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (b4 + c >= a.batch) xsv[c] = 0.f;
+        *reinterpret_cast<f4*>(&xs[sblk][b4]) = xsv;
+    }
+    __syncthreads();
+
+    f4 acc[NT];
+    small_products<NT, CH>(acc, ax, wh, wd, nc, nt0, n, g);
+    // The min term, four blocks per matrix step: lane (g, n) supplies block
+    // 4 s + g of batch row 16 mt + n (A) and of weight row 16 (nt0 + j) + n (B).
+    f4 accm[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) accm[j] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < CH / 2; ++s) {
+        if (2 * s < nc) {
+            const float xa = xs[4 * s + g][16 * mt + n];
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+                accm[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, wm[16 * (nt0 + j) + n][4 * s + g], accm[j], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] -= accm[j];
+    small_finish<NT>(a, acc, mt, nt0, n, g, tid, last);
+}
+
 // y = the sum over z of the split partials, in z order; four elements per
 // thread and step when y and the partials are 16-byte aligned, else one.
 __global__ __launch_bounds__(kMmThreads) void matmul_reduce_kernel(MatmulArgs a) {
@@ -790,15 +982,26 @@ int64_t matmul_small_x_halves(int batch, int in_dim) {
 
 int matmul_small_max_splits(int batch) { return kSmMaxPartials / (batch <= 16 ? 1 : batch <= 32 ? 2 : 4); }
 
-hipError_t launch_matmul_q8_small(const MatmulArgs& a, hipStream_t stream) {
+hipError_t launch_matmul_small(const MatmulArgs& a, hipStream_t stream) {
     if (a.batch <= 0 || a.out_dim <= 0) return hipSuccess;
-    if (a.batch > 64 || a.w_type != kWeightQ8_0 || !a.xh || !a.xl || !a.xexp ||
+    const bool q4k = a.w_type == kWeightQ4_K;
+    if (a.batch > 64 || (a.w_type != kWeightQ8_0 && !q4k) || !a.xh || !a.xl || !a.xexp ||
         a.chunks_per_split > matmul_small_chunks(a.batch) || a.splits > matmul_small_max_splits(a.batch) ||
-        (a.splits > 1 && (!a.split_out || !a.counters)))
+        (a.splits > 1 && (!a.split_out || !a.counters)) || (q4k && (!a.xsum || a.in_dim % 256 != 0)))
         return hipErrorInvalidValue;
     if (a.chunks_per_split * 16 > kMmThreads) return hipErrorInvalidValue;  // one f4 per thread
-    hipLaunchKernelGGL(matmul_split_x_range_kernel, dim3(a.batch, a.splits), dim3(kMmThreads), 0, stream, a);
     const dim3 grid((a.out_dim + kMmRowsWg - 1) / kMmRowsWg, 1, a.splits);
+    if (q4k) {
+        hipLaunchKernelGGL(matmul_split_x_range_kernel<true>, dim3(a.batch, a.splits), dim3(kMmThreads), 0, stream, a);
+        if (a.batch <= 16)
+            hipLaunchKernelGGL(matmul_q4k_f16_small_kernel<1>, grid, dim3(kMmThreads), 0, stream, a);
+        else if (a.batch <= 32)
+            hipLaunchKernelGGL(matmul_q4k_f16_small_kernel<2>, grid, dim3(kMmThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL(matmul_q4k_f16_small_kernel<4>, grid, dim3(kMmThreads), 0, stream, a);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(matmul_split_x_range_kernel<false>, dim3(a.batch, a.splits), dim3(kMmThreads), 0, stream, a);
     if (a.batch <= 16)
         hipLaunchKernelGGL((matmul_q8_f16_small_kernel<1, 8>), grid, dim3(kMmThreads), 0, stream, a);
     else if (a.batch <= 32)

@@ -85,8 +85,10 @@ struct gsp_ctx {
     size_t d_mmx_halves = 0;
     int32_t* d_mmexp = nullptr;
     size_t d_mmexp_words = 0;
-    int32_t* d_mmcnt = nullptr;  // one-launch Q8_0 form: per-tile counters, zero between launches
+    int32_t* d_mmcnt = nullptr;  // small-batch form: per-tile counters, zero between launches
     size_t d_mmcnt_words = 0;
+    float* d_mmxs = nullptr;  // small-batch Q4_K: block sums of the scaled x
+    size_t d_mmxs_floats = 0;
     hipEvent_t aux_done = nullptr;
     bool aux_pending = false;
 
@@ -386,6 +388,7 @@ void gsp_shutdown(gsp_ctx* ctx) {
     if (ctx->d_mmx) (void)hipFree(ctx->d_mmx);
     if (ctx->d_mmexp) (void)hipFree(ctx->d_mmexp);
     if (ctx->d_mmcnt) (void)hipFree(ctx->d_mmcnt);
+    if (ctx->d_mmxs) (void)hipFree(ctx->d_mmxs);
     if (ctx->part) (void)hipFree(ctx->part);
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->d_records) (void)hipFree(ctx->d_records);
@@ -862,11 +865,12 @@ int gsp_rope_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_h
 // (229376 outputs: 27.8 vs 31.2 us) upwards, slower for 8192 x 8192 at 16 rows
 // (131072 outputs: 57.5 vs 51 us) and 3584 x 512 at 64 rows (21.5 vs 16.2 us).
 constexpr int64_t kMatmulF16MinOutputs = 196608;
-// Q8_0 products of at most 64 batch rows with at least this many outputs take
-// the small-batch fp16 form: measured faster than the other two forms from
-// 8192 x 8192 at 16 rows (131072 outputs: 40.6 vs 43.7 us) and Qwen2.5-7B's
-// 3584 x 3584 at 64 rows (22.1 vs 24.3 us), slower for 896 x 896 at 8 rows
-// (7168 outputs: 15.8 vs 6.9 us), whose product is too small to fill the chip.
+// Q8_0 and Q4_K products of at most 64 batch rows with at least this many
+// outputs take the small-batch fp16 form: for Q8_0 measured faster than the
+// other two forms from 8192 x 8192 at 16 rows (131072 outputs: 40.6 vs 43.7 us)
+// and Qwen2.5-7B's 3584 x 3584 at 64 rows (22.1 vs 24.3 us), slower for
+// 896 x 896 at 8 rows (7168 outputs: 15.8 vs 6.9 us), whose product is too
+// small to fill the chip.
 constexpr int64_t kMatmulSmallMinOutputs = 65536;
 
 int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const float* x_dev, float* y_dev,
@@ -892,7 +896,8 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
                          (int)walign);
     int rc = set_device(ctx);
     if (rc) return rc;
-    if (w_type == GSP_WTYPE_Q8_0 && batch <= 64 && (int64_t)batch * out_dim >= kMatmulSmallMinOutputs &&
+    if ((w_type == GSP_WTYPE_Q8_0 || w_type == GSP_WTYPE_Q4_K) && batch <= 64 &&
+        (int64_t)batch * out_dim >= kMatmulSmallMinOutputs &&
         (in_dim / 64 + gsp::matmul_small_chunks(batch) - 1) / gsp::matmul_small_chunks(batch) <=
             gsp::matmul_small_max_splits(batch)) {
         // Small batches: about two workgroups (64 weight rows, every batch row)
@@ -919,13 +924,16 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
         if (!rc) rc = ensure_device(ctx, &ctx->d_mmexp, &ctx->d_mmexp_words, (size_t)splits * batch, false);
         if (!rc && splits > 1) rc = ensure_device(ctx, &ctx->d_mm, &ctx->d_mm_floats, (size_t)splits * batch * tiles * 64, false);
         if (!rc && splits > 1) rc = ensure_device(ctx, &ctx->d_mmcnt, &ctx->d_mmcnt_words, (size_t)tiles, true);
+        if (!rc && w_type == GSP_WTYPE_Q4_K)
+            rc = ensure_device(ctx, &ctx->d_mmxs, &ctx->d_mmxs_floats, (size_t)splits * 2 * per * 64, false);
         if (rc) return rc;
         a.xh = ctx->d_mmx;  // x in tile order, both halves
         a.xl = ctx->d_mmx;
         a.xexp = ctx->d_mmexp;
         a.split_out = splits > 1 ? ctx->d_mm : nullptr;
         a.counters = splits > 1 ? ctx->d_mmcnt : nullptr;
-        return check_hip(gsp::launch_matmul_q8_small(a, ctx->stream), "matmul launch");
+        a.xsum = w_type == GSP_WTYPE_Q4_K ? ctx->d_mmxs : nullptr;
+        return check_hip(gsp::launch_matmul_small(a, ctx->stream), "matmul launch");
     }
     // Split K over grid.z until the grid has about two workgroups (64 weight rows
     // x 64 batch rows each) per CU, keeping at least two 64-wide chunks in every

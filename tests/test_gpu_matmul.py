@@ -107,17 +107,28 @@ def test_matmul_q_projection_then_attention_shapes(torch_mod, gsp, ctx):
 
 
 @pytest.mark.parametrize("batch", [100, 60], ids=["b100", "b60"])
-@pytest.mark.parametrize("w_type", [orc.WTYPE_F32, orc.WTYPE_Q8_0], ids=["f32", "q8_0"])
+@pytest.mark.parametrize("w_type", [orc.WTYPE_F32, orc.WTYPE_Q8_0, orc.WTYPE_Q4_K], ids=["f32", "q8_0", "q4_k"])
 def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, batch):
     """Rows with one channel 1e4 times the rest, rows near 1e30 and rows near 1e-30.  Q8_0 takes an
-    fp16 path at both batches (the two-kernel form at 100 rows, the one-launch form at 60, whose
-    per-row exponents grow as larger values arrive).  There x is a scaled fp16 pair whose error is
-    bounded relative to its row's largest |x| (at most ~2^-22 of it per element), so the bar adds
-    that term; every finite row stays finite.  The F32 form keeps x in fp32 and meets the plain fp32
-    summation bar."""
+    fp16 path at both batches (the two-kernel form at 100 rows, the small-batch form at 60, with an
+    exponent per K range of each row); Q4_K the fp32 form at 100 rows and the small-batch form at 60.
+    There x is a scaled fp16 pair whose error is bounded relative to its row's largest |x| (at most
+    ~2^-22 of it per element), so the bar adds that term; every finite row stays finite.  The F32
+    form keeps x in fp32 and meets the plain fp32 summation bar.  The Q4_K small form sums the
+    quant term d1 q x and the min term m1 x separately (|d1 q| <= |w| + m1), so its bar is taken over
+    |w| + 2 m1, with m1 the weights the oracle decodes when every quant is zero."""
     in_dim, out_dim = 4096, 2048
     rng = np.random.default_rng(77 + w_type + batch)
-    data, wm = _weights(rng, w_type, out_dim, in_dim)
+    if w_type == orc.WTYPE_Q4_K:
+        data, wm = _kquant_weights(rng, w_type, out_dim, in_dim)
+        zq = data.reshape(out_dim, in_dim // orc.QK_K, orc.Q4_K_BYTES).copy()
+        zq[..., 16:] = 0
+        m1 = -orc.q4_k_decode(zq.reshape(-1), out_dim, in_dim)
+        assert np.all(m1 >= 0)
+        wabs = np.abs(wm) + 2 * m1
+    else:
+        data, wm = _weights(rng, w_type, out_dim, in_dim)
+        wabs = np.abs(wm)
     x = rng.standard_normal((batch, in_dim)).astype(np.float32)
     x[0:30, rng.integers(0, in_dim, 30)] *= 1e4           # one outlier channel per row (some shared)
     x[30:40] *= np.float32(1e30)                          # near the top of the fp32 range
@@ -127,10 +138,10 @@ def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, bat
     got = _run(torch_mod, gsp, ctx, w_type, data, x, in_dim, out_dim)
     ref = orc.matmul_batch(w_type, data, x, in_dim, out_dim)
     x64 = x.astype(np.float64)
-    mag = np.abs(x64) @ np.abs(wm).T
+    mag = np.abs(x64) @ wabs.T
     bar = 1e-5 * mag + 1e-7 * (np.abs(x64).max(axis=1, keepdims=True) > 1e-20)
-    if w_type == orc.WTYPE_Q8_0:
-        bar = bar + 2.0 ** -21 * np.abs(x64).max(axis=1, keepdims=True) * np.abs(wm).sum(axis=1)[None, :]
+    if w_type != orc.WTYPE_F32:
+        bar = bar + 2.0 ** -21 * np.abs(x64).max(axis=1, keepdims=True) * wabs.sum(axis=1)[None, :]
     assert np.all(np.isfinite(got))
     assert np.all(np.abs(got - ref) <= bar)
 
@@ -138,8 +149,10 @@ def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, bat
 # ---- K-quant weights (Q4_K, Q6_K: super-blocks of 256 weights) -------------------------------------
 # Random super-blocks are valid encodings: every byte pattern decodes to finite weights once the
 # fp16 scales are finite, so the quants, 6-bit scales/mins and high bits are random bytes and only
-# d (and dmin) are set.  The device decodes each weight to the float32 value the oracle's decoder
-# gives (pinned by closed forms in tests/test_matmul_oracle.py), so the bar is fp32 summation error.
+# d (and dmin) are set.  The fp32 form decodes each weight to the float32 value the oracle's decoder
+# gives (pinned by closed forms in tests/test_matmul_oracle.py), so the bar is fp32 summation error;
+# the Q4_K small-batch form (at most 64 rows) keeps the quants exact in fp16 and x to ~22 bits as
+# the Q8_0 one does, within the same bar.
 
 KQ_SHAPES = [
     (256, 16, 1),
@@ -150,6 +163,12 @@ KQ_SHAPES = [
     (512, 37, 3),
     (1024, 4100, 17),
     (3584, 3584, 64),  # the Q projection of a Qwen2.5-7B layer for 64 decode rows
+    # Q4_K's small-batch form (batch <= 64, batch x out_dim >= 65536): one M tile with K ranges of
+    # three chunks that start inside a super-block, four M tiles with a ragged batch and a ragged
+    # last weight-row tile, one M tile over sixteen K ranges
+    (768, 8192, 9),
+    (2048, 2100, 40),
+    (8192, 4160, 16),
 ]
 
 
