@@ -186,12 +186,15 @@ hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream);
 // The small-batch form (batch <= 64, Q8_0 or Q4_K weights): the x pre-pass in
 // tile order (xh: matmul_small_x_halves halves, xexp: splits x batch
 // exponents, one per K range of each row; for Q4_K also xsum), then one
-// product kernel that merges its K ranges itself.  Needs chunks_per_split <=
-// matmul_small_chunks(batch), splits <= matmul_small_max_splits(batch) and,
-// with splits > 1, split_out holding splits x batch x (64 * tiles) floats
-// (16-byte aligned) and one zeroed counter per tile of 64 weight rows.
+// product kernel that merges its K ranges itself.  A workgroup stages
+// matmul_small_chunks(batch) chunks of its range at a time (longer ranges take
+// several passes).  Needs chunks_per_split <= matmul_small_range_chunks_max(),
+// splits <= matmul_small_max_splits(batch) and, with splits > 1, split_out
+// holding splits x batch x (64 * tiles) floats (16-byte aligned) and one
+// zeroed counter per tile of 64 weight rows.
 hipError_t launch_matmul_small(const MatmulArgs& a, hipStream_t stream);
 int matmul_small_chunks(int batch);
+int matmul_small_range_chunks_max();
 int matmul_small_max_splits(int batch);
 int64_t matmul_small_x_halves(int batch, int in_dim);
 

@@ -402,17 +402,24 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
 // With kSums (Q4_K weights) it also writes each 32-wide block's sum of the
 // scaled x, xsum[(z * 2 chunks_per_split + block of the range) * 64 + b], for
 // the weights' min term.
-template <bool kSums>
+// kSlots f4 per thread: ranges of up to 16 kSlots chunks.
+template <bool kSums, int kSlots>
 __global__ __launch_bounds__(kMmThreads) void matmul_split_x_range_kernel(MatmulArgs a) {
     __shared__ float red[kMmThreads / 64];
     const int b = blockIdx.x;
     const int z = blockIdx.y;
     const int i0 = z * a.chunks_per_split * 16;  // first f4 of the range
-    const int n4 = min(a.in_dim / 4, i0 + a.chunks_per_split * 16) - i0;  // host: at most kMmThreads
+    const int n4 = min(a.in_dim / 4, i0 + a.chunks_per_split * 16) - i0;  // host: at most kSlots * kMmThreads
     const int t = threadIdx.x;
     const f4* xr = reinterpret_cast<const f4*>(a.x + (int64_t)b * a.in_dim) + i0;
-    const f4 raw = t < n4 ? xr[t] : f4{0.f, 0.f, 0.f, 0.f};
-    float mx = fmaxf(fmaxf(fabsf(raw[0]), fabsf(raw[1])), fmaxf(fabsf(raw[2]), fabsf(raw[3])));
+    f4 raw[kSlots];
+    float mx = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < kSlots; ++sl) {
+        const int tt = t + sl * kMmThreads;
+        raw[sl] = tt < n4 ? xr[tt] : f4{0.f, 0.f, 0.f, 0.f};
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(raw[sl][0]), fabsf(raw[sl][1])), fmaxf(fabsf(raw[sl][2]), fabsf(raw[sl][3]))));
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if ((t & 63) == 0) red[t >> 6] = mx;
@@ -422,27 +429,32 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_range_kernel(Matmul
     int ex = 0;
     if (mx > 0.f && mx <= FLT_MAX) (void)frexpf(mx, &ex);
     const int e = mx > 0.f ? (mx <= FLT_MAX ? min(115, max(-126, ex - 13)) : 115) : 0;
-    const f4 v = raw * ldexpf(1.0f, -e);
-    if constexpr (kSums) {
-        // Eight threads hold a block's 32 values: a tree over the group.
-        float s = (v[0] + v[1]) + (v[2] + v[3]);
 #pragma unroll
-        for (int off = 1; off < 8; off <<= 1) s += __shfl_xor(s, off);
-        if (t < n4 && (t & 7) == 0) a.xsum[((int64_t)z * 2 * a.chunks_per_split + (t >> 3)) * 64 + b] = s;
-    }
-    if (t < n4) {
-        const h4v h = __builtin_convertvector(v, h4v);
-        f4 l = v - __builtin_convertvector(h, f4);
+    for (int sl = 0; sl < kSlots; ++sl) {
+        if (sl * kMmThreads >= n4) break;  // the same for every thread
+        const int tt = t + sl * kMmThreads;
+        const f4 v = raw[sl] * ldexpf(1.0f, -e);
+        if constexpr (kSums) {
+            // Eight threads hold a block's 32 values: a tree over the group.
+            float s = (v[0] + v[1]) + (v[2] + v[3]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) l[c] = __builtin_isinf(v[c]) ? 0.f : l[c];
-        const h4v lh = __builtin_convertvector(l, h4v);
-        _Float16* xt = static_cast<_Float16*>(a.xh);
-        const int k = 4 * (i0 + t);
-        const int64_t tile0 = (int64_t)(b >> 4) * (a.in_dim / 64);
-        const int64_t base = ((tile0 + (k >> 6)) * 2 + ((k >> 5) & 1)) * 2 * 512 +
-                             (((k >> 3) & 3) * 16 + (b & 15)) * 8 + (k & 7);
-        *reinterpret_cast<h4v*>(xt + base) = h;
-        *reinterpret_cast<h4v*>(xt + base + 512) = lh;
+            for (int off = 1; off < 8; off <<= 1) s += __shfl_xor(s, off);
+            if (tt < n4 && (tt & 7) == 0) a.xsum[((int64_t)z * 2 * a.chunks_per_split + (tt >> 3)) * 64 + b] = s;
+        }
+        if (tt < n4) {
+            const h4v h = __builtin_convertvector(v, h4v);
+            f4 l = v - __builtin_convertvector(h, f4);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) l[c] = __builtin_isinf(v[c]) ? 0.f : l[c];
+            const h4v lh = __builtin_convertvector(l, h4v);
+            _Float16* xt = static_cast<_Float16*>(a.xh);
+            const int k = 4 * (i0 + tt);
+            const int64_t tile0 = (int64_t)(b >> 4) * (a.in_dim / 64);
+            const int64_t base = ((tile0 + (k >> 6)) * 2 + ((k >> 5) & 1)) * 2 * 512 +
+                                 (((k >> 3) & 3) * 16 + (b & 15)) * 8 + (k & 7);
+            *reinterpret_cast<h4v*>(xt + base) = h;
+            *reinterpret_cast<h4v*>(xt + base + 512) = lh;
+        }
     }
     if (t == 0) a.xexp[z * a.batch + b] = e;
 }
@@ -589,14 +601,17 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
 
 // ---- Q8_0 weights, batches of up to 64 rows ---------------------------------
 //
-// matmul_q8_f16_small_kernel<NT, CH> is the fp16 form for batches of at most
-// 64 rows (NT M tiles of 16), laid out so that nothing waits in line:
+// matmul_q8_f16_small_kernel<NT, CH, kPasses> is the fp16 form for batches of
+// at most 64 rows (NT M tiles of 16), laid out so that nothing waits in line:
 //   - x comes from the pre-pass in tile order (matmul_split_x_range_kernel):
 //     a wave loads the A operands of its M tile straight into registers, one
 //     KB per instruction, every chunk of its range at once, with no LDS and no
 //     barrier between chunks;
 //   - the workgroup's 64 weight rows over its range of at most CH chunks are
 //     expanded to fp16 once, into LDS, with their block scales as floats;
+//   - a longer range (kPasses: the merge holds too few ranges for chunks of
+//     CH, as for an 18944-wide K at 64 rows) is walked CH chunks at a time
+//     through the same LDS, with a barrier between passes;
 //   - wave w takes M tile w NT / 4 and NT of the four N tiles (16 weight rows
 //     each), so every staged operand serves several matrix steps;
 //   - two workgroups fit on a CU;
@@ -628,13 +643,11 @@ __device__ __forceinline__ void small_load_x(h8 (&ax)[CH][2][2], const MatmulArg
                 for (int part = 0; part < 2; ++part) ax[i][blk][part] = xt[i * 256 + (blk * 2 + part) * 64];
 }
 
-// The range's products: per block, hi and lo into a fresh accumulator, which
-// the block's scale (wd: [weight row][2 chunk + block]) adds into the sum.
+// One pass's products: per block, hi and lo into a fresh accumulator, which
+// the block's scale (wd: [weight row][2 chunk + block]) adds into acc.
 template <int NT, int CH>
 __device__ __forceinline__ void small_products(f4 (&acc)[NT], const h8 (&ax)[CH][2][2], const _Float16* wh,
                                                const float (*wd)[2 * CH + 1], int nc, int nt0, int n, int g) {
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
         if (i < nc) {
@@ -721,7 +734,7 @@ __device__ __forceinline__ void small_finish(const MatmulArgs& a, const f4 (&acc
     if (tid == 0) __hip_atomic_store(a.counters + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NT, int CH>
+template <int NT, int CH, bool kPasses>
 __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(MatmulArgs a) {
     static_assert(CH <= 8, "an LDS weight row holds 8 chunks");
     __shared__ _Float16 wh[kMmRowsWg * kSmRowHalves];  // [weight row][chunk][64 halves]
@@ -735,66 +748,77 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
     const int g = lane >> 4;
     const int chunks = a.in_dim / 64;
     const int c_begin = blockIdx.z * a.chunks_per_split;
-    const int nc = min(chunks, c_begin + a.chunks_per_split) - c_begin;  // 1..CH (host)
+    const int nc_range = min(chunks, c_begin + a.chunks_per_split) - c_begin;  // 1..CH, or more with kPasses (host)
     constexpr int kWavesPerM = 4 / NT;
     const int mt = wave / kWavesPerM;           // the wave's M tile
     const int nt0 = (wave % kWavesPerM) * NT;   // its first N tile
 
-    h8 ax[CH][2][2];
-    small_load_x<CH>(ax, a, mt, chunks, c_begin, nc, lane);
-
-    // Weights to fp16: unit u = 64 r + 8 i + 4 block + gg (row r, chunk i, lane
-    // group gg) is eight values; thread tid takes units tid + 256 k, that is
-    // one fixed (chunk, block, lane group) of rows tid / 64 + 4 k.  A wave's
-    // units are one row's chunks, so its loads cover whole 68-byte windows.
-    // Every unit's four dwords load first, one 16-byte raw buffer load each
-    // (dword aligned; lane offset fixed per thread plus a row step): block 0's
-    // values sit at dwords 2 gg .. 2 gg + 2 shifted by 2 bytes (the load
-    // covers 2 gg .. 2 gg + 3), block 1's at 9 + 2 gg, 10 + 2 gg (the load
-    // covers 7 + 2 gg .. 10 + 2 gg), and the scale is the low half of dword 0
-    // or the high half of dword 8, both in lane group 0's load.
-    // Units of chunks past the range load the range's last chunk and store
-    // nothing; rows past out_dim read as zero (past the buffer's end).
-    {
-        constexpr int kU = (kMmRowsWg * 64) / kMmThreads;
-        const int row_bytes = chunks * 68;
-        const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
-        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes),
-            (short)0, rows_here * row_bytes, 0x00020000);
-        const int r0 = tid >> 6;
-        const int i = (tid >> 3) & 7;
-        const int blk = (tid >> 2) & 1;
-        const int gg = tid & 3;
-        const int s0 = blk ? 7 + 2 * gg : 2 * gg;  // the unit's four dwords: s0 .. s0 + 3, inside the chunk
-        const int voff = r0 * row_bytes + (c_begin + min(i, nc - 1)) * 68;
-        u4 wdw[kU];
+    f4 acc[NT];
 #pragma unroll
-        for (int k = 0; k < kU; ++k) {
-            // The row step stays in the lane offset: the range check covers the
-            // lane offset, not the scalar one.
-            wdw[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 4 * k * row_bytes + 4 * s0, 0, 0);
-        }
-        const int sh = blk ? 0 : 2;
-        _Float16* wdst = &wh[r0 * kSmRowHalves + i * 64 + blk * 32 + gg * 8];
-        float* ddst = &wd[r0][2 * i + blk];
-        if (i < nc) {
+    for (int j = 0; j < NT; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+    // With kPasses the range is walked CH chunks at a time through the same LDS.
+    for (int c0 = 0;;) {
+        const int nc = kPasses ? min(CH, nc_range - c0) : nc_range;
+        const int cb = c_begin + c0;
+        h8 ax[CH][2][2];
+        small_load_x<CH>(ax, a, mt, chunks, cb, nc, lane);
+
+        // Weights to fp16: unit u = 64 r + 8 i + 4 block + gg (row r, chunk i, lane
+        // group gg) is eight values; thread tid takes units tid + 256 k, that is
+        // one fixed (chunk, block, lane group) of rows tid / 64 + 4 k.  A wave's
+        // units are one row's chunks, so its loads cover whole 68-byte windows.
+        // Every unit's four dwords load first, one 16-byte raw buffer load each
+        // (dword aligned; lane offset fixed per thread plus a row step): block 0's
+        // values sit at dwords 2 gg .. 2 gg + 2 shifted by 2 bytes (the load
+        // covers 2 gg .. 2 gg + 3), block 1's at 9 + 2 gg, 10 + 2 gg (the load
+        // covers 7 + 2 gg .. 10 + 2 gg), and the scale is the low half of dword 0
+        // or the high half of dword 8, both in lane group 0's load.
+        // Units of chunks past the range load the range's last chunk and store
+        // nothing; rows past out_dim read as zero (past the buffer's end).
+        {
+            constexpr int kU = (kMmRowsWg * 64) / kMmThreads;
+            const int row_bytes = chunks * 68;
+            const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
+            const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes),
+                (short)0, rows_here * row_bytes, 0x00020000);
+            const int r0 = tid >> 6;
+            const int i = (tid >> 3) & 7;
+            const int blk = (tid >> 2) & 1;
+            const int gg = tid & 3;
+            const int s0 = blk ? 7 + 2 * gg : 2 * gg;  // the unit's four dwords: s0 .. s0 + 3, inside the chunk
+            const int voff = r0 * row_bytes + (cb + min(i, nc - 1)) * 68;
+            u4 wdw[kU];
 #pragma unroll
             for (int k = 0; k < kU; ++k) {
-                const uint32_t d0 = blk ? wdw[k][2] : wdw[k][0];
-                const uint32_t d1 = blk ? wdw[k][3] : wdw[k][1];
-                const h8 q = q8_to_h8(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(wdw[k][2], d1, sh));
-                *reinterpret_cast<h8*>(wdst + 4 * k * kSmRowHalves) = q;
-                // Lane group 0 holds the block's scale: dword 0 (low half) or 8 (high half).
-                const uint32_t sw = blk ? wdw[k][1] >> 16 : wdw[k][0];
-                if (gg == 0) ddst[4 * k * (2 * CH + 1)] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xFFFFu));
+                // The row step stays in the lane offset: the range check covers the
+                // lane offset, not the scalar one.
+                wdw[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 4 * k * row_bytes + 4 * s0, 0, 0);
+            }
+            const int sh = blk ? 0 : 2;
+            _Float16* wdst = &wh[r0 * kSmRowHalves + i * 64 + blk * 32 + gg * 8];
+            float* ddst = &wd[r0][2 * i + blk];
+            if (i < nc) {
+#pragma unroll
+                for (int k = 0; k < kU; ++k) {
+                    const uint32_t d0 = blk ? wdw[k][2] : wdw[k][0];
+                    const uint32_t d1 = blk ? wdw[k][3] : wdw[k][1];
+                    const h8 q = q8_to_h8(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(wdw[k][2], d1, sh));
+                    *reinterpret_cast<h8*>(wdst + 4 * k * kSmRowHalves) = q;
+                    // Lane group 0 holds the block's scale: dword 0 (low half) or 8 (high half).
+                    const uint32_t sw = blk ? wdw[k][1] >> 16 : wdw[k][0];
+                    if (gg == 0) ddst[4 * k * (2 * CH + 1)] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xFFFFu));
+                }
             }
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    f4 acc[NT];
-    small_products<NT, CH>(acc, ax, wh, wd, nc, nt0, n, g);
+        small_products<NT, CH>(acc, ax, wh, wd, nc, nt0, n, g);
+        if constexpr (!kPasses) break;
+        c0 += CH;
+        if (c0 >= nc_range) break;
+        __syncthreads();  // every wave is done with this pass's weights
+    }
     small_finish<NT>(a, acc, mt, nt0, n, g, tid, last);
 }
 
@@ -819,7 +843,7 @@ __device__ __forceinline__ h8 nib_to_h8(uint32_t d0, uint32_t d1) {
 
 // ---- Q4_K weights, batches of up to 64 rows ---------------------------------
 //
-// matmul_q4k_f16_small_kernel<NT> is the Q8_0 small form with Q4_K weights.
+// matmul_q4k_f16_small_kernel<NT, kPasses> is the Q8_0 small form with Q4_K weights.
 // A weight is w = d1 q - m1 per 32-wide sub-block (d1 = d * sc and
 // m1 = dmin * m, both exact in fp32; q = 0..15, exact in fp16), so
 //   y[b][o] = sum over blocks of  d1 * sum_k q_k x_k  -  m1 * sum_k x_k.
@@ -832,7 +856,7 @@ __device__ __forceinline__ h8 nib_to_h8(uint32_t d0, uint32_t d1) {
 // before the scaling.  A chunk of 64 weights is one quarter p of a 256-weight
 // super-block: sub-blocks 2 p (low nibbles of quant bytes 32 p ..) and 2 p + 1
 // (their high nibbles), so ranges need not start on a super-block.
-template <int NT>
+template <int NT, bool kPasses>
 __global__ __launch_bounds__(kMmThreads, 2) void matmul_q4k_f16_small_kernel(MatmulArgs a) {
     constexpr int CH = 8;
     __shared__ _Float16 wh[kMmRowsWg * kSmRowHalves];  // quants [weight row][chunk][64 halves]
@@ -848,100 +872,108 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q4k_f16_small_kernel(Mat
     const int g = lane >> 4;
     const int chunks = a.in_dim / 64;
     const int c_begin = blockIdx.z * a.chunks_per_split;
-    const int nc = min(chunks, c_begin + a.chunks_per_split) - c_begin;  // 1..CH (host)
+    const int nc_range = min(chunks, c_begin + a.chunks_per_split) - c_begin;  // 1..CH, or more with kPasses (host)
     constexpr int kWavesPerM = 4 / NT;
     const int mt = wave / kWavesPerM;
     const int nt0 = (wave % kWavesPerM) * NT;
 
-    h8 ax[CH][2][2];
-    small_load_x<CH>(ax, a, mt, chunks, c_begin, nc, lane);
+    f4 acc[NT], accm[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = accm[j] = f4{0.f, 0.f, 0.f, 0.f};
+    // With kPasses the range is walked CH chunks at a time through the same LDS.
+    for (int c0 = 0;;) {
+        const int nc = kPasses ? min(CH, nc_range - c0) : nc_range;
+        const int cb = c_begin + c0;
+        h8 ax[CH][2][2];
+        small_load_x<CH>(ax, a, mt, chunks, cb, nc, lane);
 
-    // Weights: unit (row r, chunk i) is one super-block quarter, 64 quants in 32
-    // bytes plus the super-block's 16-byte head (d, dmin, the 12 scale bytes);
-    // thread tid takes chunk tid % 8 of rows tid / 8 and tid / 8 + 32, three
-    // 16-byte raw buffer loads each (super-blocks are 144 bytes, so every load
-    // is dword aligned), all issued before the first is used.  Units of chunks
-    // past the range load the range's last chunk and store zero scales; rows
-    // past out_dim read as zero (past the buffer's end).
-    {
-        const int row_bytes = (a.in_dim / 256) * 144;
-        const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
-        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes),
-            (short)0, rows_here * row_bytes, 0x00020000);
-        const int i = tid & 7;
-        const int r0 = tid >> 3;
-        const int c = c_begin + min(i, nc - 1);
-        const int p = c & 3;
-        const int voff = r0 * row_bytes + (c >> 2) * 144;
-        u4 hd[2], qa[2], qb[2];
+        // Weights: unit (row r, chunk i) is one super-block quarter, 64 quants in 32
+        // bytes plus the super-block's 16-byte head (d, dmin, the 12 scale bytes);
+        // thread tid takes chunk tid % 8 of rows tid / 8 and tid / 8 + 32, three
+        // 16-byte raw buffer loads each (super-blocks are 144 bytes, so every load
+        // is dword aligned), all issued before the first is used.  Units of chunks
+        // past the range load the range's last chunk and store zero scales; rows
+        // past out_dim read as zero (past the buffer's end).
+        {
+            const int row_bytes = (a.in_dim / 256) * 144;
+            const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
+            const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes),
+                (short)0, rows_here * row_bytes, 0x00020000);
+            const int i = tid & 7;
+            const int r0 = tid >> 3;
+            const int c = cb + min(i, nc - 1);
+            const int p = c & 3;
+            const int voff = r0 * row_bytes + (c >> 2) * 144;
+            u4 hd[2], qa[2], qb[2];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int off = voff + 32 * k * row_bytes;
-            hd[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
-            qa[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 16 + 32 * p, 0, 0);
-            qb[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 32 + 32 * p, 0, 0);
-        }
-        // The range's block sums, loaded after the weights (the memory counter
-        // drains in order, so the weights need not wait for them) and stored
-        // after the expansion: thread tid takes block tid / 16, batch rows
-        // 4 (tid % 16) .. + 3; blocks past the range and rows past the batch are 0.
-        const int sblk = tid >> 4;
-        const int b4 = 4 * (tid & 15);
-        f4 xsv = f4{0.f, 0.f, 0.f, 0.f};
-        if (sblk < 2 * nc)
-            xsv = *reinterpret_cast<const f4*>(a.xsum + ((int64_t)blockIdx.z * 2 * a.chunks_per_split + sblk) * 64 + b4);
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int r = r0 + 32 * k;
-            float d1[2] = {0.f, 0.f}, m1[2] = {0.f, 0.f};
-            if (i < nc) {
-                const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd[k][0] & 0xFFFFu));
-                const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd[k][0] >> 16));
-                const uint32_t sc[3] = {hd[k][1], hd[k][2], hd[k][3]};
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    uint32_t scv, mv;
-                    q4k_scale_min(sc, 2 * p + h, scv, mv);
-                    d1[h] = d * (float)scv;   // exact
-                    m1[h] = dmin * (float)mv;  // exact
-                }
-                const uint32_t q[8] = {qa[k][0], qa[k][1], qa[k][2], qa[k][3], qb[k][0], qb[k][1], qb[k][2], qb[k][3]};
-                _Float16* dst = &wh[r * kSmRowHalves + i * 64];
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    *reinterpret_cast<h8*>(dst + 8 * s) = nib_to_h8(q[2 * s] & 0x0F0F0F0Fu, q[2 * s + 1] & 0x0F0F0F0Fu);
-                    *reinterpret_cast<h8*>(dst + 32 + 8 * s) =
-                        nib_to_h8((q[2 * s] >> 4) & 0x0F0F0F0Fu, (q[2 * s + 1] >> 4) & 0x0F0F0F0Fu);
-                }
+            for (int k = 0; k < 2; ++k) {
+                const int off = voff + 32 * k * row_bytes;
+                hd[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
+                qa[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 16 + 32 * p, 0, 0);
+                qb[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 32 + 32 * p, 0, 0);
             }
-            wd[r][2 * i] = d1[0];
-            wd[r][2 * i + 1] = d1[1];
-            wm[r][2 * i] = m1[0];
-            wm[r][2 * i + 1] = m1[1];
-        }
+            // The range's block sums, loaded after the weights (the memory counter
+            // drains in order, so the weights need not wait for them) and stored
+            // after the expansion: thread tid takes block tid / 16, batch rows
+            // 4 (tid % 16) .. + 3; blocks past the range and rows past the batch are 0.
+            const int sblk = tid >> 4;
+            const int b4 = 4 * (tid & 15);
+            f4 xsv = f4{0.f, 0.f, 0.f, 0.f};
+            if (sblk < 2 * nc)
+                xsv = *reinterpret_cast<const f4*>(a.xsum + ((int64_t)blockIdx.z * 2 * a.chunks_per_split + 2 * c0 + sblk) * 64 + b4);
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (b4 + c >= a.batch) xsv[c] = 0.f;
-        *reinterpret_cast<f4*>(&xs[sblk][b4]) = xsv;
-    }
-    __syncthreads();
+            for (int k = 0; k < 2; ++k) {
+                const int r = r0 + 32 * k;
+                float d1[2] = {0.f, 0.f}, m1[2] = {0.f, 0.f};
+                if (i < nc) {
+                    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd[k][0] & 0xFFFFu));
+                    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hd[k][0] >> 16));
+                    const uint32_t sc[3] = {hd[k][1], hd[k][2], hd[k][3]};
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        uint32_t scv, mv;
+                        q4k_scale_min(sc, 2 * p + h, scv, mv);
+                        d1[h] = d * (float)scv;   // exact
+                        m1[h] = dmin * (float)mv;  // exact
+                    }
+                    const uint32_t q[8] = {qa[k][0], qa[k][1], qa[k][2], qa[k][3], qb[k][0], qb[k][1], qb[k][2], qb[k][3]};
+                    _Float16* dst = &wh[r * kSmRowHalves + i * 64];
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        *reinterpret_cast<h8*>(dst + 8 * s) = nib_to_h8(q[2 * s] & 0x0F0F0F0Fu, q[2 * s + 1] & 0x0F0F0F0Fu);
+                        *reinterpret_cast<h8*>(dst + 32 + 8 * s) =
+                            nib_to_h8((q[2 * s] >> 4) & 0x0F0F0F0Fu, (q[2 * s + 1] >> 4) & 0x0F0F0F0Fu);
+                    }
+                }
+                wd[r][2 * i] = d1[0];
+                wd[r][2 * i + 1] = d1[1];
+                wm[r][2 * i] = m1[0];
+                wm[r][2 * i + 1] = m1[1];
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (b4 + c >= a.batch) xsv[c] = 0.f;
+            *reinterpret_cast<f4*>(&xs[sblk][b4]) = xsv;
+        }
+        __syncthreads();
 
-    f4 acc[NT];
-    small_products<NT, CH>(acc, ax, wh, wd, nc, nt0, n, g);
-    // The min term, four blocks per matrix step: lane (g, n) supplies block
-    // 4 s + g of batch row 16 mt + n (A) and of weight row 16 (nt0 + j) + n (B).
-    f4 accm[NT];
+        small_products<NT, CH>(acc, ax, wh, wd, nc, nt0, n, g);
+        // The min term, four blocks per matrix step: lane (g, n) supplies block
+        // 4 s + g of batch row 16 mt + n (A) and of weight row 16 (nt0 + j) + n (B).
 #pragma unroll
-    for (int j = 0; j < NT; ++j) accm[j] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < CH / 2; ++s) {
+            if (2 * s < nc) {
+                const float xa = xs[4 * s + g][16 * mt + n];
 #pragma unroll
-    for (int s = 0; s < CH / 2; ++s) {
-        if (2 * s < nc) {
-            const float xa = xs[4 * s + g][16 * mt + n];
-#pragma unroll
-            for (int j = 0; j < NT; ++j)
-                accm[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, wm[16 * (nt0 + j) + n][4 * s + g], accm[j], 0, 0, 0);
+                for (int j = 0; j < NT; ++j)
+                    accm[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, wm[16 * (nt0 + j) + n][4 * s + g], accm[j], 0, 0, 0);
+            }
         }
+        if constexpr (!kPasses) break;
+        c0 += CH;
+        if (c0 >= nc_range) break;
+        __syncthreads();  // every wave is done with this pass's weights and sums
     }
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[j] -= accm[j];
@@ -976,38 +1008,60 @@ __global__ __launch_bounds__(kMmThreads) void matmul_reduce_kernel(MatmulArgs a)
 
 int matmul_small_chunks(int) { return 8; }
 
+int matmul_small_range_chunks_max() { return 4 * kMmThreads / 16; }  // the pre-pass: four f4 per thread
+
 int64_t matmul_small_x_halves(int batch, int in_dim) {
     return (int64_t)(batch <= 16 ? 1 : batch <= 32 ? 2 : 4) * 16 * in_dim * 2;  // NT whole M tiles, hi and lo
 }
 
 int matmul_small_max_splits(int batch) { return kSmMaxPartials / (batch <= 16 ? 1 : batch <= 32 ? 2 : 4); }
 
+namespace {
+
+template <int NT, bool kPasses>
+void launch_small_product(const MatmulArgs& a, dim3 grid, hipStream_t stream) {
+    if (a.w_type == kWeightQ4_K)
+        hipLaunchKernelGGL((matmul_q4k_f16_small_kernel<NT, kPasses>), grid, dim3(kMmThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((matmul_q8_f16_small_kernel<NT, 8, kPasses>), grid, dim3(kMmThreads), 0, stream, a);
+}
+
+template <bool kPasses>
+void launch_small_product(const MatmulArgs& a, dim3 grid, hipStream_t stream) {
+    if (a.batch <= 16)
+        launch_small_product<1, kPasses>(a, grid, stream);
+    else if (a.batch <= 32)
+        launch_small_product<2, kPasses>(a, grid, stream);
+    else
+        launch_small_product<4, kPasses>(a, grid, stream);
+}
+
+}  // namespace
+
 hipError_t launch_matmul_small(const MatmulArgs& a, hipStream_t stream) {
     if (a.batch <= 0 || a.out_dim <= 0) return hipSuccess;
     const bool q4k = a.w_type == kWeightQ4_K;
-    if (a.batch > 64 || (a.w_type != kWeightQ8_0 && !q4k) || !a.xh || !a.xl || !a.xexp ||
-        a.chunks_per_split > matmul_small_chunks(a.batch) || a.splits > matmul_small_max_splits(a.batch) ||
+    if (a.batch > 64 || (a.w_type != kWeightQ8_0 && !q4k) || !a.xh || !a.xl || !a.xexp || a.chunks_per_split < 1 ||
+        a.chunks_per_split > matmul_small_range_chunks_max() || a.splits > matmul_small_max_splits(a.batch) ||
         (a.splits > 1 && (!a.split_out || !a.counters)) || (q4k && (!a.xsum || a.in_dim % 256 != 0)))
         return hipErrorInvalidValue;
-    if (a.chunks_per_split * 16 > kMmThreads) return hipErrorInvalidValue;  // one f4 per thread
-    const dim3 grid((a.out_dim + kMmRowsWg - 1) / kMmRowsWg, 1, a.splits);
-    if (q4k) {
-        hipLaunchKernelGGL(matmul_split_x_range_kernel<true>, dim3(a.batch, a.splits), dim3(kMmThreads), 0, stream, a);
-        if (a.batch <= 16)
-            hipLaunchKernelGGL(matmul_q4k_f16_small_kernel<1>, grid, dim3(kMmThreads), 0, stream, a);
-        else if (a.batch <= 32)
-            hipLaunchKernelGGL(matmul_q4k_f16_small_kernel<2>, grid, dim3(kMmThreads), 0, stream, a);
+    const dim3 pre(a.batch, a.splits);
+    if (a.chunks_per_split * 16 <= kMmThreads) {
+        if (q4k)
+            hipLaunchKernelGGL((matmul_split_x_range_kernel<true, 1>), pre, dim3(kMmThreads), 0, stream, a);
         else
-            hipLaunchKernelGGL(matmul_q4k_f16_small_kernel<4>, grid, dim3(kMmThreads), 0, stream, a);
-        return hipGetLastError();
+            hipLaunchKernelGGL((matmul_split_x_range_kernel<false, 1>), pre, dim3(kMmThreads), 0, stream, a);
+    } else {
+        if (q4k)
+            hipLaunchKernelGGL((matmul_split_x_range_kernel<true, 4>), pre, dim3(kMmThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL((matmul_split_x_range_kernel<false, 4>), pre, dim3(kMmThreads), 0, stream, a);
     }
-    hipLaunchKernelGGL(matmul_split_x_range_kernel<false>, dim3(a.batch, a.splits), dim3(kMmThreads), 0, stream, a);
-    if (a.batch <= 16)
-        hipLaunchKernelGGL((matmul_q8_f16_small_kernel<1, 8>), grid, dim3(kMmThreads), 0, stream, a);
-    else if (a.batch <= 32)
-        hipLaunchKernelGGL((matmul_q8_f16_small_kernel<2, 8>), grid, dim3(kMmThreads), 0, stream, a);
+    const dim3 grid((a.out_dim + kMmRowsWg - 1) / kMmRowsWg, 1, a.splits);
+    if (a.chunks_per_split <= matmul_small_chunks(a.batch))
+        launch_small_product<false>(a, grid, stream);
     else
-        hipLaunchKernelGGL((matmul_q8_f16_small_kernel<4, 8>), grid, dim3(kMmThreads), 0, stream, a);
+        launch_small_product<true>(a, grid, stream);
     return hipGetLastError();
 }
 

@@ -898,16 +898,22 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
     if (rc) return rc;
     if ((w_type == GSP_WTYPE_Q8_0 || w_type == GSP_WTYPE_Q4_K) && batch <= 64 &&
         (int64_t)batch * out_dim >= kMatmulSmallMinOutputs &&
-        (in_dim / 64 + gsp::matmul_small_chunks(batch) - 1) / gsp::matmul_small_chunks(batch) <=
+        (in_dim / 64 + gsp::matmul_small_range_chunks_max() - 1) / gsp::matmul_small_range_chunks_max() <=
             gsp::matmul_small_max_splits(batch)) {
         // Small batches: about two workgroups (64 weight rows, every batch row)
-        // per CU, K cut into ranges whose weights fit the workgroup's LDS, and
-        // no more ranges than the merge holds.  The partial offsets are 32-bit.
+        // per CU and no more K ranges than the merge holds.  Ranges whose
+        // weights fit the workgroup's LDS when the merge allows enough of them;
+        // else longer ranges, which the workgroup walks in passes.  The partial
+        // offsets are 32-bit.
         const int64_t chunks = in_dim / 64;
         const int64_t tiles = (out_dim + 63) / 64;
+        const int64_t maxs = gsp::matmul_small_max_splits(batch);
         const int64_t lo = (chunks + gsp::matmul_small_chunks(batch) - 1) / gsp::matmul_small_chunks(batch);
         const int64_t want = (2 * (int64_t)std::max(1, ctx->num_cus) + tiles - 1) / tiles;
-        int64_t splits = std::max(lo, std::min({want, (int64_t)gsp::matmul_small_max_splits(batch), chunks}));
+        int64_t splits = lo <= maxs ? std::max(lo, std::min({want, maxs, chunks}))
+                                    : std::max<int64_t>((chunks + gsp::matmul_small_range_chunks_max() - 1) /
+                                                            gsp::matmul_small_range_chunks_max(),
+                                                        std::min(want, maxs));
         const int64_t per = (chunks + splits - 1) / splits;
         splits = (chunks + per - 1) / per;
         gsp::MatmulArgs a{};
