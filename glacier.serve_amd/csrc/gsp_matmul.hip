@@ -767,33 +767,35 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
         // group gg) is eight values; thread tid takes units tid + 256 k, that is
         // one fixed (chunk, block, lane group) of rows tid / 64 + 4 k.  A wave's
         // units are one row's chunks, so its loads cover whole 68-byte windows.
-        // Every unit's four dwords load first, one 16-byte raw buffer load each
-        // (dword aligned; lane offset fixed per thread plus a row step): block 0's
-        // values sit at dwords 2 gg .. 2 gg + 2 shifted by 2 bytes (the load
-        // covers 2 gg .. 2 gg + 3), block 1's at 9 + 2 gg, 10 + 2 gg (the load
-        // covers 7 + 2 gg .. 10 + 2 gg), and the scale is the low half of dword 0
-        // or the high half of dword 8, both in lane group 0's load.
+        // Every unit's three dwords load first, one 12-byte raw buffer load each
+        // (dword aligned; one lane offset per thread): block 0's values sit at
+        // dwords 2 gg .. 2 gg + 2 shifted by 2 bytes, block 1's at 9 + 2 gg,
+        // 10 + 2 gg (the load covers 8 + 2 gg .. 10 + 2 gg), and the scale is the
+        // low half of dword 0 or the high half of dword 8, both in lane group 0's
+        // load.
         // Units of chunks past the range load the range's last chunk and store
         // nothing; rows past out_dim read as zero (past the buffer's end).
         {
             constexpr int kU = (kMmRowsWg * 64) / kMmThreads;
             const int row_bytes = chunks * 68;
             const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
-            const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes),
-                (short)0, rows_here * row_bytes, 0x00020000);
+            typedef uint32_t u3 __attribute__((ext_vector_type(3)));
             const int r0 = tid >> 6;
             const int i = (tid >> 3) & 7;
             const int blk = (tid >> 2) & 1;
             const int gg = tid & 3;
-            const int s0 = blk ? 7 + 2 * gg : 2 * gg;  // the unit's four dwords: s0 .. s0 + 3, inside the chunk
-            const int voff = r0 * row_bytes + (cb + min(i, nc - 1)) * 68;
-            u4 wdw[kU];
+            const int s0 = blk ? 8 + 2 * gg : 2 * gg;  // the unit's three dwords: s0 .. s0 + 2, inside the chunk
+            const int voff = r0 * row_bytes + (cb + min(i, nc - 1)) * 68 + 4 * s0;
+            u3 wdw[kU];
 #pragma unroll
             for (int k = 0; k < kU; ++k) {
-                // The row step stays in the lane offset: the range check covers the
-                // lane offset, not the scalar one.
-                wdw[k] = __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 4 * k * row_bytes + 4 * s0, 0, 0);
+                // Rows r0 + 4 k: the row step goes into the descriptor (base and
+                // record count), so one lane offset serves every load and the
+                // range check, which covers the lane offset, still stops at out_dim.
+                const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + ((int64_t)blockIdx.x * kMmRowsWg + 4 * k) * row_bytes),
+                    (short)0, max(0, rows_here - 4 * k) * row_bytes, 0x00020000);
+                wdw[k] = __builtin_amdgcn_raw_buffer_load_b96(wr, voff, 0, 0);
             }
             const int sh = blk ? 0 : 2;
             _Float16* wdst = &wh[r0 * kSmRowHalves + i * 64 + blk * 32 + gg * 8];
@@ -801,12 +803,12 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
             if (i < nc) {
 #pragma unroll
                 for (int k = 0; k < kU; ++k) {
-                    const uint32_t d0 = blk ? wdw[k][2] : wdw[k][0];
-                    const uint32_t d1 = blk ? wdw[k][3] : wdw[k][1];
+                    const uint32_t d0 = blk ? wdw[k][1] : wdw[k][0];
+                    const uint32_t d1 = blk ? wdw[k][2] : wdw[k][1];
                     const h8 q = q8_to_h8(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(wdw[k][2], d1, sh));
                     *reinterpret_cast<h8*>(wdst + 4 * k * kSmRowHalves) = q;
                     // Lane group 0 holds the block's scale: dword 0 (low half) or 8 (high half).
-                    const uint32_t sw = blk ? wdw[k][1] >> 16 : wdw[k][0];
+                    const uint32_t sw = blk ? wdw[k][0] >> 16 : wdw[k][0];
                     if (gg == 0) ddst[4 * k * (2 * CH + 1)] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xFFFFu));
                 }
             }

@@ -204,22 +204,25 @@ def test_kquant_matmul_matches_oracle(torch_mod, gsp, ctx, shape, w_type):
     assert np.array_equal(got, again)
 
 
-# Long K on the small-batch form: when the merge holds too few K ranges for ranges of 8 chunks (more
-# than 8 ranges at 33..64 rows, 16 at 17..32, 32 at up to 16), each workgroup walks its range in
-# passes of 8 chunks through the same LDS, and the pre-pass takes up to four f4 per thread.  The
-# split choice below is the library's for a 256-CU device; other CU counts give other splits of the
-# same shapes.
+# Long K and wide outputs on the small-batch form.  When the merge holds too few K ranges for
+# ranges of 8 chunks (more than 8 ranges at 33..64 rows, 16 at 17..32, 32 at up to 16), each
+# workgroup walks its range in passes of 8 chunks through the same LDS, and the pre-pass takes up to
+# four f4 per thread.  Wide outputs run several rounds of workgroups.  The splits below are the
+# library's for a 256-CU device; other CU counts give other splits of the same shapes.
 LONG_SHAPES = [
     (5120, 1040, 64),   # 8 ranges of 10 chunks: a full pass, then a 2-chunk one; one f4 per pre-pass thread
     (18944, 1040, 64),  # Qwen2.5-7B's FFN down-projection width: 8 ranges of 37 chunks, 5 passes
     (18944, 4100, 17),  # two M tiles, a ragged last weight-row tile
     (6656, 6592, 40),   # 5 ranges of 21 chunks, the last of 20; a ragged batch tile
+    (3584, 18944, 64),  # Qwen2.5-7B's gate/up projection: 7 ranges of 296 tiles
+    (4096, 16384, 24),  # two M tiles: 8 ranges of 256 tiles
+    (512, 65536, 1),    # one range of 1024 tiles, y stored directly
 ]
 
 
 @pytest.mark.parametrize("w_type", [orc.WTYPE_Q8_0, orc.WTYPE_Q4_K], ids=["q8_0", "q4_k"])
 @pytest.mark.parametrize("shape", LONG_SHAPES, ids=lambda s: f"in{s[0]}_out{s[1]}_b{s[2]}")
-def test_small_batch_long_ranges_match_oracle(torch_mod, gsp, ctx, shape, w_type):
+def test_small_batch_long_ranges_and_wide_outputs_match_oracle(torch_mod, gsp, ctx, shape, w_type):
     in_dim, out_dim, batch = shape
     print(f"case matmul long {shape} type={w_type}", flush=True)
     rng = np.random.default_rng(in_dim * 5 + out_dim + batch + w_type)
