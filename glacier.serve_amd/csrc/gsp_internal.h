@@ -183,10 +183,11 @@ struct MatmulArgs {
     float* xsum;
 };
 hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream);
-// The small-batch form (batch <= 64, Q8_0 or Q4_K weights): the x pre-pass in
+// The small-batch form (batch <= 64, Q8_0, Q4_K or Q6_K weights): the x pre-pass in
 // tile order (xh: matmul_small_x_halves halves, xexp: splits x batch
 // exponents, one per K range of each row; for Q4_K also xsum), then one
-// product kernel that merges its K ranges itself.  A workgroup stages
+// product kernel that merges its K ranges itself (Q6_K: chunks_per_split
+// even, so that ranges start on a super-block half).  A workgroup stages
 // matmul_small_chunks(batch) chunks of its range at a time (longer ranges take
 // several passes).  Needs chunks_per_split <= matmul_small_range_chunks_max(),
 // splits <= matmul_small_max_splits(batch) and, with splits > 1, split_out

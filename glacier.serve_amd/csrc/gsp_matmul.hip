@@ -12,7 +12,7 @@
 // accumulation, so no operand is rounded below fp32.  The fp16 form
 // (matmul_q8_f16_kernel, large Q8_0 products, described further down) runs
 // one Q8_0 block per fp16 matrix step with x as a scaled fp16 pair; its
-// small-batch variants (at most 64 batch rows) take Q8_0 and Q4_K weights.
+// small-batch variants (at most 64 batch rows) take Q8_0, Q4_K and Q6_K weights.
 //
 // fp32 form:
 // A workgroup (four waves) owns 64 weight rows (16 per wave, MFMA M) and 64
@@ -982,6 +982,152 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q4k_f16_small_kernel(Mat
     small_finish<NT>(a, acc, mt, nt0, n, g, tid, last);
 }
 
+// ---- Q6_K weights, batches of up to 64 rows ---------------------------------
+//
+// matmul_q6k_f16_small_kernel<NT, kPasses> is the Q8_0 small form with Q6_K
+// weights.  A weight is w = (d * sc) * (q - 32) with the int8 scale sc per 16
+// weights: q - 32 is exact in fp16 and d * sc exact in fp32, but the scale
+// changes inside a 32-wide matrix step.  So each block runs as two masked
+// pairs of 16x16x32 fp16 steps (B operand zero outside the lanes of one
+// 16-wide half: lane groups 0-1 hold k < 16, 2-3 the rest), each half's sum
+// scaled by its own d * sc.  The unit of staging is one 128-weight half n of a
+// super-block (chunks 2 n' and 2 n' + 1 of the range, so ranges start on even
+// chunks): quant bytes 64 n .. (low 4 bits, the chunk's nibble), high-bit
+// bytes 128 + 32 n .., scales 192 + 8 n .. and d at 208.  Super-blocks are
+// 210 bytes, so the loads are only 2-byte aligned; gfx950 runs with unaligned
+// buffer access, and every load stays inside its super-block.
+template <int NT, int CH>
+__device__ __forceinline__ void small_products_q6k(f4 (&acc)[NT], const h8 (&ax)[CH][2][2], const _Float16* wh,
+                                                   const float (*ws)[4 * CH + 1], int nc, int nt0, int n, int g) {
+    const h8 zero = h8{};
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        if (i < nc) {
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    const int r = 16 * (nt0 + j) + n;
+                    const h8 wq = *reinterpret_cast<const h8*>(&wh[r * kSmRowHalves + i * 64 + blk * 32 + g * 8]);
+                    const h8 wa = g < 2 ? wq : zero;  // k < 16: the block's first scale
+                    const h8 wb = g < 2 ? zero : wq;
+                    const float sa = ws[r][4 * i + 2 * blk];
+                    const float sb = ws[r][4 * i + 2 * blk + 1];
+                    f4 pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i][blk][0], wa, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i][blk][1], wa, pa, 0, 0, 0);
+                    f4 pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i][blk][0], wb, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax[i][blk][1], wb, pb, 0, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[j][q] = fmaf(sb, pb[q], fmaf(sa, pa[q], acc[j][q]));
+                }
+            }
+        }
+    }
+}
+
+// Four six-bit values (one per byte, 0..63) as fp16 minus 32: the half
+// 0x6400 | u is 1024 + u, so subtracting 1056 leaves u - 32 exactly.
+__device__ __forceinline__ void six_to_h4(uint32_t u, h2& lo, h2& hi) {
+    lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - h2{(_Float16)1056.0f, (_Float16)1056.0f};
+    hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - h2{(_Float16)1056.0f, (_Float16)1056.0f};
+}
+
+template <int NT, bool kPasses>
+__global__ __launch_bounds__(kMmThreads, 2) void matmul_q6k_f16_small_kernel(MatmulArgs a) {
+    constexpr int CH = 8;
+    __shared__ _Float16 wh[kMmRowsWg * kSmRowHalves];  // q - 32 [weight row][chunk][64 halves]
+    __shared__ float ws[kMmRowsWg][4 * CH + 1];        // d * sc [weight row][4 chunk + 16-wide part]
+    __shared__ int last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int chunks = a.in_dim / 64;
+    const int c_begin = blockIdx.z * a.chunks_per_split;  // even (host)
+    const int nc_range = min(chunks, c_begin + a.chunks_per_split) - c_begin;  // 1..CH, or more with kPasses (host)
+    constexpr int kWavesPerM = 4 / NT;
+    const int mt = wave / kWavesPerM;
+    const int nt0 = (wave % kWavesPerM) * NT;
+
+    // Staging: thread tid takes row tid / 4 and the range's half tid % 4 (its
+    // chunks 2 (tid % 4) and 2 (tid % 4) + 1); a wave's loads cover 16 rows.
+    const int row_bytes = (a.in_dim / 256) * 210;
+    const int rows_here = min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * row_bytes), (short)0,
+        rows_here * row_bytes, 0x00020000);
+    const int r = tid >> 2;
+    const int hh = tid & 3;
+
+    f4 acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0;;) {
+        const int nc = kPasses ? min(CH, nc_range - c0) : nc_range;
+        const int cb = c_begin + c0;
+        h8 ax[CH][2][2];
+        small_load_x<CH>(ax, a, mt, chunks, cb, nc, lane);
+        {
+            // The unit's half of the super-block (the range's last when past it).
+            const int hl = min(2 * hh, nc - 1) >> 1;
+            const int half = (cb >> 1) + hl;
+            const int hn = half & 1;
+            const int off = r * row_bytes + (half >> 1) * 210;
+            u4 ql[4], qh[2];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) ql[t] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 64 * hn + 16 * t, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) qh[t] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + 128 + 32 * hn + 16 * t, 0, 0);
+            typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+            const u2 sc = __builtin_amdgcn_raw_buffer_load_b64(wr, off + 192 + 8 * hn, 0, 0);
+            const uint16_t dh = __builtin_amdgcn_raw_buffer_load_b16(wr, off + 208, 0, 0);
+            const float d = (float)__builtin_bit_cast(_Float16, dh);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int i = 2 * hh + e;  // the chunk in this pass
+                if (i < nc) {
+                    _Float16* dst = &wh[r * kSmRowHalves + i * 64];
+#pragma unroll
+                    for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) {
+                            h8 v;
+#pragma unroll
+                            for (int t2 = 0; t2 < 2; ++t2) {
+                                const int t = 2 * s + t2;  // dword of the block: its weights 4 t .. 4 t + 3
+                                const uint32_t qlw = ql[(8 * blk + t) >> 2][(8 * blk + t) & 3];
+                                const uint32_t qhw = qh[t >> 2][t & 3];
+                                const uint32_t u = ((qlw >> (4 * e)) & 0x0F0F0F0Fu) |
+                                                   (((qhw >> (4 * e + 2 * blk)) & 0x03030303u) << 4);
+                                h2 lo, hi;
+                                six_to_h4(u, lo, hi);
+                                v[4 * t2 + 0] = lo[0];
+                                v[4 * t2 + 1] = lo[1];
+                                v[4 * t2 + 2] = hi[0];
+                                v[4 * t2 + 3] = hi[1];
+                            }
+                            *reinterpret_cast<h8*>(dst + blk * 32 + 8 * s) = v;
+                        }
+                    }
+                    // Scales 8 hn + 4 e + 2 blk + part: byte 2 blk + part of scale dword e.
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+                        ws[r][4 * i + p] = d * (float)(int8_t)((sc[e] >> (8 * p)) & 0xFFu);  // exact
+                }
+            }
+        }
+        __syncthreads();
+        small_products_q6k<NT, CH>(acc, ax, wh, ws, nc, nt0, n, g);
+        if constexpr (!kPasses) break;
+        c0 += CH;
+        if (c0 >= nc_range) break;
+        __syncthreads();  // every wave is done with this pass's weights
+    }
+    small_finish<NT>(a, acc, mt, nt0, n, g, tid, last);
+}
+
 // y = the sum over z of the split partials, in z order; four elements per
 // thread and step when y and the partials are 16-byte aligned, else one.
 __global__ __launch_bounds__(kMmThreads) void matmul_reduce_kernel(MatmulArgs a) {
@@ -1024,6 +1170,8 @@ template <int NT, bool kPasses>
 void launch_small_product(const MatmulArgs& a, dim3 grid, hipStream_t stream) {
     if (a.w_type == kWeightQ4_K)
         hipLaunchKernelGGL((matmul_q4k_f16_small_kernel<NT, kPasses>), grid, dim3(kMmThreads), 0, stream, a);
+    else if (a.w_type == kWeightQ6_K)
+        hipLaunchKernelGGL((matmul_q6k_f16_small_kernel<NT, kPasses>), grid, dim3(kMmThreads), 0, stream, a);
     else
         hipLaunchKernelGGL((matmul_q8_f16_small_kernel<NT, 8, kPasses>), grid, dim3(kMmThreads), 0, stream, a);
 }
@@ -1043,9 +1191,11 @@ void launch_small_product(const MatmulArgs& a, dim3 grid, hipStream_t stream) {
 hipError_t launch_matmul_small(const MatmulArgs& a, hipStream_t stream) {
     if (a.batch <= 0 || a.out_dim <= 0) return hipSuccess;
     const bool q4k = a.w_type == kWeightQ4_K;
-    if (a.batch > 64 || (a.w_type != kWeightQ8_0 && !q4k) || !a.xh || !a.xl || !a.xexp || a.chunks_per_split < 1 ||
-        a.chunks_per_split > matmul_small_range_chunks_max() || a.splits > matmul_small_max_splits(a.batch) ||
-        (a.splits > 1 && (!a.split_out || !a.counters)) || (q4k && (!a.xsum || a.in_dim % 256 != 0)))
+    const bool q6k = a.w_type == kWeightQ6_K;
+    if (a.batch > 64 || (a.w_type != kWeightQ8_0 && !q4k && !q6k) || !a.xh || !a.xl || !a.xexp ||
+        a.chunks_per_split < 1 || a.chunks_per_split > matmul_small_range_chunks_max() ||
+        a.splits > matmul_small_max_splits(a.batch) || (a.splits > 1 && (!a.split_out || !a.counters)) ||
+        (q4k && (!a.xsum || a.in_dim % 256 != 0)) || (q6k && (a.in_dim % 256 != 0 || a.chunks_per_split % 2 != 0)))
         return hipErrorInvalidValue;
     const dim3 pre(a.batch, a.splits);
     if (a.chunks_per_split * 16 <= kMmThreads) {

@@ -896,7 +896,7 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
                          (int)walign);
     int rc = set_device(ctx);
     if (rc) return rc;
-    if ((w_type == GSP_WTYPE_Q8_0 || w_type == GSP_WTYPE_Q4_K) && batch <= 64 &&
+    if ((w_type == GSP_WTYPE_Q8_0 || w_type == GSP_WTYPE_Q4_K || w_type == GSP_WTYPE_Q6_K) && batch <= 64 &&
         (int64_t)batch * out_dim >= kMatmulSmallMinOutputs &&
         (in_dim / 64 + gsp::matmul_small_range_chunks_max() - 1) / gsp::matmul_small_range_chunks_max() <=
             gsp::matmul_small_max_splits(batch)) {
@@ -914,7 +914,8 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
                                     : std::max<int64_t>((chunks + gsp::matmul_small_range_chunks_max() - 1) /
                                                             gsp::matmul_small_range_chunks_max(),
                                                         std::min(want, maxs));
-        const int64_t per = (chunks + splits - 1) / splits;
+        int64_t per = (chunks + splits - 1) / splits;
+        if (w_type == GSP_WTYPE_Q6_K) per += per & 1;  // Q6_K ranges start on a 128-weight half of a super-block
         splits = (chunks + per - 1) / per;
         gsp::MatmulArgs a{};
         a.w = w_dev;

@@ -107,11 +107,13 @@ def test_matmul_q_projection_then_attention_shapes(torch_mod, gsp, ctx):
 
 
 @pytest.mark.parametrize("batch", [100, 60], ids=["b100", "b60"])
-@pytest.mark.parametrize("w_type", [orc.WTYPE_F32, orc.WTYPE_Q8_0, orc.WTYPE_Q4_K], ids=["f32", "q8_0", "q4_k"])
+@pytest.mark.parametrize("w_type", [orc.WTYPE_F32, orc.WTYPE_Q8_0, orc.WTYPE_Q4_K, orc.WTYPE_Q6_K],
+                         ids=["f32", "q8_0", "q4_k", "q6_k"])
 def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, batch):
     """Rows with one channel 1e4 times the rest, rows near 1e30 and rows near 1e-30.  Q8_0 takes an
     fp16 path at both batches (the two-kernel form at 100 rows, the small-batch form at 60, with an
-    exponent per K range of each row); Q4_K the fp32 form at 100 rows and the small-batch form at 60.
+    exponent per K range of each row); Q4_K and Q6_K the fp32 form at 100 rows and the small-batch
+    form at 60.
     There x is a scaled fp16 pair whose error is bounded relative to its row's largest |x| (at most
     ~2^-22 of it per element), so the bar adds that term; every finite row stays finite.  The F32
     form keeps x in fp32 and meets the plain fp32 summation bar.  The Q4_K small form sums the
@@ -126,6 +128,9 @@ def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, bat
         m1 = -orc.q4_k_decode(zq.reshape(-1), out_dim, in_dim)
         assert np.all(m1 >= 0)
         wabs = np.abs(wm) + 2 * m1
+    elif w_type == orc.WTYPE_Q6_K:
+        data, wm = _kquant_weights(rng, w_type, out_dim, in_dim)
+        wabs = np.abs(wm)
     else:
         data, wm = _weights(rng, w_type, out_dim, in_dim)
         wabs = np.abs(wm)
@@ -151,8 +156,8 @@ def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, bat
 # fp16 scales are finite, so the quants, 6-bit scales/mins and high bits are random bytes and only
 # d (and dmin) are set.  The fp32 form decodes each weight to the float32 value the oracle's decoder
 # gives (pinned by closed forms in tests/test_matmul_oracle.py), so the bar is fp32 summation error;
-# the Q4_K small-batch form (at most 64 rows) keeps the quants exact in fp16 and x to ~22 bits as
-# the Q8_0 one does, within the same bar.
+# the Q4_K and Q6_K small-batch forms (at most 64 rows) keep the quants exact in fp16 and x to ~22
+# bits as the Q8_0 one does, within the same bar.
 
 KQ_SHAPES = [
     (256, 16, 1),
@@ -220,13 +225,13 @@ LONG_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("w_type", [orc.WTYPE_Q8_0, orc.WTYPE_Q4_K], ids=["q8_0", "q4_k"])
+@pytest.mark.parametrize("w_type", [orc.WTYPE_Q8_0, orc.WTYPE_Q4_K, orc.WTYPE_Q6_K], ids=["q8_0", "q4_k", "q6_k"])
 @pytest.mark.parametrize("shape", LONG_SHAPES, ids=lambda s: f"in{s[0]}_out{s[1]}_b{s[2]}")
 def test_small_batch_long_ranges_and_wide_outputs_match_oracle(torch_mod, gsp, ctx, shape, w_type):
     in_dim, out_dim, batch = shape
     print(f"case matmul long {shape} type={w_type}", flush=True)
     rng = np.random.default_rng(in_dim * 5 + out_dim + batch + w_type)
-    if w_type == orc.WTYPE_Q4_K:
+    if w_type in (orc.WTYPE_Q4_K, orc.WTYPE_Q6_K):
         data, wm = _kquant_weights(rng, w_type, out_dim, in_dim)
     else:
         data, wm = _weights(rng, w_type, out_dim, in_dim)
