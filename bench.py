@@ -464,9 +464,9 @@ def matmul_timing(gsp, torch, ctx, stream, step, calls: int = 50) -> dict:
     hidden = n_heads * head_dim in and out, one batch row per query token of the step, random
     weights as Q8_0 and as F32.  Each call takes the next of enough weight copies to span 512 MB,
     twice the Infinity Cache, as a model's layers do (`us_per_call`); `us_per_call_warm` repeats one
-    copy.  Q8_0 runs on the fp16 matrix cores (x as scaled fp16 pairs), and so do Q4_K and Q6_K at
-    most 64 batch rows; F32, and the K-quants above 64 rows, on the fp32 ones (the K-quants are timed
-    when hidden is a multiple of 256); the bytes bound is the weights at 8 TB/s."""
+    copy.  Q8_0, Q4_K and Q6_K run on the fp16 matrix cores (x as scaled fp16 pairs), F32 on the fp32
+    ones (the K-quants are timed when hidden is a multiple of 256); the bytes bound is the weights at
+    8 TB/s."""
     hidden = step.n_heads * step.head_dim
     batch = int(step.total_q)
     gen = torch.Generator(device="cuda").manual_seed(step.seed)

@@ -6,13 +6,14 @@
 // Q8_0 (blocks of 32 int8 with an fp16 scale d: w = d * q), or the K-quant
 // super-blocks Q4_K and Q6_K (256 weights each, decoded further down).
 //
-// Two forms.  The fp32 form (matmul_batch_kernel, every F32 product and small
-// Q8_0 ones): every weight is exact in fp32 (Q8_0's d * q has at most 19
-// significant bits), and the products run on v_mfma_f32_16x16x4f32 with fp32
-// accumulation, so no operand is rounded below fp32.  The fp16 form
-// (matmul_q8_f16_kernel, large Q8_0 products, described further down) runs
-// one Q8_0 block per fp16 matrix step with x as a scaled fp16 pair; its
-// small-batch variants (at most 64 batch rows) take Q8_0, Q4_K and Q6_K weights.
+// Two forms.  The fp32 form (matmul_batch_kernel, every F32 product and the
+// quantized ones too small for the fp16 forms): every weight is exact in fp32
+// (Q8_0's d * q has at most 19 significant bits), and the products run on
+// v_mfma_f32_16x16x4f32 with fp32 accumulation, so no operand is rounded below
+// fp32.  The fp16 forms
+// (matmul_f16_kernel and the small-batch variants for at most 64 batch rows,
+// described further down) run Q8_0, Q4_K and Q6_K blocks on fp16 matrix steps
+// with the quants exact in fp16 and x as a scaled fp16 pair.
 //
 // fp32 form:
 // A workgroup (four waves) owns 64 weight rows (16 per wave, MFMA M) and 64
@@ -26,6 +27,7 @@
 // second kernel adds the partials in order, so results do not depend on
 // timing.
 #include <cfloat>
+#include <type_traits>
 
 #include "gsp_epilogue.h"
 #include "gsp_internal.h"
@@ -319,7 +321,10 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_batch_kernel(MatmulArgs 
 
 // x of one batch row as scaled fp16 pairs: one workgroup per row, four
 // elements per access (in_dim is a multiple of 64, rows 16-byte aligned).
+// With kSums (Q4_K weights) it also writes each 32-wide block's sum of the
+// scaled x, xsum[b * (in_dim / 32) + block], for the weights' min term.
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+template <bool kSums>
 __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a) {
     __shared__ float red[kMmThreads / 64];
     const int b = blockIdx.x;
@@ -372,6 +377,14 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
         const h4v lh = __builtin_convertvector(l, h4v);
         xh[i] = h;
         xl[i] = lh;
+        if constexpr (kSums) {
+            // Eight consecutive threads hold a block's 32 values (n4 is a multiple
+            // of 16, so a group is active or inactive as a whole): a tree over it.
+            float sm = (v[0] + v[1]) + (v[2] + v[3]);
+#pragma unroll
+            for (int off = 1; off < 8; off <<= 1) sm += __shfl_xor(sm, off);
+            if ((i & 7) == 0) a.xsum[(int64_t)b * (a.in_dim / 32) + (i >> 3)] = sm;
+        }
     };
     if (held) {
 #pragma unroll
@@ -482,6 +495,32 @@ __device__ __forceinline__ h8 q8_to_h8(uint32_t d0, uint32_t d1) {
     return r;
 }
 
+// Four nibbles per dword (one per byte, 0..15) as fp16: the half 0x6400 | q is
+// 1024 + q, so subtracting 1024 leaves q exactly.
+__device__ __forceinline__ h8 nib_to_h8(uint32_t d0, uint32_t d1) {
+    h8 r;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t u = k ? d1 : d0;
+        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0, 64, u1, 64
+        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2, 64, u3, 64
+        const h2 a0 = __builtin_bit_cast(h2, p0) - h2{(_Float16)1024.0f, (_Float16)1024.0f};
+        const h2 a1 = __builtin_bit_cast(h2, p1) - h2{(_Float16)1024.0f, (_Float16)1024.0f};
+        r[4 * k + 0] = a0[0];
+        r[4 * k + 1] = a0[1];
+        r[4 * k + 2] = a1[0];
+        r[4 * k + 3] = a1[1];
+    }
+    return r;
+}
+
+// Four six-bit values (one per byte, 0..63) as fp16 minus 32: the half
+// 0x6400 | u is 1024 + u, so subtracting 1056 leaves u - 32 exactly.
+__device__ __forceinline__ void six_to_h4(uint32_t u, h2& lo, h2& hi) {
+    lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - h2{(_Float16)1056.0f, (_Float16)1056.0f};
+    hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - h2{(_Float16)1056.0f, (_Float16)1056.0f};
+}
+
 // The lane's raw words of one 64-wide chunk of its weight row (68 bytes at a
 // multiple of 4): block 0's eight values at bytes 2 + 8 g (dwords 2g .. 2g + 2,
 // shifted by 2), block 1's at 36 + 8 g (dwords 9 + 2g, 10 + 2g), and the two
@@ -504,7 +543,70 @@ __device__ __forceinline__ void load_q8_raw(Q8Raw& r, const MatmulArgs& a, int o
     r.s8 = cw[8];
 }
 
-__global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs a) {
+// Q4_K: the lane's words of chunk c of its weight row: the super-block head
+// (d | dmin << 16 and the three scale words) and the two quant dwords at bytes
+// 32 p + 8 g of the chunk's quarter p, whose low nibbles are block 0's values
+// 8 g .. 8 g + 7 (sub-block 2 p) and high nibbles block 1's (sub-block 2 p + 1).
+struct Q4KRaw {
+    uint32_t hdr;
+    uint32_t sc[3];
+    uint32_t q[2];
+};
+
+__device__ __forceinline__ void load_q4k_raw(Q4KRaw& r, const MatmulArgs& a, int o, int c, int g) {
+    const int64_t row_bytes = (int64_t)(a.in_dim / 256) * 144;
+    const uint32_t* bw = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)o * row_bytes +
+                                                           (int64_t)(c >> 2) * 144);
+    r.hdr = bw[0];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) r.sc[i] = bw[1 + i];
+    r.q[0] = bw[4 + 8 * (c & 3) + 2 * g];
+    r.q[1] = bw[5 + 8 * (c & 3) + 2 * g];
+}
+
+// Q6_K: the lane's words of chunk c of its weight row (quarters 2 e and 2 e + 1
+// of half hn of the super-block, e = c % 2, hn = c % 4 / 2): the low-bit bytes
+// 64 hn + 8 g .. and 64 hn + 32 + 8 g .. (nibble e), the high-bit bytes
+// 32 hn + 8 g .. (bits 4 e .. 4 e + 3), the four scales 8 hn + 4 e .. and d.
+// Super-blocks are 210 bytes, so these are raw buffer loads at 2-byte aligned
+// offsets (gfx950 runs with unaligned buffer access), inside the super-block.
+struct Q6KRaw {
+    uint32_t l0[2], l1[2], h[2];
+    uint32_t sc;
+    uint16_t d;
+};
+
+__device__ __forceinline__ void load_q6k_raw(Q6KRaw& r, __amdgpu_buffer_rsrc_t wr, int row_off, int c, int g) {
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    const int hn = (c >> 1) & 1;
+    const int off = row_off + (c >> 2) * 210;
+    const u2 l0 = __builtin_amdgcn_raw_buffer_load_b64(wr, off + 64 * hn + 8 * g, 0, 0);
+    const u2 l1 = __builtin_amdgcn_raw_buffer_load_b64(wr, off + 64 * hn + 32 + 8 * g, 0, 0);
+    const u2 h = __builtin_amdgcn_raw_buffer_load_b64(wr, off + 128 + 32 * hn + 8 * g, 0, 0);
+    r.l0[0] = l0[0];
+    r.l0[1] = l0[1];
+    r.l1[0] = l1[0];
+    r.l1[1] = l1[1];
+    r.h[0] = h[0];
+    r.h[1] = h[1];
+    r.sc = __builtin_amdgcn_raw_buffer_load_b32(wr, off + 192 + 8 * hn + 4 * (c & 1), 0, 0);
+    r.d = __builtin_amdgcn_raw_buffer_load_b16(wr, off + 208, 0, 0);
+}
+
+// matmul_f16_kernel<WT>: Q8_0, Q4_K or Q6_K weights.  For Q4_K a block's values are
+// its quants q (exact in fp16) and its scale d1 = d * sc, and the min term
+// m1 * sum_k x_k of each block comes from the pre-pass's block sums: per chunk
+// and M tile one v_mfma_f32_16x16x4f32 of the sums (A: batch rows x the
+// chunk's two blocks, zero in lane groups 2-3) against the lane's m1 values
+// (B), into a second accumulator subtracted before the scaling.  For Q6_K a
+// block's values are q - 32 (exact in fp16) with a scale d * sc per 16: the
+// block runs as two masked pairs of matrix steps (B zero outside lane groups
+// 0-1 or 2-3), each half's sum scaled by its own d * sc.
+template <int WT>
+__global__ __launch_bounds__(kMmThreads, 2) void matmul_f16_kernel(MatmulArgs a) {
+    static_assert(WT == kWeightQ8_0 || WT == kWeightQ4_K || WT == kWeightQ6_K, "Q8_0, Q4_K or Q6_K weights");
+    constexpr bool kQ4K = WT == kWeightQ4_K;
+    constexpr bool kQ6K = WT == kWeightQ6_K;
     // The chunk of x as fp16 pairs: [buffer][hi, lo][64 batch rows][64 halves + 8 padding].
     __shared__ _Float16 xs[2][2][64][72];
 
@@ -528,13 +630,31 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
     const u4* xh_src = reinterpret_cast<const u4*>(static_cast<const _Float16*>(a.xh) + xoff);
     const u4* xl_src = reinterpret_cast<const u4*>(static_cast<const _Float16*>(a.xl) + xoff);
     u4 xreg[4];
-    Q8Raw wraw;
+    std::conditional_t<kQ4K, Q4KRaw, std::conditional_t<kQ6K, Q6KRaw, Q8Raw>> wraw;
+    // Q6_K: the workgroup's weight rows through one descriptor (the lane's row
+    // is clamped to out_dim - 1, as for the other types, so it stays inside).
+    const int q6_row_bytes = (a.in_dim / 256) * 210;
+    const __amdgpu_buffer_rsrc_t q6w = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(static_cast<const uint8_t*>(a.w) + (int64_t)blockIdx.x * kMmRowsWg * q6_row_bytes),
+        (short)0, min(kMmRowsWg, a.out_dim - (int)blockIdx.x * kMmRowsWg) * q6_row_bytes, 0x00020000);
+    float xsr[4];  // Q4_K: block sums of the lane's A operands for the min term
     auto load_chunk = [&](int c) {
         xreg[0] = xh_src[8 * c];
         xreg[1] = xh_src[8 * c + 1];
         xreg[2] = xl_src[8 * c];
         xreg[3] = xl_src[8 * c + 1];
-        load_q8_raw(wraw, a, o, c, g);
+        if constexpr (kQ4K) {
+            load_q4k_raw(wraw, a, o, c, g);
+            // Lane (n, g < 2): batch row b0 + 16 t + n, block 2 c + g.
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                xsr[t] = g < 2 && t < nt ? a.xsum[(int64_t)min(b0 + 16 * t + n, a.batch - 1) * (a.in_dim / 32) + 2 * c + g]
+                                         : 0.f;
+        } else if constexpr (kQ6K) {
+            load_q6k_raw(wraw, q6w, (o - (int)blockIdx.x * kMmRowsWg) * q6_row_bytes, c, g);
+        } else {
+            load_q8_raw(wraw, a, o, c, g);
+        }
     };
     auto store_x = [&](int buf) {
         *reinterpret_cast<u4*>(&xs[buf][0][xr][16 * xq]) = xreg[0];
@@ -543,9 +663,9 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
         *reinterpret_cast<u4*>(&xs[buf][1][xr][16 * xq + 8]) = xreg[3];
     };
 
-    f4 acc[4];
+    f4 acc[4], accm[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < 4; ++t) acc[t] = accm[t] = f4{0.f, 0.f, 0.f, 0.f};
     if (c_begin < c_end) {
         load_chunk(c_begin);
         store_x(0);
@@ -554,11 +674,53 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
     for (int c = c_begin; c < c_end; ++c) {
         const int buf = (c - c_begin) & 1;
         // This chunk's two blocks of the lane's row: values and scales.
-        const h8 wq0 = q8_to_h8(__builtin_amdgcn_alignbyte(wraw.b0[1], wraw.b0[0], 2),
-                                __builtin_amdgcn_alignbyte(wraw.b0[2], wraw.b0[1], 2));
-        const h8 wq1 = q8_to_h8(wraw.b1[0], wraw.b1[1]);
-        const float d0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(wraw.s0 & 0xFFFFu));
-        const float d1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(wraw.s8 >> 16));
+        h8 wq0, wq1;
+        float d0, d1, mb = 0.f, xsc[4];
+        float e0 = 0.f, e1 = 0.f;  // Q6_K: the blocks' scales for k >= 16 (d0, d1 for k < 16)
+        if constexpr (kQ6K) {
+            const int e = c & 1;
+            const float d = (float)__builtin_bit_cast(_Float16, wraw.d);
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) {
+                const uint32_t u0 = ((wraw.l0[t2] >> (4 * e)) & 0x0F0F0F0Fu) | (((wraw.h[t2] >> (4 * e)) & 0x03030303u) << 4);
+                const uint32_t u1 =
+                    ((wraw.l1[t2] >> (4 * e)) & 0x0F0F0F0Fu) | (((wraw.h[t2] >> (4 * e + 2)) & 0x03030303u) << 4);
+                h2 lo, hi;
+                six_to_h4(u0, lo, hi);
+                wq0[4 * t2 + 0] = lo[0];
+                wq0[4 * t2 + 1] = lo[1];
+                wq0[4 * t2 + 2] = hi[0];
+                wq0[4 * t2 + 3] = hi[1];
+                six_to_h4(u1, lo, hi);
+                wq1[4 * t2 + 0] = lo[0];
+                wq1[4 * t2 + 1] = lo[1];
+                wq1[4 * t2 + 2] = hi[0];
+                wq1[4 * t2 + 3] = hi[1];
+            }
+            d0 = d * (float)(int8_t)(wraw.sc & 0xFFu);  // exact
+            e0 = d * (float)(int8_t)((wraw.sc >> 8) & 0xFFu);
+            d1 = d * (float)(int8_t)((wraw.sc >> 16) & 0xFFu);
+            e1 = d * (float)(int8_t)(wraw.sc >> 24);
+        } else if constexpr (kQ4K) {
+            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(wraw.hdr & 0xFFFFu));
+            const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(wraw.hdr >> 16));
+            uint32_t sc0, m0, sc1, m1;
+            q4k_scale_min(wraw.sc, 2 * (c & 3), sc0, m0);
+            q4k_scale_min(wraw.sc, 2 * (c & 3) + 1, sc1, m1);
+            d0 = d * (float)sc0;  // exact
+            d1 = d * (float)sc1;
+            mb = g == 0 ? dmin * (float)m0 : g == 1 ? dmin * (float)m1 : 0.f;  // B of the min term
+            wq0 = nib_to_h8(wraw.q[0] & 0x0F0F0F0Fu, wraw.q[1] & 0x0F0F0F0Fu);
+            wq1 = nib_to_h8((wraw.q[0] >> 4) & 0x0F0F0F0Fu, (wraw.q[1] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xsc[t] = xsr[t];
+        } else {
+            wq0 = q8_to_h8(__builtin_amdgcn_alignbyte(wraw.b0[1], wraw.b0[0], 2),
+                           __builtin_amdgcn_alignbyte(wraw.b0[2], wraw.b0[1], 2));
+            wq1 = q8_to_h8(wraw.b1[0], wraw.b1[1]);
+            d0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(wraw.s0 & 0xFFFFu));
+            d1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(wraw.s8 >> 16));
+        }
         const bool more = c + 1 < c_end;
         if (more) load_chunk(c + 1);  // the next chunk loads while this one computes
 #pragma unroll
@@ -570,12 +732,25 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
                     const h8 ah = *reinterpret_cast<const h8*>(&xs[buf][0][row][32 * blk + 8 * g]);
                     const h8 al = *reinterpret_cast<const h8*>(&xs[buf][1][row][32 * blk + 8 * g]);
                     const h8 wq = blk ? wq1 : wq0;
-                    f4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, wq, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    part = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, wq, part, 0, 0, 0);
                     const float d = blk ? d1 : d0;
+                    if constexpr (kQ6K) {
+                        const h8 wa = g < 2 ? wq : h8{};  // k < 16 of the block
+                        const h8 wb = g < 2 ? h8{} : wq;
+                        f4 pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, wa, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, wa, pa, 0, 0, 0);
+                        f4 pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, wb, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, wb, pb, 0, 0, 0);
+                        const float de = blk ? e1 : e0;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(d, part[r], acc[t][r]);
+                        for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(de, pb[r], fmaf(d, pa[r], acc[t][r]));
+                    } else {
+                        f4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, wq, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        part = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, wq, part, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(d, part[r], acc[t][r]);
+                    }
                 }
+                if constexpr (kQ4K) accm[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xsc[t], mb, accm[t], 0, 0, 0);
             }
         }
         if (more) store_x(buf ^ 1);  // the other buffer's last readers passed the previous barrier
@@ -591,7 +766,7 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_kernel(MatmulArgs
         for (int r = 0; r < 4; ++r) {
             const int b = b0 + 16 * t + 4 * g + r;
             if (t >= nt || b >= a.batch) continue;
-            const float v = ldexpf(acc[t][r], a.xexp[b]);
+            const float v = ldexpf(kQ4K ? acc[t][r] - accm[t][r] : acc[t][r], a.xexp[b]);
             float* dst = a.split_out ? a.split_out + ((int64_t)blockIdx.z * a.batch + b) * a.out_dim
                                      : a.y + (int64_t)b * a.out_dim;
             dst[oo] = v;
@@ -824,25 +999,6 @@ __global__ __launch_bounds__(kMmThreads, 2) void matmul_q8_f16_small_kernel(Matm
     small_finish<NT>(a, acc, mt, nt0, n, g, tid, last);
 }
 
-// Four nibbles per dword (one per byte, 0..15) as fp16: the half 0x6400 | q is
-// 1024 + q, so subtracting 1024 leaves q exactly.
-__device__ __forceinline__ h8 nib_to_h8(uint32_t d0, uint32_t d1) {
-    h8 r;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const uint32_t u = k ? d1 : d0;
-        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes u0, 64, u1, 64
-        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes u2, 64, u3, 64
-        const h2 a0 = __builtin_bit_cast(h2, p0) - h2{(_Float16)1024.0f, (_Float16)1024.0f};
-        const h2 a1 = __builtin_bit_cast(h2, p1) - h2{(_Float16)1024.0f, (_Float16)1024.0f};
-        r[4 * k + 0] = a0[0];
-        r[4 * k + 1] = a0[1];
-        r[4 * k + 2] = a1[0];
-        r[4 * k + 3] = a1[1];
-    }
-    return r;
-}
-
 // ---- Q4_K weights, batches of up to 64 rows ---------------------------------
 //
 // matmul_q4k_f16_small_kernel<NT, kPasses> is the Q8_0 small form with Q4_K weights.
@@ -1023,13 +1179,6 @@ __device__ __forceinline__ void small_products_q6k(f4 (&acc)[NT], const h8 (&ax)
             }
         }
     }
-}
-
-// Four six-bit values (one per byte, 0..63) as fp16 minus 32: the half
-// 0x6400 | u is 1024 + u, so subtracting 1056 leaves u - 32 exactly.
-__device__ __forceinline__ void six_to_h4(uint32_t u, h2& lo, h2& hi) {
-    lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - h2{(_Float16)1056.0f, (_Float16)1056.0f};
-    hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - h2{(_Float16)1056.0f, (_Float16)1056.0f};
 }
 
 template <int NT, bool kPasses>
@@ -1223,8 +1372,14 @@ hipError_t launch_matmul(const MatmulArgs& a, hipStream_t stream) {
     if (a.w_type == kWeightF32)
         hipLaunchKernelGGL(matmul_batch_kernel<kWeightF32>, grid, dim3(kMmThreads), 0, stream, a);
     else if (a.w_type == kWeightQ8_0 && a.xh) {
-        hipLaunchKernelGGL(matmul_split_x_kernel, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
-        hipLaunchKernelGGL(matmul_q8_f16_kernel, grid, dim3(kMmThreads), 0, stream, a);
+        hipLaunchKernelGGL(matmul_split_x_kernel<false>, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
+        hipLaunchKernelGGL(matmul_f16_kernel<kWeightQ8_0>, grid, dim3(kMmThreads), 0, stream, a);
+    } else if (a.w_type == kWeightQ4_K && a.xh && a.xsum && a.in_dim % 256 == 0) {
+        hipLaunchKernelGGL(matmul_split_x_kernel<true>, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
+        hipLaunchKernelGGL(matmul_f16_kernel<kWeightQ4_K>, grid, dim3(kMmThreads), 0, stream, a);
+    } else if (a.w_type == kWeightQ6_K && a.xh && a.in_dim % 256 == 0) {
+        hipLaunchKernelGGL(matmul_split_x_kernel<false>, dim3(a.batch), dim3(kMmThreads), 0, stream, a);
+        hipLaunchKernelGGL(matmul_f16_kernel<kWeightQ6_K>, grid, dim3(kMmThreads), 0, stream, a);
     } else if (a.w_type == kWeightQ8_0)
         hipLaunchKernelGGL(matmul_batch_kernel<kWeightQ8_0>, grid, dim3(kMmThreads), 0, stream, a);
     else if (a.w_type == kWeightQ4_K && a.in_dim % 256 == 0)

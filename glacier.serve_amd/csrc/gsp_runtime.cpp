@@ -860,8 +860,9 @@ int gsp_rope_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_h
     return gsp_rope_write_step_ex(ctx, pool, layer, n_heads, &spec, q_dev, k_dev, v_dev);
 }
 
-// Q8_0 products with at least this many outputs (batch x out_dim) take the fp16
-// path: measured faster from Qwen2.5-7B's 3584 x 3584 projection at 64 rows
+// Q8_0 and K-quant products with at least this many outputs (batch x out_dim)
+// take the fp16 path (unless the small-batch form takes them): for Q8_0
+// measured faster from Qwen2.5-7B's 3584 x 3584 projection at 64 rows
 // (229376 outputs: 27.8 vs 31.2 us) upwards, slower for 8192 x 8192 at 16 rows
 // (131072 outputs: 57.5 vs 51 us) and 3584 x 512 at 64 rows (21.5 vs 16.2 us).
 constexpr int64_t kMatmulF16MinOutputs = 196608;
@@ -966,16 +967,21 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
     a.xh = nullptr;
     a.xl = nullptr;
     a.xexp = nullptr;
-    if (w_type == GSP_WTYPE_Q8_0 && (int64_t)batch * out_dim >= kMatmulF16MinOutputs) {
-        // Large Q8_0 products run on the fp16 matrix cores with x as scaled fp16
-        // pairs; below the threshold the pre-pass launch costs more than it saves.
+    if ((w_type == GSP_WTYPE_Q8_0 || w_type == GSP_WTYPE_Q4_K || w_type == GSP_WTYPE_Q6_K) &&
+        (int64_t)batch * out_dim >= kMatmulF16MinOutputs) {
+        // Large Q8_0 and K-quant products run on the fp16 matrix cores with x as
+        // scaled fp16 pairs (Q4_K also with x's block sums for its min term);
+        // below the threshold the pre-pass launch costs more than it saves.
         const size_t halves = (size_t)batch * in_dim;
         rc = ensure_device(ctx, &ctx->d_mmx, &ctx->d_mmx_halves, 2 * halves, false);
         if (!rc) rc = ensure_device(ctx, &ctx->d_mmexp, &ctx->d_mmexp_words, (size_t)batch, false);
+        if (!rc && w_type == GSP_WTYPE_Q4_K)
+            rc = ensure_device(ctx, &ctx->d_mmxs, &ctx->d_mmxs_floats, (size_t)batch * (in_dim / 32), false);
         if (rc) return rc;
         a.xh = ctx->d_mmx;
         a.xl = ctx->d_mmx + halves;
         a.xexp = ctx->d_mmexp;
+        a.xsum = w_type == GSP_WTYPE_Q4_K ? ctx->d_mmxs : nullptr;
     }
     if (splits > 1) {
         rc = ensure_device(ctx, &ctx->d_mm, &ctx->d_mm_floats, (size_t)splits * batch * out_dim, false);

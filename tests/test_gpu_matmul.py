@@ -112,8 +112,8 @@ def test_matmul_q_projection_then_attention_shapes(torch_mod, gsp, ctx):
 def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, batch):
     """Rows with one channel 1e4 times the rest, rows near 1e30 and rows near 1e-30.  Q8_0 takes an
     fp16 path at both batches (the two-kernel form at 100 rows, the small-batch form at 60, with an
-    exponent per K range of each row); Q4_K and Q6_K the fp32 form at 100 rows and the small-batch
-    form at 60.
+    exponent per K range of each row); Q4_K the two-kernel fp16 form at 100 rows and the small-batch
+    form at 60; Q6_K the fp32 form at 100 rows and the small-batch form at 60.
     There x is a scaled fp16 pair whose error is bounded relative to its row's largest |x| (at most
     ~2^-22 of it per element), so the bar adds that term; every finite row stays finite.  The F32
     form keeps x in fp32 and meets the plain fp32 summation bar.  The Q4_K small form sums the
@@ -156,8 +156,8 @@ def test_matmul_outlier_channels_and_large_rows(torch_mod, gsp, ctx, w_type, bat
 # fp16 scales are finite, so the quants, 6-bit scales/mins and high bits are random bytes and only
 # d (and dmin) are set.  The fp32 form decodes each weight to the float32 value the oracle's decoder
 # gives (pinned by closed forms in tests/test_matmul_oracle.py), so the bar is fp32 summation error;
-# the Q4_K and Q6_K small-batch forms (at most 64 rows) keep the quants exact in fp16 and x to ~22
-# bits as the Q8_0 one does, within the same bar.
+# the fp16 forms (Q4_K and Q6_K at most 64 rows, Q4_K above with enough outputs) keep the quants
+# exact in fp16 and x to ~22 bits as the Q8_0 ones do, within the same bar.
 
 KQ_SHAPES = [
     (256, 16, 1),
@@ -174,6 +174,12 @@ KQ_SHAPES = [
     (768, 8192, 9),
     (2048, 2100, 40),
     (8192, 4160, 16),
+    # more than 64 rows and at least 196608 outputs: Q4_K takes the large fp16 form (x as scaled
+    # fp16 pairs per row, block sums for the min term): two batch tiles with a ragged second one,
+    # one row in the second tile with a ragged weight-row tile, and four full batch tiles
+    (2048, 2048, 100),
+    (512, 4100, 65),
+    (3584, 3584, 256),
 ]
 
 
