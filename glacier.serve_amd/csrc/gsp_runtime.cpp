@@ -915,6 +915,15 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
                                     : std::max<int64_t>((chunks + gsp::matmul_small_range_chunks_max() - 1) /
                                                             gsp::matmul_small_range_chunks_max(),
                                                         std::min(want, maxs));
+        // Outputs that fill the CU slots (two per CU) at least twice over (an
+        // LM head) need no K split: one range per tile, walked in passes, with
+        // no partials and no merge.  Measured faster from 1024 tiles up (on 256
+        // CUs: 3584 x 65536 at 64 rows 150 -> 118 us for Q8_0, 160 -> 125 us
+        // for Q4_K; Llama-3's 4096 x 128256 head at 8 rows 208 -> 185 us for
+        // Q8_0); from 512 tiles up it lost where a second round of workgroups
+        // stays nearly empty (4096 x 40960 at 32 rows 83 -> 97 us for Q8_0).
+        if (tiles >= 4 * (int64_t)std::max(1, ctx->num_cus) && chunks <= gsp::matmul_small_range_chunks_max())
+            splits = 1;
         int64_t per = (chunks + splits - 1) / splits;
         if (w_type == GSP_WTYPE_Q6_K) per += per & 1;  // Q6_K ranges start on a 128-weight half of a super-block
         splits = (chunks + per - 1) / per;

@@ -218,8 +218,9 @@ def test_kquant_matmul_matches_oracle(torch_mod, gsp, ctx, shape, w_type):
 # Long K and wide outputs on the small-batch form.  When the merge holds too few K ranges for
 # ranges of 8 chunks (more than 8 ranges at 33..64 rows, 16 at 17..32, 32 at up to 16), each
 # workgroup walks its range in passes of 8 chunks through the same LDS, and the pre-pass takes up to
-# four f4 per thread.  Wide outputs run several rounds of workgroups.  The splits below are the
-# library's for a 256-CU device; other CU counts give other splits of the same shapes.
+# four f4 per thread.  Wide outputs run several rounds of workgroups, and from 1024 weight-row tiles
+# on 256 CUs with no K split.  The splits below are the library's for a 256-CU device; other CU
+# counts give other splits of the same shapes.
 LONG_SHAPES = [
     (5120, 1040, 64),   # 8 ranges of 10 chunks: a full pass, then a 2-chunk one; one f4 per pre-pass thread
     (18944, 1040, 64),  # Qwen2.5-7B's FFN down-projection width: 8 ranges of 37 chunks, 5 passes
@@ -228,6 +229,7 @@ LONG_SHAPES = [
     (3584, 18944, 64),  # Qwen2.5-7B's gate/up projection: 7 ranges of 296 tiles
     (4096, 16384, 24),  # two M tiles: 8 ranges of 256 tiles
     (512, 65536, 1),    # one range of 1024 tiles, y stored directly
+    (1024, 65536, 2),   # 1024 tiles fill the CU slots twice: one range per tile in two passes, no merge
 ]
 
 
