@@ -381,8 +381,9 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
             // Eight consecutive threads hold a block's 32 values (n4 is a multiple
             // of 16, so a group is active or inactive as a whole): a tree over it.
             float sm = (v[0] + v[1]) + (v[2] + v[3]);
-#pragma unroll
-            for (int off = 1; off < 8; off <<= 1) sm += __shfl_xor(sm, off);
+            sm += __shfl_xor(sm, 1);
+            sm += __shfl_xor(sm, 2);
+            sm += __shfl_xor(sm, 4);
             if ((i & 7) == 0) a.xsum[(int64_t)b * (a.in_dim / 32) + (i >> 3)] = sm;
         }
     };
@@ -392,6 +393,9 @@ __global__ __launch_bounds__(kMmThreads) void matmul_split_x_kernel(MatmulArgs a
             const int i = threadIdx.x + kMmThreads * j;
             if (i < n4) put(i, hv[j]);
         }
+    } else if constexpr (kSums) {
+        // The block sums' lane exchanges keep this loop rolled.
+        for (int i = threadIdx.x; i < n4; i += kMmThreads) put(i, xr[i]);
     } else {
 #pragma unroll 4
         for (int i = threadIdx.x; i < n4; i += kMmThreads) put(i, xr[i]);

@@ -180,6 +180,7 @@ KQ_SHAPES = [
     (2048, 2048, 100),
     (512, 4100, 65),
     (3584, 3584, 256),
+    (18944, 1024, 200),  # rows longer than the pre-pass keeps in registers (Qwen2.5-7B's down projection)
 ]
 
 
