@@ -249,12 +249,15 @@ int gsp_rope_write_step_ex(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t 
  * bits, 64 of high 2 bits, 16 int8 scales, fp16 d, w = d*sc*(q - 32);
  * 2-byte aligned).  x_dev is [batch][in_dim] fp32 (16-byte aligned), y_dev
  * [batch][out_dim] fp32, overwritten; all device pointers.  Every weight is
- * decoded to the float32 value its format defines and sums are fp32.  Small
- * products keep x in fp32, and so do all F32 and K-quant products.  Large
- * Q8_0 products take x as a scaled fp16 pair on the fp16 matrix cores: each
- * element then carries an absolute error of at most ~2^-22 of its row's
- * largest |x| (~22 significant bits for elements near the row max, fewer for
- * much smaller ones; every finite x stays finite).  in_dim must be a multiple
+ * decoded exactly (to the float32 value its format defines, or to its exact
+ * fp16 quant and fp32 scale) and sums are fp32.  Q8_0, Q4_K and Q6_K
+ * products with at least 65536 outputs (batch x out_dim) at up to 64 batch
+ * rows, or at least 196608 outputs, take x as a scaled fp16 pair on the fp16
+ * matrix cores (other products keep x in fp32, as F32 ones always do): each
+ * element then carries an absolute error of at most
+ * ~2^-22 of its row's largest |x| (~22 significant bits for elements near
+ * the row max, fewer for much smaller ones; every finite x stays finite).
+ * Results are the same bit for bit on every call.  in_dim must be a multiple
  * of 64 (256 for the K-quants; GSP_E_UNSUPPORTED otherwise, as for other
  * weight types); the reference's block sums are not needed by these types. */
 int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const float* x_dev, float* y_dev,
