@@ -866,13 +866,17 @@ int gsp_rope_write_step(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t n_h
 // (229376 outputs: 27.8 vs 31.2 us) upwards, slower for 8192 x 8192 at 16 rows
 // (131072 outputs: 57.5 vs 51 us) and 3584 x 512 at 64 rows (21.5 vs 16.2 us).
 constexpr int64_t kMatmulF16MinOutputs = 196608;
-// Q8_0 and Q4_K products of at most 64 batch rows with at least this many
+// Q8_0 and K-quant products of at most 64 batch rows with at least this many
 // outputs take the small-batch fp16 form: for Q8_0 measured faster than the
 // other two forms from 8192 x 8192 at 16 rows (131072 outputs: 40.6 vs 43.7 us)
 // and Qwen2.5-7B's 3584 x 3584 at 64 rows (22.1 vs 24.3 us), slower for
 // 896 x 896 at 8 rows (7168 outputs: 15.8 vs 6.9 us), whose product is too
-// small to fill the chip.
-constexpr int64_t kMatmulSmallMinOutputs = 65536;
+// small to fill the chip.  Between 16384 and 65536 outputs it was faster
+// than the fp32 form on most shapes measured (4096 x 1024 at 32 rows: Q8_0
+// 18.3 -> 14.8 us, Q6_K 19.6 -> 15.5 us; 8192 x 1024 at 16 rows: Q6_K 23.4
+// -> 18.2 us) and at most 0.5 us slower on the others (3584 x 512 at 64 rows:
+// Q4_K 17.0 -> 17.25 us, Q6_K 18.6 -> 19.1 us, while Q8_0 gains 16.8 -> 15.8).
+constexpr int64_t kMatmulSmallMinOutputs = 16384;
 
 int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const float* x_dev, float* y_dev,
                      int32_t in_dim, int32_t out_dim, int32_t batch) {

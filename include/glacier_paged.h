@@ -251,7 +251,7 @@ int gsp_rope_write_step_ex(gsp_ctx* ctx, gsp_pool* pool, int32_t layer, int32_t 
  * [batch][out_dim] fp32, overwritten; all device pointers.  Every weight is
  * decoded exactly (to the float32 value its format defines, or to its exact
  * fp16 quant and fp32 scale) and sums are fp32.  Q8_0, Q4_K and Q6_K
- * products with at least 65536 outputs (batch x out_dim) at up to 64 batch
+ * products with at least 16384 outputs (batch x out_dim) at up to 64 batch
  * rows, or at least 196608 outputs, take x as a scaled fp16 pair on the fp16
  * matrix cores (other products keep x in fp32, as F32 ones always do): each
  * element then carries an absolute error of at most

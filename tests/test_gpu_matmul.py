@@ -28,7 +28,7 @@ SHAPES = [
     (256, 2048, 100),
     (512, 1600, 128),
     (128, 2049, 97),
-    # batch <= 64 and batch x out_dim >= 65536: Q8_0 takes the small-batch fp16 kernel
+    # batch <= 64 and batch x out_dim >= 16384: Q8_0 takes the small-batch fp16 kernel
     # (one, two and four M tiles, ragged batch tiles and weight-row tiles, 1 to 16 K ranges)
     (3584, 1040, 64),
     (1024, 4100, 17),
@@ -168,7 +168,7 @@ KQ_SHAPES = [
     (512, 37, 3),
     (1024, 4100, 17),
     (3584, 3584, 64),  # the Q projection of a Qwen2.5-7B layer for 64 decode rows
-    # Q4_K's small-batch form (batch <= 64, batch x out_dim >= 65536): one M tile with K ranges of
+    # the K-quants' small-batch forms (batch <= 64, batch x out_dim >= 16384): one M tile with K ranges of
     # three chunks that start inside a super-block, four M tiles with a ragged batch and a ragged
     # last weight-row tile, one M tile over sixteen K ranges
     (768, 8192, 9),
