@@ -1,4 +1,4 @@
-"""A packed step captured into a HIP graph and replayed.
+"""A packed step, and the projection GEMM's fp16 forms, captured into a HIP graph and replayed.
 
 gsp_attention_step only launches kernels (and, for a step with both decode
 units and prefill tiles, forks the tiles onto a second stream and joins them
@@ -206,3 +206,72 @@ def test_capture_of_a_step_larger_than_any_earlier(torch_mod, gsp):
         fresh.set_stream(None)
         pool.destroy()
         fresh.close()
+
+
+def _raw_weights(rng, w_type, out_dim, in_dim):
+    """Random weight bytes of one GGUF type, valid encodings: random quants and scales with small
+    finite fp16 super-block (or block) scales."""
+    if w_type == 8:  # Q8_0: fp16 d, then 32 int8
+        b = rng.integers(0, 256, (out_dim, in_dim // 32, 34), dtype=np.uint8)
+        b[..., 0:2] = (rng.uniform(1e-3, 2e-2, (out_dim, in_dim // 32, 1))).astype(np.float16).view(np.uint8)
+    elif w_type == 12:  # Q4_K: fp16 d, fp16 dmin, scales, quants
+        b = rng.integers(0, 256, (out_dim, in_dim // 256, 144), dtype=np.uint8)
+        b[..., 0:4] = (rng.uniform(1e-4, 2e-2, (out_dim, in_dim // 256, 2))).astype(np.float16).view(np.uint8)
+    else:  # Q6_K: quants, scales, then fp16 d
+        b = rng.integers(0, 256, (out_dim, in_dim // 256, 210), dtype=np.uint8)
+        b[..., 208:210] = (rng.uniform(1e-5, 1e-3, (out_dim, in_dim // 256, 1))).astype(np.float16).view(np.uint8)
+    return np.ascontiguousarray(b).reshape(-1)
+
+
+@pytest.mark.parametrize(
+    "w_type, shape",
+    [
+        (8, (3584, 3584, 64)),    # Q8_0 small-batch form: 8 K ranges merged in the kernel
+        (12, (3584, 3584, 64)),   # Q4_K small-batch form
+        (14, (3584, 3584, 64)),   # Q6_K small-batch form
+        (8, (5120, 1040, 64)),    # Q8_0 small-batch form walking its ranges in two passes
+        (12, (2048, 2048, 100)),  # Q4_K fp16 form above 64 rows: pre-pass, product, split-K reduce
+        (14, (2048, 2048, 100)),  # Q6_K fp16 form above 64 rows
+    ],
+    ids=["q8_small", "q4k_small", "q6k_small", "q8_passes", "q4k_large", "q6k_large"],
+)
+def test_captured_projection_replays_match_eager(torch_mod, gsp, ctx, w_type, shape):
+    """gsp_matmul_batch on the fp16 forms, captured after one eager call (which sizes the context's
+    buffers) and replayed: the small forms' per-tile counters return to zero at the end of every
+    launch, so every replay matches the eager product bit for bit, with eager work between replays,
+    and the graph holds kernel nodes only."""
+    torch = torch_mod
+    in_dim, out_dim, batch = shape
+    print(f"graph case matmul type={w_type} {shape}", flush=True)
+    rng = np.random.default_rng(1000 + w_type + batch)
+    wd = torch.from_numpy(_raw_weights(rng, w_type, out_dim, in_dim)).cuda()
+    xd = torch.from_numpy(rng.standard_normal((batch, in_dim)).astype(np.float32)).cuda()
+    eager = torch.full((batch, out_dim), float("nan"), device="cuda")
+    stream = torch.cuda.Stream()
+    ctx.set_stream(stream.cuda_stream)
+    try:
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            ctx.matmul_batch(w_type, wd.data_ptr(), xd.data_ptr(), eager.data_ptr(), in_dim, out_dim, batch)
+        stream.synchronize()
+        assert torch.isfinite(eager).all()
+        out = torch.full_like(eager, float("nan"))
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph(keep_graph=True)
+        with torch.cuda.graph(graph, stream=stream):
+            ctx.matmul_batch(w_type, wd.data_ptr(), xd.data_ptr(), out.data_ptr(), in_dim, out_dim, batch)
+        types = _graph_node_types(graph)
+        assert set(types) == {HIP_GRAPH_NODE_KERNEL}, types
+        graph.instantiate()
+        for rep in range(4):
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {rep} differs from the eager product"
+            with torch.cuda.stream(stream):
+                ctx.matmul_batch(w_type, wd.data_ptr(), xd.data_ptr(), eager.data_ptr(), in_dim, out_dim, batch)
+            stream.synchronize()
+        del graph
+    finally:
+        ctx.set_stream(None)
