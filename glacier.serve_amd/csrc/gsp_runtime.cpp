@@ -914,7 +914,10 @@ int gsp_matmul_batch(gsp_ctx* ctx, int32_t w_type, const void* w_dev, const floa
         const int64_t tiles = (out_dim + 63) / 64;
         const int64_t maxs = gsp::matmul_small_max_splits(batch);
         const int64_t lo = (chunks + gsp::matmul_small_chunks(batch) - 1) / gsp::matmul_small_chunks(batch);
-        const int64_t want = (2 * (int64_t)std::max(1, ctx->num_cus) + tiles - 1) / tiles;
+        // Rounded down, so the grid fits the slots in one round: rounded up it
+        // spilled a few workgroups into a second round (3584 x 3584 at 32 rows:
+        // 560 workgroups, Q8_0 19.9 us, against 448 and 16.9 us).
+        const int64_t want = std::max<int64_t>(1, 2 * (int64_t)std::max(1, ctx->num_cus) / tiles);
         int64_t splits = lo <= maxs ? std::max(lo, std::min({want, maxs, chunks}))
                                     : std::max<int64_t>((chunks + gsp::matmul_small_range_chunks_max() - 1) /
                                                             gsp::matmul_small_range_chunks_max(),

@@ -226,7 +226,7 @@ LONG_SHAPES = [
     (5120, 1040, 64),   # 8 ranges of 10 chunks: a full pass, then a 2-chunk one; one f4 per pre-pass thread
     (18944, 1040, 64),  # Qwen2.5-7B's FFN down-projection width: 8 ranges of 37 chunks, 5 passes
     (18944, 4100, 17),  # two M tiles, a ragged last weight-row tile
-    (6656, 6592, 40),   # 5 ranges of 21 chunks, the last of 20; a ragged batch tile
+    (6656, 6400, 40),   # 5 ranges of 21 chunks, the last of 20; a ragged batch tile
     (3584, 18944, 64),  # Qwen2.5-7B's gate/up projection: 7 ranges of 296 tiles
     (4096, 16384, 24),  # two M tiles: 8 ranges of 256 tiles
     (512, 65536, 1),    # one range of 1024 tiles, y stored directly
